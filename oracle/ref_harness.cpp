@@ -1,0 +1,411 @@
+// Driver around the reference's own source — TEST INFRASTRUCTURE ONLY.
+//
+// Built by oracle/Makefile into oracle/_ref/libnitro_ref.so, compiling
+// src/model_q8.cpp (which includes src/pagedMemory.hpp) from where it lies
+// under the reference checkout, with the reference's flags.  Nothing from the
+// reference is copied here: this file only instantiates the reference's types
+// and calls its functions so that tests/golden/make_golden.py can record
+// golden vectors (block-manager traces, prefix-cache state, and attention
+// outputs of forward_decode_batch / forward_paged / forward_prefill_chunk /
+// forward) and so that CPU tests can cross-check the oracle live.
+//
+// Attention outputs are observed through s->xb2 = wo . xb with wo the Q8
+// identity.  forward_paged and forward use the full-row Q8 matmul, so all of
+// xb is observable there.  forward_decode_batch and forward_prefill_chunk use
+// matmul_bulk, whose block loop keeps only the last 32-column block
+// (src/model_q8.cpp:390-417), so only the last 32 entries of each row of xb
+// are observable through xb2 in those paths.
+//
+// The reference terminates the process on pool exhaustion
+// (src/pagedMemory.hpp:96,117,212); here `exit` is turned into a C++
+// exception so a trace can record the failure and continue.
+
+#include <immintrin.h>
+#include <omp.h>
+#include <fcntl.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <iomanip>
+#include <iostream>
+#include <list>
+#include <queue>
+#include <stdexcept>
+#include <unordered_map>
+#include <vector>
+
+struct RefExit {
+    int code;
+};
+#define exit(code) throw RefExit{code}
+#define private public
+#include "model_q8.cpp"
+#undef private
+#undef exit
+
+namespace {
+
+uint64_t splitmix64(uint64_t& s) {
+    uint64_t z = (s += 0x9E3779B97F4A7C15ULL);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+float uniform_pm1(uint64_t& s) {  // uniform in [-1, 1)
+    return (float)((double)(splitmix64(s) >> 11) * (1.0 / 9007199254740992.0) * 2.0 - 1.0);
+}
+
+struct World {
+    Config_Transformer c{};
+    Transformer_Weights w{};
+    RunState s{};
+    KVBlock_Manager* mem = nullptr;
+    PrefixCacheManager* cache = nullptr;
+    std::vector<Request*> reqs;  // slot -> request (owns its Sequence)
+    std::vector<float> emb, rms1, rms2, rms3, fcr, fci;
+    std::vector<BlockQ8> wq, wk, wv, wo, w1, w2, w3;
+    int kv_dim = 0, head_size = 0, max_rows = 0, total_blocks = 0;
+    std::vector<float> key_cache, value_cache;
+};
+
+void fill_q8(std::vector<BlockQ8>& m, int rows, int cols, uint64_t& rng, float scale) {
+    m.resize((size_t)rows * cols / Q_BLOCK_SIZE);
+    for (auto& b : m) {
+        b.scale = scale;
+        for (int i = 0; i < Q_BLOCK_SIZE; i++) b.weights[i] = (int8_t)((int)(splitmix64(rng) % 255) - 127);
+    }
+}
+void identity_q8(std::vector<BlockQ8>& m, int rows, int cols) {
+    m.assign((size_t)rows * cols / Q_BLOCK_SIZE, BlockQ8{});
+    int nb = cols / Q_BLOCK_SIZE;
+    for (auto& b : m) {
+        b.scale = 1.0f;
+        std::memset(b.weights, 0, sizeof(b.weights));
+    }
+    for (int i = 0; i < rows && i < cols; i++) m[(size_t)i * nb + i / Q_BLOCK_SIZE].weights[i % Q_BLOCK_SIZE] = 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t ref_hash_block_state(uint64_t parent, const int* tokens, int n) {
+    std::vector<int> t(tokens, tokens + n);
+    return hash_block_state(parent, t);
+}
+
+void ref_set_threads(int n) { omp_set_num_threads(n); }
+
+// A tiny Llama-shaped model around a KVBlock_Manager/PrefixCacheManager pair.
+// dim and kv_dim must be multiples of 32 (Q8 blocks); RoPE tables are the
+// identity rotation so K/V rows in the pool are exactly the computed k/v.
+void* ref_world_create(int n_heads, int n_kv_heads, int head_size, int n_layers, int vocab,
+                       int seq_len, int total_blocks, int max_rows, int max_seqs, uint64_t seed) {
+    World* W = new World();
+    Config_Transformer& c = W->c;
+    c.dim = n_heads * head_size;
+    c.hidden_dim = 32;
+    c.n_layers = n_layers;
+    c.n_heads = n_heads;
+    c.n_kv_heads = n_kv_heads;
+    c.vocab_size = vocab;
+    c.seq_len = seq_len;
+    W->head_size = head_size;
+    W->kv_dim = n_kv_heads * head_size;
+    W->max_rows = max_rows;
+    W->total_blocks = total_blocks;
+    uint64_t rng = seed;
+    W->emb.resize((size_t)vocab * c.dim);
+    for (auto& x : W->emb) x = uniform_pm1(rng);
+    W->rms1.assign((size_t)n_layers * c.dim, 1.0f);
+    W->rms2.assign((size_t)n_layers * c.dim, 1.0f);
+    W->rms3.assign(c.dim, 1.0f);
+    W->fcr.assign((size_t)seq_len * head_size / 2, 1.0f);
+    W->fci.assign((size_t)seq_len * head_size / 2, 0.0f);
+    fill_q8(W->wq, n_layers * c.dim, c.dim, rng, 1.0f / 64);
+    fill_q8(W->wk, n_layers * W->kv_dim, c.dim, rng, 1.0f / 64);
+    fill_q8(W->wv, n_layers * W->kv_dim, c.dim, rng, 1.0f / 64);
+    // wo = identity per layer
+    W->wo.clear();
+    for (int l = 0; l < n_layers; l++) {
+        std::vector<BlockQ8> one;
+        identity_q8(one, c.dim, c.dim);
+        W->wo.insert(W->wo.end(), one.begin(), one.end());
+    }
+    fill_q8(W->w1, n_layers * c.hidden_dim, c.dim, rng, 1.0f / 64);
+    fill_q8(W->w3, n_layers * c.hidden_dim, c.dim, rng, 1.0f / 64);
+    fill_q8(W->w2, n_layers * c.dim, c.hidden_dim, rng, 0.0f);
+    Transformer_Weights& w = W->w;
+    w.token_embedding_table = W->emb.data();
+    w.rms_attn_weights = W->rms1.data();
+    w.wq = W->wq.data();
+    w.wk = W->wk.data();
+    w.wv = W->wv.data();
+    w.wo = W->wo.data();
+    w.rms_ffn_weight = W->rms2.data();
+    w.w1 = W->w1.data();
+    w.w2 = W->w2.data();
+    w.w3 = W->w3.data();
+    w.freq_cis_real = W->fcr.data();
+    w.freq_cis_imag = W->fci.data();
+    w.rms_final_weight = W->rms3.data();
+    w.wcls = W->emb.data();
+    RunState& s = W->s;
+    s.x = (float*)calloc((size_t)max_rows * c.dim, sizeof(float));
+    s.xb = (float*)calloc((size_t)max_rows * c.dim, sizeof(float));
+    s.xb2 = (float*)calloc((size_t)max_rows * c.dim, sizeof(float));
+    s.hb = (float*)calloc((size_t)max_rows * c.hidden_dim, sizeof(float));
+    s.hb2 = (float*)calloc((size_t)max_rows * c.hidden_dim, sizeof(float));
+    s.q = (float*)calloc((size_t)max_rows * c.dim, sizeof(float));
+    s.k = (float*)calloc((size_t)max_rows * W->kv_dim, sizeof(float));
+    s.v = (float*)calloc((size_t)max_rows * W->kv_dim, sizeof(float));
+    s.logits = (float*)calloc((size_t)max_rows * vocab, sizeof(float));
+    s.attn = (float*)calloc((size_t)max_rows * n_heads * seq_len, sizeof(float));
+    W->key_cache.assign((size_t)n_layers * seq_len * W->kv_dim, 0.0f);
+    W->value_cache.assign((size_t)n_layers * seq_len * W->kv_dim, 0.0f);
+    s.key_cache = W->key_cache.data();
+    s.value_cache = W->value_cache.data();
+    W->mem = new KVBlock_Manager(total_blocks, n_layers, W->kv_dim);
+    W->cache = new PrefixCacheManager(*W->mem, total_blocks);
+    W->reqs.assign(max_seqs, nullptr);
+    return W;
+}
+
+void ref_world_destroy(void* p) {
+    World* W = (World*)p;
+    for (auto* r : W->reqs) delete r;
+    delete W->cache;
+    delete W->mem;
+    RunState& s = W->s;
+    free(s.x); free(s.xb); free(s.xb2); free(s.hb); free(s.hb2);
+    free(s.q); free(s.k); free(s.v); free(s.logits); free(s.attn);
+    delete W;
+}
+
+int ref_world_dims(void* p, int* out) {
+    World* W = (World*)p;
+    out[0] = W->c.dim;
+    out[1] = W->kv_dim;
+    out[2] = W->c.n_layers;
+    out[3] = W->total_blocks;
+    out[4] = (int)W->reqs.size();
+    return 0;
+}
+
+// ---- block manager / prefix cache / sequence operations -------------------
+// Returns 0 on success, 1 when the reference called exit().
+enum {
+    OP_ALLOC = 1, OP_INC = 2, OP_FREE = 3, OP_FORCE_FREE = 4, OP_CHECK = 5, OP_INSERT = 6,
+    OP_EVICT = 7, OP_SEQ_NEW = 8, OP_SEQ_APPEND = 9, OP_SEQ_FLUSH = 10, OP_SEQ_RELEASE = 11,
+    OP_INGEST = 12, OP_FREE_COUNT = 13, OP_IS_CACHED = 14
+};
+
+int ref_op(void* p, int op, int a, int b, uint64_t h, const int* toks, int ntoks, int64_t* result) {
+    World* W = (World*)p;
+    KVBlock_Manager& mem = *W->mem;
+    PrefixCacheManager& cache = *W->cache;
+    *result = 0;
+    try {
+        switch (op) {
+            case OP_ALLOC: *result = mem.allocate_block(cache); break;
+            case OP_INC: mem.inc_ref_count(a, cache); break;
+            case OP_FREE: mem.free_block(a, cache); break;
+            case OP_FORCE_FREE: mem.force_free_block(a); break;
+            case OP_CHECK: *result = cache.check_cache(h); break;
+            case OP_INSERT: cache.insert_cache(h, a, b); break;
+            case OP_EVICT: cache.evict_lru_block(); break;
+            case OP_FREE_COUNT: *result = mem.get_free_count(); break;
+            case OP_IS_CACHED: *result = cache.is_cached(a) ? 1 : 0; break;
+            case OP_SEQ_NEW: {
+                delete W->reqs[a];
+                std::vector<int> prompt(toks, toks + ntoks);
+                W->reqs[a] = new Request(a, prompt);
+                break;
+            }
+            case OP_SEQ_APPEND: W->reqs[a]->seq.allocate_next_token(b, mem, cache); break;
+            case OP_SEQ_FLUSH: W->reqs[a]->seq.flush_cache(cache); break;
+            case OP_SEQ_RELEASE: W->reqs[a]->seq.release(mem, cache); break;
+            case OP_INGEST: {
+                std::vector<int> prompt(toks, toks + ntoks);
+                *result = ingest_prompt(prompt, W->reqs[a]->seq, mem, cache, &W->c, &W->w, &W->s, b != 0);
+                break;
+            }
+            default: return 2;
+        }
+    } catch (const RefExit&) {
+        return 1;
+    }
+    return 0;
+}
+
+// Serialises the bookkeeping state into an int32 stream:
+//   free_list [n, ids...]; per block [ref_count, num_tokens, parent_id, child_count];
+//   evictable_leaves front->back [n, ids...]; cache_map sorted by hash [n, (lo, hi, id)...];
+//   reverse_map sorted by id [n, (id, lo, hi)...]; per sequence slot
+//   [exists, logical_token_count, hash lo, hash hi, |buffer|, buffer..., |table|, table...].
+int ref_snapshot(void* p, int32_t* buf, int cap) {
+    World* W = (World*)p;
+    std::vector<int32_t> o;
+    KVBlock_Manager& mem = *W->mem;
+    PrefixCacheManager& cache = *W->cache;
+    o.push_back((int32_t)mem.free_list.size());
+    for (int id : mem.free_list) o.push_back(id);
+    for (auto& b : mem.blocks) {
+        o.push_back(b.ref_count);
+        o.push_back(b.num_tokens);
+        o.push_back(b.parent_id);
+        o.push_back(b.child_count);
+    }
+    o.push_back((int32_t)cache.evictable_leaves.size());
+    for (int id : cache.evictable_leaves) o.push_back(id);
+    std::vector<std::pair<uint64_t, int>> cm(cache.cache_map.begin(), cache.cache_map.end());
+    std::sort(cm.begin(), cm.end());
+    o.push_back((int32_t)cm.size());
+    for (auto& e : cm) {
+        o.push_back((int32_t)(uint32_t)(e.first & 0xffffffffu));
+        o.push_back((int32_t)(uint32_t)(e.first >> 32));
+        o.push_back(e.second);
+    }
+    std::vector<std::pair<int, uint64_t>> rm(cache.reverse_map.begin(), cache.reverse_map.end());
+    std::sort(rm.begin(), rm.end());
+    o.push_back((int32_t)rm.size());
+    for (auto& e : rm) {
+        o.push_back(e.first);
+        o.push_back((int32_t)(uint32_t)(e.second & 0xffffffffu));
+        o.push_back((int32_t)(uint32_t)(e.second >> 32));
+    }
+    for (auto* r : W->reqs) {
+        if (!r) {
+            o.push_back(0);
+            continue;
+        }
+        Sequence& q = r->seq;
+        o.push_back(1);
+        o.push_back(q.logical_token_count);
+        o.push_back((int32_t)(uint32_t)(q.current_hash & 0xffffffffu));
+        o.push_back((int32_t)(uint32_t)(q.current_hash >> 32));
+        o.push_back((int32_t)q.token_buffer.size());
+        for (int t : q.token_buffer) o.push_back(t);
+        o.push_back((int32_t)q.block_table.size());
+        for (int t : q.block_table) o.push_back(t);
+    }
+    if ((int)o.size() > cap) return -(int)o.size();
+    std::memcpy(buf, o.data(), o.size() * sizeof(int32_t));
+    return (int)o.size();
+}
+
+// ---- forward passes (attention observed through xb2) ----------------------
+
+int ref_decode_batch(void* p, const int* slots, const int* tokens, int B, int* positions_out) {
+    World* W = (World*)p;
+    std::vector<int> toks(tokens, tokens + B), pos(B);
+    std::vector<Request*> rs(B);
+    for (int b = 0; b < B; b++) {
+        rs[b] = W->reqs[slots[b]];
+        pos[b] = rs[b]->seq.logical_token_count;
+        positions_out[b] = pos[b];
+    }
+    try {
+        forward_decode_batch(toks, pos, rs, &W->c, &W->w, &W->s, *W->mem, *W->cache);
+    } catch (const RefExit&) {
+        return 1;
+    }
+    return 0;
+}
+
+int ref_forward_paged(void* p, int slot, int token, int* pos_out) {
+    World* W = (World*)p;
+    Sequence& q = W->reqs[slot]->seq;
+    int pos = q.logical_token_count;
+    *pos_out = pos;
+    try {
+        forward_paged(token, pos, &W->c, &W->w, &W->s, q, *W->mem, *W->cache);
+    } catch (const RefExit&) {
+        return 1;
+    }
+    return 0;
+}
+
+int ref_prefill_chunk(void* p, int slot, const int* tokens, int n, int* start_pos_out) {
+    World* W = (World*)p;
+    Sequence& q = W->reqs[slot]->seq;
+    std::vector<int> toks(tokens, tokens + n);
+    *start_pos_out = q.logical_token_count;
+    try {
+        forward_prefill_chunk(toks, q.logical_token_count, &W->c, &W->w, &W->s, q, *W->mem, *W->cache);
+    } catch (const RefExit&) {
+        return 1;
+    }
+    return 0;
+}
+
+int ref_forward_contiguous(void* p, int token, int pos) {
+    World* W = (World*)p;
+    forward(token, pos, &W->c, &W->w, &W->s);
+    return 0;
+}
+
+// Copies rows [0, rows) of s->q, s->k, s->v (post-RoPE inputs of the last
+// layer's attention) and s->xb2 (= wo . attention output).
+int ref_read_rows(void* p, int rows, float* q, float* k, float* v, float* xb2) {
+    World* W = (World*)p;
+    if (rows > W->max_rows) return 1;
+    std::memcpy(q, W->s.q, sizeof(float) * (size_t)rows * W->c.dim);
+    std::memcpy(k, W->s.k, sizeof(float) * (size_t)rows * W->kv_dim);
+    std::memcpy(v, W->s.v, sizeof(float) * (size_t)rows * W->kv_dim);
+    std::memcpy(xb2, W->s.xb2, sizeof(float) * (size_t)rows * W->c.dim);
+    return 0;
+}
+
+static size_t pool_floats(World* W) {
+    return (size_t)W->total_blocks * W->c.n_layers * BLOCK_SIZE * W->kv_dim;
+}
+
+int ref_read_pool(void* p, float* k_pool, float* v_pool) {
+    World* W = (World*)p;
+    KVBlock_Manager& mem = *W->mem;
+    std::memcpy(k_pool, mem.global_k_pool, sizeof(float) * pool_floats(W));
+    std::memcpy(v_pool, mem.global_v_pool, sizeof(float) * pool_floats(W));
+    return 0;
+}
+
+int ref_write_pool(void* p, const float* k_pool, const float* v_pool) {
+    World* W = (World*)p;
+    KVBlock_Manager& mem = *W->mem;
+    std::memcpy(mem.global_k_pool, k_pool, sizeof(float) * pool_floats(W));
+    std::memcpy(mem.global_v_pool, v_pool, sizeof(float) * pool_floats(W));
+    return 0;
+}
+
+int ref_read_contiguous_cache(void* p, float* key_cache, float* value_cache) {
+    World* W = (World*)p;
+    std::memcpy(key_cache, W->key_cache.data(), sizeof(float) * W->key_cache.size());
+    std::memcpy(value_cache, W->value_cache.data(), sizeof(float) * W->value_cache.size());
+    return 0;
+}
+
+int ref_write_contiguous_cache(void* p, const float* key_cache, const float* value_cache) {
+    World* W = (World*)p;
+    std::memcpy(W->key_cache.data(), key_cache, sizeof(float) * W->key_cache.size());
+    std::memcpy(W->value_cache.data(), value_cache, sizeof(float) * W->value_cache.size());
+    return 0;
+}
+
+int ref_block_table(void* p, int slot, int* out, int cap) {
+    World* W = (World*)p;
+    if (!W->reqs[slot]) return -1;
+    auto& t = W->reqs[slot]->seq.block_table;
+    if ((int)t.size() > cap) return -(int)t.size();
+    for (size_t i = 0; i < t.size(); i++) out[i] = t[i];
+    return (int)t.size();
+}
+
+}  // extern "C"

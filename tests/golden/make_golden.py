@@ -1,0 +1,359 @@
+"""Records golden vectors from the reference's own compiled code.
+
+Run in a container that has the reference checkout (needs oracle/_ref, built
+by `make -C oracle ref`):
+
+    python tests/golden/make_golden.py
+
+Writes, next to this script:
+  fnv.json                   hash_block_state outputs (src/pagedMemory.hpp:14-24)
+  block_manager_traces.json  op scripts over KVBlock_Manager / PrefixCacheManager /
+                             Sequence / ingest_prompt with, per op, the status, the
+                             result and a digest of the full bookkeeping state, plus
+                             the final state (src/pagedMemory.hpp:86-285,
+                             src/model_q8.cpp:695-724)
+  attention.json + attention.npz
+                             inputs and outputs of forward_decode_batch, forward_paged,
+                             forward_prefill_chunk (fresh, continued, after a prefix
+                             hit) and forward, observed through xb2 (see
+                             oracle/ref_harness.cpp).  Pools are regenerated in the
+                             tests from counter_pool(seed); the npz holds q, the K/V
+                             rows written by the call, the block tables and the
+                             observed outputs.  Pool digests are over the observed
+                             layer only.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import random
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, HERE)
+
+from oracle import paged_memory as pm  # noqa: E402
+from oracle import ref  # noqa: E402
+from synth import counter_pool  # noqa: E402
+
+
+def state_digest(snap: dict) -> str:
+    return hashlib.sha256(json.dumps(snap, sort_keys=True, separators=(",", ":"))
+                          .encode()).hexdigest()[:16]
+
+
+def array_digest(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()[:16]
+
+
+# ---------------------------------------------------------------- FNV -------
+def make_fnv():
+    rng = random.Random(0xF17)
+    cases = []
+    for n in [0, 1, 2, 15, 16, 16, 16, 17, 33, 64]:
+        toks = [rng.randrange(-2**31, 2**31) if rng.random() < 0.3 else rng.randrange(0, 32000)
+                for _ in range(n)]
+        parent = pm.FNV_OFFSET_BASIS if rng.random() < 0.5 else rng.getrandbits(64)
+        cases.append({"parent": parent, "tokens": toks,
+                      "hash": ref.hash_block_state(parent, toks)})
+    shared = [263] * 16  # the reference benchmark's shared prompt token (src/model_q8.cpp:788)
+    h = pm.FNV_OFFSET_BASIS
+    chain = []
+    for _ in range(16):
+        h = ref.hash_block_state(h, shared)
+        chain.append(h)
+    return {"cases": cases, "shared_263_chain": chain}
+
+
+# ---------------------------------------------------- block manager traces --
+def run_trace(name, total_blocks, max_seqs, ops):
+    W = ref.RefWorld(n_heads=2, n_kv_heads=2, head_dim=16, n_layers=1, vocab=512, seq_len=512,
+                     total_blocks=total_blocks, max_rows=512, max_seqs=max_seqs, seed=3)
+    steps = []
+    for op in ops:
+        st, res = W.op(op["op"], op.get("a", 0), op.get("b", 0), op.get("h", 0),
+                       op.get("toks", ()))
+        steps.append([st, res, state_digest(W.snapshot())])
+    final = W.snapshot()
+    W.close()
+    return {"name": name, "total_blocks": total_blocks, "max_seqs": max_seqs, "ops": ops,
+            "steps": steps, "final": final}
+
+
+def seq_workload(seed, total_blocks, max_seqs, n_ops, families=3, max_tokens=380):
+    """Sequences ingesting prompts from a few shared-prefix families, appending,
+    flushing and releasing, under pool pressure (evictions, exhaustion)."""
+    rng = random.Random(seed)
+    fams = [[rng.randrange(1, 500) for _ in range(rng.choice([16, 32, 48, 64]))]
+            for _ in range(families)]
+    live = {}
+    ops = []
+    for _ in range(n_ops):
+        r = rng.random()
+        free_slots = [s for s in range(max_seqs) if s not in live]
+        if free_slots and (r < 0.25 or not live):
+            s = rng.choice(free_slots)
+            ops.append({"op": pm.OP_SEQ_NEW, "a": s})
+            fam = rng.choice(fams)
+            tail = [rng.randrange(1, 500) for _ in range(rng.randrange(0, 40))]
+            prompt = fam[: rng.choice([len(fam), len(fam) - 16 if len(fam) > 16 else len(fam)])] + tail
+            if rng.random() < 0.2:
+                prompt = [rng.randrange(1, 500) for _ in range(rng.randrange(1, 50))]
+            ops.append({"op": pm.OP_INGEST, "a": s, "b": int(rng.random() < 0.8), "toks": prompt})
+            live[s] = len(prompt)
+        elif r < 0.55:
+            s = rng.choice(list(live))
+            for _ in range(rng.randrange(1, 20)):
+                if live[s] >= max_tokens:
+                    break
+                ops.append({"op": pm.OP_SEQ_APPEND, "a": s, "b": rng.randrange(1, 500)})
+                live[s] += 1
+        elif r < 0.65:
+            s = rng.choice(list(live))
+            ops.append({"op": pm.OP_SEQ_FLUSH, "a": s})
+        elif r < 0.85:
+            s = rng.choice(list(live))
+            ops.append({"op": pm.OP_SEQ_RELEASE, "a": s})
+            del live[s]
+        elif r < 0.9:
+            ops.append({"op": pm.OP_FREE_COUNT})
+        else:
+            ops.append({"op": pm.OP_IS_CACHED, "a": rng.randrange(total_blocks)})
+    return ops
+
+
+def low_level_workload(seed, total_blocks, n_ops):
+    rng = random.Random(seed)
+    hashes = [rng.getrandbits(64) for _ in range(12)]
+    ops = []
+    allocated = []
+    for _ in range(n_ops):
+        r = rng.random()
+        if r < 0.3:
+            ops.append({"op": pm.OP_ALLOC})
+            allocated.append(None)
+        elif r < 0.4:
+            ops.append({"op": pm.OP_INC, "a": rng.randrange(total_blocks)})
+        elif r < 0.6:
+            ops.append({"op": pm.OP_FREE, "a": rng.randrange(total_blocks)})
+        elif r < 0.62:
+            ops.append({"op": pm.OP_FORCE_FREE, "a": rng.randrange(total_blocks)})
+        elif r < 0.8:
+            parent = -1 if rng.random() < 0.4 else rng.randrange(total_blocks)
+            ops.append({"op": pm.OP_INSERT, "a": rng.randrange(total_blocks), "b": parent,
+                        "h": rng.choice(hashes)})
+        elif r < 0.9:
+            ops.append({"op": pm.OP_CHECK, "h": rng.choice(hashes)})
+        elif r < 0.95:
+            ops.append({"op": pm.OP_EVICT})
+        else:
+            ops.append({"op": pm.OP_FREE_COUNT})
+    return ops
+
+
+def exp4_workload():
+    """The reference benchmark's prefix-cache experiment shape (src/model_q8.cpp:917-939):
+    user A ingests 256 x token 263 and flushes; user B hits every page."""
+    p = [263] * 256
+    return [{"op": pm.OP_SEQ_NEW, "a": 0}, {"op": pm.OP_INGEST, "a": 0, "b": 1, "toks": p},
+            {"op": pm.OP_SEQ_FLUSH, "a": 0}, {"op": pm.OP_SEQ_NEW, "a": 1},
+            {"op": pm.OP_INGEST, "a": 1, "b": 1, "toks": p}, {"op": pm.OP_SEQ_FLUSH, "a": 1},
+            {"op": pm.OP_SEQ_APPEND, "a": 1, "b": 7}, {"op": pm.OP_SEQ_RELEASE, "a": 0},
+            {"op": pm.OP_SEQ_RELEASE, "a": 1}, {"op": pm.OP_FREE_COUNT}]
+
+
+def make_traces():
+    return [
+        run_trace("seq_pressure_24", 24, 6, seq_workload(11, 24, 6, 160)),
+        run_trace("seq_roomy_96", 96, 8, seq_workload(12, 96, 8, 220, families=4)),
+        run_trace("seq_tight_12", 12, 4, seq_workload(13, 12, 4, 120, families=2, max_tokens=120)),
+        run_trace("low_level_16", 16, 1, low_level_workload(14, 16, 300)),
+        run_trace("low_level_40", 40, 1, low_level_workload(15, 40, 400)),
+        run_trace("exp4_shared_prompt", 1000 // 10, 2, exp4_workload()),
+    ]
+
+
+# ------------------------------------------------------------- attention ---
+class Recorder:
+    def __init__(self):
+        self.meta = []
+        self.arrays = {}
+
+    def add(self, name, meta, **arrays):
+        meta = dict(meta, name=name)
+        self.meta.append(meta)
+        for k, v in arrays.items():
+            self.arrays[f"{name}/{k}"] = v
+
+
+def tables_of(W, slots, max_pages):
+    t = np.zeros((len(slots), max_pages), dtype=np.int32)
+    for i, s in enumerate(slots):
+        bt = W.block_table(s)
+        t[i, : len(bt)] = bt
+    return t
+
+
+def case_decode(rec, name, H, Hkv, hd, L, blocks, lens, seed):
+    W = ref.RefWorld(n_heads=H, n_kv_heads=Hkv, head_dim=hd, n_layers=L, total_blocks=blocks,
+                     seed=seed, max_seqs=len(lens))
+    for s, n in enumerate(lens):
+        W.op(pm.OP_SEQ_NEW, s)
+        for t in range(n):
+            W.op(pm.OP_SEQ_APPEND, s, 1 + (t * 7 + s) % 400)
+    pool_seed = 1000 + seed
+    W.write_pool(counter_pool(pool_seed, blocks, L, W.kv_dim),
+                 counter_pool(pool_seed + 1, blocks, L, W.kv_dim))
+    toks = [5 + 3 * s for s in range(len(lens))]
+    pos = W.decode_batch(list(range(len(lens))), toks)
+    q, k, v, xb2 = W.rows(len(lens))
+    max_pages = max(p // 16 + 1 for p in pos) + 1
+    tables = tables_of(W, range(len(lens)), max_pages)
+    kp, vp = W.pool()
+    rec.add(name, {"kind": "decode_batch", "H": H, "Hkv": Hkv, "hd": hd, "layers": L,
+                   "pages": blocks, "layer": L - 1, "pool_seed": pool_seed, "observed": 32,
+                   "k_pool_digest": array_digest(kp[:, L - 1]),
+                   "v_pool_digest": array_digest(vp[:, L - 1])},
+            q=q, k=k, v=v, xb2_obs=xb2[:, -32:], tables=tables, positions=pos)
+    W.close()
+
+
+def case_single(rec, name, H, Hkv, hd, L, blocks, n_past, seed):
+    W = ref.RefWorld(n_heads=H, n_kv_heads=Hkv, head_dim=hd, n_layers=L, total_blocks=blocks,
+                     seed=seed, max_seqs=1)
+    W.op(pm.OP_SEQ_NEW, 0)
+    for t in range(n_past):
+        W.op(pm.OP_SEQ_APPEND, 0, 1 + (t * 5) % 300)
+    pool_seed = 2000 + seed
+    W.write_pool(counter_pool(pool_seed, blocks, L, W.kv_dim),
+                 counter_pool(pool_seed + 1, blocks, L, W.kv_dim))
+    pos = W.forward_paged(0, 42)
+    q, k, v, xb2 = W.rows(1)
+    table = W.block_table(0)
+    kp, vp = W.pool()
+    rec.add(name, {"kind": "decode_single", "H": H, "Hkv": Hkv, "hd": hd, "layers": L,
+                   "pages": blocks, "layer": L - 1, "pool_seed": pool_seed, "pos": int(pos),
+                   "observed": H * hd, "k_pool_digest": array_digest(kp[:, L - 1]),
+                   "v_pool_digest": array_digest(vp[:, L - 1])},
+            q=q, k=k, v=v, xb2_obs=xb2, table=table)
+    W.close()
+
+
+def case_prefill(rec, name, H, Hkv, hd, L, blocks, chunks, seed):
+    """One sequence, prefill chunks of the given sizes; records the last chunk."""
+    W = ref.RefWorld(n_heads=H, n_kv_heads=Hkv, head_dim=hd, n_layers=L, total_blocks=blocks,
+                     seed=seed, max_seqs=1)
+    W.op(pm.OP_SEQ_NEW, 0)
+    pool_seed = 3000 + seed
+    W.write_pool(counter_pool(pool_seed, blocks, L, W.kv_dim),
+                 counter_pool(pool_seed + 1, blocks, L, W.kv_dim))
+    earlier_k, earlier_v, starts = [], [], []
+    tok = 1
+    for ci, n in enumerate(chunks):
+        toks = list(range(tok, tok + n))
+        tok += n
+        sp = W.prefill_chunk(0, toks)
+        starts.append(sp)
+        q, k, v, xb2 = W.rows(n)
+        if ci < len(chunks) - 1:
+            earlier_k.append(k)
+            earlier_v.append(v)
+    table = W.block_table(0)
+    kp, vp = W.pool()
+    arrays = dict(q=q, k=k, v=v, xb2_obs=xb2[:, -32:], table=table,
+                  chunk_starts=np.array(starts, dtype=np.int32))
+    if earlier_k:
+        arrays["earlier_k"] = np.concatenate(earlier_k)
+        arrays["earlier_v"] = np.concatenate(earlier_v)
+    rec.add(name, {"kind": "prefill", "H": H, "Hkv": Hkv, "hd": hd, "layers": L,
+                   "pages": blocks, "layer": L - 1, "pool_seed": pool_seed,
+                   "start_pos": int(starts[-1]), "observed": 32,
+                   "k_pool_digest": array_digest(kp[:, L - 1]),
+                   "v_pool_digest": array_digest(vp[:, L - 1])}, **arrays)
+    W.close()
+
+
+def case_prefix_hit(rec, name, H, Hkv, hd, L, blocks, shared, tail_a, tail_b, seed):
+    """Seq A ingests shared+tail_a with the prefix cache on and flushes; seq B
+    ingests shared+tail_b, hits the shared pages and prefills only its tail."""
+    W = ref.RefWorld(n_heads=H, n_kv_heads=Hkv, head_dim=hd, n_layers=L, total_blocks=blocks,
+                     seed=seed, max_seqs=2)
+    pool_seed = 4000 + seed
+    W.write_pool(counter_pool(pool_seed, blocks, L, W.kv_dim),
+                 counter_pool(pool_seed + 1, blocks, L, W.kv_dim))
+    base = list(range(100, 100 + shared))
+    pa = base + list(range(300, 300 + tail_a))
+    pb = base + list(range(400, 400 + tail_b))
+    W.op(pm.OP_SEQ_NEW, 0)
+    W.op(pm.OP_INGEST, 0, 1, toks=pa)
+    qa, ka, va, _ = W.rows(len(pa))
+    W.op(pm.OP_SEQ_FLUSH, 0)
+    W.op(pm.OP_SEQ_NEW, 1)
+    st, count = W.op(pm.OP_INGEST, 1, 1, toks=pb)
+    hits = shared // 16
+    n_b = len(pb) - 16 * hits
+    qb, kb, vb, xb2 = W.rows(n_b)
+    ta, tb = W.block_table(0), W.block_table(1)
+    kp, vp = W.pool()
+    rec.add(name, {"kind": "prefix_hit", "H": H, "Hkv": Hkv, "hd": hd, "layers": L,
+                   "pages": blocks, "layer": L - 1, "pool_seed": pool_seed,
+                   "start_pos": 16 * hits, "hits": hits, "observed": 32,
+                   "k_pool_digest": array_digest(kp[:, L - 1]),
+                   "v_pool_digest": array_digest(vp[:, L - 1])},
+            q=qb, k=kb, v=vb, xb2_obs=xb2[:, -32:], table=tb, table_a=ta, k_a=ka, v_a=va)
+    W.close()
+
+
+def case_contiguous(rec, name, H, Hkv, hd, n_pos, seed):
+    W = ref.RefWorld(n_heads=H, n_kv_heads=Hkv, head_dim=hd, n_layers=1, total_blocks=4,
+                     seed=seed, max_seqs=1, seq_len=256)
+    for pos in range(n_pos):
+        W.forward_contiguous(1 + (pos * 11) % 400, pos)
+    q, k, v, xb2 = W.rows(1)
+    kc, vc = W.contiguous_cache()
+    rec.add(name, {"kind": "contiguous", "H": H, "Hkv": Hkv, "hd": hd, "pos": n_pos - 1,
+                   "observed": H * hd},
+            q=q, xb2_obs=xb2, key_rows=kc[0, :n_pos], value_rows=vc[0, :n_pos])
+    W.close()
+
+
+def make_attention():
+    rec = Recorder()
+    case_decode(rec, "decode_mha_hd16_l2", 4, 4, 16, 2, 24, [0, 15, 16, 37], 21)
+    case_decode(rec, "decode_gqa_h8kv2_hd16", 8, 2, 16, 1, 32, [3, 31, 32, 50, 64], 22)
+    case_decode(rec, "decode_hd64", 2, 2, 64, 1, 32, [1, 47, 80], 23)
+    case_decode(rec, "decode_hd128", 1, 1, 128, 1, 16, [0, 20, 33], 24)
+    case_single(rec, "single_hd32_l2", 4, 4, 32, 2, 16, 45, 31)
+    case_single(rec, "single_gqa_hd64", 4, 2, 64, 1, 16, 70, 32)
+    case_single(rec, "single_pos0", 2, 2, 64, 1, 8, 0, 33)
+    case_prefill(rec, "prefill_fresh_hd16_l2", 4, 4, 16, 2, 16, [37], 41)
+    case_prefill(rec, "prefill_continued_gqa", 4, 2, 16, 1, 16, [20, 25], 42)
+    case_prefill(rec, "prefill_hd64", 2, 2, 64, 1, 16, [33], 43)
+    case_prefix_hit(rec, "prefix_hit_gqa_l2", 4, 2, 16, 2, 24, 32, 8, 20, 51)
+    case_contiguous(rec, "contiguous_hd16", 4, 4, 16, 30, 61)
+    case_contiguous(rec, "contiguous_gqa_hd32", 4, 2, 32, 19, 62)
+    return rec
+
+
+def main():
+    if not ref.available():
+        sys.exit("oracle/_ref/libnitro_ref.so is missing: run `make -C oracle ref` first")
+    with open(os.path.join(HERE, "fnv.json"), "w") as f:
+        json.dump(make_fnv(), f, indent=0)
+    with open(os.path.join(HERE, "block_manager_traces.json"), "w") as f:
+        json.dump(make_traces(), f, separators=(",", ":"))
+    rec = make_attention()
+    with open(os.path.join(HERE, "attention.json"), "w") as f:
+        json.dump(rec.meta, f, indent=1)
+    np.savez_compressed(os.path.join(HERE, "attention.npz"), **rec.arrays)
+    for fn in ("fnv.json", "block_manager_traces.json", "attention.json", "attention.npz"):
+        print(fn, os.path.getsize(os.path.join(HERE, fn)))
+
+
+if __name__ == "__main__":
+    main()
