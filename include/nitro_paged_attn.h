@@ -1,0 +1,198 @@
+/*
+ * nitro_paged_attn.h — C ABI of the MI355X (gfx950) paged-attention path for
+ * NitroRAG's inference engine.
+ *
+ * The reference (nvivek17/NitroRAG) has no attention function of its own: its
+ * attention is inlined in the forward passes of src/model_q8.cpp, and its page
+ * bookkeeping lives in src/pagedMemory.hpp.  This header is the boundary a
+ * maintainer binds in place of those regions.  Every entry point names the
+ * reference code it replaces (file:line, relative to the reference checkout).
+ *
+ * Conventions
+ *  - Every function returns an int status (NITRO_OK = 0).  Where the reference
+ *    calls exit(1) (pool exhaustion, src/pagedMemory.hpp:96,117,212) this
+ *    library returns a status instead; nitro_last_error() gives the message.
+ *  - Device pointers are caller-owned fp32 buffers in HBM; `stream` is a
+ *    hipStream_t passed as void* (NULL = the null stream).  Launches are
+ *    asynchronous on that stream.  One host thread drives a pool at a time.
+ *  - KV pool layout is the reference's (src/pagedMemory.hpp:86-106):
+ *      pool[page][layer][tok 0..15][kv_dim], kv_dim = n_kv_heads * head_dim.
+ *    Element (page, l, tok, kv_h, d) sits at
+ *      base + page*L*16*kv_dim + l*16*kv_dim + tok*kv_dim + kv_h*head_dim + d.
+ *  - A block table is the reference's Sequence::block_table: logical page i
+ *    of a sequence is physical page table[i].  `pos` is the slot written this
+ *    step; attention covers keys 0..pos inclusive (src/model_q8.cpp:634-638).
+ */
+#ifndef NITRO_PAGED_ATTN_H
+#define NITRO_PAGED_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Page size in tokens — src/pagedMemory.hpp:9 (BLOCK_SIZE). */
+#define NITRO_PAGE_TOKENS 16
+
+enum {
+    NITRO_OK = 0,
+    NITRO_ERR_INVALID_ARGUMENT = 1, /* bad pointer, id, shape or layer */
+    NITRO_ERR_UNSUPPORTED = 2,      /* head_dim outside {32, 64, 128, 256}, n_heads % n_kv_heads != 0 */
+    NITRO_ERR_DEVICE_ALLOC = 3,     /* hipMalloc failed (reference: src/pagedMemory.hpp:96) */
+    NITRO_ERR_OUT_OF_PAGES = 4,     /* no free page and nothing evictable (src/pagedMemory.hpp:117,212) */
+    NITRO_ERR_BAD_BLOCK_TABLE = 5,  /* page id outside the pool, or pos beyond the table */
+    NITRO_ERR_HIP = 6,              /* a HIP runtime call failed */
+    NITRO_ERR_NO_BATCH = 7          /* attention/append called before a batch was uploaded */
+};
+
+const char* nitro_status_string(int status);
+/* Message of the last failure on the calling thread ("" if none). */
+const char* nitro_last_error(void);
+
+/* ======================= host page bookkeeping ============================
+ * Bit-exact restatement of src/pagedMemory.hpp in C++ (no device memory):
+ * LIFO free list, reference counts, FNV-1a prefix cache with parent/child
+ * topology and leaf-first LRU eviction, per-sequence block tables.  Not
+ * thread-safe: the reference calls Sequence::allocate_next_token from an
+ * OpenMP loop (src/model_q8.cpp:578-582), a data race; callers of this
+ * library allocate sequentially in batch order, which is what the reference
+ * does with one thread.
+ */
+typedef struct nitro_block_manager nitro_block_manager; /* KVBlock_Manager + PrefixCacheManager */
+typedef struct nitro_sequence nitro_sequence;           /* Sequence */
+
+typedef struct nitro_block_info {
+    int32_t num_tokens;
+    int32_t ref_count;
+    int32_t parent_id;
+    int32_t child_count;
+} nitro_block_info; /* KVBlock fields, src/pagedMemory.hpp:28-37 */
+
+/* hash_block_state — src/pagedMemory.hpp:14-24 */
+uint64_t nitro_hash_block_state(uint64_t parent_hash, const int32_t* tokens, int32_t n);
+
+/* KVBlock_Manager::KVBlock_Manager + PrefixCacheManager::PrefixCacheManager —
+ * src/pagedMemory.hpp:86-111, 163-167 (bookkeeping only; K/V live in a nitro_kvpool). */
+int nitro_bm_create(int32_t total_blocks, nitro_block_manager** out);
+int nitro_bm_destroy(nitro_block_manager* bm); /* ~KVBlock_Manager, :157-160 */
+int nitro_bm_allocate_block(nitro_block_manager* bm, int32_t* id);                 /* :113-128 */
+int nitro_bm_inc_ref_count(nitro_block_manager* bm, int32_t id);                   /* :129-132 */
+int nitro_bm_free_block(nitro_block_manager* bm, int32_t id);                      /* :137-144 */
+int nitro_bm_force_free_block(nitro_block_manager* bm, int32_t id);                /* :145-151 */
+int nitro_bm_get_free_count(const nitro_block_manager* bm, int32_t* n);           /* :134-136 */
+int nitro_bm_get_block(const nitro_block_manager* bm, int32_t id, nitro_block_info* out); /* :154-156 */
+int nitro_bm_is_cached(const nitro_block_manager* bm, int32_t id, int32_t* cached); /* :168-170 */
+int nitro_bm_check_cache(const nitro_block_manager* bm, uint64_t block_hash, int32_t* id); /* :187-192 */
+int nitro_bm_insert_cache(nitro_block_manager* bm, uint64_t block_hash, int32_t id,
+                          int32_t parent_id);                                      /* :193-205 */
+int nitro_bm_evict_lru_block(nitro_block_manager* bm);                             /* :206-229 */
+/* Introspection of the same state the reference keeps privately
+ * (free_list order, evictable_leaves front->back, cache_map, reverse_map). */
+int nitro_bm_free_list(const nitro_block_manager* bm, int32_t* ids, int32_t cap, int32_t* n);
+int nitro_bm_evictable_leaves(const nitro_block_manager* bm, int32_t* ids, int32_t cap, int32_t* n);
+int nitro_bm_cache_entries(const nitro_block_manager* bm, uint64_t* hashes, int32_t* ids,
+                           int32_t cap, int32_t* n); /* sorted by hash */
+int nitro_bm_reverse_entries(const nitro_block_manager* bm, int32_t* ids, uint64_t* hashes,
+                             int32_t cap, int32_t* n); /* sorted by id */
+
+/* Sequence — src/pagedMemory.hpp:233-285 */
+int nitro_seq_create(int32_t seq_id, nitro_sequence** out);                        /* :240-244 */
+int nitro_seq_destroy(nitro_sequence* seq);
+int nitro_seq_allocate_next_token(nitro_sequence* seq, nitro_block_manager* bm, int32_t token); /* :245-264 */
+int nitro_seq_flush_cache(nitro_sequence* seq, nitro_block_manager* bm);           /* :265-273 */
+int nitro_seq_release(nitro_sequence* seq, nitro_block_manager* bm);               /* :274-283 */
+/* Prefix-hit walk over full 16-token chunks of prompt[start..n): on a hit,
+ * inc_ref_count + push the shared page + advance current_hash; stops at the
+ * first miss.  require_empty_buffer=1 is the scheduler's variant
+ * (src/pagedMemory.hpp:346-359), 0 is ingest_prompt's (src/model_q8.cpp:699-714).
+ * *next receives the index of the first token not covered by a hit. */
+int nitro_seq_prefix_walk(nitro_sequence* seq, nitro_block_manager* bm, const int32_t* prompt,
+                          int32_t n, int32_t start, int32_t require_empty_buffer, int32_t* next);
+/* Bookkeeping of ingest_prompt (src/model_q8.cpp:695-724): the walk (if
+ * enabled), then allocate_next_token for every remaining token, as
+ * forward_prefill_chunk does first (:428-430).  *count = logical_token_count. */
+int nitro_seq_ingest_prompt(nitro_sequence* seq, nitro_block_manager* bm, const int32_t* prompt,
+                            int32_t n, int32_t enable_prefix_caching, int32_t* count);
+int nitro_seq_state(const nitro_sequence* seq, int32_t* logical_token_count,
+                    uint64_t* current_hash, int32_t* buffered_tokens, int32_t* num_pages);
+int nitro_seq_block_table(const nitro_sequence* seq, int32_t* pages, int32_t cap, int32_t* n);
+int nitro_seq_token_buffer(const nitro_sequence* seq, int32_t* tokens, int32_t cap, int32_t* n);
+/* Packs the block tables of `batch` sequences into a dense host array
+ * tables[batch][max_pages] (unused entries 0), the form the device takes. */
+int nitro_pack_block_tables(const nitro_sequence* const* seqs, int32_t batch, int32_t max_pages,
+                            int32_t* tables);
+
+/* ============================ device KV pool ============================== */
+typedef struct nitro_kvpool nitro_kvpool;
+
+/* Device K and V pools with the reference layout — replaces the
+ * aligned_alloc pools of KVBlock_Manager (src/pagedMemory.hpp:86-111).
+ * nitro_kvpool_create owns (hipMalloc, zero-filled) memory; nitro_kvpool_wrap
+ * borrows two caller buffers of num_pages*num_layers*16*kv_dim floats each. */
+int nitro_kvpool_create(int32_t num_pages, int32_t num_layers, int32_t kv_dim, nitro_kvpool** out);
+int nitro_kvpool_wrap(float* k_pool, float* v_pool, int32_t num_pages, int32_t num_layers,
+                      int32_t kv_dim, nitro_kvpool** out);
+int nitro_kvpool_destroy(nitro_kvpool* pool); /* ~KVBlock_Manager, src/pagedMemory.hpp:157-160 */
+int nitro_kvpool_data(const nitro_kvpool* pool, float** k_pool, float** v_pool);
+int nitro_kvpool_shape(const nitro_kvpool* pool, int32_t* num_pages, int32_t* num_layers,
+                       int32_t* kv_dim);
+
+/* ----------------------------- decode ------------------------------------
+ * The decode batch of forward_decode_batch (src/model_q8.cpp:571-662):
+ * host tables[batch][max_pages] and positions[batch] (pos_b = the sequence's
+ * logical_token_count before this step's token, src/pagedMemory.hpp:334-341).
+ * Validated on the host (every page id of pages 0..pos/16 inside the pool),
+ * then copied to device memory owned by the pool, on `stream`. */
+int nitro_decode_batch_upload(nitro_kvpool* pool, const int32_t* tables, const int32_t* positions,
+                              int32_t batch, int32_t max_pages, void* stream);
+
+/* KV append for the decode batch — src/model_q8.cpp:616-623 (and the
+ * single-sequence append :279-287): k, v are device [batch][kv_dim]; row
+ * pos%16 of page table[pos/16] at `layer` receives them. */
+int nitro_kv_append(nitro_kvpool* pool, int32_t layer, const float* k, const float* v, void* stream);
+
+/* Batched paged-attention decode — src/model_q8.cpp:625-662 (batched) and
+ * :290-347 (single sequence, batch = 1).  q, out: device [batch][n_heads*head_dim].
+ * For each (b, h): softmax over keys 0..pos_b of q.k/sqrt(head_dim), times V,
+ * with kv head h / (n_heads/n_kv_heads).  One kernel launch: split-K over
+ * pages with an online softmax; the last workgroup of each (b, h) merges the
+ * partials.  Not re-entrant per pool: launches that overlap on one pool race
+ * on its split-K workspace. */
+int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
+                            int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void* stream);
+
+/* ----------------------------- prefill -----------------------------------
+ * A prefill batch of chunks, one per sequence — forward_prefill_chunk
+ * (src/model_q8.cpp:424-523) over several sequences at once.  Sequence b's
+ * chunk has num_tokens[b] tokens at positions start_pos[b] .. start_pos[b] +
+ * num_tokens[b] - 1 (start_pos = logical_token_count before the chunk,
+ * src/pagedMemory.hpp:379).  Q/K/V/out rows of all chunks are packed in batch
+ * order: rows [off_b, off_b + num_tokens[b]) with off_b = sum of earlier
+ * num_tokens.  Validated on the host like the decode batch. */
+int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const int32_t* start_pos,
+                               const int32_t* num_tokens, int32_t batch, int32_t max_pages,
+                               void* stream);
+
+/* KV scatter of the prefill batch — src/model_q8.cpp:473-484.
+ * k, v: device [total_tokens][kv_dim]. */
+int nitro_kv_append_prefill(nitro_kvpool* pool, int32_t layer, const float* k, const float* v,
+                            void* stream);
+
+/* Causal paged prefill attention — src/model_q8.cpp:485-523.  q, out: device
+ * [total_tokens][n_heads*head_dim]; the token at pos attends keys 0..pos
+ * (prefix-hit pages, earlier chunks and this chunk's own rows). */
+int nitro_paged_attn_prefill(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
+                             int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void* stream);
+
+/* ------------------------------ checks ------------------------------------
+ * Kernels re-check every page id they dereference against the pool size and
+ * skip (and record) any outside it instead of faulting.  This reads and
+ * clears that record (synchronising the pool's last stream): *bad_pages = 0
+ * when no kernel saw a bad id. */
+int nitro_kvpool_take_device_errors(nitro_kvpool* pool, int32_t* bad_pages);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NITRO_PAGED_ATTN_H */

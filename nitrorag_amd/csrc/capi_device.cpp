@@ -1,0 +1,404 @@
+// C ABI of the device KV pool, batch uploads and kernel launches
+// (declared in include/nitro_paged_attn.h).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "capi_common.hpp"
+#include "device_pool.hpp"
+#include "nitro_paged_attn.h"
+
+using namespace nitro;
+
+namespace {
+
+constexpr int kDecodeWaves = 4;             // waves per decode workgroup (kernel constant)
+constexpr int kDecodeTargetGroups = 4096;   // ~16 workgroups per CU on 256 CUs
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+void require_pool(const nitro_kvpool* pool) {
+    require(pool != nullptr, ERR_INVALID_ARGUMENT, "null pool");
+}
+
+void check_table_rows(const nitro_kvpool* pool, const int32_t* tables, int b, int max_pages,
+                      int last_pos) {
+    require(last_pos >= 0, ERR_BAD_BLOCK_TABLE, "negative position");
+    const int last_page = last_pos >> 4;
+    if (last_page >= max_pages)
+        throw Error(ERR_BAD_BLOCK_TABLE, "sequence " + std::to_string(b) + ": position " +
+                                             std::to_string(last_pos) + " needs page " +
+                                             std::to_string(last_page) + " but max_pages is " +
+                                             std::to_string(max_pages));
+    const int32_t* row = tables + (size_t)b * max_pages;
+    for (int i = 0; i <= last_page; i++)
+        if (row[i] < 0 || row[i] >= pool->num_pages)
+            throw Error(ERR_BAD_BLOCK_TABLE, "sequence " + std::to_string(b) + ": page id " +
+                                                 std::to_string(row[i]) + " at logical page " +
+                                                 std::to_string(i) + " is outside [0, " +
+                                                 std::to_string(pool->num_pages) + ")");
+}
+
+void check_shape(const nitro_kvpool* pool, int layer, int n_heads, int n_kv_heads, int head_dim) {
+    require(layer >= 0 && layer < pool->num_layers, ERR_INVALID_ARGUMENT, "layer out of range");
+    require(n_heads > 0 && n_kv_heads > 0, ERR_INVALID_ARGUMENT, "head counts must be positive");
+    require(n_heads % n_kv_heads == 0, ERR_UNSUPPORTED, "n_heads must be a multiple of n_kv_heads");
+    require(supported_head_dim(head_dim), ERR_UNSUPPORTED, "head_dim must be 32, 64, 128 or 256");
+    require(n_kv_heads * head_dim == pool->kv_dim, ERR_INVALID_ARGUMENT,
+            "n_kv_heads * head_dim must equal the pool's kv_dim");
+}
+
+int env_int(const char* name, int fallback) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoi(v) : fallback;
+}
+
+}  // namespace
+
+extern "C" {
+
+static int make_pool(float* k, float* v, bool owned, int32_t num_pages, int32_t num_layers,
+                     int32_t kv_dim, nitro_kvpool** out) {
+    return guarded([&] {
+        require(out != nullptr, ERR_INVALID_ARGUMENT, "null output pointer");
+        *out = nullptr;
+        require(num_pages > 0 && num_layers > 0 && kv_dim > 0, ERR_INVALID_ARGUMENT,
+                "pool dimensions must be positive");
+        require(kv_dim % 4 == 0, ERR_UNSUPPORTED, "kv_dim must be a multiple of 4");
+        nitro_kvpool* pool = new nitro_kvpool();
+        try {
+            hip_check(hipGetDevice(&pool->device), "hipGetDevice");
+            pool->num_pages = num_pages;
+            pool->num_layers = num_layers;
+            pool->kv_dim = kv_dim;
+            pool->owned = owned;
+            const size_t bytes = (size_t)num_pages * num_layers * BLOCK_SIZE * kv_dim * sizeof(float);
+            if (owned) {
+                hip_check(hipMalloc((void**)&pool->k, bytes), "hipMalloc(K pool)");
+                hip_check(hipMalloc((void**)&pool->v, bytes), "hipMalloc(V pool)");
+                hip_check(hipMemset(pool->k, 0, bytes), "hipMemset");
+                hip_check(hipMemset(pool->v, 0, bytes), "hipMemset");
+            } else {
+                require(k != nullptr && v != nullptr, ERR_INVALID_ARGUMENT, "null pool buffer");
+                require(((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0, ERR_INVALID_ARGUMENT,
+                        "pool buffers must be 16-byte aligned");
+                pool->k = k;
+                pool->v = v;
+            }
+            pool->bad_pages.reserve(1);
+            hip_check(hipMemset(pool->bad_pages.ptr, 0, sizeof(int32_t)), "hipMemset");
+            hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        } catch (...) {
+            if (owned) {
+                if (pool->k) (void)hipFree(pool->k);
+                if (pool->v) (void)hipFree(pool->v);
+            }
+            delete pool;
+            throw;
+        }
+        *out = pool;
+    });
+}
+
+int nitro_kvpool_create(int32_t num_pages, int32_t num_layers, int32_t kv_dim, nitro_kvpool** out) {
+    return make_pool(nullptr, nullptr, true, num_pages, num_layers, kv_dim, out);
+}
+
+int nitro_kvpool_wrap(float* k_pool, float* v_pool, int32_t num_pages, int32_t num_layers,
+                      int32_t kv_dim, nitro_kvpool** out) {
+    return make_pool(k_pool, v_pool, false, num_pages, num_layers, kv_dim, out);
+}
+
+int nitro_kvpool_destroy(nitro_kvpool* pool) {
+    if (!pool) return NITRO_OK;
+    return guarded([&] {
+        (void)hipDeviceSynchronize();
+        if (pool->owned) {
+            (void)hipFree(pool->k);
+            (void)hipFree(pool->v);
+        }
+        delete pool;
+    });
+}
+
+int nitro_kvpool_data(const nitro_kvpool* pool, float** k_pool, float** v_pool) {
+    return guarded([&] {
+        require_pool(pool);
+        if (k_pool) *k_pool = pool->k;
+        if (v_pool) *v_pool = pool->v;
+    });
+}
+
+int nitro_kvpool_shape(const nitro_kvpool* pool, int32_t* num_pages, int32_t* num_layers,
+                       int32_t* kv_dim) {
+    return guarded([&] {
+        require_pool(pool);
+        if (num_pages) *num_pages = pool->num_pages;
+        if (num_layers) *num_layers = pool->num_layers;
+        if (kv_dim) *kv_dim = pool->kv_dim;
+    });
+}
+
+int nitro_decode_batch_upload(nitro_kvpool* pool, const int32_t* tables, const int32_t* positions,
+                              int32_t batch, int32_t max_pages, void* stream) {
+    return guarded([&] {
+        require_pool(pool);
+        require(tables != nullptr && positions != nullptr, ERR_INVALID_ARGUMENT, "null array");
+        require(batch > 0 && max_pages > 0, ERR_INVALID_ARGUMENT, "batch and max_pages must be positive");
+        for (int b = 0; b < batch; b++) check_table_rows(pool, tables, b, max_pages, positions[b]);
+        DecodeBatch& d = pool->decode;
+        const size_t nt = (size_t)batch * max_pages;
+        d.batch = 0;  // invalid until the copies are issued
+        d.tables.reserve(nt);
+        d.pos.reserve(batch);
+        hipStream_t s = as_stream(stream);
+        Staging& st = pool->decode_staging;
+        int32_t* h = st.acquire(nt + batch);
+        std::memcpy(h, tables, nt * sizeof(int32_t));
+        std::memcpy(h + nt, positions, batch * sizeof(int32_t));
+        st.copy(d.tables.ptr, h, nt, s);
+        st.copy(d.pos.ptr, h + nt, batch, s);
+        st.finish(s);
+        d.positions.assign(positions, positions + batch);
+        d.batch = batch;
+        d.max_pages = max_pages;
+        pool->last_stream = s;
+    });
+}
+
+int nitro_kv_append(nitro_kvpool* pool, int32_t layer, const float* k, const float* v, void* stream) {
+    return guarded([&] {
+        require_pool(pool);
+        require(k != nullptr && v != nullptr, ERR_INVALID_ARGUMENT, "null k/v");
+        require(layer >= 0 && layer < pool->num_layers, ERR_INVALID_ARGUMENT, "layer out of range");
+        const DecodeBatch& d = pool->decode;
+        require(d.batch > 0, ERR_NO_BATCH, "no decode batch uploaded");
+        hipStream_t s = as_stream(stream);
+        hip_check(launch_kv_append_decode(pool->k, pool->v, k, v, d.tables.ptr, d.pos.ptr, d.batch,
+                                          d.max_pages, pool->kv_dim, pool->page_stride(),
+                                          pool->layer_offset(layer), pool->num_pages,
+                                          pool->bad_pages.ptr, s),
+                  "kv_append launch");
+        pool->last_stream = s;
+    });
+}
+
+int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
+                            int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void* stream) {
+    return guarded([&] {
+        require_pool(pool);
+        require(q != nullptr && out != nullptr, ERR_INVALID_ARGUMENT, "null q/out");
+        check_shape(pool, layer, n_heads, n_kv_heads, head_dim);
+        const DecodeBatch& d = pool->decode;
+        require(d.batch > 0, ERR_NO_BATCH, "no decode batch uploaded");
+
+        const int tile = decode_tile_rows(head_dim);
+        int max_tiles = 0;
+        long long total_tiles = 0;
+        for (int p : d.positions) {
+            const int n = (p + 1 + tile - 1) / tile;
+            max_tiles = std::max(max_tiles, n);
+            total_tiles += n;
+        }
+        total_tiles *= n_heads;
+        // Tiles per split: enough splits to give ~kDecodeTargetGroups workgroups,
+        // at least one tile per wave, and a block-table slice that fits in LDS.
+        int tps = env_int("NITRO_DECODE_SPLIT_TILES", 0);
+        if (tps <= 0) {
+            long long want = (total_tiles + kDecodeTargetGroups - 1) / kDecodeTargetGroups;
+            tps = (int)std::max<long long>(kDecodeWaves, (want + kDecodeWaves - 1) / kDecodeWaves * kDecodeWaves);
+        }
+        const int max_tps = (DECODE_MAX_SPLIT_PAGES - 2) * BLOCK_SIZE / tile;
+        tps = std::min(tps, max_tps);
+        tps = std::max(tps, 1);
+        const int splits = (max_tiles + tps - 1) / tps;
+
+        hipStream_t s = as_stream(stream);
+        const size_t bh = (size_t)d.batch * n_heads;
+        if (splits > 1) {
+            pool->partials.reserve(bh * splits * (head_dim + 2));
+            if (pool->counters.reserve(bh))
+                hip_check(hipMemsetAsync(pool->counters.ptr, 0, bh * sizeof(uint32_t), s), "hipMemsetAsync");
+        }
+        DecodeLaunch a{};
+        a.q = q;
+        a.out = out;
+        a.k_pool = pool->k;
+        a.v_pool = pool->v;
+        a.tables = d.tables.ptr;
+        a.positions = d.pos.ptr;
+        a.partials = pool->partials.ptr;
+        a.counters = pool->counters.ptr;
+        a.bad_pages = pool->bad_pages.ptr;
+        a.page_stride = pool->page_stride();
+        a.layer_off = pool->layer_offset(layer);
+        a.kv_dim = pool->kv_dim;
+        a.batch = d.batch;
+        a.n_heads = n_heads;
+        a.kv_mul = n_heads / n_kv_heads;
+        a.head_dim = head_dim;
+        a.max_pages = d.max_pages;
+        a.num_pages = pool->num_pages;
+        a.tiles_per_split = tps;
+        a.num_splits = splits;
+        a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+        hip_check(launch_paged_attn_decode(a, s), "paged_attn_decode launch");
+        pool->last_stream = s;
+    });
+}
+
+int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const int32_t* start_pos,
+                               const int32_t* num_tokens, int32_t batch, int32_t max_pages,
+                               void* stream) {
+    return guarded([&] {
+        require_pool(pool);
+        require(tables != nullptr && start_pos != nullptr && num_tokens != nullptr,
+                ERR_INVALID_ARGUMENT, "null array");
+        require(batch > 0 && max_pages > 0, ERR_INVALID_ARGUMENT, "batch and max_pages must be positive");
+        PrefillBatch& p = pool->prefill;
+        p.batch = 0;
+        std::vector<int32_t> row_off(batch);
+        long long total = 0;
+        int max_tokens = 0;
+        for (int b = 0; b < batch; b++) {
+            require(num_tokens[b] >= 0 && start_pos[b] >= 0, ERR_INVALID_ARGUMENT,
+                    "negative start_pos or num_tokens");
+            if (num_tokens[b] > 0) check_table_rows(pool, tables, b, max_pages, start_pos[b] + num_tokens[b] - 1);
+            row_off[b] = (int32_t)total;
+            total += num_tokens[b];
+            max_tokens = std::max(max_tokens, num_tokens[b]);
+        }
+        require(total > 0 && total < (1LL << 30), ERR_INVALID_ARGUMENT, "bad total token count");
+        const int bm = prefill_block_m(0);
+        // Work items (seq, first query row), longest key range first.
+        std::vector<std::pair<long long, std::pair<int, int>>> items;
+        for (int b = 0; b < batch; b++)
+            for (int q0 = 0; q0 < num_tokens[b]; q0 += bm) {
+                const int last = start_pos[b] + std::min(num_tokens[b], q0 + bm) - 1;
+                items.push_back({-(long long)last, {b, q0}});
+            }
+        std::stable_sort(items.begin(), items.end(),
+                         [](const auto& x, const auto& y) { return x.first < y.first; });
+
+        const size_t nt = (size_t)batch * max_pages;
+        const size_t n_work = items.size() * 2;
+        const size_t need = nt + 3 * (size_t)batch + (size_t)total + n_work;
+        hipStream_t s = as_stream(stream);
+        Staging& st = pool->prefill_staging;
+        int32_t* h = st.acquire(need);
+        int32_t* h_tables = h;
+        int32_t* h_start = h_tables + nt;
+        int32_t* h_len = h_start + batch;
+        int32_t* h_off = h_len + batch;
+        int32_t* h_slots = h_off + batch;
+        int32_t* h_work = h_slots + total;
+        std::memcpy(h_tables, tables, nt * sizeof(int32_t));
+        std::memcpy(h_start, start_pos, batch * sizeof(int32_t));
+        std::memcpy(h_len, num_tokens, batch * sizeof(int32_t));
+        std::memcpy(h_off, row_off.data(), batch * sizeof(int32_t));
+        for (int b = 0; b < batch; b++)
+            for (int t = 0; t < num_tokens[b]; t++) {
+                const int pos = start_pos[b] + t;
+                h_slots[row_off[b] + t] = tables[(size_t)b * max_pages + (pos >> 4)] * BLOCK_SIZE + (pos & 15);
+            }
+        for (size_t i = 0; i < items.size(); i++) {
+            h_work[2 * i] = items[i].second.first;
+            h_work[2 * i + 1] = items[i].second.second;
+        }
+        p.tables.reserve(nt);
+        p.d_start.reserve(batch);
+        p.d_len.reserve(batch);
+        p.d_row_off.reserve(batch);
+        p.slots.reserve(total);
+        p.work.reserve(n_work);
+        st.copy(p.tables.ptr, h_tables, nt, s);
+        st.copy(p.d_start.ptr, h_start, batch, s);
+        st.copy(p.d_len.ptr, h_len, batch, s);
+        st.copy(p.d_row_off.ptr, h_off, batch, s);
+        st.copy(p.slots.ptr, h_slots, total, s);
+        st.copy(p.work.ptr, h_work, n_work, s);
+        st.finish(s);
+        p.start_pos.assign(start_pos, start_pos + batch);
+        p.num_tokens.assign(num_tokens, num_tokens + batch);
+        p.row_off = row_off;
+        p.total_rows = (int32_t)total;
+        p.max_tokens = max_tokens;
+        p.work_items = (int32_t)items.size();
+        p.work_block_m = bm;
+        p.max_pages = max_pages;
+        p.batch = batch;
+        pool->last_stream = s;
+    });
+}
+
+int nitro_kv_append_prefill(nitro_kvpool* pool, int32_t layer, const float* k, const float* v,
+                            void* stream) {
+    return guarded([&] {
+        require_pool(pool);
+        require(k != nullptr && v != nullptr, ERR_INVALID_ARGUMENT, "null k/v");
+        require(layer >= 0 && layer < pool->num_layers, ERR_INVALID_ARGUMENT, "layer out of range");
+        const PrefillBatch& p = pool->prefill;
+        require(p.batch > 0, ERR_NO_BATCH, "no prefill batch uploaded");
+        hipStream_t s = as_stream(stream);
+        hip_check(launch_kv_scatter_rows(pool->k, pool->v, k, v, p.slots.ptr, p.total_rows,
+                                         pool->kv_dim, pool->page_stride(), pool->layer_offset(layer),
+                                         pool->num_pages, pool->bad_pages.ptr, s),
+                  "kv_scatter launch");
+        pool->last_stream = s;
+    });
+}
+
+int nitro_paged_attn_prefill(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
+                             int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void* stream) {
+    return guarded([&] {
+        require_pool(pool);
+        require(q != nullptr && out != nullptr, ERR_INVALID_ARGUMENT, "null q/out");
+        check_shape(pool, layer, n_heads, n_kv_heads, head_dim);
+        const PrefillBatch& p = pool->prefill;
+        require(p.batch > 0, ERR_NO_BATCH, "no prefill batch uploaded");
+        PrefillLaunch a{};
+        a.q = q;
+        a.out = out;
+        a.k_pool = pool->k;
+        a.v_pool = pool->v;
+        a.tables = p.tables.ptr;
+        a.start_pos = p.d_start.ptr;
+        a.num_tokens = p.d_len.ptr;
+        a.row_off = p.d_row_off.ptr;
+        a.work = p.work.ptr;
+        a.bad_pages = pool->bad_pages.ptr;
+        a.page_stride = pool->page_stride();
+        a.layer_off = pool->layer_offset(layer);
+        a.kv_dim = pool->kv_dim;
+        a.n_heads = n_heads;
+        a.kv_mul = n_heads / n_kv_heads;
+        a.head_dim = head_dim;
+        a.max_pages = p.max_pages;
+        a.num_pages = pool->num_pages;
+        a.work_items = p.work_items;
+        a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+        hipStream_t s = as_stream(stream);
+        hip_check(launch_paged_attn_prefill(a, s), "paged_attn_prefill launch");
+        pool->last_stream = s;
+    });
+}
+
+int nitro_kvpool_take_device_errors(nitro_kvpool* pool, int32_t* bad_pages) {
+    return guarded([&] {
+        require_pool(pool);
+        require(bad_pages != nullptr, ERR_INVALID_ARGUMENT, "null output pointer");
+        hip_check(hipStreamSynchronize(pool->last_stream), "hipStreamSynchronize");
+        int32_t v = 0;
+        hip_check(hipMemcpy(&v, pool->bad_pages.ptr, sizeof(int32_t), hipMemcpyDeviceToHost), "hipMemcpy");
+        hip_check(hipMemset(pool->bad_pages.ptr, 0, sizeof(int32_t)), "hipMemset");
+        hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        *bad_pages = v;
+    });
+}
+
+}  // extern "C"

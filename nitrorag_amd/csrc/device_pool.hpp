@@ -1,0 +1,179 @@
+// Device-side state behind a nitro_kvpool handle: the K/V pools, the
+// uploaded decode / prefill batches, the split-K workspace and the device
+// error counter.  Host code only (kernels take plain pointers).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "paged_memory.hpp"
+
+namespace nitro {
+
+inline void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess)
+        throw Error(e == hipErrorOutOfMemory ? ERR_DEVICE_ALLOC : ERR_HIP,
+                    std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// A device allocation that only grows (hipMalloc outside any capture).
+template <class T>
+struct DeviceBuffer {
+    T* ptr = nullptr;
+    size_t count = 0;
+    DeviceBuffer() = default;
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    ~DeviceBuffer() { reset(); }
+    void reset() {
+        if (ptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        count = 0;
+    }
+    // Ensures room for n elements; returns true when (re)allocated (contents
+    // of a fresh allocation are undefined).
+    bool reserve(size_t n) {
+        if (n <= count && ptr) return false;
+        reset();
+        hip_check(hipMalloc((void**)&ptr, (n ? n : 1) * sizeof(T)), "hipMalloc");
+        count = n;
+        return true;
+    }
+};
+
+// Pinned host staging for uploads: reused once the copies that read it have
+// completed (tracked with an event), so callers may free their arrays at once.
+struct Staging {
+    int32_t* host = nullptr;
+    size_t count = 0;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+    Staging() = default;
+    Staging(const Staging&) = delete;
+    Staging& operator=(const Staging&) = delete;
+    ~Staging() {
+        if (pending) (void)hipEventSynchronize(done);
+        if (host) (void)hipHostFree(host);
+        if (done) (void)hipEventDestroy(done);
+    }
+    int32_t* acquire(size_t n) {
+        if (!done) hip_check(hipEventCreateWithFlags(&done, hipEventDisableTiming), "hipEventCreate");
+        if (pending) {
+            hip_check(hipEventSynchronize(done), "hipEventSynchronize");
+            pending = false;
+        }
+        if (n > count || !host) {
+            if (host) hip_check(hipHostFree(host), "hipHostFree");
+            host = nullptr;
+            count = 0;
+            hip_check(hipHostMalloc((void**)&host, (n ? n : 1) * sizeof(int32_t)), "hipHostMalloc");
+            count = n;
+        }
+        return host;
+    }
+    void copy(int32_t* dst, const int32_t* src, size_t n, hipStream_t s) {
+        hip_check(hipMemcpyAsync(dst, src, n * sizeof(int32_t), hipMemcpyHostToDevice, s),
+                  "hipMemcpyAsync");
+    }
+    void finish(hipStream_t s) {
+        hip_check(hipEventRecord(done, s), "hipEventRecord");
+        pending = true;
+    }
+};
+
+// Which head_dim values have kernels (template instantiations).
+inline bool supported_head_dim(int hd) { return hd == 32 || hd == 64 || hd == 128 || hd == 256; }
+
+struct DecodeBatch {
+    int32_t batch = 0, max_pages = 0;
+    std::vector<int32_t> positions;  // host copy (launch geometry)
+    DeviceBuffer<int32_t> tables, pos;
+};
+
+struct PrefillBatch {
+    int32_t batch = 0, max_pages = 0, total_rows = 0, max_tokens = 0;
+    std::vector<int32_t> start_pos, num_tokens, row_off;
+    DeviceBuffer<int32_t> tables, d_start, d_len, d_row_off;
+    DeviceBuffer<int32_t> slots;      // per packed row: page*16 + row-in-page
+    DeviceBuffer<int32_t> work;       // per work item: (seq, first query) pairs
+    int32_t work_items = 0;
+    int32_t work_block_m = 0;         // query rows per work item the list was built for
+};
+
+}  // namespace nitro
+
+struct nitro_kvpool {
+    float* k = nullptr;
+    float* v = nullptr;
+    bool owned = false;
+    int32_t num_pages = 0, num_layers = 0, kv_dim = 0;
+    int device = 0;
+    hipStream_t last_stream = nullptr;
+    nitro::DecodeBatch decode;
+    nitro::PrefillBatch prefill;
+    nitro::DeviceBuffer<float> partials;      // split-K (m, l, acc[hd]) per (b, h, split)
+    nitro::DeviceBuffer<uint32_t> counters;   // arrivals per (b, h); self-resetting
+    nitro::DeviceBuffer<int32_t> bad_pages;   // [1] device error counter
+    nitro::Staging decode_staging, prefill_staging;
+
+    int64_t page_stride() const { return (int64_t)num_layers * nitro::BLOCK_SIZE * kv_dim; }
+    int64_t layer_offset(int layer) const { return (int64_t)layer * nitro::BLOCK_SIZE * kv_dim; }
+};
+
+namespace nitro {
+
+// Kernel launchers (defined in the .hip files).
+struct DecodeLaunch {
+    const float* q;
+    float* out;
+    const float* k_pool;
+    const float* v_pool;
+    const int32_t* tables;
+    const int32_t* positions;
+    float* partials;
+    uint32_t* counters;
+    int32_t* bad_pages;
+    int64_t page_stride, layer_off;
+    int32_t kv_dim, batch, n_heads, kv_mul, head_dim, max_pages, num_pages;
+    int32_t tiles_per_split, num_splits;
+    float qscale;
+};
+// Rows per decode tile for a head_dim (the unit split-K partitions).
+int decode_tile_rows(int head_dim);
+// Largest number of pages one split may cover (its block-table slice lives in LDS).
+constexpr int DECODE_MAX_SPLIT_PAGES = 1024;
+hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream);
+
+hipError_t launch_kv_append_decode(float* k_pool, float* v_pool, const float* k, const float* v,
+                                   const int32_t* tables, const int32_t* positions, int batch,
+                                   int max_pages, int kv_dim, int64_t page_stride,
+                                   int64_t layer_off, int num_pages, int32_t* bad_pages,
+                                   hipStream_t stream);
+hipError_t launch_kv_scatter_rows(float* k_pool, float* v_pool, const float* k, const float* v,
+                                  const int32_t* slots, int rows, int kv_dim, int64_t page_stride,
+                                  int64_t layer_off, int num_pages, int32_t* bad_pages,
+                                  hipStream_t stream);
+
+struct PrefillLaunch {
+    const float* q;
+    float* out;
+    const float* k_pool;
+    const float* v_pool;
+    const int32_t* tables;
+    const int32_t* start_pos;
+    const int32_t* num_tokens;
+    const int32_t* row_off;
+    const int32_t* work;  // pairs (seq, first query row of the chunk)
+    int32_t* bad_pages;
+    int64_t page_stride, layer_off;
+    int32_t kv_dim, n_heads, kv_mul, head_dim, max_pages, num_pages, work_items;
+    float qscale;
+};
+// Query rows per prefill work item.
+int prefill_block_m(int head_dim);
+hipError_t launch_paged_attn_prefill(const PrefillLaunch& a, hipStream_t stream);
+
+}  // namespace nitro

@@ -1,0 +1,304 @@
+// Batched paged-attention decode for gfx950 (MI355X).
+//
+// Computes, for every (sequence b, query head h), what the reference's
+// forward_decode_batch attention computes (src/model_q8.cpp:625-662):
+//   s_t = q_h . k_t / sqrt(hd) over keys t = 0..pos_b (pages via the block
+//   table, kv head h / (H/Hkv)), p = softmax(s), o_h = sum_t p_t v_t.
+//
+// Design (bandwidth-bound: K and V are read exactly once per query head):
+//  - Grid: one workgroup of W=4 wavefronts per (b, h, split).  A split is a
+//    run of `tiles_per_split` tiles of TILE consecutive context rows; waves
+//    take the split's tiles round-robin.
+//  - Lane layout: LPR = hd/16 lanes share one K/V row, each lane holding 16
+//    floats of it as four float4 (columns c*4 + j*4*LPR, j = 0..3), so each
+//    global_load_dwordx4 reads whole 4*LPR-float quarter-rows per lane group
+//    (128 B for hd=128).  A wave covers RPS = 64/LPR rows per load set and two
+//    load sets per tile (TILE = 2*RPS rows: one 16-token page for hd=128, two
+//    for hd=64).  All 16 K/V float4 loads of a tile are issued before use.
+//  - q.k: 16 FMAs per lane, then a DPP butterfly across the LPR lanes.
+//  - Softmax: every lane group keeps its own running (max, sum, acc) in base 2
+//    (q is pre-scaled by log2(e)/sqrt(hd)); groups, then waves (through LDS),
+//    then splits are merged with the usual rescaling.  No score scratch.
+//  - Split-K merge: each workgroup writes (m, l, acc[hd]) for its split; the
+//    last to arrive for (b, h) (agent-scope atomic counter, release/acquire
+//    fences) merges all splits and resets the counter, so decode is a single
+//    launch and needs no memset between launches.
+//  - The split's block-table slice is staged in LDS once; page ids outside
+//    the pool are counted in *bad_pages and their rows skipped (no fault).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "device_pool.hpp"
+
+namespace nitro {
+namespace {
+
+constexpr int WAVES = 4;
+constexpr int THREADS = 64 * WAVES;
+
+template <int HD>
+struct DecodeGeom {
+    static constexpr int LPR = HD / 16;   // lanes per K/V row
+    static constexpr int RPS = 64 / LPR;  // rows per load set
+    static constexpr int SETS = 2;        // load sets per tile
+    static constexpr int TILE = RPS * SETS;
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over the LPR consecutive lanes of a group (result in every lane).
+template <int LPR>
+__device__ __forceinline__ float group_sum(float x) {
+    if constexpr (LPR >= 2) x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
+    if constexpr (LPR >= 4) x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
+    if constexpr (LPR >= 8) x += dpp_mov<0x141>(x);  // row_half_mirror: other quad of the 8
+    if constexpr (LPR >= 16) x += dpp_mov<0x140>(x); // row_mirror: other 8 of the 16
+    return x;
+}
+
+__device__ __forceinline__ float dot4(float4 a, float4 b, float acc) {
+    acc = fmaf(a.x, b.x, acc);
+    acc = fmaf(a.y, b.y, acc);
+    acc = fmaf(a.z, b.z, acc);
+    acc = fmaf(a.w, b.w, acc);
+    return acc;
+}
+
+__device__ __forceinline__ float scale_of(float m, float m_new) {
+    return m == -INFINITY ? 0.0f : exp2f(m - m_new);
+}
+
+template <int HD>
+__global__ __launch_bounds__(THREADS) void paged_attn_decode_kernel(DecodeLaunch a) {
+    using G = DecodeGeom<HD>;
+    constexpr int LPR = G::LPR, RPS = G::RPS, TILE = G::TILE;
+    __shared__ int32_t s_pages[DECODE_MAX_SPLIT_PAGES];
+    __shared__ float s_acc[WAVES][HD];
+    __shared__ float s_m[WAVES], s_l[WAVES];
+    __shared__ int s_last;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane / LPR;
+    const int c = lane % LPR;
+
+    const int split = blockIdx.x % a.num_splits;
+    const int bh = blockIdx.x / a.num_splits;
+    const int b = bh / a.n_heads;
+    const int h = bh - b * a.n_heads;
+    const int ctx = a.positions[b] + 1;
+    const int n_tiles = (ctx + TILE - 1) / TILE;
+    const int tile_begin = split * a.tiles_per_split;
+    if (tile_begin >= n_tiles) return;  // uniform for the workgroup
+    const int tile_end = min(n_tiles, tile_begin + a.tiles_per_split);
+    const int splits_b = (n_tiles + a.tiles_per_split - 1) / a.tiles_per_split;
+    const int kv_h = h / a.kv_mul;
+
+    // Block-table slice of this split -> LDS (checked against the pool size).
+    const int page_begin = (tile_begin * TILE) >> 4;
+    const int page_end = ((min(ctx, tile_end * TILE) - 1) >> 4) + 1;
+    const int32_t* trow = a.tables + (size_t)b * a.max_pages;
+    for (int i = threadIdx.x; i < page_end - page_begin; i += THREADS) {
+        int p = trow[page_begin + i];
+        if ((unsigned)p >= (unsigned)a.num_pages) {
+            atomicAdd(a.bad_pages, 1);
+            p = -1;
+        }
+        s_pages[i] = p;
+    }
+
+    // q slice of this lane, pre-scaled to base-2 logits.
+    const float* qp = a.q + (size_t)bh * HD;
+    float4 qv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        float4 t = *reinterpret_cast<const float4*>(qp + (c + j * LPR) * 4);
+        qv[j] = make_float4(t.x * a.qscale, t.y * a.qscale, t.z * a.qscale, t.w * a.qscale);
+    }
+    __syncthreads();
+
+    const float* kbase = a.k_pool + a.layer_off + (size_t)kv_h * HD;
+    const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * HD;
+
+    float m = -INFINITY, l = 0.0f;
+    float4 acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    for (int t = tile_begin + wave; t < tile_end; t += WAVES) {
+        float4 kr[G::SETS][4], vr[G::SETS][4];
+        bool valid[G::SETS];
+#pragma unroll
+        for (int i = 0; i < G::SETS; i++) {
+            const int row = t * TILE + g + i * RPS;
+            int page = row < ctx ? s_pages[(row >> 4) - page_begin] : -1;
+            valid[i] = page >= 0;
+            if (valid[i]) {
+                const size_t off = (size_t)page * a.page_stride + (size_t)(row & 15) * a.kv_dim;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    kr[i][j] = *reinterpret_cast<const float4*>(kbase + off + (c + j * LPR) * 4);
+                    vr[i][j] = *reinterpret_cast<const float4*>(vbase + off + (c + j * LPR) * 4);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    kr[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    vr[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+            }
+        }
+        float s[G::SETS];
+#pragma unroll
+        for (int i = 0; i < G::SETS; i++) {
+            float d = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) d = dot4(qv[j], kr[i][j], d);
+            d = group_sum<LPR>(d);
+            s[i] = valid[i] ? d : -INFINITY;
+        }
+        float m_new = m;
+#pragma unroll
+        for (int i = 0; i < G::SETS; i++) m_new = fmaxf(m_new, s[i]);
+        if (m_new == -INFINITY) continue;  // no valid row for this lane group yet
+        const float alpha = scale_of(m, m_new);
+        float p[G::SETS];
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < G::SETS; i++) {
+            p[i] = valid[i] ? exp2f(s[i] - m_new) : 0.0f;
+            psum += p[i];
+        }
+        l = l * alpha + psum;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float4 r = make_float4(acc[j].x * alpha, acc[j].y * alpha, acc[j].z * alpha, acc[j].w * alpha);
+#pragma unroll
+            for (int i = 0; i < G::SETS; i++) {
+                r.x = fmaf(p[i], vr[i][j].x, r.x);
+                r.y = fmaf(p[i], vr[i][j].y, r.y);
+                r.z = fmaf(p[i], vr[i][j].z, r.z);
+                r.w = fmaf(p[i], vr[i][j].w, r.w);
+            }
+            acc[j] = r;
+        }
+        m = m_new;
+    }
+
+    // Merge the lane groups of the wave (lanes with equal c, across g).
+#pragma unroll
+    for (int mask = LPR; mask < 64; mask <<= 1) {
+        const float mo = __shfl_xor(m, mask);
+        const float lo = __shfl_xor(l, mask);
+        const float mm = fmaxf(m, mo);
+        const float f = scale_of(m, mm), fo = scale_of(mo, mm);
+        l = l * f + lo * fo;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float4 o;
+            o.x = __shfl_xor(acc[j].x, mask);
+            o.y = __shfl_xor(acc[j].y, mask);
+            o.z = __shfl_xor(acc[j].z, mask);
+            o.w = __shfl_xor(acc[j].w, mask);
+            acc[j] = make_float4(acc[j].x * f + o.x * fo, acc[j].y * f + o.y * fo,
+                                 acc[j].z * f + o.z * fo, acc[j].w * f + o.w * fo);
+        }
+        m = mm;
+    }
+    if (g == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            *reinterpret_cast<float4*>(&s_acc[wave][(c + j * LPR) * 4]) = acc[j];
+        if (c == 0) {
+            s_m[wave] = m;
+            s_l[wave] = l;
+        }
+    }
+    __syncthreads();
+
+    // Merge the waves: thread d < HD owns output column d.
+    const int d = threadIdx.x;
+    float M = -INFINITY, L = 0.0f, A = 0.0f;
+    if (d < HD) {
+#pragma unroll
+        for (int w = 0; w < WAVES; w++) M = fmaxf(M, s_m[w]);
+#pragma unroll
+        for (int w = 0; w < WAVES; w++) {
+            const float f = scale_of(s_m[w], M);
+            L += s_l[w] * f;
+            A += s_acc[w][d] * f;
+        }
+    }
+    float* out = a.out + (size_t)bh * HD;
+    if (splits_b == 1) {
+        if (d < HD) out[d] = A / L;
+        return;
+    }
+
+    float* part = a.partials + ((size_t)bh * a.num_splits + split) * (HD + 2);
+    if (d < HD) part[d] = A;
+    if (d == 0) {
+        part[HD] = M;
+        part[HD + 1] = L;
+    }
+    __threadfence();  // release this split's partial to the whole device
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(a.counters + bh, 1u, __ATOMIC_ACQ_REL,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (prev == (unsigned)(splits_b - 1));
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();  // acquire the other splits' partials
+
+    const float* pb = a.partials + (size_t)bh * a.num_splits * (HD + 2);
+    if (d < HD) {
+        float MM = -INFINITY;
+        for (int sp = 0; sp < splits_b; sp++)
+            MM = fmaxf(MM, __hip_atomic_load(pb + sp * (HD + 2) + HD, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT));
+        float LL = 0.0f, AA = 0.0f;
+        for (int sp = 0; sp < splits_b; sp++) {
+            const float* ps = pb + sp * (HD + 2);
+            const float ms = __hip_atomic_load(ps + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float f = scale_of(ms, MM);
+            LL += __hip_atomic_load(ps + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * f;
+            AA += __hip_atomic_load(ps + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * f;
+        }
+        out[d] = AA / LL;
+    }
+    if (threadIdx.x == 0)
+        __hip_atomic_store(a.counters + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+int decode_tile_rows(int head_dim) {
+    switch (head_dim) {
+        case 32: return DecodeGeom<32>::TILE;
+        case 64: return DecodeGeom<64>::TILE;
+        case 128: return DecodeGeom<128>::TILE;
+        case 256: return DecodeGeom<256>::TILE;
+        default: return 0;
+    }
+}
+
+hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream) {
+    const dim3 grid((unsigned)((size_t)a.batch * a.n_heads * a.num_splits));
+    const dim3 block(THREADS);
+    switch (a.head_dim) {
+        case 32: hipLaunchKernelGGL(paged_attn_decode_kernel<32>, grid, block, 0, stream, a); break;
+        case 64: hipLaunchKernelGGL(paged_attn_decode_kernel<64>, grid, block, 0, stream, a); break;
+        case 128: hipLaunchKernelGGL(paged_attn_decode_kernel<128>, grid, block, 0, stream, a); break;
+        case 256: hipLaunchKernelGGL(paged_attn_decode_kernel<256>, grid, block, 0, stream, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace nitro

@@ -1,0 +1,195 @@
+// Causal paged-attention prefill for gfx950 (MI355X).
+//
+// Computes what the reference's forward_prefill_chunk attention computes
+// (src/model_q8.cpp:485-523) for a batch of chunks: the token at position
+// pos = start_pos + t attends keys 0..pos of its sequence (prefix-hit pages,
+// earlier chunks and the chunk's own rows, already scattered into the pool).
+//
+// Design: flash-attention style with fp32 VALU FMAs (fp32-exact products, no
+// reduced-precision MFMA):
+//  - A work item is up to BM=64 query rows of one chunk; grid = (work items,
+//    heads).  The host sorts work items by key count, longest first.
+//  - 256 threads: 4 lanes per query row, each lane holding hd/4 of q and of
+//    the output accumulator (float4 slots c, c+4, ... so the 4 lanes of a row
+//    read 64 contiguous bytes of an LDS row: no bank conflicts).
+//  - Keys stream in tiles of BN=32 rows (two pages) staged in LDS through the
+//    block table; the next tile is prefetched into registers while the current
+//    one is consumed.
+//  - Scores in base 2 (q pre-scaled by log2(e)/sqrt(hd)), causal mask per row,
+//    online softmax rescaled once per 8 keys.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "device_pool.hpp"
+
+namespace nitro {
+namespace {
+
+constexpr int BM = 64;
+constexpr int BN = 32;
+constexpr int THREADS = 256;  // BM rows x 4 lanes
+constexpr int KCHUNK = 8;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float sum4(float x) {
+    x += dpp_mov<0xB1>(x);  // lane ^ 1
+    x += dpp_mov<0x4E>(x);  // lane ^ 2
+    return x;
+}
+
+__device__ __forceinline__ float scale_of(float m, float m_new) {
+    return m == -INFINITY ? 0.0f : exp2f(m - m_new);
+}
+
+template <int HD>
+__global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaunch a) {
+    constexpr int F4 = HD / 4;               // float4 per row
+    constexpr int SLOTS = F4 / 4;            // float4 per lane
+    constexpr int LOADS = BN * F4 / THREADS; // float4 per thread per tile per matrix
+    static_assert(LOADS >= 1 && BN * F4 % THREADS == 0, "tile shape");
+    __shared__ float4 ks[BN][F4];
+    __shared__ float4 vs[BN][F4];
+
+    const int seq = a.work[2 * blockIdx.x];
+    const int q0 = a.work[2 * blockIdx.x + 1];
+    const int h = blockIdx.y;
+    const int kv_h = h / a.kv_mul;
+    const int start = a.start_pos[seq];
+    const int qcount = min(BM, a.num_tokens[seq] - q0);
+    const int row = threadIdx.x >> 2;
+    const int c = threadIdx.x & 3;
+    const int last_pos = start + q0 + qcount - 1;
+    const int my_pos = start + q0 + min(row, qcount - 1);
+    const int32_t* trow = a.tables + (size_t)seq * a.max_pages;
+    const int n_tiles = last_pos / BN + 1;
+    const size_t dim = (size_t)a.n_heads * HD;
+    const size_t qrow = (size_t)(a.row_off[seq] + q0 + min(row, qcount - 1));
+
+    float4 qv[SLOTS];
+    {
+        const float4* qp = reinterpret_cast<const float4*>(a.q + qrow * dim + (size_t)h * HD);
+#pragma unroll
+        for (int e = 0; e < SLOTS; e++) {
+            float4 t = qp[c + 4 * e];
+            qv[e] = make_float4(t.x * a.qscale, t.y * a.qscale, t.z * a.qscale, t.w * a.qscale);
+        }
+    }
+    float4 acc[SLOTS];
+#pragma unroll
+    for (int e = 0; e < SLOTS; e++) acc[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+    float m = -INFINITY, l = 0.0f;
+
+    const float* kbase = a.k_pool + a.layer_off + (size_t)kv_h * HD;
+    const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * HD;
+    float4 kreg[LOADS], vreg[LOADS];
+
+    auto fetch = [&](int tile) {
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int f = threadIdx.x + i * THREADS;
+            const int r = f / F4, col = f % F4;
+            const int key = tile * BN + r;
+            kreg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            vreg[i] = kreg[i];
+            if (key <= last_pos) {
+                const int page = trow[key >> 4];
+                if ((unsigned)page < (unsigned)a.num_pages) {
+                    const size_t off = (size_t)page * a.page_stride + (size_t)(key & 15) * a.kv_dim;
+                    kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
+                    vreg[i] = reinterpret_cast<const float4*>(vbase + off)[col];
+                } else if (col == 0) {
+                    atomicAdd(a.bad_pages, 1);
+                }
+            }
+        }
+    };
+
+    fetch(0);
+    for (int tile = 0; tile < n_tiles; tile++) {
+        __syncthreads();  // previous tile fully consumed
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int f = threadIdx.x + i * THREADS;
+            ks[f / F4][f % F4] = kreg[i];
+            vs[f / F4][f % F4] = vreg[i];
+        }
+        __syncthreads();
+        if (tile + 1 < n_tiles) fetch(tile + 1);
+
+        const int key0 = tile * BN;
+#pragma unroll 1
+        for (int jc = 0; jc < BN; jc += KCHUNK) {
+            if (key0 + jc > my_pos) break;  // row-uniform (the 4 lanes of a row agree)
+            float s[KCHUNK];
+            float cmax = -INFINITY;
+#pragma unroll
+            for (int jj = 0; jj < KCHUNK; jj++) {
+                const int j = jc + jj;
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < SLOTS; e++) {
+                    const float4 kk = ks[j][c + 4 * e];
+                    d = fmaf(qv[e].x, kk.x, d);
+                    d = fmaf(qv[e].y, kk.y, d);
+                    d = fmaf(qv[e].z, kk.z, d);
+                    d = fmaf(qv[e].w, kk.w, d);
+                }
+                d = sum4(d);
+                s[jj] = (key0 + j <= my_pos) ? d : -INFINITY;
+                cmax = fmaxf(cmax, s[jj]);
+            }
+            const float m_new = fmaxf(m, cmax);
+            const float alpha = scale_of(m, m_new);
+            l *= alpha;
+#pragma unroll
+            for (int e = 0; e < SLOTS; e++)
+                acc[e] = make_float4(acc[e].x * alpha, acc[e].y * alpha, acc[e].z * alpha,
+                                     acc[e].w * alpha);
+#pragma unroll
+            for (int jj = 0; jj < KCHUNK; jj++) {
+                const float p = s[jj] == -INFINITY ? 0.0f : exp2f(s[jj] - m_new);
+                l += p;
+#pragma unroll
+                for (int e = 0; e < SLOTS; e++) {
+                    const float4 vv = vs[jc + jj][c + 4 * e];
+                    acc[e].x = fmaf(p, vv.x, acc[e].x);
+                    acc[e].y = fmaf(p, vv.y, acc[e].y);
+                    acc[e].z = fmaf(p, vv.z, acc[e].z);
+                    acc[e].w = fmaf(p, vv.w, acc[e].w);
+                }
+            }
+            m = m_new;
+        }
+    }
+
+    if (row < qcount) {
+        const float inv = 1.0f / l;
+        float4* op = reinterpret_cast<float4*>(a.out + qrow * dim + (size_t)h * HD);
+#pragma unroll
+        for (int e = 0; e < SLOTS; e++)
+            op[c + 4 * e] = make_float4(acc[e].x * inv, acc[e].y * inv, acc[e].z * inv, acc[e].w * inv);
+    }
+}
+
+}  // namespace
+
+int prefill_block_m(int) { return BM; }
+
+hipError_t launch_paged_attn_prefill(const PrefillLaunch& a, hipStream_t stream) {
+    const dim3 grid((unsigned)a.work_items, (unsigned)a.n_heads);
+    switch (a.head_dim) {
+        case 32: hipLaunchKernelGGL(paged_attn_prefill_kernel<32>, grid, dim3(THREADS), 0, stream, a); break;
+        case 64: hipLaunchKernelGGL(paged_attn_prefill_kernel<64>, grid, dim3(THREADS), 0, stream, a); break;
+        case 128: hipLaunchKernelGGL(paged_attn_prefill_kernel<128>, grid, dim3(THREADS), 0, stream, a); break;
+        case 256: hipLaunchKernelGGL(paged_attn_prefill_kernel<256>, grid, dim3(THREADS), 0, stream, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace nitro

@@ -335,6 +335,9 @@ def make_attention():
     case_prefill(rec, "prefill_continued_gqa", 4, 2, 16, 1, 16, [20, 25], 42)
     case_prefill(rec, "prefill_hd64", 2, 2, 64, 1, 16, [33], 43)
     case_prefix_hit(rec, "prefix_hit_gqa_l2", 4, 2, 16, 2, 24, 32, 8, 20, 51)
+    case_decode(rec, "decode_gqa_h4kv2_hd32", 4, 2, 32, 2, 32, [0, 16, 31, 77], 25)
+    case_prefill(rec, "prefill_gqa_hd32_l2", 4, 2, 32, 2, 16, [19, 30], 44)
+    case_prefix_hit(rec, "prefix_hit_hd32", 2, 2, 32, 1, 24, 48, 5, 21, 52)
     case_contiguous(rec, "contiguous_hd16", 4, 4, 16, 30, 61)
     case_contiguous(rec, "contiguous_gqa_hd32", 4, 2, 32, 19, 62)
     return rec

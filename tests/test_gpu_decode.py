@@ -1,0 +1,296 @@
+"""GPU parity of the paged-attention decode path and KV append, through the
+C ABI, against the CPU oracle (and the reference's golden vectors)."""
+import ctypes
+import sys
+import zlib
+
+import numpy as np
+import pytest
+
+from gpu_helpers import DecodeCase, assert_parity, random_tables, to_gpu
+from oracle import attn
+from replay import pools_after_call
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    import nitrorag_amd  # noqa: F401  (fails loudly without the built library)
+    yield
+    torch.cuda.synchronize()
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+GOLDEN_DECODE = ["decode_hd64", "decode_hd128", "decode_gqa_h4kv2_hd32", "single_hd32_l2",
+                 "single_gqa_hd64", "single_pos0"]
+
+
+@pytest.mark.parametrize("name", GOLDEN_DECODE)
+def test_decode_matches_reference_golden(golden_attention, name):
+    import torch
+
+    import nitrorag_amd as na
+
+    meta, arr = golden_attention[name]
+    say(f"golden decode {name}")
+    k, v = pools_after_call(meta, arr)
+    if meta["kind"] == "decode_batch":
+        tables, positions = arr["tables"], arr["positions"]
+    else:
+        tables, positions = arr["table"][None, :], np.array([meta["pos"]], np.int32)
+    pool = na.KVPool.wrap(to_gpu(k), to_gpu(v))
+    pool.upload_decode_batch(tables, positions)
+    q = to_gpu(arr["q"])
+    out = torch.empty_like(q)
+    pool.decode(meta["layer"], q, out, meta["H"], meta["Hkv"], meta["hd"])
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    obs = meta["observed"]
+    assert_parity(got[:, -obs:], arr["xb2_obs"], name)
+    want = attn.decode_batch(k, v, meta["layer"], arr["q"], tables, positions, meta["H"],
+                             meta["Hkv"], meta["hd"])
+    assert_parity(got, want, name + " (all heads vs oracle)")
+    assert pool.take_device_errors() == 0
+
+
+SHAPES = {
+    # name: (ctx list or (B, lo, hi), H, Hkv, hd, pages, layers, layer)
+    "llama110m_single_ctx256": ([256], 12, 12, 64, 64, 12, 7),
+    "batched_12x64_b32": ((32, 16, 1024), 12, 12, 64, 2200, 2, 1),
+    "gqa_8x2_hd64": ((5, 1, 300), 8, 2, 64, 128, 1, 0),
+    "gqa_32x8_hd128": ([1, 700, 2049], 32, 8, 128, 200, 1, 0),
+    "mha_hd32": ((4, 1, 500), 4, 4, 32, 140, 1, 0),
+    "mha_hd256": ((3, 1, 300), 2, 2, 256, 64, 1, 0),
+    "edges_hd128": ([1, 15, 16, 17, 32, 33, 4096], 4, 4, 128, 300, 1, 0),
+    "edges_hd64": ([1, 2, 31, 32, 33, 63, 64, 65], 3, 3, 64, 40, 2, 1),
+}
+
+
+def make_case(name, seed=0, **kw):
+    spec, H, Hkv, hd, pages, layers, layer = SHAPES[name]
+    rng = np.random.default_rng(zlib.crc32(name.encode()) + seed)
+    if isinstance(spec, tuple):
+        B, lo, hi = spec
+        ctx = rng.integers(lo, hi + 1, size=B)
+    else:
+        ctx = np.array(spec)
+    return DecodeCase(rng, ctx, H, Hkv, hd, pages, layers, layer, **kw)
+
+
+@pytest.mark.parametrize("name", sorted(SHAPES))
+def test_decode_vs_oracle(name):
+    say(f"decode vs oracle {name}")
+    c = make_case(name)
+    assert_parity(c.run_gpu(), c.run_oracle(), name)
+    assert c.pool.take_device_errors() == 0
+
+
+@pytest.mark.parametrize("tiles", ["1", "3", "4", "8", "100000"])
+def test_decode_split_k_partitions_agree(tiles, monkeypatch):
+    """Any split-K partition (1 tile per split .. a single split) gives the
+    same answer within the bar; repeated launches reuse the self-resetting
+    arrival counters."""
+    say(f"split-K tiles_per_split={tiles}")
+    monkeypatch.setenv("NITRO_DECODE_SPLIT_TILES", tiles)
+    c = make_case("edges_hd128")
+    want = c.run_oracle()
+    first = c.run_gpu()
+    assert_parity(first, want, f"tiles={tiles}")
+    for _ in range(3):
+        again = c.run_gpu()
+        assert np.array_equal(again, first)
+
+
+def test_decode_page_permutation_is_bit_identical():
+    """Renaming physical pages consistently leaves the result bit-identical."""
+    say("page permutation")
+    rng = np.random.default_rng(11)
+    c = make_case("batched_12x64_b32")
+    base = c.run_gpu()
+    perm = rng.permutation(c.k.shape[0]).astype(np.int32)
+    k2 = np.empty_like(c.k)
+    v2 = np.empty_like(c.v)
+    k2[perm] = c.k
+    v2[perm] = c.v
+    import nitrorag_amd as na
+
+    pool = na.KVPool.wrap(to_gpu(k2), to_gpu(v2))
+    pool.upload_decode_batch(perm[c.tables], c.positions)
+    import torch
+
+    q = to_gpu(c.q)
+    out = torch.empty_like(q)
+    pool.decode(c.layer, q, out, c.H, c.Hkv, c.hd)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), base)
+
+
+def test_decode_constant_v_and_single_key():
+    say("constant V / ctx=1")
+    import torch
+
+    import nitrorag_amd as na
+
+    rng = np.random.default_rng(5)
+    H, hd, pages = 4, 128, 80
+    kv_dim = H * hd
+    ctx = np.array([1, 17, 600])
+    tables = random_tables(rng, ctx, pages)
+    k = rng.standard_normal((pages, 1, 16, kv_dim)).astype(np.float32)
+    row = rng.standard_normal(kv_dim).astype(np.float32)
+    v = np.broadcast_to(row, k.shape).copy()
+    q = rng.standard_normal((3, kv_dim)).astype(np.float32)
+    pool = na.KVPool.wrap(to_gpu(k), to_gpu(v))
+    pool.upload_decode_batch(tables, ctx - 1)
+    out = torch.empty_like(to_gpu(q))
+    pool.decode(0, to_gpu(q), out, H, H, hd)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out.cpu().numpy(), np.broadcast_to(row, (3, kv_dim)), rtol=1e-5,
+                               atol=1e-6)
+
+
+def test_kv_append_bit_exact_and_then_attended():
+    """forward_decode_batch's order: append this step's K/V at pos, then attend 0..pos."""
+    say("kv append")
+    import torch
+
+    c = make_case("gqa_8x2_hd64")
+    B, kv_dim = len(c.ctx), c.Hkv * c.hd
+    rng = np.random.default_rng(3)
+    knew = rng.standard_normal((B, kv_dim)).astype(np.float32)
+    vnew = rng.standard_normal((B, kv_dim)).astype(np.float32)
+    c.pool.kv_append(c.layer, to_gpu(knew), to_gpu(vnew))
+    got = c.run_gpu()
+    attn.kv_append_decode(c.k, c.v, c.layer, knew, vnew, c.tables, c.positions)
+    torch.cuda.synchronize()
+    assert np.array_equal(c.dk.cpu().numpy(), c.k)
+    assert np.array_equal(c.dv.cpu().numpy(), c.v)
+    assert_parity(got, c.run_oracle(), "after append")
+
+
+def test_owned_pool_create_and_layer_offsets():
+    """nitro_kvpool_create owns zeroed memory with the reference layout."""
+    say("owned pool")
+    import torch
+
+    import nitrorag_amd as na
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    pages, layers, H, hd = 24, 3, 2, 64
+    kv_dim = H * hd
+    pool = na.KVPool(pages, layers, kv_dim)
+    kp, vp = pool.data_ptrs()
+    nbytes = pages * layers * 16 * kv_dim * 4
+    back = np.ones(pages * layers * 16 * kv_dim, np.float32)
+    assert hip.hipMemcpy(back.ctypes.data, kp, nbytes, 2) == 0  # device -> host
+    assert not back.any()
+    rng = np.random.default_rng(8)
+    k = rng.standard_normal((pages, layers, 16, kv_dim)).astype(np.float32)
+    v = rng.standard_normal((pages, layers, 16, kv_dim)).astype(np.float32)
+    assert hip.hipMemcpy(kp, k.ctypes.data, nbytes, 1) == 0  # host -> device
+    assert hip.hipMemcpy(vp, v.ctypes.data, nbytes, 1) == 0
+    ctx = np.array([5, 100, 200])
+    tables = random_tables(rng, ctx, pages)
+    pool.upload_decode_batch(tables, ctx - 1)
+    q = rng.standard_normal((3, kv_dim)).astype(np.float32)
+    for layer in range(layers):
+        out = torch.empty((3, kv_dim), device="cuda")
+        pool.decode(layer, to_gpu(q), out, H, H, hd)
+        torch.cuda.synchronize()
+        assert_parity(out.cpu().numpy(), attn.decode_batch(k, v, layer, q, tables, ctx - 1, H, H,
+                                                           hd), f"layer {layer}")
+    pool.close()
+
+
+def test_decode_argument_errors():
+    say("argument errors")
+    import torch
+
+    import nitrorag_amd as na
+    from nitrorag_amd import _native as N
+
+    k = torch.zeros((8, 1, 16, 128), device="cuda")
+    v = torch.zeros_like(k)
+    pool = na.KVPool.wrap(k, v)
+    q = torch.zeros((1, 128), device="cuda")
+    out = torch.zeros_like(q)
+    with pytest.raises(na.NitroError) as e:
+        pool.decode(0, q, out, 1, 1, 128)
+    assert e.value.status == N.NO_BATCH
+    with pytest.raises(na.NitroError) as e:
+        pool.upload_decode_batch([[0, 8]], [17])  # page id 8 outside an 8-page pool
+    assert e.value.status == N.BAD_BLOCK_TABLE
+    with pytest.raises(na.NitroError) as e:
+        pool.upload_decode_batch([[0, 1]], [32])  # pos 32 needs a third page
+    assert e.value.status == N.BAD_BLOCK_TABLE
+    with pytest.raises(na.NitroError) as e:
+        pool.upload_decode_batch([[0, -1]], [20])
+    assert e.value.status == N.BAD_BLOCK_TABLE
+    pool.upload_decode_batch([[3, 5]], [20])
+
+    def raw(layer, H, Hkv, hd):  # the C entry point itself (no Python-side size checks)
+        return N.lib().nitro_paged_attn_decode(pool.handle, layer, ctypes.c_void_p(q.data_ptr()),
+                                               ctypes.c_void_p(out.data_ptr()), H, Hkv, hd, None)
+
+    assert raw(0, 1, 1, 96) == N.UNSUPPORTED
+    assert raw(0, 3, 2, 64) == N.UNSUPPORTED
+    assert raw(1, 1, 1, 128) == N.INVALID_ARGUMENT  # layer outside a 1-layer pool
+    assert raw(0, 2, 1, 64) == N.INVALID_ARGUMENT   # kv_dim mismatch (1*64 != 128)
+    assert raw(0, 1, 1, 128) == N.OK
+    torch.cuda.synchronize()
+    assert pool.take_device_errors() == 0
+
+
+def test_full_size_b64_ctx4096_32x128_subset_vs_oracle():
+    """The benchmark workload at its real size (B=64, ctx 4096, 32 heads x 128,
+    20k-page pool): every sequence decoded on the GPU; four checked against the
+    oracle on host copies of just their pages; all outputs finite, and the
+    batch is invariant to the order of sequences."""
+    import torch
+
+    import nitrorag_amd as na
+
+    say("full-size B=64 ctx=4096 32x128")
+    B, H, hd, ctx, pages = 64, 32, 128, 4096, 20000
+    kv_dim = H * hd
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x4E4954525005)
+    k = torch.randn((pages, 1, 16, kv_dim), device="cuda", generator=g)
+    v = torch.randn((pages, 1, 16, kv_dim), device="cuda", generator=g)
+    q = torch.randn((B, kv_dim), device="cuda", generator=g)
+    rng = np.random.default_rng(5)
+    tables = random_tables(rng, np.full(B, ctx), pages)
+    positions = np.full(B, ctx - 1, np.int32)
+    pool = na.KVPool.wrap(k, v)
+    pool.upload_decode_batch(tables, positions)
+    out = torch.empty_like(q)
+    pool.decode(0, q, out, H, H, hd)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    for b in (0, 17, 42, 63):
+        idx = torch.from_numpy(tables[b].astype(np.int64)).cuda()
+        kb = k.index_select(0, idx).cpu().numpy()
+        vb = v.index_select(0, idx).cpu().numpy()
+        local = np.arange(tables.shape[1], dtype=np.int32)[None, :]
+        want = attn.decode_batch(kb, vb, 0, q[b:b + 1].cpu().numpy(), local, positions[b:b + 1],
+                                 H, H, hd)
+        assert_parity(got[b:b + 1], want, f"sequence {b}")
+    order = rng.permutation(B)
+    pool.upload_decode_batch(tables[order], positions[order])
+    out2 = torch.empty_like(q)
+    pool.decode(0, q[torch.from_numpy(order).cuda()].contiguous(), out2, H, H, hd)
+    torch.cuda.synchronize()
+    assert np.array_equal(out2.cpu().numpy(), got[order])
+    assert pool.take_device_errors() == 0
+    del k, v
+    torch.cuda.empty_cache()

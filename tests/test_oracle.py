@@ -41,7 +41,8 @@ def closed_form_case(meta, arr, k, v):
 
 PAGED_CASES = ["decode_mha_hd16_l2", "decode_gqa_h8kv2_hd16", "decode_hd64", "decode_hd128",
                "single_hd32_l2", "single_gqa_hd64", "single_pos0", "prefill_fresh_hd16_l2",
-               "prefill_continued_gqa", "prefill_hd64", "prefix_hit_gqa_l2"]
+               "prefill_continued_gqa", "prefill_hd64", "prefix_hit_gqa_l2",
+               "decode_gqa_h4kv2_hd32", "prefill_gqa_hd32_l2", "prefix_hit_hd32"]
 
 
 @pytest.mark.parametrize("name", PAGED_CASES)
