@@ -55,6 +55,19 @@ def seeded_tables(B: int, ctx: int, pages: int, seed: int) -> np.ndarray:
     return perm[: B * n].reshape(B, n).copy()
 
 
+def measured_traffic(path: str):
+    """HBM bytes per decode launch recorded from rocprofv3 FETCH_SIZE + WRITE_SIZE
+    runs (calibrated against a copy of known size) in the profile summary, or None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(k, v, tables, positions, q, knew, vnew, H, Hkv, hd, seconds=10.0,
                  sample=8):
     """Times the CPU oracle (append + batched decode, all host cores) on the
@@ -108,6 +121,12 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0x4E49545205)
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="also run a plain device-to-device copy of this many MiB three times "
+                         "(the known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--traffic-profile",
+                    default=os.path.join(ROOT, "profiles", "paged_attn_decode_b64_ctx4096_32x128.md"),
+                    help="rocprofv3 summary holding the measured HBM traffic per decode launch")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the paged-attention path shards by sequence or "
@@ -133,6 +152,14 @@ def main():
     out = torch.empty_like(q)
     tables = seeded_tables(B, ctx, pages, args.seed)
     positions = np.full(B, ctx - 1, np.int32)
+
+    if args.copy_calibration_mib:
+        src = torch.randn(args.copy_calibration_mib * 2**18, device=dev, generator=g)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     stream = torch.cuda.current_stream()
     pool = na.KVPool.wrap(k, v)
@@ -196,7 +223,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.traffic_profile),
             "bytes_per_launch": nbytes,
             "kernel_ms": round(kernel_ms, 4),
         },

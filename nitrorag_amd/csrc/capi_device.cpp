@@ -17,8 +17,10 @@ using namespace nitro;
 
 namespace {
 
-constexpr int kDecodeWaves = 4;             // waves per decode workgroup (kernel constant)
-constexpr int kDecodeTargetGroups = 4096;   // ~16 workgroups per CU on 256 CUs
+constexpr int kDecodeWaves = 4;  // waves per decode workgroup (kernel constant)
+// Decode workgroups resident per CU at the kernel's occupancy (4 waves/SIMD,
+// 4 SIMDs, 4-wave workgroups); one such wave of workgroups fills the GPU.
+constexpr int kDecodeGroupsPerCU = 4;
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -73,6 +75,9 @@ static int make_pool(float* k, float* v, bool owned, int32_t num_pages, int32_t 
         nitro_kvpool* pool = new nitro_kvpool();
         try {
             hip_check(hipGetDevice(&pool->device), "hipGetDevice");
+            hip_check(hipDeviceGetAttribute(&pool->num_cus, hipDeviceAttributeMultiprocessorCount,
+                                            pool->device),
+                      "hipDeviceGetAttribute");
             pool->num_pages = num_pages;
             pool->num_layers = num_layers;
             pool->kv_dim = kv_dim;
@@ -199,32 +204,30 @@ int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, f
 
         const int tile = decode_tile_rows(head_dim);
         int max_tiles = 0;
-        long long total_tiles = 0;
-        for (int p : d.positions) {
-            const int n = (p + 1 + tile - 1) / tile;
-            max_tiles = std::max(max_tiles, n);
-            total_tiles += n;
-        }
-        total_tiles *= n_heads;
-        // Tiles per split: enough splits to give ~kDecodeTargetGroups workgroups,
-        // at least one tile per wave, and a block-table slice that fits in LDS.
+        for (int p : d.positions) max_tiles = std::max(max_tiles, (p + 1 + tile - 1) / tile);
+        // Split-K only when one workgroup per (b, h) cannot fill the GPU: then
+        // split the longest context into enough runs of tiles to give about
+        // two rounds of workgroups, at least one tile per wave.  Each split's
+        // block-table slice must fit in LDS.
+        const long long bh_count = (long long)d.batch * n_heads;
+        const long long fill = 2LL * kDecodeGroupsPerCU * std::max(pool->num_cus, 1);
         int tps = env_int("NITRO_DECODE_SPLIT_TILES", 0);
         if (tps <= 0) {
-            long long want = (total_tiles + kDecodeTargetGroups - 1) / kDecodeTargetGroups;
-            tps = (int)std::max<long long>(kDecodeWaves, (want + kDecodeWaves - 1) / kDecodeWaves * kDecodeWaves);
+            if (bh_count >= fill / 2) {
+                tps = max_tiles;
+            } else {
+                const long long want_splits = (fill + bh_count - 1) / bh_count;
+                tps = (int)((max_tiles + want_splits - 1) / want_splits);
+                tps = (tps + kDecodeWaves - 1) / kDecodeWaves * kDecodeWaves;
+            }
         }
         const int max_tps = (DECODE_MAX_SPLIT_PAGES - 2) * BLOCK_SIZE / tile;
-        tps = std::min(tps, max_tps);
-        tps = std::max(tps, 1);
+        tps = std::max(1, std::min(tps, max_tps));
         const int splits = (max_tiles + tps - 1) / tps;
 
         hipStream_t s = as_stream(stream);
         const size_t bh = (size_t)d.batch * n_heads;
-        if (splits > 1) {
-            pool->partials.reserve(bh * splits * (head_dim + 2));
-            if (pool->counters.reserve(bh))
-                hip_check(hipMemsetAsync(pool->counters.ptr, 0, bh * sizeof(uint32_t), s), "hipMemsetAsync");
-        }
+        if (splits > 1) pool->partials.reserve(bh * splits * (head_dim + 2));
         DecodeLaunch a{};
         a.q = q;
         a.out = out;
@@ -233,7 +236,6 @@ int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, f
         a.tables = d.tables.ptr;
         a.positions = d.pos.ptr;
         a.partials = pool->partials.ptr;
-        a.counters = pool->counters.ptr;
         a.bad_pages = pool->bad_pages.ptr;
         a.page_stride = pool->page_stride();
         a.layer_off = pool->layer_offset(layer);

@@ -111,11 +111,11 @@ struct nitro_kvpool {
     bool owned = false;
     int32_t num_pages = 0, num_layers = 0, kv_dim = 0;
     int device = 0;
+    int num_cus = 256;  // compute units of the pool's device (launch geometry)
     hipStream_t last_stream = nullptr;
     nitro::DecodeBatch decode;
     nitro::PrefillBatch prefill;
     nitro::DeviceBuffer<float> partials;      // split-K (m, l, acc[hd]) per (b, h, split)
-    nitro::DeviceBuffer<uint32_t> counters;   // arrivals per (b, h); self-resetting
     nitro::DeviceBuffer<int32_t> bad_pages;   // [1] device error counter
     nitro::Staging decode_staging, prefill_staging;
 
@@ -134,7 +134,6 @@ struct DecodeLaunch {
     const int32_t* tables;
     const int32_t* positions;
     float* partials;
-    uint32_t* counters;
     int32_t* bad_pages;
     int64_t page_stride, layer_off;
     int32_t kv_dim, batch, n_heads, kv_mul, head_dim, max_pages, num_pages;

@@ -19,10 +19,13 @@
 //  - Softmax: every lane group keeps its own running (max, sum, acc) in base 2
 //    (q is pre-scaled by log2(e)/sqrt(hd)); groups, then waves (through LDS),
 //    then splits are merged with the usual rescaling.  No score scratch.
-//  - Split-K merge: each workgroup writes (m, l, acc[hd]) for its split; the
-//    last to arrive for (b, h) (agent-scope atomic counter, release/acquire
-//    fences) merges all splits and resets the counter, so decode is a single
-//    launch and needs no memset between launches.
+//  - Split-K: when one split per (b, h) would leave the GPU underfilled, each
+//    workgroup writes (m, l, acc[hd]) for its split and a second, small
+//    kernel merges the splits.  With one split the workgroup writes the output
+//    directly and decode is a single launch.  (Merging inside the kernel by
+//    the last-arriving workgroup needs agent-scope release/acquire fences,
+//    which write back and invalidate the whole XCD L2 per workgroup on
+//    gfx950; measured, that halved throughput at two splits.)
 //  - The split's block-table slice is staged in LDS once; page ids outside
 //    the pool are counted in *bad_pages and their rows skipped (no fault).
 #include <hip/hip_runtime.h>
@@ -79,7 +82,6 @@ __global__ __launch_bounds__(THREADS) void paged_attn_decode_kernel(DecodeLaunch
     __shared__ int32_t s_pages[DECODE_MAX_SPLIT_PAGES];
     __shared__ float s_acc[WAVES][HD];
     __shared__ float s_m[WAVES], s_l[WAVES];
-    __shared__ int s_last;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -245,35 +247,30 @@ __global__ __launch_bounds__(THREADS) void paged_attn_decode_kernel(DecodeLaunch
         part[HD] = M;
         part[HD + 1] = L;
     }
-    __threadfence();  // release this split's partial to the whole device
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(a.counters + bh, 1u, __ATOMIC_ACQ_REL,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == (unsigned)(splits_b - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();  // acquire the other splits' partials
+}
 
+// Merges the per-split partials of every (b, h) that has more than one split.
+template <int HD>
+__global__ __launch_bounds__(HD < 64 ? 64 : HD) void paged_attn_decode_merge_kernel(DecodeLaunch a) {
+    constexpr int TILE = DecodeGeom<HD>::TILE;
+    const int bh = blockIdx.x;
+    const int b = bh / a.n_heads;
+    const int ctx = a.positions[b] + 1;
+    const int n_tiles = (ctx + TILE - 1) / TILE;
+    const int splits_b = (n_tiles + a.tiles_per_split - 1) / a.tiles_per_split;
+    const int d = threadIdx.x;
+    if (splits_b <= 1 || d >= HD) return;  // single split: written by the main kernel
     const float* pb = a.partials + (size_t)bh * a.num_splits * (HD + 2);
-    if (d < HD) {
-        float MM = -INFINITY;
-        for (int sp = 0; sp < splits_b; sp++)
-            MM = fmaxf(MM, __hip_atomic_load(pb + sp * (HD + 2) + HD, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT));
-        float LL = 0.0f, AA = 0.0f;
-        for (int sp = 0; sp < splits_b; sp++) {
-            const float* ps = pb + sp * (HD + 2);
-            const float ms = __hip_atomic_load(ps + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float f = scale_of(ms, MM);
-            LL += __hip_atomic_load(ps + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * f;
-            AA += __hip_atomic_load(ps + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * f;
-        }
-        out[d] = AA / LL;
+    float M = -INFINITY;
+    for (int sp = 0; sp < splits_b; sp++) M = fmaxf(M, pb[sp * (HD + 2) + HD]);
+    float L = 0.0f, A = 0.0f;
+    for (int sp = 0; sp < splits_b; sp++) {
+        const float* ps = pb + sp * (HD + 2);
+        const float f = scale_of(ps[HD], M);
+        L += ps[HD + 1] * f;
+        A += ps[d] * f;
     }
-    if (threadIdx.x == 0)
-        __hip_atomic_store(a.counters + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    a.out[(size_t)bh * HD + d] = A / L;
 }
 
 }  // namespace
@@ -288,17 +285,27 @@ int decode_tile_rows(int head_dim) {
     }
 }
 
-hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream) {
+template <int HD>
+static hipError_t launch_hd(const DecodeLaunch& a, hipStream_t stream) {
     const dim3 grid((unsigned)((size_t)a.batch * a.n_heads * a.num_splits));
-    const dim3 block(THREADS);
-    switch (a.head_dim) {
-        case 32: hipLaunchKernelGGL(paged_attn_decode_kernel<32>, grid, block, 0, stream, a); break;
-        case 64: hipLaunchKernelGGL(paged_attn_decode_kernel<64>, grid, block, 0, stream, a); break;
-        case 128: hipLaunchKernelGGL(paged_attn_decode_kernel<128>, grid, block, 0, stream, a); break;
-        case 256: hipLaunchKernelGGL(paged_attn_decode_kernel<256>, grid, block, 0, stream, a); break;
-        default: return hipErrorInvalidValue;
+    hipLaunchKernelGGL(paged_attn_decode_kernel<HD>, grid, dim3(THREADS), 0, stream, a);
+    if (a.num_splits > 1) {
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(paged_attn_decode_merge_kernel<HD>, dim3((unsigned)(a.batch * a.n_heads)),
+                           dim3(HD < 64 ? 64 : HD), 0, stream, a);
     }
     return hipGetLastError();
+}
+
+hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream) {
+    switch (a.head_dim) {
+        case 32: return launch_hd<32>(a, stream);
+        case 64: return launch_hd<64>(a, stream);
+        case 128: return launch_hd<128>(a, stream);
+        case 256: return launch_hd<256>(a, stream);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace nitro
