@@ -1,25 +1,38 @@
-"""Benchmark of the MI355X paged-attention decode path.
+"""Benchmark of the MI355X paged-attention path.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode-b64-ctx4096]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
-Workload (one GPU): batched paged-attention decode at the Llama-2-7B attention
-shape — B=64 sequences, 32 query heads = 32 KV heads, head_dim 128, context
-4096 tokens each (256 pages of 16 tokens), fp32 K/V ~ N(0,1) in a 20,000-page
-pool with block tables drawn from one seeded permutation of the pool, one
-layer.  A step is what forward_decode_batch does per layer for attention
-(src/model_q8.cpp:616-662): append this step's K/V row of every sequence at
-its position, then attend over positions 0..4095.  Inputs are resident in HBM
-before timing starts.
+Default workload (the headline line): batched paged-attention decode at the
+Llama-2-7B attention shape — B=64 sequences, 32 query heads = 32 KV heads,
+head_dim 128, context 4096 tokens each (256 pages of 16 tokens), fp32 K/V ~
+N(0,1) in a 20,000-page pool with block tables drawn from one seeded
+permutation of the pool, one layer.  A step is what forward_decode_batch does
+per layer for attention (src/model_q8.cpp:616-662): append this step's K/V row
+of every sequence at its position, then attend over positions 0..4095.
+Inputs are resident in HBM before timing starts.
 
 Reported:
   value / unit      algorithmic GB/s of the whole step (append + decode)
-  roofline          the decode kernel alone: algorithmic bytes per launch /
+  roofline          the dominant kernel alone: algorithmic bytes per launch /
                     mean launch time from HIP events on the launch stream,
-                    against MI355X's 8 TB/s HBM peak
+                    against MI355X's 8 TB/s HBM peak; `traffic` is the HBM bytes
+                    per launch measured with rocprofv3 (profiles/)
   cpu_baseline      the CPU oracle (C restatement of the reference's OpenMP
                     loops, all host cores) on a sample of the same workload
 Algorithmic bytes per decode launch: sum_b ctx_b*Hkv*hd*4*2 (K and V) +
 B*H*hd*4*2 (q in, out) + sum_b ceil(ctx_b/16)*4 (block-table entries).
+
+Other workloads (parity-test shapes, measured for the design notes):
+  decode-single-110m     1 sequence, 12 layers x 12 heads x 64, ctx 256, 64-page pool;
+                         a step is one token through all 12 layers' append + attention
+  decode-b32-mixed       B=32, 12x64, ctx ~ U[16,1024], 4096-page pool (12 layers, one timed)
+  decode-prefix-shared   B=48, 12x64, 512 shared prefix tokens (32 pages, FNV-1a cache
+                         hits) + private suffixes ~ U[64,512]
+  prefill-b8-12x64       B=8 prompts, lengths ~ U[128,1024], 12x64, KV scattered into
+                         fresh pages then attended causally; FLOPs = sum 2*H*hd*L(L+1)
+The three small decode workloads fit in the 256 MB Infinity Cache, so a 1 GiB
+buffer is read before every timed launch and only the launch itself is timed
+(events).
 """
 from __future__ import annotations
 
@@ -35,24 +48,28 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
 METRIC = "paged-attn decode GB/s (% HBM peak) + tokens/s at B=64 ctx4096"
-
-WORKLOADS = {
-    # name: (B, ctx, H, Hkv, hd, pool pages, layers)
-    "decode-b64-ctx4096": (64, 4096, 32, 32, 128, 20000, 1),
-}
+DEFAULT_WORKLOAD = "decode-b64-ctx4096"
 
 
-def decode_bytes(ctx: np.ndarray, B: int, H: int, Hkv: int, hd: int) -> int:
+def decode_bytes(ctx, B: int, H: int, Hkv: int, hd: int) -> int:
     ctx = np.asarray(ctx, dtype=np.int64)
     return int((ctx * Hkv * hd * 4 * 2).sum() + B * H * hd * 4 * 2 + ((ctx + 15) // 16 * 4).sum())
 
 
-def seeded_tables(B: int, ctx: int, pages: int, seed: int) -> np.ndarray:
+def seeded_tables(ctx, pages: int, seed: int) -> np.ndarray:
+    """Block tables consumed sequentially from one seeded permutation of the pool."""
+    ctx = np.asarray(ctx)
+    need = (ctx + 15) // 16
+    assert need.sum() <= pages
     perm = np.random.default_rng(seed).permutation(pages).astype(np.int32)
-    n = (ctx + 15) // 16
-    assert B * n <= pages
-    return perm[: B * n].reshape(B, n).copy()
+    t = np.zeros((len(ctx), int(need.max())), np.int32)
+    off = 0
+    for b, n in enumerate(need):
+        t[b, :n] = perm[off:off + n]
+        off += n
+    return t
 
 
 def measured_traffic(path: str):
@@ -68,48 +85,275 @@ def measured_traffic(path: str):
     return None
 
 
-def cpu_baseline(k, v, tables, positions, q, knew, vnew, H, Hkv, hd, seconds=10.0,
-                 sample=8):
-    """Times the CPU oracle (append + batched decode, all host cores) on the
-    first `sample` sequences, their pages copied to a compact host pool."""
-    import torch
-
-    from oracle import attn
-
-    n_pages = tables.shape[1]
-    sel = tables[:sample]
-    idx = torch.from_numpy(sel.reshape(-1).astype(np.int64)).to(k.device)
-    kh = k.index_select(0, idx).cpu().numpy()
-    vh = v.index_select(0, idx).cpu().numpy()
-    local = np.arange(sample * n_pages, dtype=np.int32).reshape(sample, n_pages)
-    qh = q[:sample].cpu().numpy()
-    kn = knew[:sample].cpu().numpy()
-    vn = vnew[:sample].cpu().numpy()
-    pos = positions[:sample]
-    threads = attn.max_threads()
-    attn.kv_append_decode(kh, vh, 0, kn, vn, local, pos)
-    attn.decode_batch(kh, vh, 0, qh, local, pos, H, Hkv, hd, threads)  # warm-up
+def time_cpu(fn, seconds: float):
+    fn()  # warm-up
     reps, t0 = 0, time.perf_counter()
     while True:
-        attn.kv_append_decode(kh, vh, 0, kn, vn, local, pos)
-        attn.decode_batch(kh, vh, 0, qh, local, pos, H, Hkv, hd, threads)
+        fn()
         reps += 1
         el = time.perf_counter() - t0
         if el >= seconds:
-            break
-    per_rep = el / reps
-    b = decode_bytes(pos + 1, sample, H, Hkv, hd)
-    return {
-        "value": round(b / per_rep / 1e9, 3),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"{sample} of the {len(positions)} sequences (same shape, ctx {int(pos[0]) + 1}, "
-                   f"{H}x{hd}), append + batched decode, {reps} reps in {el:.1f} s; "
-                   f"{sample / per_rep:.1f} tokens/s"),
-        "tokens_per_s": round(sample / per_rep, 3),
-        "ms_per_rep": round(per_rep * 1e3, 3),
-    }
+            return el / reps, reps, el
+
+
+class DecodeWorkload:
+    """Paged decode: per layer, append every sequence's new K/V row, then attend."""
+
+    bound = "hbm"
+
+    def __init__(self, name, B, H, Hkv, hd, pages, layers, steps_layers, ctx, flush, seed,
+                 tables=None, unique_pages=None, describe=""):
+        self.name, self.B, self.H, self.Hkv, self.hd = name, B, H, Hkv, hd
+        self.pages, self.layers, self.steps_layers = pages, layers, steps_layers
+        self.ctx = np.asarray(ctx, dtype=np.int64)
+        self.positions = (self.ctx - 1).astype(np.int32)
+        self.flush, self.seed, self.describe = flush, seed, describe
+        self.tables = seeded_tables(self.ctx, pages, seed) if tables is None else tables
+        self.unique_pages = unique_pages
+
+    def setup(self, dev, g):
+        import torch
+
+        import nitrorag_amd as na
+
+        kv_dim = self.Hkv * self.hd
+        self.k = torch.randn((self.pages, self.layers, 16, kv_dim), device=dev, generator=g)
+        self.v = torch.randn((self.pages, self.layers, 16, kv_dim), device=dev, generator=g)
+        L = len(self.steps_layers)
+        self.q = torch.randn((L, self.B, self.H * self.hd), device=dev, generator=g)
+        self.knew = torch.randn((L, self.B, kv_dim), device=dev, generator=g)
+        self.vnew = torch.randn((L, self.B, kv_dim), device=dev, generator=g)
+        self.out = torch.empty((L, self.B, self.H * self.hd), device=dev)
+        self.pool = na.KVPool.wrap(self.k, self.v)
+        self.pool.upload_decode_batch(self.tables, self.positions)
+        # 1 GiB read before each timed launch evicts the 256 MB Infinity Cache and the
+        # L2s with clean lines (a write would leave dirty lines draining during the launch)
+        self.scratch = torch.ones(2**28, device=dev) if self.flush else None
+        self.flush_out = torch.empty((), device=dev)
+
+    def step(self, stream, events=None):
+        import torch
+
+        for i, layer in enumerate(self.steps_layers):
+            if self.scratch is not None:
+                torch.sum(self.scratch, dim=0, out=self.flush_out)
+            self.pool.kv_append(layer, self.knew[i], self.vnew[i], stream)
+            if events is not None:
+                events[i][0].record(stream)
+            self.pool.decode(layer, self.q[i], self.out[i], self.H, self.Hkv, self.hd, stream)
+            if events is not None:
+                events[i][1].record(stream)
+
+    def launches_per_step(self):
+        return len(self.steps_layers)
+
+    def work_per_launch(self):
+        return decode_bytes(self.ctx, self.B, self.H, self.Hkv, self.hd)
+
+    def tokens_per_step(self):
+        return self.B
+
+    def check(self):
+        import torch
+
+        assert torch.isfinite(self.out).all().item(), "non-finite decode output"
+
+    def cpu_baseline(self, seconds, sample):
+        """Oracle append + decode on `sample` sequences (their pages copied to a compact pool)."""
+        import torch
+
+        from oracle import attn
+
+        sample = min(sample, self.B)
+        n_pages = self.tables.shape[1]
+        sel = self.tables[:sample]
+        idx = torch.from_numpy(sel.reshape(-1).astype(np.int64)).to(self.k.device)
+        kh = self.k.index_select(0, idx).cpu().numpy()
+        vh = self.v.index_select(0, idx).cpu().numpy()
+        local = np.arange(sample * n_pages, dtype=np.int32).reshape(sample, n_pages)
+        q = self.q[:, :sample].cpu().numpy()
+        kn = self.knew[:, :sample].cpu().numpy()
+        vn = self.vnew[:, :sample].cpu().numpy()
+        pos = self.positions[:sample]
+        threads = attn.max_threads()
+
+        def run():
+            for i, layer in enumerate(self.steps_layers):
+                attn.kv_append_decode(kh, vh, layer, kn[i], vn[i], local, pos)
+                attn.decode_batch(kh, vh, layer, q[i], local, pos, self.H, self.Hkv, self.hd,
+                                  threads)
+
+        per_rep, reps, el = time_cpu(run, seconds)
+        nbytes = decode_bytes(pos + 1, sample, self.H, self.Hkv, self.hd) * len(self.steps_layers)
+        return {
+            "value": round(nbytes / per_rep / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"{sample} of the {self.B} sequences of this workload, append + batched "
+                       f"decode over {len(self.steps_layers)} layer(s), {reps} reps in {el:.1f} s; "
+                       f"{sample / per_rep:.1f} tokens/s"),
+            "tokens_per_s": round(sample / per_rep, 3),
+        }
+
+    def extra(self, kernel_s):
+        if self.unique_pages is None:
+            return {}
+        ub = self.unique_pages * 16 * self.Hkv * self.hd * 4 * 2
+        return {"unique_kv_bytes_per_launch": int(ub),
+                "unique_kv_gbps": round(ub / kernel_s / 1e9, 2)}
+
+
+class PrefillWorkload:
+    """Causal paged prefill: scatter the chunk's K/V rows, then attend."""
+
+    bound = "fp32"
+    flush = False
+
+    def __init__(self, name, B, H, Hkv, hd, lens, seed, describe):
+        import nitrorag_amd as na
+
+        self.name, self.B, self.H, self.Hkv, self.hd = name, B, H, Hkv, hd
+        self.lens = np.asarray(lens, dtype=np.int64)
+        self.starts = np.zeros(B, np.int32)
+        self.seed, self.describe = seed, describe
+        self.pages = int(((self.lens + 15) // 16).sum())
+        bm = na.BlockManager(self.pages)  # fresh pool: LIFO page ids, as the reference hands out
+        seqs = []
+        rng = np.random.default_rng(seed)
+        for b in range(B):
+            s = na.Sequence(b)
+            s.ingest_prompt(rng.integers(1, 32000, size=int(self.lens[b])), bm, False)
+            seqs.append(s)
+        self.tables = na.pack_block_tables(seqs)
+
+    def setup(self, dev, g):
+        import torch
+
+        import nitrorag_amd as na
+
+        kv_dim = self.Hkv * self.hd
+        total = int(self.lens.sum())
+        self.k = torch.zeros((self.pages, 1, 16, kv_dim), device=dev)
+        self.v = torch.zeros_like(self.k)
+        self.q = torch.randn((total, self.H * self.hd), device=dev, generator=g)
+        self.kc = torch.randn((total, kv_dim), device=dev, generator=g)
+        self.vc = torch.randn((total, kv_dim), device=dev, generator=g)
+        self.out = torch.empty_like(self.q)
+        self.pool = na.KVPool.wrap(self.k, self.v)
+        self.pool.upload_prefill_batch(self.tables, self.starts, self.lens)
+
+    def step(self, stream, events=None):
+        self.pool.kv_append_prefill(0, self.kc, self.vc, stream)
+        if events is not None:
+            events[0][0].record(stream)
+        self.pool.prefill(0, self.q, self.out, self.H, self.Hkv, self.hd, stream)
+        if events is not None:
+            events[0][1].record(stream)
+
+    def launches_per_step(self):
+        return 1
+
+    def work_per_launch(self):
+        return int((2 * self.H * self.hd * self.lens * (self.lens + 1)).sum())
+
+    def tokens_per_step(self):
+        return int(self.lens.sum())
+
+    def check(self):
+        import torch
+
+        assert torch.isfinite(self.out).all().item(), "non-finite prefill output"
+
+    def cpu_baseline(self, seconds, sample):
+        from oracle import attn
+
+        sample = min(sample, self.B)
+        k = self.k.cpu().numpy()
+        v = self.v.cpu().numpy()
+        q = self.q.cpu().numpy()
+        kc, vc = self.kc.cpu().numpy(), self.vc.cpu().numpy()
+        off = np.concatenate([[0], np.cumsum(self.lens)])
+        threads = attn.max_threads()
+
+        def run():
+            for b in range(sample):
+                rows = slice(int(off[b]), int(off[b + 1]))
+                attn.kv_scatter_prefill(k, v, 0, kc[rows], vc[rows], self.tables[b], 0)
+                attn.prefill_chunk(k, v, 0, q[rows], self.tables[b], 0, self.H, self.Hkv,
+                                   self.hd, threads)
+
+        per_rep, reps, el = time_cpu(run, seconds)
+        flops = float((2 * self.H * self.hd * self.lens[:sample] * (self.lens[:sample] + 1)).sum())
+        toks = int(self.lens[:sample].sum())
+        return {"value": round(flops / per_rep / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+                "kind": "port",
+                "sample": (f"prompts 0..{sample - 1} of the {self.B} ({toks} tokens), scatter + "
+                           f"causal prefill, {reps} reps in {el:.1f} s; {toks / per_rep:.1f} tokens/s"),
+                "tokens_per_s": round(toks / per_rep, 3)}
+
+    def extra(self, kernel_s):
+        return {}
+
+
+def prefix_shared_workload(seed):
+    """48 sequences: 512 shared prefix tokens (32 pages via FNV-1a prefix-cache hits),
+    private suffixes ~ U[64,512], then one decode token each."""
+    import nitrorag_amd as na
+
+    rng = np.random.default_rng(seed)
+    B, prefix = 48, 512
+    suffix = rng.integers(64, 513, size=B)
+    pages = 32 + int(((suffix + 1 + 15) // 16).sum()) + 16
+    bm = na.BlockManager(pages)
+    shared = rng.integers(1, 32000, size=prefix).tolist()
+    seqs = []
+    for b in range(B):
+        s = na.Sequence(b)
+        s.ingest_prompt(shared + rng.integers(1, 32000, size=int(suffix[b])).tolist(), bm, True)
+        if b == 0:
+            s.flush_cache(bm)
+        seqs.append(s)
+    positions = np.array([s.logical_token_count for s in seqs], np.int32)
+    for s in seqs:
+        s.allocate_next_token(7, bm)
+    tables = na.pack_block_tables(seqs)
+    unique = len({p for s in seqs for p in s.block_table})
+    return DecodeWorkload("decode-prefix-shared", B, 12, 12, 64, pages, 1, [0], positions + 1,
+                          True, seed, tables=tables, unique_pages=unique,
+                          describe=(f"prefix-shared decode, B=48, 12 heads x 64, 512 shared tokens "
+                                    f"(32 pages, ref_count 48) + private suffixes U[64,512], "
+                                    f"{pages}-page pool, one layer, Infinity Cache flushed per launch"))
+
+
+def make_workload(name, seed):
+    if name == "decode-b64-ctx4096":
+        return DecodeWorkload(name, 64, 32, 32, 128, 20000, 1, [0], np.full(64, 4096), False, seed,
+                              describe=("paged-attention decode, B=64, ctx=4096, 32 heads x 128 "
+                                        "(kv heads 32), 20000-page pool, 16-token pages, one layer, "
+                                        "append + attend per step"))
+    if name == "decode-single-110m":
+        return DecodeWorkload(name, 1, 12, 12, 64, 64, 12, list(range(12)), [256], True, seed,
+                              describe=("single-sequence decode, 12 layers x 12 heads x 64, ctx 256 "
+                                        "in a 64-page pool; one token through all 12 layers, "
+                                        "Infinity Cache flushed per launch"))
+    if name == "decode-b32-mixed":
+        rng = np.random.default_rng(seed)
+        return DecodeWorkload(name, 32, 12, 12, 64, 4096, 12, [0], rng.integers(16, 1025, size=32),
+                              True, seed,
+                              describe=("batched decode, B=32, 12 heads x 64, ctx ~ U[16,1024], "
+                                        "4096-page pool of 12 layers (layer 0 timed), "
+                                        "Infinity Cache flushed per launch"))
+    if name == "decode-prefix-shared":
+        return prefix_shared_workload(seed)
+    if name == "prefill-b8-12x64":
+        rng = np.random.default_rng(seed)
+        return PrefillWorkload(name, 8, 12, 12, 64, rng.integers(128, 1025, size=8), seed,
+                               describe=("causal prefill, B=8 prompts, lengths ~ U[128,1024], "
+                                         "12 heads x 64, fresh 16-token pages (LIFO ids)"))
+    raise ValueError(name)
+
+
+WORKLOADS = ["decode-b64-ctx4096", "decode-single-110m", "decode-b32-mixed",
+             "decode-prefix-shared", "prefill-b8-12x64"]
 
 
 def main():
@@ -117,8 +361,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="decode-b64-ctx4096", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=WORKLOADS)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-sample", type=int, default=8,
+                    help="sequences (prompts) of the workload the CPU baseline runs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0x4E49545205)
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -136,22 +382,12 @@ def main():
 
     import torch
 
-    import nitrorag_amd as na
-
-    B, ctx, H, Hkv, hd, pages, layers = WORKLOADS[args.workload]
-    kv_dim = Hkv * hd
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     g = torch.Generator(device=dev)
     g.manual_seed(args.seed)
-    k = torch.randn((pages, layers, 16, kv_dim), device=dev, generator=g)
-    v = torch.randn((pages, layers, 16, kv_dim), device=dev, generator=g)
-    q = torch.randn((B, H * hd), device=dev, generator=g)
-    knew = torch.randn((B, kv_dim), device=dev, generator=g)
-    vnew = torch.randn((B, kv_dim), device=dev, generator=g)
-    out = torch.empty_like(q)
-    tables = seeded_tables(B, ctx, pages, args.seed)
-    positions = np.full(B, ctx - 1, np.int32)
+    w = make_workload(args.workload, args.seed)
+    w.setup(dev, g)
 
     if args.copy_calibration_mib:
         src = torch.randn(args.copy_calibration_mib * 2**18, device=dev, generator=g)
@@ -162,42 +398,42 @@ def main():
         del src, dst
 
     stream = torch.cuda.current_stream()
-    pool = na.KVPool.wrap(k, v)
-    pool.upload_decode_batch(tables, positions, stream)
-
-    def step(ev=None):
-        pool.kv_append(0, knew, vnew, stream)
-        if ev is not None:
-            ev[0].record(stream)
-        pool.decode(0, q, out, H, Hkv, hd, stream)
-        if ev is not None:
-            ev[1].record(stream)
-
     for _ in range(args.warmup):
-        step()
+        w.step(stream)
     torch.cuda.synchronize()
 
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(args.steps)]
+    nl = w.launches_per_step()
+    events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(nl)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(events[i])
+        w.step(stream, events[i])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    kernel_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
-    assert torch.isfinite(out).all().item(), "non-finite decode output"
-    assert pool.take_device_errors() == 0
+    launch_ms = [a.elapsed_time(b) for ev in events for a, b in ev]
+    kernel_ms = float(np.mean(launch_ms))
+    w.check()
+    assert w.pool.take_device_errors() == 0
 
-    ms_per_step = elapsed / args.steps * 1e3
-    nbytes = decode_bytes(positions + 1, B, H, Hkv, hd)
-    step_gbps = nbytes / (ms_per_step * 1e-3) / 1e9
-    kernel_gbps = nbytes / (kernel_ms * 1e-3) / 1e9
-
+    work = w.work_per_launch()
+    if w.flush:
+        # interleaved cache flushes are not part of the step: the step is its launches
+        ms_per_step = kernel_ms * nl
+    else:
+        ms_per_step = elapsed / args.steps * 1e3
+    kernel_s = kernel_ms * 1e-3
+    if w.bound == "hbm":
+        unit, scale, peak = "GB/s", 1e9, HBM_PEAK_GBPS
+    else:
+        unit, scale, peak = "TFLOP/s", 1e12, FP32_PEAK_TFLOPS
+    step_rate = work * nl / (ms_per_step * 1e-3) / scale
+    kernel_rate = work / kernel_s / scale
+    default = args.workload == DEFAULT_WORKLOAD
     line = {
-        "metric": METRIC,
-        "value": round(step_gbps, 2),
-        "unit": "GB/s",
+        "metric": METRIC if default else f"{args.workload} {unit}",
+        "value": round(step_rate, 2 if unit == "GB/s" else 4),
+        "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -207,31 +443,26 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {
-            "workload": (f"paged-attention decode, B={B}, ctx={ctx}, {H} heads x {hd} "
-                         f"(kv heads {Hkv}), {pages}-page pool, 16-token pages, one layer, "
-                         "append + attend per step"),
-            "batch": B, "context": ctx, "n_heads": H, "n_kv_heads": Hkv, "head_dim": hd,
-            "pool_pages": pages, "parallelism": "single GPU",
-        },
-        "tokens_per_s": round(B / (ms_per_step * 1e-3), 1),
-        "hbm_fraction_step": round(step_gbps / HBM_PEAK_GBPS, 4),
+        "config": {"workload": w.describe, "batch": w.B, "n_heads": w.H, "n_kv_heads": w.Hkv,
+                   "head_dim": w.hd, "pool_pages": w.pages, "parallelism": "single GPU"},
+        "tokens_per_s": round(w.tokens_per_step() / (ms_per_step * 1e-3), 1),
         "roofline": {
-            "bound": "hbm",
-            "kernel": "paged_attn_decode_kernel<128>",
-            "achieved": round(kernel_gbps, 2),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic(args.traffic_profile),
-            "bytes_per_launch": nbytes,
+            "bound": w.bound,
+            "kernel": (f"paged_attn_decode_kernel<{w.hd}>" if w.bound == "hbm"
+                       else f"paged_attn_prefill_kernel<{w.hd}>"),
+            "achieved": round(kernel_rate, 2 if unit == "GB/s" else 4),
+            "peak": peak,
+            "unit": unit,
+            "frac": round(kernel_rate / peak, 4),
+            "traffic": measured_traffic(args.traffic_profile) if default else None,
+            ("bytes_per_launch" if w.bound == "hbm" else "flops_per_launch"): work,
             "kernel_ms": round(kernel_ms, 4),
         },
         "cpu_baseline": None,
     }
+    line.update(w.extra(kernel_s))
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(k, v, tables, positions, q, knew, vnew, H, Hkv, hd,
-                                            seconds=args.cpu_seconds)
+        line["cpu_baseline"] = w.cpu_baseline(args.cpu_seconds, args.cpu_sample)
     print(json.dumps(line), flush=True)
 
 

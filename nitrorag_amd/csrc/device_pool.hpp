@@ -170,6 +170,7 @@ struct PrefillLaunch {
     int64_t page_stride, layer_off;
     int32_t kv_dim, n_heads, kv_mul, head_dim, max_pages, num_pages, work_items;
     float qscale;
+    int32_t use_valu;  // 1: the VALU kernel even where an MFMA one exists
 };
 // Query rows per prefill work item.
 int prefill_block_m(int head_dim);

@@ -5,8 +5,27 @@
 // pos = start_pos + t attends keys 0..pos of its sequence (prefix-hit pages,
 // earlier chunks and the chunk's own rows, already scattered into the pool).
 //
-// Design: flash-attention style with fp32 VALU FMAs (fp32-exact products, no
-// reduced-precision MFMA):
+// Two kernels, both fp32 throughout (no reduced-precision inputs):
+//
+// paged_attn_prefill_mfma_kernel<hd> (hd 32/64/128, the default) runs both
+// matrix products on v_mfma_f32_16x16x4_f32 (fp32 inputs, fp32 accumulate):
+//  - Work item = 64 query rows (16 per wave) of one chunk x one head; keys
+//    stream in tiles of 32 rows (two pages) staged in LDS through the block
+//    table with a row stride of hd+4 floats (conflict-free reads below), the
+//    next tile prefetched into registers while the current one is consumed.
+//  - Per 16-key block a wave computes S^T = K Q^T (16 keys x 16 queries):
+//    lane l supplies K[key l%16][d] and Q[query l%16][d] for d = g*hd/4 + kk
+//    (g = l/16; the reduction order over d is permuted so each lane's K reads
+//    are contiguous ds_read_b128).  The accumulator leaves lane l holding
+//    S[query l%16][keys 4g..4g+3], so all softmax statistics of a query stay
+//    in the four lanes l%16 (two shuffles per block max), and the same four
+//    registers are exactly the B operand of O^T += V^T P^T (keys 4g+kk at
+//    step kk), whose output leaves lane l holding O[query l%16][16n+4g..+3]:
+//    rescaling by the query's factor is lane-local.
+//  - Online softmax in base 2 (q pre-scaled by log2(e)/sqrt(hd)), causal mask
+//    per element, blocks above a wave's last query skipped.
+//
+// paged_attn_prefill_kernel<hd> (all hd; used for hd 256) is the VALU form:
 //  - A work item is up to BM=64 query rows of one chunk; grid = (work items,
 //    heads).  The host sorts work items by key count, longest first.
 //  - 256 threads: 4 lanes per query row, each lane holding hd/4 of q and of
@@ -176,12 +195,163 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaun
     }
 }
 
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int HD>
+__global__ __launch_bounds__(THREADS) void paged_attn_prefill_mfma_kernel(PrefillLaunch a) {
+    constexpr int F4 = HD / 4;                 // float4 per K/V row
+    constexpr int DG = HD / 4;                 // d values per lane group (S^T reduction steps)
+    constexpr int NB = HD / 16;                // 16-column blocks of the output
+    constexpr int STRIDE = HD + 4;             // padded LDS row (floats)
+    constexpr int LOADS = BN * F4 / THREADS;   // float4 per thread per tile per matrix
+    static_assert(LOADS >= 1 && BN * F4 % THREADS == 0, "tile shape");
+    __shared__ __attribute__((aligned(16))) float ks[BN * STRIDE];
+    __shared__ __attribute__((aligned(16))) float vs[BN * STRIDE];
+
+    const int seq = a.work[2 * blockIdx.x];
+    const int q0 = a.work[2 * blockIdx.x + 1];
+    const int h = blockIdx.y;
+    const int kv_h = h / a.kv_mul;
+    const int start = a.start_pos[seq];
+    const int qcount = min(BM, a.num_tokens[seq] - q0);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int ql = lane & 15;   // query within the wave's 16
+    const int g = lane >> 4;    // lane group: K/V rows 4g..4g+3 of a block, d slice g
+    const int row = wave * 16 + ql;
+    const int last_pos = start + q0 + qcount - 1;
+    const int my_pos = start + q0 + min(row, qcount - 1);
+    const int wave_last = start + q0 + min(wave * 16 + 15, qcount - 1);
+    const int32_t* trow = a.tables + (size_t)seq * a.max_pages;
+    const int n_tiles = last_pos / BN + 1;
+    const size_t dim = (size_t)a.n_heads * HD;
+    const size_t qrow = (size_t)(a.row_off[seq] + q0 + min(row, qcount - 1));
+
+    float qv[DG];
+    {
+        const float4* qp = reinterpret_cast<const float4*>(a.q + qrow * dim + (size_t)h * HD + g * DG);
+#pragma unroll
+        for (int i = 0; i < DG / 4; i++) {
+            const float4 t = qp[i];
+            qv[4 * i + 0] = t.x * a.qscale;
+            qv[4 * i + 1] = t.y * a.qscale;
+            qv[4 * i + 2] = t.z * a.qscale;
+            qv[4 * i + 3] = t.w * a.qscale;
+        }
+    }
+    f32x4 acc[NB];
+#pragma unroll
+    for (int n = 0; n < NB; n++) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, lsum = 0.0f;
+
+    const float* kbase = a.k_pool + a.layer_off + (size_t)kv_h * HD;
+    const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * HD;
+    float4 kreg[LOADS], vreg[LOADS];
+
+    auto fetch = [&](int tile) {
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int f = threadIdx.x + i * THREADS;
+            const int r = f / F4, col = f % F4;
+            const int key = tile * BN + r;
+            kreg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            vreg[i] = kreg[i];
+            if (key <= last_pos) {
+                const int page = trow[key >> 4];
+                if ((unsigned)page < (unsigned)a.num_pages) {
+                    const size_t off = (size_t)page * a.page_stride + (size_t)(key & 15) * a.kv_dim;
+                    kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
+                    vreg[i] = reinterpret_cast<const float4*>(vbase + off)[col];
+                } else if (col == 0) {
+                    atomicAdd(a.bad_pages, 1);
+                }
+            }
+        }
+    };
+
+    fetch(0);
+    for (int tile = 0; tile < n_tiles; tile++) {
+        __syncthreads();  // previous tile fully consumed
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int f = threadIdx.x + i * THREADS;
+            const int r = f / F4, col = f % F4;
+            *reinterpret_cast<float4*>(&ks[r * STRIDE + col * 4]) = kreg[i];
+            *reinterpret_cast<float4*>(&vs[r * STRIDE + col * 4]) = vreg[i];
+        }
+        __syncthreads();
+        if (tile + 1 < n_tiles) fetch(tile + 1);
+
+#pragma unroll
+        for (int kb = 0; kb < BN / 16; kb++) {
+            const int key0 = tile * BN + kb * 16;
+            if (key0 > wave_last) break;  // wave-uniform: no query of this wave sees these keys
+            // S^T block: lane holds S[query ql][keys key0 + 4g + r], r = 0..3
+            f32x4 st = {0.f, 0.f, 0.f, 0.f};
+            const float* krow = &ks[(kb * 16 + ql) * STRIDE + g * DG];
+#pragma unroll
+            for (int i = 0; i < DG / 4; i++) {
+                const float4 kk4 = *reinterpret_cast<const float4*>(krow + 4 * i);
+                st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk4.x, qv[4 * i + 0], st, 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk4.y, qv[4 * i + 1], st, 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk4.z, qv[4 * i + 2], st, 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk4.w, qv[4 * i + 3], st, 0, 0, 0);
+            }
+            float s[4];
+            float bmax = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                s[r] = (key0 + 4 * g + r <= my_pos) ? st[r] : -INFINITY;
+                bmax = fmaxf(bmax, s[r]);
+            }
+            bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+            bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+            const float m_new = fmaxf(m, bmax);  // finite: key 0 precedes every query
+            const float alpha = scale_of(m, m_new);
+            float p[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) p[r] = s[r] == -INFINITY ? 0.0f : exp2f(s[r] - m_new);
+            lsum = lsum * alpha + (p[0] + p[1]) + (p[2] + p[3]);
+#pragma unroll
+            for (int n = 0; n < NB; n++) {
+                f32x4 o = acc[n] * alpha;
+                const float* vcol = &vs[(kb * 16 + 4 * g) * STRIDE + 16 * n + ql];
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++)
+                    o = __builtin_amdgcn_mfma_f32_16x16x4f32(vcol[kk * STRIDE], p[kk], o, 0, 0, 0);
+                acc[n] = o;
+            }
+            m = m_new;
+        }
+    }
+
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    if (row < qcount) {
+        const float inv = 1.0f / lsum;
+        float* op = a.out + qrow * dim + (size_t)h * HD;
+#pragma unroll
+        for (int n = 0; n < NB; n++)
+            *reinterpret_cast<float4*>(op + 16 * n + 4 * g) =
+                make_float4(acc[n][0] * inv, acc[n][1] * inv, acc[n][2] * inv, acc[n][3] * inv);
+    }
+}
+
 }  // namespace
 
 int prefill_block_m(int) { return BM; }
 
 hipError_t launch_paged_attn_prefill(const PrefillLaunch& a, hipStream_t stream) {
     const dim3 grid((unsigned)a.work_items, (unsigned)a.n_heads);
+    if (!a.use_valu) {
+        switch (a.head_dim) {
+            case 32: hipLaunchKernelGGL(paged_attn_prefill_mfma_kernel<32>, grid, dim3(THREADS), 0, stream, a); return hipGetLastError();
+            case 64: hipLaunchKernelGGL(paged_attn_prefill_mfma_kernel<64>, grid, dim3(THREADS), 0, stream, a); return hipGetLastError();
+            case 128: hipLaunchKernelGGL(paged_attn_prefill_mfma_kernel<128>, grid, dim3(THREADS), 0, stream, a); return hipGetLastError();
+            default: break;  // hd 256: VALU kernel
+        }
+    }
     switch (a.head_dim) {
         case 32: hipLaunchKernelGGL(paged_attn_prefill_kernel<32>, grid, dim3(THREADS), 0, stream, a); break;
         case 64: hipLaunchKernelGGL(paged_attn_prefill_kernel<64>, grid, dim3(THREADS), 0, stream, a); break;

@@ -22,6 +22,14 @@ def gpu():
     torch.cuda.synchronize()
 
 
+@pytest.fixture(params=["mfma", "valu"], autouse=True)
+def prefill_kernel(request, monkeypatch):
+    """Every prefill test runs on both kernels: MFMA fp32 (default for hd <= 128)
+    and the VALU one (hd 256, or NITRO_PREFILL_KERNEL=valu)."""
+    monkeypatch.setenv("NITRO_PREFILL_KERNEL", request.param)
+    return request.param
+
+
 def say(msg):
     print(msg, flush=True)
     sys.stdout.flush()
