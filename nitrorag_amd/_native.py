@@ -9,7 +9,8 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libnitro_paged_attn.so")
+# NITRO_LIB_PATH selects another build of the same library (e.g. for A/B timing).
+LIB_PATH = os.environ.get("NITRO_LIB_PATH") or os.path.join(_HERE, "libnitro_paged_attn.so")
 
 STATUS = {
     0: "NITRO_OK",

@@ -17,10 +17,11 @@ using namespace nitro;
 
 namespace {
 
-constexpr int kDecodeWaves = 4;  // waves per decode workgroup (kernel constant)
-// Decode workgroups resident per CU at the kernel's occupancy (4 waves/SIMD,
-// 4 SIMDs, 4-wave workgroups); one such wave of workgroups fills the GPU.
-constexpr int kDecodeGroupsPerCU = 4;
+// Decode launch shape: waves resident per CU at the kernel's occupancy
+// (4 waves/SIMD x 4 SIMDs), and the range of waves per workgroup.
+constexpr int kDecodeWavesPerCU = 16;
+constexpr int kDecodeMinWaves = 4;
+constexpr int kDecodeMaxWaves = 16;
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -205,20 +206,28 @@ int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, f
         const int tile = decode_tile_rows(head_dim);
         int max_tiles = 0;
         for (int p : d.positions) max_tiles = std::max(max_tiles, (p + 1 + tile - 1) / tile);
-        // Split-K only when one workgroup per (b, h) cannot fill the GPU: then
-        // split the longest context into enough runs of tiles to give about
-        // two rounds of workgroups, at least one tile per wave.  Each split's
-        // block-table slice must fit in LDS.
+        // Launch shape: ~16 resident waves per CU.  Give each (b, h) as many
+        // waves (4, 8 or 16, never more than it has tiles) as keep every
+        // workgroup resident in one dispatch round, then split the context
+        // (split-K, one extra merge launch) only if the GPU is still less than
+        // half full.  Each split's block-table slice must fit in LDS.
         const long long bh_count = (long long)d.batch * n_heads;
-        const long long fill = 2LL * kDecodeGroupsPerCU * std::max(pool->num_cus, 1);
+        const long long target = (long long)kDecodeWavesPerCU * std::max(pool->num_cus, 1);
+        int waves = env_int("NITRO_DECODE_WAVES", 0);
+        if (waves <= 0) {
+            waves = kDecodeMinWaves;
+            while (waves < kDecodeMaxWaves && bh_count * waves * 2 <= target && waves < max_tiles)
+                waves *= 2;
+        }
+        waves = std::max(kDecodeMinWaves, std::min(waves, kDecodeMaxWaves));
         int tps = env_int("NITRO_DECODE_SPLIT_TILES", 0);
         if (tps <= 0) {
-            if (bh_count >= fill / 2) {
+            if (bh_count * waves >= target / 2 || max_tiles <= 2 * waves) {
                 tps = max_tiles;
             } else {
-                const long long want_splits = (fill + bh_count - 1) / bh_count;
+                const long long want_splits = (target + bh_count * waves - 1) / (bh_count * waves);
                 tps = (int)((max_tiles + want_splits - 1) / want_splits);
-                tps = (tps + kDecodeWaves - 1) / kDecodeWaves * kDecodeWaves;
+                tps = (tps + waves - 1) / waves * waves;
             }
         }
         const int max_tps = (DECODE_MAX_SPLIT_PAGES - 2) * BLOCK_SIZE / tile;
@@ -248,6 +257,7 @@ int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, f
         a.num_pages = pool->num_pages;
         a.tiles_per_split = tps;
         a.num_splits = splits;
+        a.waves = waves;
         a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
         hip_check(launch_paged_attn_decode(a, s), "paged_attn_decode launch");
         pool->last_stream = s;

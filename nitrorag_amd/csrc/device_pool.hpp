@@ -138,6 +138,7 @@ struct DecodeLaunch {
     int64_t page_stride, layer_off;
     int32_t kv_dim, batch, n_heads, kv_mul, head_dim, max_pages, num_pages;
     int32_t tiles_per_split, num_splits;
+    int32_t waves;  // wavefronts per workgroup, 1..16, 64*waves >= head_dim
     float qscale;
 };
 // Rows per decode tile for a head_dim (the unit split-K partitions).

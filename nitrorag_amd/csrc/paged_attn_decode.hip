@@ -6,8 +6,10 @@
 //   table, kv head h / (H/Hkv)), p = softmax(s), o_h = sum_t p_t v_t.
 //
 // Design (bandwidth-bound: K and V are read exactly once per query head):
-//  - Grid: one workgroup of W=4 wavefronts per (b, h, split).  A split is a
-//    run of `tiles_per_split` tiles of TILE consecutive context rows; waves
+//  - Grid: one workgroup of W wavefronts per (b, h, split), W = 4..16 chosen
+//    per launch (more waves per sequence when the batch is small, so enough
+//    loads are in flight and long contexts finish in few rounds).  A split is
+//    a run of `tiles_per_split` tiles of TILE consecutive context rows; waves
 //    take the split's tiles round-robin.
 //  - Lane layout: LPR = hd/16 lanes share one K/V row, each lane holding 16
 //    floats of it as four float4 (columns c*4 + j*4*LPR, j = 0..3), so each
@@ -37,8 +39,8 @@
 namespace nitro {
 namespace {
 
-constexpr int WAVES = 4;
-constexpr int THREADS = 64 * WAVES;
+constexpr int MAX_WAVES = 16;
+constexpr int MAX_THREADS = 64 * MAX_WAVES;
 
 template <int HD>
 struct DecodeGeom {
@@ -76,12 +78,14 @@ __device__ __forceinline__ float scale_of(float m, float m_new) {
 }
 
 template <int HD>
-__global__ __launch_bounds__(THREADS) void paged_attn_decode_kernel(DecodeLaunch a) {
+__global__ __launch_bounds__(MAX_THREADS) void paged_attn_decode_kernel(DecodeLaunch a) {
     using G = DecodeGeom<HD>;
     constexpr int LPR = G::LPR, RPS = G::RPS, TILE = G::TILE;
     __shared__ int32_t s_pages[DECODE_MAX_SPLIT_PAGES];
-    __shared__ float s_acc[WAVES][HD];
-    __shared__ float s_m[WAVES], s_l[WAVES];
+    __shared__ float s_acc[MAX_WAVES][HD];
+    __shared__ float s_m[MAX_WAVES], s_l[MAX_WAVES];
+    const int waves = blockDim.x >> 6;
+    const int threads = blockDim.x;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -104,7 +108,7 @@ __global__ __launch_bounds__(THREADS) void paged_attn_decode_kernel(DecodeLaunch
     const int page_begin = (tile_begin * TILE) >> 4;
     const int page_end = ((min(ctx, tile_end * TILE) - 1) >> 4) + 1;
     const int32_t* trow = a.tables + (size_t)b * a.max_pages;
-    for (int i = threadIdx.x; i < page_end - page_begin; i += THREADS) {
+    for (int i = threadIdx.x; i < page_end - page_begin; i += threads) {
         int p = trow[page_begin + i];
         if ((unsigned)p >= (unsigned)a.num_pages) {
             atomicAdd(a.bad_pages, 1);
@@ -131,7 +135,7 @@ __global__ __launch_bounds__(THREADS) void paged_attn_decode_kernel(DecodeLaunch
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
 
-    for (int t = tile_begin + wave; t < tile_end; t += WAVES) {
+    for (int t = tile_begin + wave; t < tile_end; t += waves) {
         float4 kr[G::SETS][4], vr[G::SETS][4];
         bool valid[G::SETS];
 #pragma unroll
@@ -226,10 +230,8 @@ __global__ __launch_bounds__(THREADS) void paged_attn_decode_kernel(DecodeLaunch
     const int d = threadIdx.x;
     float M = -INFINITY, L = 0.0f, A = 0.0f;
     if (d < HD) {
-#pragma unroll
-        for (int w = 0; w < WAVES; w++) M = fmaxf(M, s_m[w]);
-#pragma unroll
-        for (int w = 0; w < WAVES; w++) {
+        for (int w = 0; w < waves; w++) M = fmaxf(M, s_m[w]);
+        for (int w = 0; w < waves; w++) {
             const float f = scale_of(s_m[w], M);
             L += s_l[w] * f;
             A += s_acc[w][d] * f;
@@ -288,7 +290,7 @@ int decode_tile_rows(int head_dim) {
 template <int HD>
 static hipError_t launch_hd(const DecodeLaunch& a, hipStream_t stream) {
     const dim3 grid((unsigned)((size_t)a.batch * a.n_heads * a.num_splits));
-    hipLaunchKernelGGL(paged_attn_decode_kernel<HD>, grid, dim3(THREADS), 0, stream, a);
+    hipLaunchKernelGGL(paged_attn_decode_kernel<HD>, grid, dim3(64 * a.waves), 0, stream, a);
     if (a.num_splits > 1) {
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -299,6 +301,7 @@ static hipError_t launch_hd(const DecodeLaunch& a, hipStream_t stream) {
 }
 
 hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream) {
+    if (a.waves < 1 || a.waves > MAX_WAVES || 64 * a.waves < a.head_dim) return hipErrorInvalidValue;
     switch (a.head_dim) {
         case 32: return launch_hd<32>(a, stream);
         case 64: return launch_hd<64>(a, stream);

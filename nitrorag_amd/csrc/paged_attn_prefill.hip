@@ -10,9 +10,11 @@
 // paged_attn_prefill_mfma_kernel<hd> (hd 32/64/128, the default) runs both
 // matrix products on v_mfma_f32_16x16x4_f32 (fp32 inputs, fp32 accumulate):
 //  - Work item = 64 query rows (16 per wave) of one chunk x one head; keys
-//    stream in tiles of 32 rows (two pages) staged in LDS through the block
-//    table with a row stride of hd+4 floats (conflict-free reads below), the
-//    next tile prefetched into registers while the current one is consumed.
+//    stream in tiles of 64 rows (hd <= 64; 32 rows for hd 128) staged in LDS
+//    with a row stride of hd+4 floats (conflict-free reads below), the next
+//    tile prefetched into registers while the current one is consumed.  The
+//    workgroup's block-table slice is staged in LDS once, so a tile's loads
+//    do not wait on a table load.
 //  - Per 16-key block a wave computes S^T = K Q^T (16 keys x 16 queries):
 //    lane l supplies K[key l%16][d] and Q[query l%16][d] for d = g*hd/4 + kk
 //    (g = l/16; the reduction order over d is permuted so each lane's K reads
@@ -74,9 +76,12 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaun
     __shared__ float4 ks[BN][F4];
     __shared__ float4 vs[BN][F4];
 
-    const int seq = a.work[2 * blockIdx.x];
-    const int q0 = a.work[2 * blockIdx.x + 1];
-    const int h = blockIdx.y;
+    // 1-D grid, heads fastest: the work list is sorted longest first, so every
+    // head of the longest items is dispatched before any shorter item.
+    const int item = blockIdx.x / a.n_heads;
+    const int h = blockIdx.x - item * a.n_heads;
+    const int seq = a.work[2 * item];
+    const int q0 = a.work[2 * item + 1];
     const int kv_h = h / a.kv_mul;
     const int start = a.start_pos[seq];
     const int qcount = min(BM, a.num_tokens[seq] - q0);
@@ -198,35 +203,62 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaun
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <int HD>
-__global__ __launch_bounds__(THREADS) void paged_attn_prefill_mfma_kernel(PrefillLaunch a) {
+// Block-table entries a prefill workgroup keeps in LDS (32k tokens); pages
+// beyond that are read from the table in global memory.
+constexpr int TABLE_LDS = 2048;
+// Key groups per work item in the MFMA kernel: waves = 4 query sub-tiles x
+// PREFILL_KSPLIT, each key group taking every PREFILL_KSPLIT-th 16-key block.
+#ifndef PREFILL_KSPLIT
+#define PREFILL_KSPLIT 2
+#endif
+
+template <int HD, int KSPLIT>
+__global__ __launch_bounds__(THREADS * KSPLIT) void paged_attn_prefill_mfma_kernel(PrefillLaunch a) {
+    constexpr int NT = THREADS * KSPLIT;       // 4 query sub-tiles x KSPLIT key groups of waves
+    constexpr int BNM = HD <= 64 ? 64 : 32;    // keys per LDS tile
+    constexpr int KB = BNM / 16;               // 16-key blocks per tile
     constexpr int F4 = HD / 4;                 // float4 per K/V row
     constexpr int DG = HD / 4;                 // d values per lane group (S^T reduction steps)
     constexpr int NB = HD / 16;                // 16-column blocks of the output
     constexpr int STRIDE = HD + 4;             // padded LDS row (floats)
-    constexpr int LOADS = BN * F4 / THREADS;   // float4 per thread per tile per matrix
-    static_assert(LOADS >= 1 && BN * F4 % THREADS == 0, "tile shape");
-    __shared__ __attribute__((aligned(16))) float ks[BN * STRIDE];
-    __shared__ __attribute__((aligned(16))) float vs[BN * STRIDE];
+    constexpr int LOADS = BNM * F4 / NT;       // float4 per thread per tile per matrix
+    static_assert(LOADS >= 1 && BNM * F4 % NT == 0, "tile shape");
+    static_assert(KB % KSPLIT == 0, "key blocks split evenly over key groups");
+    // K and V tiles in one array; after the key loop the same LDS holds the
+    // partials (16 queries x HD per sub-tile) of key groups 1..KSPLIT-1.
+    static_assert((KSPLIT - 1) * 4 * 16 * HD <= 2 * BNM * STRIDE, "partials fit the tile LDS");
+    __shared__ __attribute__((aligned(16))) float kv_lds[2 * BNM * STRIDE];
+    float* const ks = kv_lds;
+    float* const vs = kv_lds + BNM * STRIDE;
+    __shared__ int32_t s_table[TABLE_LDS];
+    __shared__ float s_ml[KSPLIT > 1 ? 4 * (KSPLIT - 1) * 16 * 2 : 1];
 
-    const int seq = a.work[2 * blockIdx.x];
-    const int q0 = a.work[2 * blockIdx.x + 1];
-    const int h = blockIdx.y;
+    const int item = blockIdx.x / a.n_heads;
+    const int h = blockIdx.x - item * a.n_heads;
+    const int seq = a.work[2 * item];
+    const int q0 = a.work[2 * item + 1];
     const int kv_h = h / a.kv_mul;
     const int start = a.start_pos[seq];
     const int qcount = min(BM, a.num_tokens[seq] - q0);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int ql = lane & 15;   // query within the wave's 16
-    const int g = lane >> 4;    // lane group: K/V rows 4g..4g+3 of a block, d slice g
-    const int row = wave * 16 + ql;
+    const int qs = wave & 3;     // query sub-tile (16 rows)
+    const int kg = wave >> 2;    // key group: blocks kg, kg + KSPLIT, ... of each tile
+    const int ql = lane & 15;    // query within the sub-tile
+    const int g = lane >> 4;     // lane group: K/V rows 4g..4g+3 of a block, d slice g
+    const int row = qs * 16 + ql;
     const int last_pos = start + q0 + qcount - 1;
     const int my_pos = start + q0 + min(row, qcount - 1);
-    const int wave_last = start + q0 + min(wave * 16 + 15, qcount - 1);
+    const int wave_last = start + q0 + min(qs * 16 + 15, qcount - 1);
     const int32_t* trow = a.tables + (size_t)seq * a.max_pages;
-    const int n_tiles = last_pos / BN + 1;
+    const int n_tiles = last_pos / BNM + 1;
     const size_t dim = (size_t)a.n_heads * HD;
     const size_t qrow = (size_t)(a.row_off[seq] + q0 + min(row, qcount - 1));
+
+    // The workgroup's block-table slice -> LDS (read once instead of per tile).
+    const int n_pages = min((last_pos >> 4) + 1, TABLE_LDS);
+    for (int i = threadIdx.x; i < n_pages; i += NT) s_table[i] = trow[i];
+    __syncthreads();
 
     float qv[DG];
     {
@@ -252,13 +284,14 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_mfma_kernel(Prefil
     auto fetch = [&](int tile) {
 #pragma unroll
         for (int i = 0; i < LOADS; i++) {
-            const int f = threadIdx.x + i * THREADS;
+            const int f = threadIdx.x + i * NT;
             const int r = f / F4, col = f % F4;
-            const int key = tile * BN + r;
+            const int key = tile * BNM + r;
             kreg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             vreg[i] = kreg[i];
             if (key <= last_pos) {
-                const int page = trow[key >> 4];
+                const int pi = key >> 4;
+                const int page = pi < TABLE_LDS ? s_table[pi] : trow[pi];
                 if ((unsigned)page < (unsigned)a.num_pages) {
                     const size_t off = (size_t)page * a.page_stride + (size_t)(key & 15) * a.kv_dim;
                     kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
@@ -275,7 +308,7 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_mfma_kernel(Prefil
         __syncthreads();  // previous tile fully consumed
 #pragma unroll
         for (int i = 0; i < LOADS; i++) {
-            const int f = threadIdx.x + i * THREADS;
+            const int f = threadIdx.x + i * NT;
             const int r = f / F4, col = f % F4;
             *reinterpret_cast<float4*>(&ks[r * STRIDE + col * 4]) = kreg[i];
             *reinterpret_cast<float4*>(&vs[r * STRIDE + col * 4]) = vreg[i];
@@ -284,8 +317,8 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_mfma_kernel(Prefil
         if (tile + 1 < n_tiles) fetch(tile + 1);
 
 #pragma unroll
-        for (int kb = 0; kb < BN / 16; kb++) {
-            const int key0 = tile * BN + kb * 16;
+        for (int kb = kg; kb < KB; kb += KSPLIT) {
+            const int key0 = tile * BNM + kb * 16;
             if (key0 > wave_last) break;  // wave-uniform: no query of this wave sees these keys
             // S^T block: lane holds S[query ql][keys key0 + 4g + r], r = 0..3
             f32x4 st = {0.f, 0.f, 0.f, 0.f};
@@ -307,11 +340,14 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_mfma_kernel(Prefil
             }
             bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
             bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-            const float m_new = fmaxf(m, bmax);  // finite: key 0 precedes every query
-            const float alpha = scale_of(m, m_new);
+            const float m_new = fmaxf(m, bmax);
+            if (m_new == -INFINITY) continue;  // every key of the block lies after this wave's queries
+            // arguments are <= 0: the raw v_exp_f32 (no denormal-range scaling) suffices
+            const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - m_new);
             float p[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) p[r] = s[r] == -INFINITY ? 0.0f : exp2f(s[r] - m_new);
+            for (int r = 0; r < 4; r++)
+                p[r] = s[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[r] - m_new);
             lsum = lsum * alpha + (p[0] + p[1]) + (p[2] + p[3]);
 #pragma unroll
             for (int n = 0; n < NB; n++) {
@@ -328,6 +364,41 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_mfma_kernel(Prefil
 
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
+    if constexpr (KSPLIT > 1) {
+        // Key groups 1.. hand (m, l, O) to key group 0 through LDS (the K tile area).
+        __syncthreads();  // every wave is done with the K/V tiles
+        float* part = kv_lds;  // [(KSPLIT-1) x 4 sub-tiles][16 queries][HD]
+        if (kg > 0) {
+            const int slot = (kg - 1) * 4 + qs;
+            float* o = part + (size_t)slot * 16 * HD + ql * HD;
+#pragma unroll
+            for (int n = 0; n < NB; n++)
+                *reinterpret_cast<float4*>(o + 16 * n + 4 * g) =
+                    make_float4(acc[n][0], acc[n][1], acc[n][2], acc[n][3]);
+            if (g == 0) {
+                s_ml[(slot * 16 + ql) * 2 + 0] = m;
+                s_ml[(slot * 16 + ql) * 2 + 1] = lsum;
+            }
+        }
+        __syncthreads();
+        if (kg > 0) return;
+#pragma unroll
+        for (int k = 1; k < KSPLIT; k++) {
+            const int slot = (k - 1) * 4 + qs;
+            const float mo = s_ml[(slot * 16 + ql) * 2 + 0];
+            const float lo = s_ml[(slot * 16 + ql) * 2 + 1];
+            const float mm = fmaxf(m, mo);
+            const float f = scale_of(m, mm), fo = scale_of(mo, mm);
+            lsum = lsum * f + lo * fo;
+            const float* o = part + (size_t)slot * 16 * HD + ql * HD;
+#pragma unroll
+            for (int n = 0; n < NB; n++) {
+                const float4 t = *reinterpret_cast<const float4*>(o + 16 * n + 4 * g);
+                acc[n] = acc[n] * f + f32x4{t.x, t.y, t.z, t.w} * fo;
+            }
+            m = mm;
+        }
+    }
     if (row < qcount) {
         const float inv = 1.0f / lsum;
         float* op = a.out + qrow * dim + (size_t)h * HD;
@@ -343,12 +414,13 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_mfma_kernel(Prefil
 int prefill_block_m(int) { return BM; }
 
 hipError_t launch_paged_attn_prefill(const PrefillLaunch& a, hipStream_t stream) {
-    const dim3 grid((unsigned)a.work_items, (unsigned)a.n_heads);
+    const dim3 grid((unsigned)((size_t)a.work_items * a.n_heads));
     if (!a.use_valu) {
+        const dim3 block(THREADS * PREFILL_KSPLIT);
         switch (a.head_dim) {
-            case 32: hipLaunchKernelGGL(paged_attn_prefill_mfma_kernel<32>, grid, dim3(THREADS), 0, stream, a); return hipGetLastError();
-            case 64: hipLaunchKernelGGL(paged_attn_prefill_mfma_kernel<64>, grid, dim3(THREADS), 0, stream, a); return hipGetLastError();
-            case 128: hipLaunchKernelGGL(paged_attn_prefill_mfma_kernel<128>, grid, dim3(THREADS), 0, stream, a); return hipGetLastError();
+            case 32: hipLaunchKernelGGL((paged_attn_prefill_mfma_kernel<32, PREFILL_KSPLIT>), grid, block, 0, stream, a); return hipGetLastError();
+            case 64: hipLaunchKernelGGL((paged_attn_prefill_mfma_kernel<64, PREFILL_KSPLIT>), grid, block, 0, stream, a); return hipGetLastError();
+            case 128: hipLaunchKernelGGL((paged_attn_prefill_mfma_kernel<128, PREFILL_KSPLIT>), grid, block, 0, stream, a); return hipGetLastError();
             default: break;  // hd 256: VALU kernel
         }
     }

@@ -93,13 +93,15 @@ def test_decode_vs_oracle(name):
     assert c.pool.take_device_errors() == 0
 
 
-@pytest.mark.parametrize("tiles", ["1", "3", "4", "8", "100000"])
-def test_decode_split_k_partitions_agree(tiles, monkeypatch):
-    """Any split-K partition (1 tile per split .. a single split) gives the
-    same answer within the bar; repeated launches reuse the self-resetting
-    arrival counters."""
-    say(f"split-K tiles_per_split={tiles}")
+@pytest.mark.parametrize("tiles,waves", [("1", "4"), ("3", "4"), ("4", "8"), ("8", "16"),
+                                         ("100000", "4"), ("100000", "16"), ("", "")])
+def test_decode_split_k_partitions_agree(tiles, waves, monkeypatch):
+    """Any launch shape (1 tile per split .. one split; 4..16 waves per
+    workgroup; the default heuristic) gives the same answer within the bar,
+    and repeated launches are bit-identical."""
+    say(f"split-K tiles_per_split={tiles} waves={waves}")
     monkeypatch.setenv("NITRO_DECODE_SPLIT_TILES", tiles)
+    monkeypatch.setenv("NITRO_DECODE_WAVES", waves)
     c = make_case("edges_hd128")
     want = c.run_oracle()
     first = c.run_gpu()
