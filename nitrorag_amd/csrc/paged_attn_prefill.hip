@@ -340,8 +340,10 @@ __global__ __launch_bounds__(THREADS * KSPLIT) void paged_attn_prefill_mfma_kern
             }
             bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
             bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+            // m_new stays -inf for a query none of whose keys so far precede it
+            // (possible in key groups > 0); alpha and p are then 0.  No lane may
+            // skip the block: MFMA operands are shared across lanes.
             const float m_new = fmaxf(m, bmax);
-            if (m_new == -INFINITY) continue;  // every key of the block lies after this wave's queries
             // arguments are <= 0: the raw v_exp_f32 (no denormal-range scaling) suffices
             const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - m_new);
             float p[4];
