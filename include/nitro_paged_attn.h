@@ -185,6 +185,25 @@ int nitro_kv_append_prefill(nitro_kvpool* pool, int32_t layer, const float* k, c
 int nitro_paged_attn_prefill(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
                              int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void* stream);
 
+/* ------------------------------- RoPE --------------------------------------
+ * RoPE fused with the KV append, as the reference does it in one loop: each
+ * pair (j, j+1) of q (all heads) and of k (kv heads) is rotated in place by
+ * (c, s) = (freq_real, freq_imag)[pos*(head_dim/2) + (j % head_dim)/2] —
+ * q' = (q0*c - q1*s, q0*s + q1*c) — then the rotated k and the unrotated v
+ * are appended at pos.  freq_real/freq_imag: device [seq_len][head_dim/2]
+ * (the reference's freq_cis_real/imag); every position must be < seq_len. */
+/* Decode batch — src/model_q8.cpp:601-623 (single sequence :262-287).
+ * q [batch][n_heads*head_dim], k and v [batch][kv_dim]. */
+int nitro_rope_kv_append(nitro_kvpool* pool, int32_t layer, float* q, float* k, const float* v,
+                         const float* freq_real, const float* freq_imag, int32_t seq_len,
+                         int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void* stream);
+/* Prefill batch rows — src/model_q8.cpp:451-484.  Rows packed as for
+ * nitro_kv_append_prefill. */
+int nitro_rope_kv_append_prefill(nitro_kvpool* pool, int32_t layer, float* q, float* k,
+                                 const float* v, const float* freq_real, const float* freq_imag,
+                                 int32_t seq_len, int32_t n_heads, int32_t n_kv_heads,
+                                 int32_t head_dim, void* stream);
+
 /* ------------------------------ checks ------------------------------------
  * Kernels re-check every page id they dereference against the pool size and
  * skip (and record) any outside it instead of faulting.  This reads and

@@ -86,6 +86,9 @@ SIGNATURES = {
     "nitro_prefill_batch_upload": [_vp, _i32p, _i32p, _i32p, _i32, _i32, _vp],
     "nitro_kv_append_prefill": [_vp, _i32, _fp, _fp, _vp],
     "nitro_paged_attn_prefill": [_vp, _i32, _fp, _fp, _i32, _i32, _i32, _vp],
+    "nitro_rope_kv_append": [_vp, _i32, _fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32, _vp],
+    "nitro_rope_kv_append_prefill": [_vp, _i32, _fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32,
+                                     _vp],
     "nitro_kvpool_take_device_errors": [_vp, _i32p],
 }
 _RESTYPES = {

@@ -142,6 +142,33 @@ class KVPool:
         N.call("nitro_paged_attn_prefill", self._h, layer, _dev(q, "q"), _dev(out, "out"), n_heads,
                n_kv_heads, head_dim, _stream_ptr(stream))
 
+    # ------------------------------------------------------------------ RoPE
+    def rope_kv_append(self, layer: int, q, k, v, freq_real, freq_imag, n_heads: int,
+                       n_kv_heads: int, head_dim: int, stream=None) -> None:
+        """Rotates q and k in place (src/model_q8.cpp:601-615), appends k and v (:616-623)."""
+        self._need(q, self.decode_batch * n_heads * head_dim, "q")
+        self._need(k, self.decode_batch * self.kv_dim, "k")
+        self._need(v, self.decode_batch * self.kv_dim, "v")
+        self._rope("nitro_rope_kv_append", layer, q, k, v, freq_real, freq_imag, n_heads,
+                   n_kv_heads, head_dim, stream)
+
+    def rope_kv_append_prefill(self, layer: int, q, k, v, freq_real, freq_imag, n_heads: int,
+                               n_kv_heads: int, head_dim: int, stream=None) -> None:
+        """The same for the prefill batch rows (src/model_q8.cpp:451-484)."""
+        self._need(q, self.prefill_rows * n_heads * head_dim, "q")
+        self._need(k, self.prefill_rows * self.kv_dim, "k")
+        self._need(v, self.prefill_rows * self.kv_dim, "v")
+        self._rope("nitro_rope_kv_append_prefill", layer, q, k, v, freq_real, freq_imag, n_heads,
+                   n_kv_heads, head_dim, stream)
+
+    def _rope(self, fn, layer, q, k, v, freq_real, freq_imag, n_heads, n_kv_heads, head_dim,
+              stream):
+        if freq_real.shape != freq_imag.shape or freq_real.shape[-1] != head_dim // 2:
+            raise ValueError("RoPE tables must both be [seq_len][head_dim/2]")
+        N.call(fn, self._h, layer, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"),
+               _dev(freq_real, "freq_real"), _dev(freq_imag, "freq_imag"), freq_real.shape[0],
+               n_heads, n_kv_heads, head_dim, _stream_ptr(stream))
+
     def take_device_errors(self) -> int:
         out = ctypes.c_int32()
         N.call("nitro_kvpool_take_device_errors", self._h, ctypes.byref(out))

@@ -299,7 +299,7 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
 
         const size_t nt = (size_t)batch * max_pages;
         const size_t n_work = items.size() * 2;
-        const size_t need = nt + 3 * (size_t)batch + (size_t)total + n_work;
+        const size_t need = nt + 3 * (size_t)batch + 2 * (size_t)total + n_work;
         hipStream_t s = as_stream(stream);
         Staging& st = pool->prefill_staging;
         int32_t* h = st.acquire(need);
@@ -308,7 +308,8 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
         int32_t* h_len = h_start + batch;
         int32_t* h_off = h_len + batch;
         int32_t* h_slots = h_off + batch;
-        int32_t* h_work = h_slots + total;
+        int32_t* h_row_pos = h_slots + total;
+        int32_t* h_work = h_row_pos + total;
         std::memcpy(h_tables, tables, nt * sizeof(int32_t));
         std::memcpy(h_start, start_pos, batch * sizeof(int32_t));
         std::memcpy(h_len, num_tokens, batch * sizeof(int32_t));
@@ -317,6 +318,7 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
             for (int t = 0; t < num_tokens[b]; t++) {
                 const int pos = start_pos[b] + t;
                 h_slots[row_off[b] + t] = tables[(size_t)b * max_pages + (pos >> 4)] * BLOCK_SIZE + (pos & 15);
+                h_row_pos[row_off[b] + t] = pos;
             }
         for (size_t i = 0; i < items.size(); i++) {
             h_work[2 * i] = items[i].second.first;
@@ -327,12 +329,14 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
         p.d_len.reserve(batch);
         p.d_row_off.reserve(batch);
         p.slots.reserve(total);
+        p.row_pos.reserve(total);
         p.work.reserve(n_work);
         st.copy(p.tables.ptr, h_tables, nt, s);
         st.copy(p.d_start.ptr, h_start, batch, s);
         st.copy(p.d_len.ptr, h_len, batch, s);
         st.copy(p.d_row_off.ptr, h_off, batch, s);
         st.copy(p.slots.ptr, h_slots, total, s);
+        st.copy(p.row_pos.ptr, h_row_pos, total, s);
         st.copy(p.work.ptr, h_work, n_work, s);
         st.finish(s);
         p.start_pos.assign(start_pos, start_pos + batch);
@@ -340,6 +344,10 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
         p.row_off = row_off;
         p.total_rows = (int32_t)total;
         p.max_tokens = max_tokens;
+        int max_pos = 0;
+        for (int b = 0; b < batch; b++)
+            if (num_tokens[b] > 0) max_pos = std::max(max_pos, start_pos[b] + num_tokens[b] - 1);
+        p.max_pos = max_pos;
         p.work_items = (int32_t)items.size();
         p.work_block_m = bm;
         p.max_pages = max_pages;
@@ -399,6 +407,57 @@ int nitro_paged_attn_prefill(nitro_kvpool* pool, int32_t layer, const float* q, 
         a.use_valu = (kern && std::strcmp(kern, "valu") == 0) ? 1 : 0;
         hipStream_t s = as_stream(stream);
         hip_check(launch_paged_attn_prefill(a, s), "paged_attn_prefill launch");
+        pool->last_stream = s;
+    });
+}
+
+static void check_rope(const nitro_kvpool* pool, int layer, int n_heads, int n_kv_heads,
+                       int head_dim, int seq_len, int max_pos, const void* q, const void* k,
+                       const void* v, const void* fr, const void* fi) {
+    require(q && k && v && fr && fi, ERR_INVALID_ARGUMENT, "null q/k/v or RoPE table");
+    check_shape(pool, layer, n_heads, n_kv_heads, head_dim);
+    require(seq_len > max_pos, ERR_INVALID_ARGUMENT, "a position lies beyond the RoPE tables");
+}
+
+int nitro_rope_kv_append(nitro_kvpool* pool, int32_t layer, float* q, float* k, const float* v,
+                         const float* freq_real, const float* freq_imag, int32_t seq_len,
+                         int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void* stream) {
+    return guarded([&] {
+        require_pool(pool);
+        const DecodeBatch& d = pool->decode;
+        require(d.batch > 0, ERR_NO_BATCH, "no decode batch uploaded");
+        int max_pos = 0;
+        for (int p : d.positions) max_pos = std::max(max_pos, p);
+        check_rope(pool, layer, n_heads, n_kv_heads, head_dim, seq_len, max_pos, q, k, v,
+                   freq_real, freq_imag);
+        hipStream_t s = as_stream(stream);
+        hip_check(launch_rope_kv_append(pool->k, pool->v, q, k, v, freq_real, freq_imag,
+                                        d.tables.ptr, d.pos.ptr, nullptr, nullptr, d.batch,
+                                        d.max_pages, n_heads * head_dim, pool->kv_dim, head_dim,
+                                        pool->page_stride(), pool->layer_offset(layer),
+                                        pool->num_pages, pool->bad_pages.ptr, s),
+                  "rope_kv_append launch");
+        pool->last_stream = s;
+    });
+}
+
+int nitro_rope_kv_append_prefill(nitro_kvpool* pool, int32_t layer, float* q, float* k,
+                                 const float* v, const float* freq_real, const float* freq_imag,
+                                 int32_t seq_len, int32_t n_heads, int32_t n_kv_heads,
+                                 int32_t head_dim, void* stream) {
+    return guarded([&] {
+        require_pool(pool);
+        const PrefillBatch& p = pool->prefill;
+        require(p.batch > 0, ERR_NO_BATCH, "no prefill batch uploaded");
+        check_rope(pool, layer, n_heads, n_kv_heads, head_dim, seq_len, p.max_pos, q, k, v,
+                   freq_real, freq_imag);
+        hipStream_t s = as_stream(stream);
+        hip_check(launch_rope_kv_append(pool->k, pool->v, q, k, v, freq_real, freq_imag, nullptr,
+                                        nullptr, p.slots.ptr, p.row_pos.ptr, p.total_rows,
+                                        p.max_pages, n_heads * head_dim, pool->kv_dim, head_dim,
+                                        pool->page_stride(), pool->layer_offset(layer),
+                                        pool->num_pages, pool->bad_pages.ptr, s),
+                  "rope_kv_append_prefill launch");
         pool->last_stream = s;
     });
 }

@@ -98,9 +98,11 @@ struct PrefillBatch {
     std::vector<int32_t> start_pos, num_tokens, row_off;
     DeviceBuffer<int32_t> tables, d_start, d_len, d_row_off;
     DeviceBuffer<int32_t> slots;      // per packed row: page*16 + row-in-page
+    DeviceBuffer<int32_t> row_pos;    // per packed row: its position in the sequence
     DeviceBuffer<int32_t> work;       // per work item: (seq, first query) pairs
     int32_t work_items = 0;
     int32_t work_block_m = 0;         // query rows per work item the list was built for
+    int32_t max_pos = 0;              // largest position of any row
 };
 
 }  // namespace nitro
@@ -152,6 +154,13 @@ hipError_t launch_kv_append_decode(float* k_pool, float* v_pool, const float* k,
                                    int max_pages, int kv_dim, int64_t page_stride,
                                    int64_t layer_off, int num_pages, int32_t* bad_pages,
                                    hipStream_t stream);
+hipError_t launch_rope_kv_append(float* k_pool, float* v_pool, float* q, float* k, const float* v,
+                                 const float* freq_real, const float* freq_imag,
+                                 const int32_t* tables, const int32_t* positions,
+                                 const int32_t* slots, const int32_t* row_pos, int rows,
+                                 int max_pages, int dim, int kv_dim, int head_dim,
+                                 int64_t page_stride, int64_t layer_off, int num_pages,
+                                 int32_t* bad_pages, hipStream_t stream);
 hipError_t launch_kv_scatter_rows(float* k_pool, float* v_pool, const float* k, const float* v,
                                   const int32_t* slots, int rows, int kv_dim, int64_t page_stride,
                                   int64_t layer_off, int num_pages, int32_t* bad_pages,

@@ -6,6 +6,12 @@
 // resolved on the host into slots[r] = page*16 + pos%16.
 // One float4 per thread (kv_dim is a multiple of 4); page ids outside the pool
 // are counted in *bad_pages and skipped.
+//
+// RoPE + append (src/model_q8.cpp:601-623 decode, :451-484 prefill, :262-287
+// single sequence): one workgroup per row rotates each pair (j, j+1) of q (all
+// heads) and of k (kv heads) in place by the table entry at
+// pos*(head_dim/2) + (j % head_dim)/2 — q' = (q0*c - q1*s, q0*s + q1*c) — and
+// writes the rotated k and the unrotated v into the row's page slot.
 #include <hip/hip_runtime.h>
 
 #include "device_pool.hpp"
@@ -54,7 +60,70 @@ __global__ __launch_bounds__(APPEND_THREADS) void kv_scatter_rows_kernel(
     reinterpret_cast<float4*>(v_pool + dst)[i] = reinterpret_cast<const float4*>(v + src)[i];
 }
 
+// Decode rows: position positions[row], page tables[row][pos/16].  Prefill
+// rows: position row_pos[row], slot slots[row] (page*16 + pos%16).
+__global__ __launch_bounds__(APPEND_THREADS) void rope_kv_append_kernel(
+    float* __restrict__ k_pool, float* __restrict__ v_pool, float* __restrict__ q,
+    float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ freq_real,
+    const float* __restrict__ freq_imag, const int32_t* __restrict__ tables,
+    const int32_t* __restrict__ positions, const int32_t* __restrict__ slots,
+    const int32_t* __restrict__ row_pos, int max_pages, int dim, int kv_dim, int head_dim,
+    int64_t page_stride, int64_t layer_off, int num_pages, int32_t* bad_pages) {
+    const int row = blockIdx.x;
+    int pos, page, slot_row;
+    if (slots) {
+        pos = row_pos[row];
+        const int slot = slots[row];
+        page = slot >> 4;
+        slot_row = slot & 15;
+    } else {
+        pos = positions[row];
+        page = tables[(size_t)row * max_pages + (pos >> 4)];
+        slot_row = pos & 15;
+    }
+    const bool page_ok = page >= 0 && page < num_pages;
+    if (!page_ok && threadIdx.x == 0) atomicAdd(bad_pages, 1);
+    const float* fr = freq_real + (size_t)pos * (head_dim / 2);
+    const float* fi = freq_imag + (size_t)pos * (head_dim / 2);
+    float2* qrow = reinterpret_cast<float2*>(q + (size_t)row * dim);
+    float2* krow = reinterpret_cast<float2*>(k + (size_t)row * kv_dim);
+    const float2* vrow = reinterpret_cast<const float2*>(v + (size_t)row * kv_dim);
+    float2* kdst = reinterpret_cast<float2*>(k_pool + (size_t)page * page_stride + layer_off +
+                                            (size_t)slot_row * kv_dim);
+    float2* vdst = reinterpret_cast<float2*>(v_pool + (size_t)page * page_stride + layer_off +
+                                            (size_t)slot_row * kv_dim);
+    for (int p = threadIdx.x; p < dim / 2; p += APPEND_THREADS) {
+        const int f = (2 * p % head_dim) / 2;
+        const float c = fr[f], sn = fi[f];
+        const float2 x = qrow[p];
+        qrow[p] = make_float2(x.x * c - x.y * sn, x.x * sn + x.y * c);
+        if (2 * p < kv_dim) {
+            const float2 y = krow[p];
+            const float2 r = make_float2(y.x * c - y.y * sn, y.x * sn + y.y * c);
+            krow[p] = r;
+            if (page_ok) {
+                kdst[p] = r;
+                vdst[p] = vrow[p];
+            }
+        }
+    }
+}
+
 }  // namespace
+
+hipError_t launch_rope_kv_append(float* k_pool, float* v_pool, float* q, float* k, const float* v,
+                                 const float* freq_real, const float* freq_imag,
+                                 const int32_t* tables, const int32_t* positions,
+                                 const int32_t* slots, const int32_t* row_pos, int rows,
+                                 int max_pages, int dim, int kv_dim, int head_dim,
+                                 int64_t page_stride, int64_t layer_off, int num_pages,
+                                 int32_t* bad_pages, hipStream_t stream) {
+    hipLaunchKernelGGL(rope_kv_append_kernel, dim3(rows), dim3(APPEND_THREADS), 0, stream, k_pool,
+                       v_pool, q, k, v, freq_real, freq_imag, tables, positions, slots, row_pos,
+                       max_pages, dim, kv_dim, head_dim, page_stride, layer_off, num_pages,
+                       bad_pages);
+    return hipGetLastError();
+}
 
 hipError_t launch_kv_append_decode(float* k_pool, float* v_pool, const float* k, const float* v,
                                    const int32_t* tables, const int32_t* positions, int batch,

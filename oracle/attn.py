@@ -42,6 +42,8 @@ def lib() -> ctypes.CDLL:
                                            c_int, c_int, c_int, c_int, c_int, c_int]
         L.oracle_contiguous_attention.argtypes = [_f32p, _f32p, c_int, c_int, c_int, _f32p, _f32p,
                                                   c_int, c_int, c_int, c_int, c_int]
+        L.oracle_rope.argtypes = [_f32p, _f32p, c_int, _i32p, _f32p, _f32p, c_int, c_int, c_int]
+        L.oracle_rope.restype = None
         for name in ("oracle_decode_batch", "oracle_decode_single_avx2", "oracle_prefill_chunk",
                      "oracle_contiguous_attention", "oracle_max_threads"):
             getattr(L, name).restype = c_int
@@ -144,6 +146,20 @@ def contiguous_attention(key_cache, value_cache, layer, q, pos, n_heads, n_kv_he
     if rc != 0:
         raise RuntimeError(f"oracle_contiguous_attention failed: {rc}")
     return out
+
+
+def rope(q, k, positions, freq_real, freq_imag, head_dim):
+    """RoPE of the paged paths (src/model_q8.cpp:601-615); returns rotated copies.
+    q: [rows][dim], k: [rows][kv_dim], positions: [rows], freq_*: [seq_len][hd/2]."""
+    q = np.ascontiguousarray(q, dtype=np.float32).copy()
+    k = np.ascontiguousarray(k, dtype=np.float32).copy()
+    positions = np.ascontiguousarray(positions, dtype=np.int32)
+    fr = np.ascontiguousarray(freq_real, dtype=np.float32)
+    fi = np.ascontiguousarray(freq_imag, dtype=np.float32)
+    assert positions.max() < fr.shape[0]
+    lib().oracle_rope(_f(q), _f(k), q.shape[0], _i(positions), _f(fr), _f(fi), q.shape[1],
+                      k.shape[1], head_dim)
+    return q, k
 
 
 def max_threads() -> int:

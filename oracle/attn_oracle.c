@@ -40,6 +40,38 @@ void oracle_softmax(float* x, int size) {
     for (int i = 0; i < size; i++) x[i] /= sum;
 }
 
+/*
+ * src/model_q8.cpp:601-615 (decode; the same loop at :457-471 for prefill rows
+ * and :262-274 for the single-sequence path): for each pair (j, j+1) of a row,
+ * with hd_j = j % head_size, (fcr, fci) = freq[pos*(head_size/2) + hd_j/2],
+ * q' = (q0*fcr - q1*fci, q0*fci + q1*fcr); the first kv_dim entries of k
+ * rotate the same way.  Row r is at position positions[r].
+ */
+void oracle_rope(float* q, float* k, int rows, const int32_t* positions,
+                 const float* freq_real, const float* freq_imag, int dim, int kv_dim,
+                 int head_size) {
+    for (int r = 0; r < rows; r++) {
+        int pos = positions[r];
+        float* qb = q + (size_t)r * dim;
+        float* kb = k + (size_t)r * kv_dim;
+        for (int j = 0; j < dim; j += 2) {
+            int head_dim = j % head_size;
+            float fcr = freq_real[pos * (head_size / 2) + (head_dim / 2)];
+            float fci = freq_imag[pos * (head_size / 2) + (head_dim / 2)];
+            float q0 = qb[j];
+            float q1 = qb[j + 1];
+            qb[j] = q0 * (fcr)-q1 * fci;
+            qb[j + 1] = q0 * fci + q1 * fcr;
+            if (j < kv_dim) {
+                float k0 = kb[j];
+                float k1 = kb[j + 1];
+                kb[j] = k0 * fcr - k1 * fci;
+                kb[j + 1] = k0 * fci + k1 * fcr;
+            }
+        }
+    }
+}
+
 /* src/model_q8.cpp:616-623 — page = table[pos/16], row = pos%16, layer offset l*16*kv_dim. */
 void oracle_kv_append_decode(float* k_pool, float* v_pool, int n_layers, int kv_dim, int layer,
                              const float* k, const float* v, const int32_t* tables, int max_pages,

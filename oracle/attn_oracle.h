@@ -23,6 +23,9 @@
  *   oracle_contiguous_attention  reference build golden vectors (forward), paged == contiguous invariant
  *   oracle_kv_append_decode      reference build golden vectors (pool bytes after forward_decode_batch)
  *   oracle_kv_scatter_prefill    reference build golden vectors (pool bytes after forward_prefill_chunk)
+ *   oracle_rope                  reference build golden vectors (q, k before/after RoPE in
+ *                                forward_decode_batch, forward_paged, forward_prefill_chunk),
+ *                                rotation invariants (norm of each pair, identity at angle 0)
  */
 #ifndef NITRO_ATTN_ORACLE_H
 #define NITRO_ATTN_ORACLE_H
@@ -62,6 +65,10 @@ int oracle_prefill_chunk(const float* k_pool, const float* v_pool, int n_layers,
 int oracle_contiguous_attention(const float* key_cache, const float* value_cache, int seq_len,
                                 int kv_dim, int layer, const float* q, float* out, int pos,
                                 int n_heads, int n_kv_heads, int head_dim, int n_threads);
+
+void oracle_rope(float* q, float* k, int rows, const int32_t* positions,
+                 const float* freq_real, const float* freq_imag, int dim, int kv_dim,
+                 int head_size);
 
 int oracle_max_threads(void);
 

@@ -39,6 +39,7 @@ def lib() -> ctypes.CDLL:
         L.ref_world_create.restype = vp
         L.ref_world_destroy.argtypes = [vp]
         L.ref_world_dims.argtypes = [vp, _i32p]
+        L.ref_world_set_rope.argtypes = [vp, _f32p, _f32p]
         L.ref_op.argtypes = [vp, ci, ci, ci, u64, _i32p, ci, ctypes.POINTER(ctypes.c_int64)]
         L.ref_snapshot.argtypes = [vp, _i32p, ci]
         L.ref_decode_batch.argtypes = [vp, _i32p, _i32p, ci, _i32p]
@@ -86,6 +87,13 @@ class RefWorld:
             self.close()
         except Exception:
             pass
+
+    def set_rope(self, real, imag):
+        """RoPE tables [seq_len][head_dim/2] (the world starts with the identity rotation)."""
+        real = np.ascontiguousarray(real, dtype=np.float32)
+        imag = np.ascontiguousarray(imag, dtype=np.float32)
+        assert real.shape == imag.shape == (self.seq_len, self.head_dim // 2)
+        lib().ref_world_set_rope(self.h, real.ctypes.data_as(_f32p), imag.ctypes.data_as(_f32p))
 
     def op(self, op, a=0, b=0, h=0, toks=()):
         t = np.ascontiguousarray(toks, dtype=np.int32)

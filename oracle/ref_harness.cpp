@@ -190,6 +190,15 @@ void ref_world_destroy(void* p) {
     delete W;
 }
 
+// Replaces the RoPE tables (seq_len x head_size/2 each); the world is created
+// with the identity rotation (real 1, imaginary 0).
+int ref_world_set_rope(void* p, const float* real, const float* imag) {
+    World* W = (World*)p;
+    std::memcpy(W->fcr.data(), real, sizeof(float) * W->fcr.size());
+    std::memcpy(W->fci.data(), imag, sizeof(float) * W->fci.size());
+    return 0;
+}
+
 int ref_world_dims(void* p, int* out) {
     World* W = (World*)p;
     out[0] = W->c.dim;

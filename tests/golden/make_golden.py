@@ -39,7 +39,7 @@ sys.path.insert(0, HERE)
 
 from oracle import paged_memory as pm  # noqa: E402
 from oracle import ref  # noqa: E402
-from synth import counter_pool  # noqa: E402
+from synth import counter_pool, rope_tables  # noqa: E402
 
 
 def state_digest(snap: dict) -> str:
@@ -322,6 +322,105 @@ def case_contiguous(rec, name, H, Hkv, hd, n_pos, seed):
     W.close()
 
 
+def rope_pair(H, Hkv, hd, blocks, seed, max_seqs, seq_len=128):
+    """Two one-layer worlds with equal weights: A keeps the identity rotation, so
+    its q/k are the pre-RoPE values of B, which uses Llama-style tables."""
+    A = ref.RefWorld(n_heads=H, n_kv_heads=Hkv, head_dim=hd, n_layers=1, total_blocks=blocks,
+                     seed=seed, max_seqs=max_seqs, seq_len=seq_len)
+    B = ref.RefWorld(n_heads=H, n_kv_heads=Hkv, head_dim=hd, n_layers=1, total_blocks=blocks,
+                     seed=seed, max_seqs=max_seqs, seq_len=seq_len)
+    fr, fi = rope_tables(seq_len, hd)
+    B.set_rope(fr, fi)
+    return A, B
+
+
+def case_rope_decode(rec, name, H, Hkv, hd, blocks, lens, seed):
+    A, B = rope_pair(H, Hkv, hd, blocks, seed, len(lens))
+    pool_seed = 5000 + seed
+    for W in (A, B):
+        for s, n in enumerate(lens):
+            W.op(pm.OP_SEQ_NEW, s)
+            for t in range(n):
+                W.op(pm.OP_SEQ_APPEND, s, 1 + (t * 7 + s) % 400)
+        W.write_pool(counter_pool(pool_seed, blocks, 1, W.kv_dim),
+                     counter_pool(pool_seed + 1, blocks, 1, W.kv_dim))
+    toks = [5 + 3 * s for s in range(len(lens))]
+    pa = A.decode_batch(list(range(len(lens))), toks)
+    pb = B.decode_batch(list(range(len(lens))), toks)
+    assert np.array_equal(pa, pb)
+    qa, ka, va, _ = A.rows(len(lens))
+    qb, kb, vb, xb2 = B.rows(len(lens))
+    assert np.array_equal(va, vb)
+    max_pages = max(p // 16 + 1 for p in pb) + 1
+    tables = tables_of(B, range(len(lens)), max_pages)
+    kp, vp = B.pool()
+    rec.add(name, {"kind": "rope_decode", "H": H, "Hkv": Hkv, "hd": hd, "layers": 1,
+                   "pages": blocks, "layer": 0, "pool_seed": pool_seed, "observed": 32,
+                   "seq_len": B.seq_len, "rope_base": 10000.0,
+                   "k_pool_digest": array_digest(kp[:, 0]), "v_pool_digest": array_digest(vp[:, 0])},
+            q_pre=qa, k_pre=ka, v=vb, q=qb, k=kb, xb2_obs=xb2[:, -32:], tables=tables,
+            positions=pb)
+    A.close()
+    B.close()
+
+
+def case_rope_single(rec, name, H, Hkv, hd, blocks, n_past, seed):
+    A, B = rope_pair(H, Hkv, hd, blocks, seed, 1)
+    pool_seed = 6000 + seed
+    for W in (A, B):
+        W.op(pm.OP_SEQ_NEW, 0)
+        for t in range(n_past):
+            W.op(pm.OP_SEQ_APPEND, 0, 1 + (t * 5) % 300)
+        W.write_pool(counter_pool(pool_seed, blocks, 1, W.kv_dim),
+                     counter_pool(pool_seed + 1, blocks, 1, W.kv_dim))
+    pos = A.forward_paged(0, 42)
+    assert B.forward_paged(0, 42) == pos
+    qa, ka, va, _ = A.rows(1)
+    qb, kb, vb, xb2 = B.rows(1)
+    kp, vp = B.pool()
+    rec.add(name, {"kind": "rope_single", "H": H, "Hkv": Hkv, "hd": hd, "layers": 1,
+                   "pages": blocks, "layer": 0, "pool_seed": pool_seed, "pos": int(pos),
+                   "observed": H * hd, "seq_len": B.seq_len, "rope_base": 10000.0,
+                   "k_pool_digest": array_digest(kp[:, 0]), "v_pool_digest": array_digest(vp[:, 0])},
+            q_pre=qa, k_pre=ka, v=vb, q=qb, k=kb, xb2_obs=xb2, table=B.block_table(0))
+    A.close()
+    B.close()
+
+
+def case_rope_prefill(rec, name, H, Hkv, hd, blocks, chunks, seed):
+    """One sequence, prefill chunks of the given sizes with RoPE; records every chunk's
+    pre/post q and k and the last chunk's observed output."""
+    A, B = rope_pair(H, Hkv, hd, blocks, seed, 1)
+    pool_seed = 7000 + seed
+    for W in (A, B):
+        W.op(pm.OP_SEQ_NEW, 0)
+        W.write_pool(counter_pool(pool_seed, blocks, 1, W.kv_dim),
+                     counter_pool(pool_seed + 1, blocks, 1, W.kv_dim))
+    arrays = {}
+    tok = 1
+    starts = []
+    for ci, n in enumerate(chunks):
+        toks = list(range(tok, tok + n))
+        tok += n
+        sa = A.prefill_chunk(0, toks)
+        sb = B.prefill_chunk(0, toks)
+        assert sa == sb
+        starts.append(sb)
+        qa, ka, va, _ = A.rows(n)
+        qb, kb, vb, xb2 = B.rows(n)
+        arrays.update({f"q_pre{ci}": qa, f"k_pre{ci}": ka, f"v{ci}": vb, f"q{ci}": qb,
+                       f"k{ci}": kb})
+    kp, vp = B.pool()
+    rec.add(name, {"kind": "rope_prefill", "H": H, "Hkv": Hkv, "hd": hd, "layers": 1,
+                   "pages": blocks, "layer": 0, "pool_seed": pool_seed, "chunks": len(chunks),
+                   "observed": 32, "seq_len": B.seq_len, "rope_base": 10000.0,
+                   "k_pool_digest": array_digest(kp[:, 0]), "v_pool_digest": array_digest(vp[:, 0])},
+            xb2_obs=xb2[:, -32:], table=B.block_table(0), chunk_starts=np.array(starts, np.int32),
+            **arrays)
+    A.close()
+    B.close()
+
+
 def make_attention():
     rec = Recorder()
     case_decode(rec, "decode_mha_hd16_l2", 4, 4, 16, 2, 24, [0, 15, 16, 37], 21)
@@ -338,6 +437,10 @@ def make_attention():
     case_decode(rec, "decode_gqa_h4kv2_hd32", 4, 2, 32, 2, 32, [0, 16, 31, 77], 25)
     case_prefill(rec, "prefill_gqa_hd32_l2", 4, 2, 32, 2, 16, [19, 30], 44)
     case_prefix_hit(rec, "prefix_hit_hd32", 2, 2, 32, 1, 24, 48, 5, 21, 52)
+    case_rope_decode(rec, "rope_decode_gqa_hd32", 4, 2, 32, 32, [0, 17, 40, 63], 71)
+    case_rope_decode(rec, "rope_decode_hd64", 2, 2, 64, 24, [5, 33], 72)
+    case_rope_single(rec, "rope_single_hd32", 4, 4, 32, 16, 50, 73)
+    case_rope_prefill(rec, "rope_prefill_hd32", 4, 4, 32, 16, [21, 30], 74)
     case_contiguous(rec, "contiguous_hd16", 4, 4, 16, 30, 61)
     case_contiguous(rec, "contiguous_gqa_hd32", 4, 2, 32, 19, 62)
     return rec

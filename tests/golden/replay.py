@@ -36,11 +36,11 @@ def pools_after_call(meta, arr):
     k, v = base_pools(meta)
     layer = meta["layer"]
     kind = meta["kind"]
-    if kind == "decode_batch":
+    if kind in ("decode_batch", "rope_decode"):
         for b, pos in enumerate(arr["positions"]):
             write_rows(k, layer, arr["tables"][b], int(pos), arr["k"][b:b + 1])
             write_rows(v, layer, arr["tables"][b], int(pos), arr["v"][b:b + 1])
-    elif kind == "decode_single":
+    elif kind in ("decode_single", "rope_single"):
         write_rows(k, layer, arr["table"], meta["pos"], arr["k"])
         write_rows(v, layer, arr["table"], meta["pos"], arr["v"])
     elif kind == "prefill":
@@ -55,6 +55,10 @@ def pools_after_call(meta, arr):
         write_rows(v, layer, arr["table_a"], 0, arr["v_a"])
         write_rows(k, layer, arr["table"], meta["start_pos"], arr["k"])
         write_rows(v, layer, arr["table"], meta["start_pos"], arr["v"])
+    elif kind == "rope_prefill":
+        for ci, st in enumerate(arr["chunk_starts"]):
+            write_rows(k, layer, arr["table"], int(st), arr[f"k{ci}"])
+            write_rows(v, layer, arr["table"], int(st), arr[f"v{ci}"])
     else:
         raise ValueError(kind)
     return k, v

@@ -33,3 +33,12 @@ def counter_uniform(seed: int, n: int) -> np.ndarray:
 def counter_pool(seed: int, pages: int, layers: int, kv_dim: int) -> np.ndarray:
     n = pages * layers * 16 * kv_dim
     return counter_uniform(seed, n).reshape(pages, layers, 16, kv_dim)
+
+
+def rope_tables(seq_len: int, head_dim: int, base: float = 10000.0):
+    """Llama-style RoPE tables: angle(pos, i) = pos * base^(-2i/head_dim), i < head_dim/2,
+    evaluated in float64 and rounded to float32 (real = cos, imag = sin)."""
+    i = np.arange(head_dim // 2, dtype=np.float64)
+    theta = base ** (-2.0 * i / head_dim)
+    ang = np.arange(seq_len, dtype=np.float64)[:, None] * theta[None, :]
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)

@@ -6,7 +6,7 @@ import pytest
 
 from oracle import attn, closed_form as cf, paged_memory as pm
 from replay import base_pools, digest, pools_after_call
-from synth import counter_pool
+from synth import counter_pool, rope_tables
 
 # The oracle is a restatement compiled with the reference's flags; against the
 # reference build it must agree far inside the path's 1e-4/1e-3 parity bar.
@@ -226,3 +226,76 @@ def test_counter_pool_is_exact_and_reproducible():
     assert a.min() >= -1 and a.max() < 1
     # every value is a multiple of 2^-23 (24 random bits, exact in fp32)
     assert np.all((a.astype(np.float64) * 2 ** 23) % 1 == 0)
+
+
+ROPE_CASES = ["rope_decode_gqa_hd32", "rope_decode_hd64", "rope_single_hd32", "rope_prefill_hd32"]
+
+
+def rope_rows(meta, arr):
+    """(q_pre, k_pre, positions, q_post, k_post) of every recorded row."""
+    if meta["kind"] == "rope_decode":
+        return arr["q_pre"], arr["k_pre"], arr["positions"], arr["q"], arr["k"]
+    if meta["kind"] == "rope_single":
+        return arr["q_pre"], arr["k_pre"], np.array([meta["pos"]], np.int32), arr["q"], arr["k"]
+    qs, ks, ps, qo, ko = [], [], [], [], []
+    for ci, st in enumerate(arr["chunk_starts"]):
+        n = arr[f"q{ci}"].shape[0]
+        qs.append(arr[f"q_pre{ci}"])
+        ks.append(arr[f"k_pre{ci}"])
+        ps.append(np.arange(st, st + n, dtype=np.int32))
+        qo.append(arr[f"q{ci}"])
+        ko.append(arr[f"k{ci}"])
+    return (np.concatenate(qs), np.concatenate(ks), np.concatenate(ps), np.concatenate(qo),
+            np.concatenate(ko))
+
+
+@pytest.mark.parametrize("name", ROPE_CASES)
+def test_oracle_rope_matches_reference_golden(golden_attention, name):
+    meta, arr = golden_attention[name]
+    fr, fi = rope_tables(meta["seq_len"], meta["hd"], meta["rope_base"])
+    q_pre, k_pre, pos, q_post, k_post = rope_rows(meta, arr)
+    q, k = attn.rope(q_pre, k_pre, pos, fr, fi, meta["hd"])
+    # contraction of the two products into FMAs may differ by an ulp or two
+    np.testing.assert_allclose(q, q_post, rtol=1e-6, atol=1e-5)
+    np.testing.assert_allclose(k, k_post, rtol=1e-6, atol=1e-5)
+    # a plausible slip (cos/sin swapped, pair order, position off by one) is far outside that
+    q_bad, _ = attn.rope(q_pre, k_pre, pos + 1, fr, fi, meta["hd"])
+    assert np.max(np.abs(q_bad - q_post)) > 1e-2
+
+
+@pytest.mark.parametrize("name", ROPE_CASES)
+def test_oracle_attention_after_rope_matches_reference(golden_attention, name):
+    meta, arr = golden_attention[name]
+    k, v = pools_after_call(meta, arr)
+    assert digest(k[:, 0]) == meta["k_pool_digest"] and digest(v[:, 0]) == meta["v_pool_digest"]
+    H, Hkv, hd = meta["H"], meta["Hkv"], meta["hd"]
+    if meta["kind"] == "rope_decode":
+        out = attn.decode_batch(k, v, 0, arr["q"], arr["tables"], arr["positions"], H, Hkv, hd)
+    elif meta["kind"] == "rope_single":
+        out = attn.decode_single_avx2(k, v, 0, arr["q"][0], arr["table"], meta["pos"], H, Hkv,
+                                      hd)[None, :]
+    else:
+        last = meta["chunks"] - 1
+        out = attn.prefill_chunk(k, v, 0, arr[f"q{last}"], arr["table"],
+                                 int(arr["chunk_starts"][last]), H, Hkv, hd)
+    np.testing.assert_allclose(out[:, -meta["observed"]:], arr["xb2_obs"], **TIGHT)
+
+
+def test_rope_closed_form():
+    """Each pair rotates by its angle: norms kept, position 0 is the identity,
+    and rotating by the table equals multiplying by exp(i*angle) in fp64."""
+    rng = np.random.default_rng(2)
+    H, Hkv, hd, S = 4, 2, 64, 300
+    fr, fi = rope_tables(S, hd)
+    q = rng.standard_normal((5, H * hd)).astype(np.float32)
+    k = rng.standard_normal((5, Hkv * hd)).astype(np.float32)
+    pos = np.array([0, 1, 17, 150, 299], np.int32)
+    qr, kr = attn.rope(q, k, pos, fr, fi, hd)
+    np.testing.assert_array_equal(qr[0], q[0])
+    np.testing.assert_array_equal(kr[0], k[0])
+    for x, xr, heads in ((q, qr, H), (k, kr, Hkv)):
+        z = (x[:, 0::2] + 1j * x[:, 1::2]).astype(np.complex128)
+        ang = fr.astype(np.float64)[pos][:, None, :] + 1j * fi.astype(np.float64)[pos][:, None, :]
+        want = (z.reshape(5, heads, hd // 2) * ang).reshape(5, -1)
+        np.testing.assert_allclose(xr[:, 0::2], want.real, atol=2e-6)
+        np.testing.assert_allclose(xr[:, 1::2], want.imag, atol=2e-6)
