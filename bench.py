@@ -356,6 +356,14 @@ WORKLOADS = ["decode-b64-ctx4096", "decode-single-110m", "decode-b32-mixed",
              "decode-prefix-shared", "prefill-b8-12x64"]
 
 
+def kernel_name(w) -> str:
+    if w.bound == "hbm":
+        return f"paged_attn_decode_kernel<{w.hd}>"
+    if w.hd == 256 or os.environ.get("NITRO_PREFILL_KERNEL") == "valu":
+        return f"paged_attn_prefill_kernel<{w.hd}> (VALU)"
+    return f"paged_attn_prefill_mfma_kernel<{w.hd}, 2> (MFMA fp32)"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -448,8 +456,7 @@ def main():
         "tokens_per_s": round(w.tokens_per_step() / (ms_per_step * 1e-3), 1),
         "roofline": {
             "bound": w.bound,
-            "kernel": (f"paged_attn_decode_kernel<{w.hd}>" if w.bound == "hbm"
-                       else f"paged_attn_prefill_kernel<{w.hd}>"),
+            "kernel": kernel_name(w),
             "achieved": round(kernel_rate, 2 if unit == "GB/s" else 4),
             "peak": peak,
             "unit": unit,
