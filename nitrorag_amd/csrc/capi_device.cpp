@@ -47,6 +47,28 @@ void check_table_rows(const nitro_kvpool* pool, const int32_t* tables, int b, in
                                                  std::to_string(pool->num_pages) + ")");
 }
 
+// True when a page id occurs in the used part of more than one table row (a
+// prefix shared through the prefix cache), or twice in one row.  Decode then
+// keeps plain loads so that the page's lines stay cached for the other readers.
+bool any_page_shared(const nitro_kvpool* pool, DecodeBatch& d, const int32_t* tables,
+                     const int32_t* positions, int batch, int max_pages) {
+    if (d.page_mark.size() != (size_t)pool->num_pages || d.stamp == UINT32_MAX) {
+        d.page_mark.assign(pool->num_pages, 0);
+        d.stamp = 0;
+    }
+    const uint32_t stamp = ++d.stamp;
+    bool shared = false;
+    for (int b = 0; b < batch; b++) {
+        const int32_t* row = tables + (size_t)b * max_pages;
+        for (int i = 0; i <= (positions[b] >> 4); i++) {
+            uint32_t& m = d.page_mark[row[i]];  // ids were checked against the pool
+            shared |= m == stamp;
+            m = stamp;
+        }
+    }
+    return shared;
+}
+
 void check_shape(const nitro_kvpool* pool, int layer, int n_heads, int n_kv_heads, int head_dim) {
     require(layer >= 0 && layer < pool->num_layers, ERR_INVALID_ARGUMENT, "layer out of range");
     require(n_heads > 0 && n_kv_heads > 0, ERR_INVALID_ARGUMENT, "head counts must be positive");
@@ -171,6 +193,7 @@ int nitro_decode_batch_upload(nitro_kvpool* pool, const int32_t* tables, const i
         st.copy(d.pos.ptr, h + nt, batch, s);
         st.finish(s);
         d.positions.assign(positions, positions + batch);
+        d.shared_pages = any_page_shared(pool, d, tables, positions, batch, max_pages);
         d.batch = batch;
         d.max_pages = max_pages;
         pool->last_stream = s;
@@ -258,6 +281,12 @@ int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, f
         a.tiles_per_split = tps;
         a.num_splits = splits;
         a.waves = waves;
+        // Non-temporal K/V loads when every K/V line is read once per launch:
+        // one query head per KV head and no page shared between sequences.
+        const int stream_env = env_int("NITRO_DECODE_STREAM", -1);
+        a.stream_kv = stream_env >= 0 ? stream_env != 0 : (a.kv_mul == 1 && !d.shared_pages);
+        const int remap_env = env_int("NITRO_DECODE_XCD_REMAP", -1);
+        a.xcd_remap = remap_env >= 0 ? remap_env != 0 : a.kv_mul > 1;
         a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
         hip_check(launch_paged_attn_decode(a, s), "paged_attn_decode launch");
         pool->last_stream = s;

@@ -89,7 +89,10 @@ inline bool supported_head_dim(int hd) { return hd == 32 || hd == 64 || hd == 12
 
 struct DecodeBatch {
     int32_t batch = 0, max_pages = 0;
+    bool shared_pages = false;       // some page id is read by more than one sequence
     std::vector<int32_t> positions;  // host copy (launch geometry)
+    std::vector<uint32_t> page_mark; // per pool page: upload stamp (shared-page scan)
+    uint32_t stamp = 0;
     DeviceBuffer<int32_t> tables, pos;
 };
 
@@ -141,6 +144,8 @@ struct DecodeLaunch {
     int32_t kv_dim, batch, n_heads, kv_mul, head_dim, max_pages, num_pages;
     int32_t tiles_per_split, num_splits;
     int32_t waves;  // wavefronts per workgroup, 1..16, 64*waves >= head_dim
+    int32_t stream_kv;  // non-temporal K/V loads (lines read once per launch)
+    int32_t xcd_remap;  // keep the query heads of one KV head on one XCD
     float qscale;
 };
 // Rows per decode tile for a head_dim (the unit split-K partitions).

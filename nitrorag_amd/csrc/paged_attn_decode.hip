@@ -11,13 +11,13 @@
 //    loads are in flight and long contexts finish in few rounds).  A split is
 //    a run of `tiles_per_split` tiles of TILE consecutive context rows; waves
 //    take the split's tiles round-robin.
-//  - Lane layout: LPR = hd/16 lanes share one K/V row, each lane holding 16
-//    floats of it as four float4 (columns c*4 + j*4*LPR, j = 0..3), so each
-//    global_load_dwordx4 reads whole 4*LPR-float quarter-rows per lane group
-//    (128 B for hd=128).  A wave covers RPS = 64/LPR rows per load set and two
-//    load sets per tile (TILE = 2*RPS rows: one 16-token page for hd=128, two
-//    for hd=64).  All 16 K/V float4 loads of a tile are issued before use.
-//  - q.k: 16 FMAs per lane, then a DPP butterfly across the LPR lanes.
+//  - Lane layout: LG = 8 lanes share one K/V row (16 for hd=256) so that every
+//    global_load_dwordx4 reads whole 128-byte lines; a lane holds hd/LG floats
+//    of each of its RL rows (columns c*4 + j*4*LG).  The 64/LG row groups of a
+//    wave take interleaved rows of a TILE-row tile (64, 32, 16, 8 rows for
+//    hd = 32, 64, 128, 256); all 16 K/V float4 loads of a tile are issued
+//    before use.
+//  - q.k: hd/LG FMAs per lane and row, then a DPP butterfly across the LG lanes.
 //  - Softmax: every lane group keeps its own running (max, sum, acc) in base 2
 //    (q is pre-scaled by log2(e)/sqrt(hd)); groups, then waves (through LDS),
 //    then splits are merged with the usual rescaling.  No score scratch.
@@ -44,10 +44,16 @@ constexpr int MAX_THREADS = 64 * MAX_WAVES;
 
 template <int HD>
 struct DecodeGeom {
-    static constexpr int LPR = HD / 16;   // lanes per K/V row
-    static constexpr int RPS = 64 / LPR;  // rows per load set
-    static constexpr int SETS = 2;        // load sets per tile
-    static constexpr int TILE = RPS * SETS;
+    // LG lanes share a K/V row so that one load instruction reads whole
+    // 128-byte lines (8 lanes x 16 B; 16 lanes for hd=256, two lines).  Each
+    // lane holds NF4 float4 of a row (columns c*4 + j*4*LG) for RL rows per
+    // tile: RL*NF4 = 8 float4 of K and 8 of V in flight per lane.
+    static constexpr int LG = HD <= 128 ? 8 : 16;
+    static constexpr int NF4 = HD / (4 * LG);
+    static constexpr int RL = 8 / NF4;
+    static constexpr int GROUPS = 64 / LG;  // row groups per wave
+    static constexpr int TILE = RL * GROUPS;
+    static_assert(NF4 >= 1 && RL * NF4 == 8, "head_dim 32, 64, 128 or 256");
 };
 
 template <int CTRL>
@@ -55,13 +61,13 @@ __device__ __forceinline__ float dpp_mov(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
-// Sum over the LPR consecutive lanes of a group (result in every lane).
-template <int LPR>
+// Sum over the LG consecutive lanes of a group (result in every lane).
+template <int LG>
 __device__ __forceinline__ float group_sum(float x) {
-    if constexpr (LPR >= 2) x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
-    if constexpr (LPR >= 4) x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
-    if constexpr (LPR >= 8) x += dpp_mov<0x141>(x);  // row_half_mirror: other quad of the 8
-    if constexpr (LPR >= 16) x += dpp_mov<0x140>(x); // row_mirror: other 8 of the 16
+    if constexpr (LG >= 2) x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
+    if constexpr (LG >= 4) x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
+    if constexpr (LG >= 8) x += dpp_mov<0x141>(x);  // row_half_mirror: other quad of the 8
+    if constexpr (LG >= 16) x += dpp_mov<0x140>(x); // row_mirror: other 8 of the 16
     return x;
 }
 
@@ -73,14 +79,30 @@ __device__ __forceinline__ float dot4(float4 a, float4 b, float acc) {
     return acc;
 }
 
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// K/V row loads.  STREAM issues them non-temporal (global_load_dwordx4 ... nt):
+// lines read once per launch are not kept in L2 / MALL, which raises the
+// achievable streaming rate; plain loads keep lines that other workgroups read
+// again (pages shared between sequences, query heads of one KV group).
+template <bool STREAM>
+__device__ __forceinline__ float4 load_kv(const float* p) {
+    if constexpr (STREAM) {
+        const f4v v = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(p));
+        return make_float4(v.x, v.y, v.z, v.w);
+    } else {
+        return *reinterpret_cast<const float4*>(p);
+    }
+}
+
 __device__ __forceinline__ float scale_of(float m, float m_new) {
     return m == -INFINITY ? 0.0f : exp2f(m - m_new);
 }
 
-template <int HD>
+template <int HD, bool STREAM>
 __global__ __launch_bounds__(MAX_THREADS) void paged_attn_decode_kernel(DecodeLaunch a) {
     using G = DecodeGeom<HD>;
-    constexpr int LPR = G::LPR, RPS = G::RPS, TILE = G::TILE;
+    constexpr int LG = G::LG, NF4 = G::NF4, RL = G::RL, GROUPS = G::GROUPS, TILE = G::TILE;
     __shared__ int32_t s_pages[DECODE_MAX_SPLIT_PAGES];
     __shared__ float s_acc[MAX_WAVES][HD];
     __shared__ float s_m[MAX_WAVES], s_l[MAX_WAVES];
@@ -89,13 +111,28 @@ __global__ __launch_bounds__(MAX_THREADS) void paged_attn_decode_kernel(DecodeLa
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int g = lane / LPR;
-    const int c = lane % LPR;
+    const int g = lane / LG;
+    const int c = lane % LG;
 
-    const int split = blockIdx.x % a.num_splits;
-    const int bh = blockIdx.x / a.num_splits;
-    const int b = bh / a.n_heads;
-    const int h = bh - b * a.n_heads;
+    // Work order: ((b*Hkv + kv_h)*splits + split)*kv_mul + r, query head
+    // h = kv_h*kv_mul + r, so the query heads that read one K/V range are
+    // consecutive.  With xcd_remap, block ids are dealt to the 8 XCDs round-
+    // robin, so XCD x takes the x-th contiguous eighth of that order: a
+    // group's heads run together on one XCD and re-read K/V from its L2.
+    int w = blockIdx.x;
+    if (a.xcd_remap) {
+        const int n = gridDim.x, per = n >> 3, rem = n & 7;
+        const int x = w & 7;
+        w = x * per + min(x, rem) + (w >> 3);
+    }
+    const int r = w % a.kv_mul;
+    const int rest = w / a.kv_mul;
+    const int split = rest % a.num_splits;
+    const int grp = rest / a.num_splits;  // b*Hkv + kv_h
+    const int n_kv = a.n_heads / a.kv_mul;
+    const int b = grp / n_kv;
+    const int h = (grp - b * n_kv) * a.kv_mul + r;
+    const int bh = b * a.n_heads + h;
     const int ctx = a.positions[b] + 1;
     const int n_tiles = (ctx + TILE - 1) / TILE;
     const int tile_begin = split * a.tiles_per_split;
@@ -119,10 +156,10 @@ __global__ __launch_bounds__(MAX_THREADS) void paged_attn_decode_kernel(DecodeLa
 
     // q slice of this lane, pre-scaled to base-2 logits.
     const float* qp = a.q + (size_t)bh * HD;
-    float4 qv[4];
+    float4 qv[NF4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        float4 t = *reinterpret_cast<const float4*>(qp + (c + j * LPR) * 4);
+    for (int j = 0; j < NF4; j++) {
+        float4 t = *reinterpret_cast<const float4*>(qp + (c + j * LG) * 4);
         qv[j] = make_float4(t.x * a.qscale, t.y * a.qscale, t.z * a.qscale, t.w * a.qscale);
     }
     __syncthreads();
@@ -131,60 +168,60 @@ __global__ __launch_bounds__(MAX_THREADS) void paged_attn_decode_kernel(DecodeLa
     const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * HD;
 
     float m = -INFINITY, l = 0.0f;
-    float4 acc[4];
+    float4 acc[NF4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < NF4; j++) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
 
     for (int t = tile_begin + wave; t < tile_end; t += waves) {
-        float4 kr[G::SETS][4], vr[G::SETS][4];
-        bool valid[G::SETS];
+        float4 kr[RL][NF4], vr[RL][NF4];
+        bool valid[RL];
 #pragma unroll
-        for (int i = 0; i < G::SETS; i++) {
-            const int row = t * TILE + g + i * RPS;
+        for (int i = 0; i < RL; i++) {
+            const int row = t * TILE + g + i * GROUPS;
             int page = row < ctx ? s_pages[(row >> 4) - page_begin] : -1;
             valid[i] = page >= 0;
             if (valid[i]) {
                 const size_t off = (size_t)page * a.page_stride + (size_t)(row & 15) * a.kv_dim;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    kr[i][j] = *reinterpret_cast<const float4*>(kbase + off + (c + j * LPR) * 4);
-                    vr[i][j] = *reinterpret_cast<const float4*>(vbase + off + (c + j * LPR) * 4);
+                for (int j = 0; j < NF4; j++) {
+                    kr[i][j] = load_kv<STREAM>(kbase + off + (c + j * LG) * 4);
+                    vr[i][j] = load_kv<STREAM>(vbase + off + (c + j * LG) * 4);
                 }
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
+                for (int j = 0; j < NF4; j++) {
                     kr[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
                     vr[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
                 }
             }
         }
-        float s[G::SETS];
+        float s[RL];
 #pragma unroll
-        for (int i = 0; i < G::SETS; i++) {
+        for (int i = 0; i < RL; i++) {
             float d = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 4; j++) d = dot4(qv[j], kr[i][j], d);
-            d = group_sum<LPR>(d);
+            for (int j = 0; j < NF4; j++) d = dot4(qv[j], kr[i][j], d);
+            d = group_sum<LG>(d);
             s[i] = valid[i] ? d : -INFINITY;
         }
         float m_new = m;
 #pragma unroll
-        for (int i = 0; i < G::SETS; i++) m_new = fmaxf(m_new, s[i]);
+        for (int i = 0; i < RL; i++) m_new = fmaxf(m_new, s[i]);
         if (m_new == -INFINITY) continue;  // no valid row for this lane group yet
         const float alpha = scale_of(m, m_new);
-        float p[G::SETS];
+        float p[RL];
         float psum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < G::SETS; i++) {
+        for (int i = 0; i < RL; i++) {
             p[i] = valid[i] ? exp2f(s[i] - m_new) : 0.0f;
             psum += p[i];
         }
         l = l * alpha + psum;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < NF4; j++) {
             float4 r = make_float4(acc[j].x * alpha, acc[j].y * alpha, acc[j].z * alpha, acc[j].w * alpha);
 #pragma unroll
-            for (int i = 0; i < G::SETS; i++) {
+            for (int i = 0; i < RL; i++) {
                 r.x = fmaf(p[i], vr[i][j].x, r.x);
                 r.y = fmaf(p[i], vr[i][j].y, r.y);
                 r.z = fmaf(p[i], vr[i][j].z, r.z);
@@ -197,14 +234,14 @@ __global__ __launch_bounds__(MAX_THREADS) void paged_attn_decode_kernel(DecodeLa
 
     // Merge the lane groups of the wave (lanes with equal c, across g).
 #pragma unroll
-    for (int mask = LPR; mask < 64; mask <<= 1) {
+    for (int mask = LG; mask < 64; mask <<= 1) {
         const float mo = __shfl_xor(m, mask);
         const float lo = __shfl_xor(l, mask);
         const float mm = fmaxf(m, mo);
         const float f = scale_of(m, mm), fo = scale_of(mo, mm);
         l = l * f + lo * fo;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < NF4; j++) {
             float4 o;
             o.x = __shfl_xor(acc[j].x, mask);
             o.y = __shfl_xor(acc[j].y, mask);
@@ -217,8 +254,8 @@ __global__ __launch_bounds__(MAX_THREADS) void paged_attn_decode_kernel(DecodeLa
     }
     if (g == 0) {
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            *reinterpret_cast<float4*>(&s_acc[wave][(c + j * LPR) * 4]) = acc[j];
+        for (int j = 0; j < NF4; j++)
+            *reinterpret_cast<float4*>(&s_acc[wave][(c + j * LG) * 4]) = acc[j];
         if (c == 0) {
             s_m[wave] = m;
             s_l[wave] = l;
@@ -290,7 +327,10 @@ int decode_tile_rows(int head_dim) {
 template <int HD>
 static hipError_t launch_hd(const DecodeLaunch& a, hipStream_t stream) {
     const dim3 grid((unsigned)((size_t)a.batch * a.n_heads * a.num_splits));
-    hipLaunchKernelGGL(paged_attn_decode_kernel<HD>, grid, dim3(64 * a.waves), 0, stream, a);
+    if (a.stream_kv)
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HD, true>), grid, dim3(64 * a.waves), 0, stream, a);
+    else
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HD, false>), grid, dim3(64 * a.waves), 0, stream, a);
     if (a.num_splits > 1) {
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

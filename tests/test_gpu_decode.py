@@ -111,6 +111,21 @@ def test_decode_split_k_partitions_agree(tiles, waves, monkeypatch):
         assert np.array_equal(again, first)
 
 
+@pytest.mark.parametrize("name", ["gqa_32x8_hd128", "gqa_8x2_hd64", "batched_12x64_b32", "mha_hd32"])
+@pytest.mark.parametrize("stream,remap,tiles", [("0", "0", ""), ("1", "0", ""), ("0", "1", ""),
+                                                ("1", "1", ""), ("1", "1", "3"), ("0", "1", "2")])
+def test_decode_load_kind_and_work_order_agree(name, stream, remap, tiles, monkeypatch):
+    """Non-temporal or plain K/V loads, XCD-grouped or plain work order, with
+    and without split-K: every combination matches the oracle."""
+    say(f"decode {name} stream={stream} remap={remap} tiles={tiles}")
+    monkeypatch.setenv("NITRO_DECODE_STREAM", stream)
+    monkeypatch.setenv("NITRO_DECODE_XCD_REMAP", remap)
+    monkeypatch.setenv("NITRO_DECODE_SPLIT_TILES", tiles)
+    c = make_case(name, seed=3)
+    assert_parity(c.run_gpu(), c.run_oracle(), name)
+    assert c.pool.take_device_errors() == 0
+
+
 def test_decode_page_permutation_is_bit_identical():
     """Renaming physical pages consistently leaves the result bit-identical."""
     say("page permutation")
