@@ -229,20 +229,34 @@ int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, f
         const int tile = decode_tile_rows(head_dim);
         int max_tiles = 0;
         for (int p : d.positions) max_tiles = std::max(max_tiles, (p + 1 + tile - 1) / tile);
-        // Launch shape: ~16 resident waves per CU.  Give each (b, h) as many
-        // waves (4, 8 or 16, never more than it has tiles) as keep every
+        // Query heads per workgroup: the most (1, 2, 4, 8) that divides the
+        // group size kv_mul within the register budget, so K/V rows are
+        // loaded once for all of them.
+        const int kv_mul = n_heads / n_kv_heads;
+        int qh = env_int("NITRO_DECODE_HEADS_PER_WG", 0);
+        if (qh <= 0) {
+            qh = 1;
+            while (qh * 2 <= decode_max_heads_per_wg(head_dim) && kv_mul % (qh * 2) == 0) qh *= 2;
+        }
+        require(qh <= decode_max_heads_per_wg(head_dim) && kv_mul % qh == 0, ERR_INVALID_ARGUMENT,
+                "NITRO_DECODE_HEADS_PER_WG must divide n_heads/n_kv_heads and fit the head_dim");
+        // Launch shape: ~16 resident waves per CU (8 with several heads per
+        // workgroup, which take twice the registers).  Give each workgroup as
+        // many waves (4, 8 or 16, never more than it has tiles) as keep every
         // workgroup resident in one dispatch round, then split the context
         // (split-K, one extra merge launch) only if the GPU is still less than
         // half full.  Each split's block-table slice must fit in LDS.
-        const long long bh_count = (long long)d.batch * n_heads;
-        const long long target = (long long)kDecodeWavesPerCU * std::max(pool->num_cus, 1);
+        const long long bh_count = (long long)d.batch * (n_heads / qh);
+        const int max_waves = qh == 1 ? kDecodeMaxWaves : kDecodeMaxWaves / 2;
+        const long long target =
+            (long long)(qh == 1 ? kDecodeWavesPerCU : kDecodeWavesPerCU / 2) * std::max(pool->num_cus, 1);
         int waves = env_int("NITRO_DECODE_WAVES", 0);
         if (waves <= 0) {
             waves = kDecodeMinWaves;
-            while (waves < kDecodeMaxWaves && bh_count * waves * 2 <= target && waves < max_tiles)
+            while (waves < max_waves && bh_count * waves * 2 <= target && waves < max_tiles)
                 waves *= 2;
         }
-        waves = std::max(kDecodeMinWaves, std::min(waves, kDecodeMaxWaves));
+        waves = std::max(kDecodeMinWaves, std::min(waves, max_waves));
         int tps = env_int("NITRO_DECODE_SPLIT_TILES", 0);
         if (tps <= 0) {
             if (bh_count * waves >= target / 2 || max_tiles <= 2 * waves) {
@@ -274,7 +288,7 @@ int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, f
         a.kv_dim = pool->kv_dim;
         a.batch = d.batch;
         a.n_heads = n_heads;
-        a.kv_mul = n_heads / n_kv_heads;
+        a.kv_mul = kv_mul;
         a.head_dim = head_dim;
         a.max_pages = d.max_pages;
         a.num_pages = pool->num_pages;
@@ -282,11 +296,12 @@ int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, f
         a.num_splits = splits;
         a.waves = waves;
         // Non-temporal K/V loads when every K/V line is read once per launch:
-        // one query head per KV head and no page shared between sequences.
+        // one workgroup per KV head and no page shared between sequences.
         const int stream_env = env_int("NITRO_DECODE_STREAM", -1);
-        a.stream_kv = stream_env >= 0 ? stream_env != 0 : (a.kv_mul == 1 && !d.shared_pages);
+        a.heads_per_wg = qh;
+        a.stream_kv = stream_env >= 0 ? stream_env != 0 : (qh == kv_mul && !d.shared_pages);
         const int remap_env = env_int("NITRO_DECODE_XCD_REMAP", -1);
-        a.xcd_remap = remap_env >= 0 ? remap_env != 0 : a.kv_mul > 1;
+        a.xcd_remap = remap_env >= 0 ? remap_env != 0 : qh < kv_mul;
         a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
         hip_check(launch_paged_attn_decode(a, s), "paged_attn_decode launch");
         pool->last_stream = s;

@@ -145,11 +145,14 @@ struct DecodeLaunch {
     int32_t tiles_per_split, num_splits;
     int32_t waves;  // wavefronts per workgroup, 1..16, 64*waves >= head_dim
     int32_t stream_kv;  // non-temporal K/V loads (lines read once per launch)
-    int32_t xcd_remap;  // keep the query heads of one KV head on one XCD
+    int32_t xcd_remap;  // keep the workgroups that read one K/V range on one XCD
+    int32_t heads_per_wg;  // query heads of one KV head per workgroup (divides kv_mul)
     float qscale;
 };
 // Rows per decode tile for a head_dim (the unit split-K partitions).
 int decode_tile_rows(int head_dim);
+// Most query heads one decode workgroup serves for a head_dim (1, 2, 4 or 8).
+int decode_max_heads_per_wg(int head_dim);
 // Largest number of pages one split may cover (its block-table slice lives in LDS).
 constexpr int DECODE_MAX_SPLIT_PAGES = 1024;
 hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream);

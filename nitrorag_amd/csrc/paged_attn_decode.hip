@@ -99,13 +99,18 @@ __device__ __forceinline__ float scale_of(float m, float m_new) {
     return m == -INFINITY ? 0.0f : exp2f(m - m_new);
 }
 
-template <int HD, bool STREAM>
-__global__ __launch_bounds__(MAX_THREADS) void paged_attn_decode_kernel(DecodeLaunch a) {
+// QH query heads of one KV head per workgroup (QH = 1 for MHA): each K/V
+// row is loaded once and scored against all QH queries.  QH > 1 needs about
+// twice the registers, so those workgroups hold at most 8 waves.
+template <int HD, int QH, bool STREAM>
+__global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged_attn_decode_kernel(
+    DecodeLaunch a) {
     using G = DecodeGeom<HD>;
     constexpr int LG = G::LG, NF4 = G::NF4, RL = G::RL, GROUPS = G::GROUPS, TILE = G::TILE;
+    constexpr int MAXW = QH == 1 ? MAX_WAVES : MAX_WAVES / 2;
     __shared__ int32_t s_pages[DECODE_MAX_SPLIT_PAGES];
-    __shared__ float s_acc[MAX_WAVES][HD];
-    __shared__ float s_m[MAX_WAVES], s_l[MAX_WAVES];
+    __shared__ float s_acc[MAXW][QH][HD];
+    __shared__ float s_m[MAXW][QH], s_l[MAXW][QH];
     const int waves = blockDim.x >> 6;
     const int threads = blockDim.x;
 
@@ -114,32 +119,34 @@ __global__ __launch_bounds__(MAX_THREADS) void paged_attn_decode_kernel(DecodeLa
     const int g = lane / LG;
     const int c = lane % LG;
 
-    // Work order: ((b*Hkv + kv_h)*splits + split)*kv_mul + r, query head
-    // h = kv_h*kv_mul + r, so the query heads that read one K/V range are
-    // consecutive.  With xcd_remap, block ids are dealt to the 8 XCDs round-
-    // robin, so XCD x takes the x-th contiguous eighth of that order: a
-    // group's heads run together on one XCD and re-read K/V from its L2.
+    // Work order: ((b*Hkv + kv_h)*splits + split)*(kv_mul/QH) + r; the
+    // workgroup serves query heads h0 .. h0+QH-1, h0 = kv_h*kv_mul + r*QH, so
+    // the workgroups that read one K/V range are consecutive.  With
+    // xcd_remap, block ids are dealt to the 8 XCDs round-robin, so XCD x takes
+    // the x-th contiguous eighth of that order: workgroups sharing a K/V range
+    // run together on one XCD and re-read it from its L2.
     int w = blockIdx.x;
     if (a.xcd_remap) {
         const int n = gridDim.x, per = n >> 3, rem = n & 7;
         const int x = w & 7;
         w = x * per + min(x, rem) + (w >> 3);
     }
-    const int r = w % a.kv_mul;
-    const int rest = w / a.kv_mul;
+    const int hsubs = a.kv_mul / QH;
+    const int r = w % hsubs;
+    const int rest = w / hsubs;
     const int split = rest % a.num_splits;
     const int grp = rest / a.num_splits;  // b*Hkv + kv_h
     const int n_kv = a.n_heads / a.kv_mul;
     const int b = grp / n_kv;
-    const int h = (grp - b * n_kv) * a.kv_mul + r;
-    const int bh = b * a.n_heads + h;
+    const int kv_h = grp - b * n_kv;
+    const int bh0 = b * a.n_heads + kv_h * a.kv_mul + r * QH;
     const int ctx = a.positions[b] + 1;
+
     const int n_tiles = (ctx + TILE - 1) / TILE;
     const int tile_begin = split * a.tiles_per_split;
     if (tile_begin >= n_tiles) return;  // uniform for the workgroup
     const int tile_end = min(n_tiles, tile_begin + a.tiles_per_split);
     const int splits_b = (n_tiles + a.tiles_per_split - 1) / a.tiles_per_split;
-    const int kv_h = h / a.kv_mul;
 
     // Block-table slice of this split -> LDS (checked against the pool size).
     const int page_begin = (tile_begin * TILE) >> 4;
@@ -154,32 +161,42 @@ __global__ __launch_bounds__(MAX_THREADS) void paged_attn_decode_kernel(DecodeLa
         s_pages[i] = p;
     }
 
-    // q slice of this lane, pre-scaled to base-2 logits.
-    const float* qp = a.q + (size_t)bh * HD;
-    float4 qv[NF4];
+    // q slices of this lane, pre-scaled to base-2 logits.
+    float4 qv[QH][NF4];
 #pragma unroll
-    for (int j = 0; j < NF4; j++) {
-        float4 t = *reinterpret_cast<const float4*>(qp + (c + j * LG) * 4);
-        qv[j] = make_float4(t.x * a.qscale, t.y * a.qscale, t.z * a.qscale, t.w * a.qscale);
+    for (int qi = 0; qi < QH; qi++) {
+        const float* qp = a.q + (size_t)(bh0 + qi) * HD;
+#pragma unroll
+        for (int j = 0; j < NF4; j++) {
+            float4 t = *reinterpret_cast<const float4*>(qp + (c + j * LG) * 4);
+            qv[qi][j] = make_float4(t.x * a.qscale, t.y * a.qscale, t.z * a.qscale, t.w * a.qscale);
+        }
     }
     __syncthreads();
 
     const float* kbase = a.k_pool + a.layer_off + (size_t)kv_h * HD;
     const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * HD;
 
-    float m = -INFINITY, l = 0.0f;
-    float4 acc[NF4];
+    float m[QH], l[QH];
+    float4 acc[QH][NF4];
 #pragma unroll
-    for (int j = 0; j < NF4; j++) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int qi = 0; qi < QH; qi++) {
+        m[qi] = -INFINITY;
+        l[qi] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NF4; j++) acc[qi][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 
     for (int t = tile_begin + wave; t < tile_end; t += waves) {
         float4 kr[RL][NF4], vr[RL][NF4];
         bool valid[RL];
+        bool any = false;
 #pragma unroll
         for (int i = 0; i < RL; i++) {
             const int row = t * TILE + g + i * GROUPS;
             int page = row < ctx ? s_pages[(row >> 4) - page_begin] : -1;
             valid[i] = page >= 0;
+            any |= valid[i];
             if (valid[i]) {
                 const size_t off = (size_t)page * a.page_stride + (size_t)(row & 15) * a.kv_dim;
 #pragma unroll
@@ -195,96 +212,104 @@ __global__ __launch_bounds__(MAX_THREADS) void paged_attn_decode_kernel(DecodeLa
                 }
             }
         }
-        float s[RL];
+        // Rows are valid or not for the whole lane group (same rows), so this
+        // skip is uniform across the lanes that the DPP sums combine.
+        if (!any) continue;
 #pragma unroll
-        for (int i = 0; i < RL; i++) {
-            float d = 0.0f;
-#pragma unroll
-            for (int j = 0; j < NF4; j++) d = dot4(qv[j], kr[i][j], d);
-            d = group_sum<LG>(d);
-            s[i] = valid[i] ? d : -INFINITY;
-        }
-        float m_new = m;
-#pragma unroll
-        for (int i = 0; i < RL; i++) m_new = fmaxf(m_new, s[i]);
-        if (m_new == -INFINITY) continue;  // no valid row for this lane group yet
-        const float alpha = scale_of(m, m_new);
-        float p[RL];
-        float psum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < RL; i++) {
-            p[i] = valid[i] ? exp2f(s[i] - m_new) : 0.0f;
-            psum += p[i];
-        }
-        l = l * alpha + psum;
-#pragma unroll
-        for (int j = 0; j < NF4; j++) {
-            float4 r = make_float4(acc[j].x * alpha, acc[j].y * alpha, acc[j].z * alpha, acc[j].w * alpha);
+        for (int qi = 0; qi < QH; qi++) {
+            float s[RL];
 #pragma unroll
             for (int i = 0; i < RL; i++) {
-                r.x = fmaf(p[i], vr[i][j].x, r.x);
-                r.y = fmaf(p[i], vr[i][j].y, r.y);
-                r.z = fmaf(p[i], vr[i][j].z, r.z);
-                r.w = fmaf(p[i], vr[i][j].w, r.w);
+                float d = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NF4; j++) d = dot4(qv[qi][j], kr[i][j], d);
+                d = group_sum<LG>(d);
+                s[i] = valid[i] ? d : -INFINITY;
             }
-            acc[j] = r;
+            float m_new = m[qi];
+#pragma unroll
+            for (int i = 0; i < RL; i++) m_new = fmaxf(m_new, s[i]);
+            const float alpha = scale_of(m[qi], m_new);
+            float p[RL];
+            float psum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < RL; i++) {
+                p[i] = valid[i] ? exp2f(s[i] - m_new) : 0.0f;
+                psum += p[i];
+            }
+            l[qi] = l[qi] * alpha + psum;
+#pragma unroll
+            for (int j = 0; j < NF4; j++) {
+                float4 o = make_float4(acc[qi][j].x * alpha, acc[qi][j].y * alpha,
+                                       acc[qi][j].z * alpha, acc[qi][j].w * alpha);
+#pragma unroll
+                for (int i = 0; i < RL; i++) {
+                    o.x = fmaf(p[i], vr[i][j].x, o.x);
+                    o.y = fmaf(p[i], vr[i][j].y, o.y);
+                    o.z = fmaf(p[i], vr[i][j].z, o.z);
+                    o.w = fmaf(p[i], vr[i][j].w, o.w);
+                }
+                acc[qi][j] = o;
+            }
+            m[qi] = m_new;
         }
-        m = m_new;
     }
 
     // Merge the lane groups of the wave (lanes with equal c, across g).
 #pragma unroll
-    for (int mask = LG; mask < 64; mask <<= 1) {
-        const float mo = __shfl_xor(m, mask);
-        const float lo = __shfl_xor(l, mask);
-        const float mm = fmaxf(m, mo);
-        const float f = scale_of(m, mm), fo = scale_of(mo, mm);
-        l = l * f + lo * fo;
+    for (int qi = 0; qi < QH; qi++) {
 #pragma unroll
-        for (int j = 0; j < NF4; j++) {
-            float4 o;
-            o.x = __shfl_xor(acc[j].x, mask);
-            o.y = __shfl_xor(acc[j].y, mask);
-            o.z = __shfl_xor(acc[j].z, mask);
-            o.w = __shfl_xor(acc[j].w, mask);
-            acc[j] = make_float4(acc[j].x * f + o.x * fo, acc[j].y * f + o.y * fo,
-                                 acc[j].z * f + o.z * fo, acc[j].w * f + o.w * fo);
+        for (int mask = LG; mask < 64; mask <<= 1) {
+            const float mo = __shfl_xor(m[qi], mask);
+            const float lo = __shfl_xor(l[qi], mask);
+            const float mm = fmaxf(m[qi], mo);
+            const float f = scale_of(m[qi], mm), fo = scale_of(mo, mm);
+            l[qi] = l[qi] * f + lo * fo;
+#pragma unroll
+            for (int j = 0; j < NF4; j++) {
+                float4 o;
+                o.x = __shfl_xor(acc[qi][j].x, mask);
+                o.y = __shfl_xor(acc[qi][j].y, mask);
+                o.z = __shfl_xor(acc[qi][j].z, mask);
+                o.w = __shfl_xor(acc[qi][j].w, mask);
+                acc[qi][j] = make_float4(acc[qi][j].x * f + o.x * fo, acc[qi][j].y * f + o.y * fo,
+                                         acc[qi][j].z * f + o.z * fo, acc[qi][j].w * f + o.w * fo);
+            }
+            m[qi] = mm;
         }
-        m = mm;
-    }
-    if (g == 0) {
+        if (g == 0) {
 #pragma unroll
-        for (int j = 0; j < NF4; j++)
-            *reinterpret_cast<float4*>(&s_acc[wave][(c + j * LG) * 4]) = acc[j];
-        if (c == 0) {
-            s_m[wave] = m;
-            s_l[wave] = l;
+            for (int j = 0; j < NF4; j++)
+                *reinterpret_cast<float4*>(&s_acc[wave][qi][(c + j * LG) * 4]) = acc[qi][j];
+            if (c == 0) {
+                s_m[wave][qi] = m[qi];
+                s_l[wave][qi] = l[qi];
+            }
         }
     }
     __syncthreads();
 
-    // Merge the waves: thread d < HD owns output column d.
-    const int d = threadIdx.x;
-    float M = -INFINITY, L = 0.0f, A = 0.0f;
-    if (d < HD) {
-        for (int w = 0; w < waves; w++) M = fmaxf(M, s_m[w]);
-        for (int w = 0; w < waves; w++) {
-            const float f = scale_of(s_m[w], M);
-            L += s_l[w] * f;
-            A += s_acc[w][d] * f;
+    // Merge the waves: thread o owns output column o % HD of head o / HD.
+    for (int o = threadIdx.x; o < QH * HD; o += threads) {
+        const int qi = o / HD, d = o - qi * HD;
+        float M = -INFINITY, L = 0.0f, A = 0.0f;
+        for (int wv = 0; wv < waves; wv++) M = fmaxf(M, s_m[wv][qi]);
+        for (int wv = 0; wv < waves; wv++) {
+            const float f = scale_of(s_m[wv][qi], M);
+            L += s_l[wv][qi] * f;
+            A += s_acc[wv][qi][d] * f;
         }
-    }
-    float* out = a.out + (size_t)bh * HD;
-    if (splits_b == 1) {
-        if (d < HD) out[d] = A / L;
-        return;
-    }
-
-    float* part = a.partials + ((size_t)bh * a.num_splits + split) * (HD + 2);
-    if (d < HD) part[d] = A;
-    if (d == 0) {
-        part[HD] = M;
-        part[HD + 1] = L;
+        const int bh = bh0 + qi;
+        if (splits_b == 1) {
+            a.out[(size_t)bh * HD + d] = A / L;
+        } else {
+            float* part = a.partials + ((size_t)bh * a.num_splits + split) * (HD + 2);
+            part[d] = A;
+            if (d == 0) {
+                part[HD] = M;
+                part[HD + 1] = L;
+            }
+        }
     }
 }
 
@@ -314,6 +339,10 @@ __global__ __launch_bounds__(HD < 64 ? 64 : HD) void paged_attn_decode_merge_ker
 
 }  // namespace
 
+int decode_max_heads_per_wg(int head_dim) {
+    return head_dim <= 64 ? 8 : head_dim == 128 ? 4 : 2;  // QH * head_dim <= 512
+}
+
 int decode_tile_rows(int head_dim) {
     switch (head_dim) {
         case 32: return DecodeGeom<32>::TILE;
@@ -324,13 +353,34 @@ int decode_tile_rows(int head_dim) {
     }
 }
 
+template <int HD, int QH>
+static void launch_main(const DecodeLaunch& a, dim3 grid, hipStream_t stream) {
+    if (a.stream_kv)
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HD, QH, true>), grid, dim3(64 * a.waves), 0,
+                           stream, a);
+    else
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HD, QH, false>), grid, dim3(64 * a.waves), 0,
+                           stream, a);
+}
+
 template <int HD>
 static hipError_t launch_hd(const DecodeLaunch& a, hipStream_t stream) {
-    const dim3 grid((unsigned)((size_t)a.batch * a.n_heads * a.num_splits));
-    if (a.stream_kv)
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HD, true>), grid, dim3(64 * a.waves), 0, stream, a);
-    else
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HD, false>), grid, dim3(64 * a.waves), 0, stream, a);
+    if (a.heads_per_wg < 1 || a.kv_mul % a.heads_per_wg != 0 ||
+        a.heads_per_wg > decode_max_heads_per_wg(HD) ||
+        (a.heads_per_wg > 1 && a.waves > MAX_WAVES / 2))
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((size_t)a.batch * (a.n_heads / a.heads_per_wg) * a.num_splits));
+    switch (a.heads_per_wg) {
+        case 1: launch_main<HD, 1>(a, grid, stream); break;
+        case 2: launch_main<HD, 2>(a, grid, stream); break;
+        case 4:
+            if constexpr (4 * HD <= 512) launch_main<HD, 4>(a, grid, stream);
+            break;
+        case 8:
+            if constexpr (8 * HD <= 512) launch_main<HD, 8>(a, grid, stream);
+            break;
+        default: return hipErrorInvalidValue;
+    }
     if (a.num_splits > 1) {
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

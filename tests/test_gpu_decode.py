@@ -71,6 +71,10 @@ SHAPES = {
     "mha_hd256": ((3, 1, 300), 2, 2, 256, 64, 1, 0),
     "edges_hd128": ([1, 15, 16, 17, 32, 33, 4096], 4, 4, 128, 300, 1, 0),
     "edges_hd64": ([1, 2, 31, 32, 33, 63, 64, 65], 3, 3, 64, 40, 2, 1),
+    "gqa_16x2_hd64": ((6, 1, 400), 16, 2, 64, 160, 1, 0),
+    "gqa_8x1_hd32": ((4, 1, 900), 8, 1, 32, 240, 2, 1),
+    "gqa_4x2_hd256": ((3, 1, 300), 4, 2, 256, 64, 1, 0),
+    "gqa_24x4_hd128": ([5, 16, 17, 600], 24, 4, 128, 60, 1, 0),
 }
 
 
@@ -111,7 +115,8 @@ def test_decode_split_k_partitions_agree(tiles, waves, monkeypatch):
         assert np.array_equal(again, first)
 
 
-@pytest.mark.parametrize("name", ["gqa_32x8_hd128", "gqa_8x2_hd64", "batched_12x64_b32", "mha_hd32"])
+@pytest.mark.parametrize("name", ["gqa_32x8_hd128", "gqa_8x2_hd64", "batched_12x64_b32", "mha_hd32",
+                                  "gqa_16x2_hd64", "gqa_4x2_hd256"])
 @pytest.mark.parametrize("stream,remap,tiles", [("0", "0", ""), ("1", "0", ""), ("0", "1", ""),
                                                 ("1", "1", ""), ("1", "1", "3"), ("0", "1", "2")])
 def test_decode_load_kind_and_work_order_agree(name, stream, remap, tiles, monkeypatch):
@@ -124,6 +129,41 @@ def test_decode_load_kind_and_work_order_agree(name, stream, remap, tiles, monke
     c = make_case(name, seed=3)
     assert_parity(c.run_gpu(), c.run_oracle(), name)
     assert c.pool.take_device_errors() == 0
+
+
+HEADS_PER_WG = [("gqa_16x2_hd64", q) for q in (1, 2, 4, 8)] + \
+    [("gqa_8x1_hd32", q) for q in (1, 2, 4, 8)] + \
+    [("gqa_32x8_hd128", q) for q in (1, 2, 4)] + \
+    [("gqa_24x4_hd128", q) for q in (1, 2)] + \
+    [("gqa_4x2_hd256", q) for q in (1, 2)] + [("gqa_8x2_hd64", 4)]
+
+
+@pytest.mark.parametrize("name,qh", HEADS_PER_WG)
+@pytest.mark.parametrize("waves,tiles", [("", ""), ("8", "2"), ("4", "1")])
+def test_decode_heads_per_workgroup_agree(name, qh, waves, tiles, monkeypatch):
+    """One workgroup serving 1, 2, 4 or 8 query heads of a KV head (each K/V
+    row loaded once for all of them) matches the oracle, with split-K too."""
+    say(f"decode {name} heads_per_wg={qh} waves={waves} tiles={tiles}")
+    monkeypatch.setenv("NITRO_DECODE_HEADS_PER_WG", str(qh))
+    monkeypatch.setenv("NITRO_DECODE_WAVES", waves)
+    monkeypatch.setenv("NITRO_DECODE_SPLIT_TILES", tiles)
+    c = make_case(name, seed=5)
+    want = c.run_oracle()
+    first = c.run_gpu()
+    assert_parity(first, want, f"{name} qh={qh}")
+    assert np.array_equal(c.run_gpu(), first)
+    assert c.pool.take_device_errors() == 0
+
+
+def test_decode_heads_per_workgroup_rejects_bad_override(monkeypatch):
+    import nitrorag_amd as na
+
+    for name, qh in [("gqa_16x2_hd64", "3"), ("gqa_24x4_hd128", "4"), ("gqa_4x2_hd256", "4")]:
+        monkeypatch.setenv("NITRO_DECODE_HEADS_PER_WG", qh)  # not a divisor of 8 / 6; over the budget
+        c = make_case(name)
+        with pytest.raises(na.NitroError) as e:
+            c.run_gpu()
+        assert "NITRO_DECODE_HEADS_PER_WG" in str(e.value)
 
 
 def test_decode_page_permutation_is_bit_identical():
