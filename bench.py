@@ -358,7 +358,15 @@ WORKLOADS = ["decode-b64-ctx4096", "decode-single-110m", "decode-b32-mixed",
 
 def kernel_name(w) -> str:
     if w.bound == "hbm":
-        return f"paged_attn_decode_kernel<{w.hd}>"
+        # <head_dim, query heads per workgroup, non-temporal K/V loads>: the
+        # library streams K/V unless pages are shared or a KV head has several
+        # workgroups; every workload here is MHA (one query head per workgroup).
+        kv_mul = w.H // w.Hkv
+        qh = 1
+        while qh * 2 <= (8 if w.hd <= 64 else 4 if w.hd == 128 else 2) and kv_mul % (qh * 2) == 0:
+            qh *= 2
+        stream = qh == kv_mul and w.unique_pages is None
+        return f"paged_attn_decode_kernel<{w.hd}, {qh}, {str(stream).lower()}>"
     if w.hd == 256 or os.environ.get("NITRO_PREFILL_KERNEL") == "valu":
         return f"paged_attn_prefill_kernel<{w.hd}> (VALU)"
     return f"paged_attn_prefill_mfma_kernel<{w.hd}, 2> (MFMA fp32)"
