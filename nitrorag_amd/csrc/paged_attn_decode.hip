@@ -140,26 +140,22 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     const int b = grp / n_kv;
     const int kv_h = grp - b * n_kv;
     const int bh0 = b * a.n_heads + kv_h * a.kv_mul + r * QH;
-    const int ctx = a.positions[b] + 1;
-
-    const int n_tiles = (ctx + TILE - 1) / TILE;
+    // The position, q and this split's block-table slice are independent
+    // loads: issue them together.  The slice is read speculatively over the
+    // split's whole page range (clipped to the table row) and only the
+    // entries below the context length are validated and used.
+    constexpr int TBL_PER_THREAD = DECODE_MAX_SPLIT_PAGES / 256;  // >= 4 waves per workgroup
     const int tile_begin = split * a.tiles_per_split;
-    if (tile_begin >= n_tiles) return;  // uniform for the workgroup
-    const int tile_end = min(n_tiles, tile_begin + a.tiles_per_split);
-    const int splits_b = (n_tiles + a.tiles_per_split - 1) / a.tiles_per_split;
-
-    // Block-table slice of this split -> LDS (checked against the pool size).
     const int page_begin = (tile_begin * TILE) >> 4;
-    const int page_end = ((min(ctx, tile_end * TILE) - 1) >> 4) + 1;
+    const int spec_end = min(a.max_pages, ((tile_begin + a.tiles_per_split) * TILE + 15) >> 4);
     const int32_t* trow = a.tables + (size_t)b * a.max_pages;
-    for (int i = threadIdx.x; i < page_end - page_begin; i += threads) {
-        int p = trow[page_begin + i];
-        if ((unsigned)p >= (unsigned)a.num_pages) {
-            atomicAdd(a.bad_pages, 1);
-            p = -1;
-        }
-        s_pages[i] = p;
+    int tv[TBL_PER_THREAD];
+#pragma unroll
+    for (int k = 0; k < TBL_PER_THREAD; k++) {
+        const int i = threadIdx.x + k * threads;
+        tv[k] = i < spec_end - page_begin ? trow[page_begin + i] : -1;
     }
+    const int ctx = a.positions[b] + 1;
 
     // q slices of this lane, pre-scaled to base-2 logits.
     float4 qv[QH][NF4];
@@ -170,6 +166,26 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
         for (int j = 0; j < NF4; j++) {
             float4 t = *reinterpret_cast<const float4*>(qp + (c + j * LG) * 4);
             qv[qi][j] = make_float4(t.x * a.qscale, t.y * a.qscale, t.z * a.qscale, t.w * a.qscale);
+        }
+    }
+
+    const int n_tiles = (ctx + TILE - 1) / TILE;
+    if (tile_begin >= n_tiles) return;  // uniform for the workgroup
+    const int tile_end = min(n_tiles, tile_begin + a.tiles_per_split);
+    const int splits_b = (n_tiles + a.tiles_per_split - 1) / a.tiles_per_split;
+
+    // Used part of the slice -> LDS (page ids checked against the pool size).
+    const int page_end = ((min(ctx, tile_end * TILE) - 1) >> 4) + 1;
+#pragma unroll
+    for (int k = 0; k < TBL_PER_THREAD; k++) {
+        const int i = threadIdx.x + k * threads;
+        if (i < page_end - page_begin) {
+            int p = tv[k];
+            if ((unsigned)p >= (unsigned)a.num_pages) {
+                atomicAdd(a.bad_pages, 1);
+                p = -1;
+            }
+            s_pages[i] = p;
         }
     }
     __syncthreads();
@@ -391,7 +407,9 @@ static hipError_t launch_hd(const DecodeLaunch& a, hipStream_t stream) {
 }
 
 hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream) {
-    if (a.waves < 1 || a.waves > MAX_WAVES || 64 * a.waves < a.head_dim) return hipErrorInvalidValue;
+    // >= 4 waves: the block-table slice (<= DECODE_MAX_SPLIT_PAGES entries) is
+    // loaded at most 4 entries per thread.
+    if (a.waves < 4 || a.waves > MAX_WAVES || 64 * a.waves < a.head_dim) return hipErrorInvalidValue;
     switch (a.head_dim) {
         case 32: return launch_hd<32>(a, stream);
         case 64: return launch_hd<64>(a, stream);
