@@ -203,6 +203,30 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaun
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Max / sum over the four lanes l%16 + 16g (g = 0..3) of a wave, on gfx950's
+// row-swap permutes (VALU only; no LDS round trip).  permlane16_swap(x, x)
+// returns rows (0,0,2,2) and (1,1,3,3); permlane32_swap(y, y) returns halves
+// (lo,lo) and (hi,hi).
+__device__ __forceinline__ float max_over_rows(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float sum_over_rows(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+
+// The MFMA kernel's lazy rescaling threshold (log2 units): the running max
+// used as the exponent reference moves only when a block's max exceeds it by
+// more than this, so unnormalised weights stay <= 2^8.
+constexpr float kLazyRescaleLog2 = 8.0f;
+
 // Block-table entries a prefill workgroup keeps in LDS (32k tokens); pages
 // beyond that are read from the table in global memory.
 constexpr int TABLE_LDS = 2048;
@@ -250,6 +274,7 @@ __global__ __launch_bounds__(THREADS * KSPLIT) void paged_attn_prefill_mfma_kern
     const int last_pos = start + q0 + qcount - 1;
     const int my_pos = start + q0 + min(row, qcount - 1);
     const int wave_last = start + q0 + min(qs * 16 + 15, qcount - 1);
+    const int wave_first = start + q0 + min(qs * 16, qcount - 1);
     const int32_t* trow = a.tables + (size_t)seq * a.max_pages;
     const int n_tiles = last_pos / BNM + 1;
     const size_t dim = (size_t)a.n_heads * HD;
@@ -331,41 +356,61 @@ __global__ __launch_bounds__(THREADS * KSPLIT) void paged_attn_prefill_mfma_kern
                 st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk4.z, qv[4 * i + 2], st, 0, 0, 0);
                 st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk4.w, qv[4 * i + 3], st, 0, 0, 0);
             }
-            float s[4];
-            float bmax = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                s[r] = (key0 + 4 * g + r <= my_pos) ? st[r] : -INFINITY;
-                bmax = fmaxf(bmax, s[r]);
-            }
-            bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-            bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-            // m_new stays -inf for a query none of whose keys so far precede it
-            // (possible in key groups > 0); alpha and p are then 0.  No lane may
-            // skip the block: MFMA operands are shared across lanes.
-            const float m_new = fmaxf(m, bmax);
-            // arguments are <= 0: the raw v_exp_f32 (no denormal-range scaling) suffices
-            const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - m_new);
             float p[4];
+            if (key0 + 15 <= wave_first) {
+                // Every key of the block precedes every query of the wave: no
+                // mask, finite scores.  The reference point m moves (rescaling
+                // O and l) only when some row's block max exceeds it by more
+                // than kLazyRescaleLog2; otherwise p = 2^(s - m) <= 2^8 and O, l
+                // carry the same common factor, which the final O/l cancels.
+                const float bmax = max_over_rows(fmaxf(fmaxf(st[0], st[1]), fmaxf(st[2], st[3])));
+                if (__builtin_amdgcn_ballot_w64(bmax > m + kLazyRescaleLog2) != 0) {  // wave-uniform
+                    const float m_new = fmaxf(m, bmax);
+                    const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // m = -inf: 0
+                    lsum *= alpha;
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                p[r] = s[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[r] - m_new);
-            lsum = lsum * alpha + (p[0] + p[1]) + (p[2] + p[3]);
+                    for (int n = 0; n < NB; n++) acc[n] *= alpha;
+                    m = m_new;
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) p[r] = __builtin_amdgcn_exp2f(st[r] - m);
+            } else {
+                // Diagonal block: causal mask per element.  m_new stays -inf for a
+                // query none of whose keys so far precede it (possible in key
+                // groups > 0); alpha and p are then 0.  No lane may skip the
+                // block: MFMA operands are shared across lanes.
+                float sm[4];
+                float bmax = -INFINITY;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    sm[r] = (key0 + 4 * g + r <= my_pos) ? st[r] : -INFINITY;
+                    bmax = fmaxf(bmax, sm[r]);
+                }
+                bmax = max_over_rows(bmax);
+                const float m_new = fmaxf(m, bmax);
+                const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - m_new);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    p[r] = sm[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sm[r] - m_new);
+                lsum *= alpha;
+#pragma unroll
+                for (int n = 0; n < NB; n++) acc[n] *= alpha;
+                m = m_new;
+            }
+            lsum += (p[0] + p[1]) + (p[2] + p[3]);
 #pragma unroll
             for (int n = 0; n < NB; n++) {
-                f32x4 o = acc[n] * alpha;
+                f32x4 o = acc[n];
                 const float* vcol = &vs[(kb * 16 + 4 * g) * STRIDE + 16 * n + ql];
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++)
                     o = __builtin_amdgcn_mfma_f32_16x16x4f32(vcol[kk * STRIDE], p[kk], o, 0, 0, 0);
                 acc[n] = o;
             }
-            m = m_new;
         }
     }
 
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
+    lsum = sum_over_rows(lsum);
     if constexpr (KSPLIT > 1) {
         // Key groups 1.. hand (m, l, O) to key group 0 through LDS (the K tile area).
         __syncthreads();  // every wave is done with the K/V tiles

@@ -144,6 +144,45 @@ def test_prefill_batch_vs_oracle(name):
     assert_parity(got, want, name)
 
 
+@pytest.mark.parametrize("hd", [32, 64, 128])
+def test_prefill_rising_and_falling_scores(hd):
+    """Scores that climb by ~17 (log2 units) per 16-key block for four blocks,
+    climb by ~5 per block for twelve, or fall: the running max moves every
+    block, lags the true max by up to 2^8 in the weights, or never moves after
+    the first keys.  Ranges stay within ~70 log2 units (|q.k| ~ 500), where
+    fp32 summation order alone keeps any two implementations within the bar."""
+    say(f"prefill score profiles hd={hd}")
+    H = Hkv = 2
+    c = prefill_batch_case(7, 3, 250, 400, H, Hkv, hd, 1, 0, 0, 0)
+    rng = np.random.default_rng(70 + hd)
+    u = rng.standard_normal((Hkv, hd)).astype(np.float32)
+    u /= np.linalg.norm(u, axis=1, keepdims=True)
+    # q = a*u: q.k_t / sqrt(hd) * log2(e) = a * c_t * log2(e) / sqrt(hd)
+    a = 6.0 * np.sqrt(hd) / 8.0
+    per_log2 = a * np.log2(np.e) / np.sqrt(hd)  # log2 units per unit of c_t
+    off = 0
+    for b, n in enumerate(c["lens"]):
+        n = int(n)
+        t = np.arange(n, dtype=np.float64)
+        # log2-unit score of key t for an aligned query
+        s2 = [17.0 / 16 * np.minimum(t, 64), 5.0 / 16 * np.minimum(t, 200),
+              np.minimum(60.0, 3.0 / 16 * (n - t))][b]
+        ct = s2 / per_log2
+        for kh in range(Hkv):
+            cols = slice(kh * hd, (kh + 1) * hd)
+            noise = 0.05 * rng.standard_normal((n, hd))
+            c["kc"][off:off + n, cols] = (ct[:, None] * u[kh] + noise).astype(np.float32)
+        for h in range(H):
+            qn = 0.05 * rng.standard_normal((n, hd))
+            c["q"][off:off + n, h * hd:(h + 1) * hd] = (a * u[h // (H // Hkv)] + qn).astype(np.float32)
+        off += n
+    got, _, _ = run_prefill(c["k"], c["v"], 0, c["tables"], c["starts"], c["lens"], c["q"],
+                            c["kc"], c["vc"], H, Hkv, hd)
+    want, _, _ = oracle_prefill_batch(c)
+    assert np.isfinite(got).all()
+    assert_parity(got, want, f"score profiles hd={hd}")
+
+
 def test_prefill_errors():
     import torch
 
