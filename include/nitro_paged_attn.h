@@ -204,6 +204,25 @@ int nitro_rope_kv_append_prefill(nitro_kvpool* pool, int32_t layer, float* q, fl
                                  int32_t seq_len, int32_t n_heads, int32_t n_kv_heads,
                                  int32_t head_dim, void* stream);
 
+/* ------------------------- Q8_0 matrix product -----------------------------
+ * out[b][i] = sum_k w[i][k] * x[b][k], b < batch, i < d, k < n, with w in the
+ * reference's BlockQ8 layout (src/model_q8.cpp:28-32; scripts/quantize.py):
+ * row i is n/32 blocks of {float scale; int8 q[32]} (36 bytes), weight
+ * (i, 32j + t) = float(q_t) * scale_j.  x is fp32 [batch][n] (16-byte
+ * aligned), out fp32 [batch][d]; all device pointers.  n % 32 == 0.
+ *   NITRO_Q8_FULL_ROWS — matmul (src/model_q8.cpp:92-125), used by forward
+ *     and forward_paged;
+ *   NITRO_Q8_LAST_BLOCK — matmul_bulk (src/model_q8.cpp:382-420), used by
+ *     forward_prefill_chunk and forward_decode_batch: its block loop stores
+ *     each block's sum over the previous one, so only block n/32-1 of every
+ *     row reaches out.
+ * fp32 products and accumulation; the summation order differs from the
+ * reference's 8-lane AVX2 order (results agree to fp32 rounding). */
+#define NITRO_Q8_FULL_ROWS 0
+#define NITRO_Q8_LAST_BLOCK 1
+int nitro_q8_matmul(const void* w, const float* x, float* out, int32_t batch, int32_t n,
+                    int32_t d, int32_t semantics, void* stream);
+
 /* ------------------------------ checks ------------------------------------
  * Kernels re-check every page id they dereference against the pool size and
  * skip (and record) any outside it instead of faulting.  This reads and

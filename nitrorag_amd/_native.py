@@ -89,6 +89,7 @@ SIGNATURES = {
     "nitro_rope_kv_append": [_vp, _i32, _fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32, _vp],
     "nitro_rope_kv_append_prefill": [_vp, _i32, _fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32,
                                      _vp],
+    "nitro_q8_matmul": [_vp, _fp, _fp, _i32, _i32, _i32, _i32, _vp],
     "nitro_kvpool_take_device_errors": [_vp, _i32p],
 }
 _RESTYPES = {

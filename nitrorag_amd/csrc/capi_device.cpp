@@ -506,6 +506,22 @@ int nitro_rope_kv_append_prefill(nitro_kvpool* pool, int32_t layer, float* q, fl
     });
 }
 
+int nitro_q8_matmul(const void* w, const float* x, float* out, int32_t batch, int32_t n, int32_t d,
+                    int32_t semantics, void* stream) {
+    return guarded([&] {
+        require(w != nullptr && x != nullptr && out != nullptr, ERR_INVALID_ARGUMENT, "null pointer");
+        require(batch > 0 && n > 0 && d > 0, ERR_INVALID_ARGUMENT, "batch, n and d must be positive");
+        require(n % 32 == 0, ERR_INVALID_ARGUMENT, "n must be a multiple of 32 (Q8 block)");
+        require(semantics == NITRO_Q8_FULL_ROWS || semantics == NITRO_Q8_LAST_BLOCK, ERR_INVALID_ARGUMENT,
+                "semantics must be NITRO_Q8_FULL_ROWS or NITRO_Q8_LAST_BLOCK");
+        require(reinterpret_cast<uintptr_t>(w) % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0,
+                ERR_INVALID_ARGUMENT, "w must be 4-byte and x 16-byte aligned");
+        hip_check(launch_q8_matmul(w, x, out, batch, n, d, semantics == NITRO_Q8_LAST_BLOCK,
+                                   as_stream(stream)),
+                  "q8_matmul launch");
+    });
+}
+
 int nitro_kvpool_take_device_errors(nitro_kvpool* pool, int32_t* bad_pages) {
     return guarded([&] {
         require_pool(pool);

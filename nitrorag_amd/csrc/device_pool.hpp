@@ -162,6 +162,10 @@ hipError_t launch_kv_append_decode(float* k_pool, float* v_pool, const float* k,
                                    int max_pages, int kv_dim, int64_t page_stride,
                                    int64_t layer_off, int num_pages, int32_t* bad_pages,
                                    hipStream_t stream);
+// Q8_0 matrix product (rows of BlockQ8, fp32 activations); last_block_only
+// selects the reference's matmul_bulk semantics.
+hipError_t launch_q8_matmul(const void* w, const float* x, float* out, int batch, int n, int d,
+                            bool last_block_only, hipStream_t stream);
 hipError_t launch_rope_kv_append(float* k_pool, float* v_pool, float* q, float* k, const float* v,
                                  const float* freq_real, const float* freq_imag,
                                  const int32_t* tables, const int32_t* positions,

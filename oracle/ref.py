@@ -35,6 +35,10 @@ def lib() -> ctypes.CDLL:
         L.ref_hash_block_state.argtypes = [u64, _i32p, ci]
         L.ref_hash_block_state.restype = u64
         L.ref_set_threads.argtypes = [ci]
+        L.ref_q8_matmul.argtypes = [_f32p, _f32p, vp, ci, ci]
+        L.ref_q8_matmul.restype = None
+        L.ref_q8_matmul_bulk.argtypes = [_f32p, _f32p, vp, ci, ci, ci]
+        L.ref_q8_matmul_bulk.restype = None
         L.ref_world_create.argtypes = [ci, ci, ci, ci, ci, ci, ci, ci, ci, u64]
         L.ref_world_create.restype = vp
         L.ref_world_destroy.argtypes = [vp]
@@ -54,6 +58,27 @@ def lib() -> ctypes.CDLL:
         L.ref_block_table.argtypes = [vp, ci, _i32p, ci]
         _lib = L
     return _lib
+
+
+def q8_matmul(w: np.ndarray, x: np.ndarray, n: int, d: int) -> np.ndarray:
+    """The reference's matmul (BlockQ8) on one activation row x[n] -> [d]."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(d, np.float32)
+    lib().ref_q8_matmul(out.ctypes.data_as(_f32p), x.ctypes.data_as(_f32p),
+                        w.ctypes.data_as(ctypes.c_void_p), n, d)
+    return out
+
+
+def q8_matmul_bulk(w: np.ndarray, x: np.ndarray, n: int, d: int) -> np.ndarray:
+    """The reference's matmul_bulk (BlockQ8) on x[batch][n] -> [batch][d]."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    batch = x.shape[0]
+    out = np.zeros((batch, d), np.float32)
+    lib().ref_q8_matmul_bulk(out.ctypes.data_as(_f32p), x.ctypes.data_as(_f32p),
+                             w.ctypes.data_as(ctypes.c_void_p), batch, n, d)
+    return out
 
 
 def hash_block_state(parent: int, tokens) -> int:

@@ -104,6 +104,15 @@ uint64_t ref_hash_block_state(uint64_t parent, const int* tokens, int n) {
 
 void ref_set_threads(int n) { omp_set_num_threads(n); }
 
+// The reference's Q8 products called as units (src/model_q8.cpp:92-125,
+// :382-420); w is packed BlockQ8 rows.
+void ref_q8_matmul(float* out, const float* x, const void* w, int n, int d) {
+    matmul(out, const_cast<float*>(x), (BlockQ8*)const_cast<void*>(w), n, d);
+}
+void ref_q8_matmul_bulk(float* out, const float* x, const void* w, int batch, int n, int d) {
+    matmul_bulk(out, const_cast<float*>(x), (BlockQ8*)const_cast<void*>(w), batch, n, d);
+}
+
 // A tiny Llama-shaped model around a KVBlock_Manager/PrefixCacheManager pair.
 // dim and kv_dim must be multiples of 32 (Q8 blocks); RoPE tables are the
 // identity rotation so K/V rows in the pool are exactly the computed k/v.

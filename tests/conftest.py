@@ -39,3 +39,13 @@ def golden_traces():
 def golden_fnv():
     with open(os.path.join(GOLDEN, "fnv.json")) as f:
         return json.load(f)
+
+
+@pytest.fixture(scope="session")
+def golden_q8():
+    with open(os.path.join(GOLDEN, "q8_matmul.json")) as f:
+        meta = json.load(f)
+    arrays = np.load(os.path.join(GOLDEN, "q8_matmul.npz"))
+    return {name: (m, {k.split("/", 1)[1]: arrays[k] for k in arrays.files
+                       if k.startswith(name + "/")})
+            for name, m in meta.items()}

@@ -21,6 +21,9 @@ Writes, next to this script:
                              rows written by the call, the block tables and the
                              observed outputs.  Pool digests are over the observed
                              layer only.
+  q8_matmul.json + q8_matmul.npz
+                             the reference's matmul and matmul_bulk (BlockQ8) on
+                             packed Q8 matrices and fp32 activations
 """
 from __future__ import annotations
 
@@ -39,7 +42,7 @@ sys.path.insert(0, HERE)
 
 from oracle import paged_memory as pm  # noqa: E402
 from oracle import ref  # noqa: E402
-from synth import counter_pool, rope_tables  # noqa: E402
+from synth import counter_pool, counter_uniform, rope_tables  # noqa: E402
 
 
 def state_digest(snap: dict) -> str:
@@ -446,6 +449,43 @@ def make_attention():
     return rec
 
 
+Q8_CASES = [
+    # name, n, d, batch, seed
+    ("q8_n64_d48_b3", 64, 48, 3, 91),
+    ("q8_n96_d40_b2", 96, 40, 2, 92),      # odd number of blocks per row
+    ("q8_n32_d16_b4", 32, 16, 4, 93),      # one block per row
+    ("q8_n256_d96_b5", 256, 96, 5, 94),
+    ("q8_n128_d33_b1", 128, 33, 1, 95),    # rows not a multiple of 16
+]
+
+
+def make_q8():
+    """Q8 products (src/model_q8.cpp:92-125 matmul, :382-420 matmul_bulk) of the
+    reference build on matrices quantised with oracle.model.quantize_q8 (a
+    restatement of scripts/quantize.py).  Row 0 holds an all-zero block (scale
+    1e-9) and a block with one large outlier."""
+    from oracle import model as om
+
+    arrays, meta = {}, {}
+    for name, n, d, batch, seed in Q8_CASES:
+        W = counter_uniform(seed, d * n).reshape(d, n) * np.float32(0.05)
+        W[0, :32] = 0.0
+        if n >= 64:
+            W[0, 32:64] *= np.float32(0.01)
+            W[0, 40] = np.float32(3.0)
+        scale, q = om.quantize_q8(W)
+        w = om.pack_q8(scale, q)
+        x = counter_uniform(seed + 1000, batch * n).reshape(batch, n)
+        full = np.stack([ref.q8_matmul(w, x[b], n, d) for b in range(batch)])
+        bulk = ref.q8_matmul_bulk(w, x, n, d)
+        arrays[f"{name}/w"] = w
+        arrays[f"{name}/x"] = x
+        arrays[f"{name}/full"] = full
+        arrays[f"{name}/bulk"] = bulk
+        meta[name] = dict(n=n, d=d, batch=batch)
+    return meta, arrays
+
+
 def main():
     if not ref.available():
         sys.exit("oracle/_ref/libnitro_ref.so is missing: run `make -C oracle ref` first")
@@ -457,7 +497,12 @@ def main():
     with open(os.path.join(HERE, "attention.json"), "w") as f:
         json.dump(rec.meta, f, indent=1)
     np.savez_compressed(os.path.join(HERE, "attention.npz"), **rec.arrays)
-    for fn in ("fnv.json", "block_manager_traces.json", "attention.json", "attention.npz"):
+    q8_meta, q8_arrays = make_q8()
+    with open(os.path.join(HERE, "q8_matmul.json"), "w") as f:
+        json.dump(q8_meta, f, indent=1)
+    np.savez_compressed(os.path.join(HERE, "q8_matmul.npz"), **q8_arrays)
+    for fn in ("fnv.json", "block_manager_traces.json", "attention.json", "attention.npz",
+               "q8_matmul.json", "q8_matmul.npz"):
         print(fn, os.path.getsize(os.path.join(HERE, fn)))
 
 
