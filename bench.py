@@ -22,7 +22,7 @@ Reported:
 Algorithmic bytes per decode launch: sum_b ctx_b*Hkv*hd*4*2 (K and V) +
 B*H*hd*4*2 (q in, out) + sum_b ceil(ctx_b/16)*4 (block-table entries).
 
-Other workloads (parity-test shapes, measured for the design notes):
+Other workloads (survey configs and the next rows, measured for the design notes):
   decode-single-110m     1 sequence, 12 layers x 12 heads x 64, ctx 256, 64-page pool;
                          a step is one token through all 12 layers' append + attention
   decode-b32-mixed       B=32, 12x64, ctx ~ U[16,1024], 4096-page pool (12 layers, one timed)
@@ -30,6 +30,8 @@ Other workloads (parity-test shapes, measured for the design notes):
                          hits) + private suffixes ~ U[64,512]
   prefill-b8-12x64       B=8 prompts, lengths ~ U[128,1024], 12x64, KV scattered into
                          fresh pages then attended causally; FLOPs = sum 2*H*hd*L(L+1)
+  q8-gemv-7b-ffn         Q8_0 product, W 11008 x 4096 BlockQ8, 1 activation row
+  q8-matmul-110m-b32     Q8_0 product, W 2048 x 768 BlockQ8, 32 activation rows
 The three small decode workloads fit in the 256 MB Infinity Cache, so a 1 GiB
 buffer is read before every timed launch and only the launch itself is timed
 (events).
@@ -294,6 +296,88 @@ class PrefillWorkload:
         return {}
 
 
+class Q8Workload:
+    """One Q8_0 matrix product, out[B][d] = x[B][n] . W[d][n]^T with W in the
+    reference's BlockQ8 layout (36 bytes per 32 weights).  Algorithmic bytes
+    per launch: d*(n/32)*36 (weights) + B*n*4 (x) + B*d*4 (out)."""
+
+    bound = "hbm"
+    flush = True
+
+    def __init__(self, name, n, d, B, seed, describe):
+        self.name, self.n, self.d, self.B, self.seed, self.describe = name, n, d, B, seed, describe
+
+    def setup(self, dev, g):
+        import torch
+
+        nb = self.n // 32
+        q = torch.randint(-127, 128, (self.d, nb, 32), device=dev, generator=g, dtype=torch.int32)
+        scale = torch.rand((self.d, nb, 1), device=dev, generator=g) * 0.01 + 0.005
+        self.w = torch.cat([scale.view(torch.uint8), q.to(torch.int8).view(torch.uint8)],
+                           dim=2).contiguous().view(-1)
+        self.x = torch.randn((self.B, self.n), device=dev, generator=g)
+        self.out = torch.empty((self.B, self.d), device=dev)
+        self.scratch = torch.ones(2**28, device=dev)  # 1 GiB read evicts L2 and MALL
+        self.flush_out = torch.empty((), device=dev)
+
+    def step(self, stream, events=None):
+        import torch
+
+        import nitrorag_amd as na
+
+        torch.sum(self.scratch, dim=0, out=self.flush_out)
+        if events is not None:
+            events[0][0].record(stream)
+        na.q8_matmul(self.w, self.x, self.out, 0, stream)
+        if events is not None:
+            events[0][1].record(stream)
+
+    def launches_per_step(self):
+        return 1
+
+    def work_per_launch(self):
+        return self.d * (self.n // 32) * 36 + self.B * self.n * 4 + self.B * self.d * 4
+
+    def tokens_per_step(self):
+        return self.B
+
+    def kernel(self):
+        return ("q8_gemv_kernel (VALU)" if self.B <= 4 else "q8_matmul_kernel (MFMA fp32)")
+
+    def config(self):
+        return {"workload": self.describe, "batch": self.B, "n": self.n, "d": self.d,
+                "parallelism": "single GPU"}
+
+    def check(self):
+        import torch
+
+        assert torch.isfinite(self.out).all().item(), "non-finite Q8 product"
+
+    def device_errors(self):
+        return 0
+
+    def cpu_baseline(self, seconds, sample):
+        """The oracle's AVX2 restatement of the reference's matmul on all host cores."""
+        from oracle import attn
+        from oracle import model as om
+
+        w = self.w.cpu().numpy()
+        x = self.x.cpu().numpy()
+        threads = attn.max_threads()
+        rows = min(sample, self.B)
+        per_rep, reps, el = time_cpu(lambda: om.q8_matmul(w, x[:rows], self.n, self.d, threads),
+                                     seconds)
+        nbytes = self.d * (self.n // 32) * 36 * rows + rows * (self.n + self.d) * 4
+        return {"value": round(nbytes / per_rep / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "kind": "port",
+                "sample": (f"{rows} of the {self.B} activation rows of this workload, one matmul "
+                           f"(src/model_q8.cpp:92-125) per row over the full matrix, {reps} reps "
+                           f"in {el:.1f} s")}
+
+    def extra(self, kernel_s):
+        return {}
+
+
 def prefix_shared_workload(seed):
     """48 sequences: 512 shared prefix tokens (32 pages via FNV-1a prefix-cache hits),
     private suffixes ~ U[64,512], then one decode token each."""
@@ -349,14 +433,26 @@ def make_workload(name, seed):
         return PrefillWorkload(name, 8, 12, 12, 64, rng.integers(128, 1025, size=8), seed,
                                describe=("causal prefill, B=8 prompts, lengths ~ U[128,1024], "
                                          "12 heads x 64, fresh 16-token pages (LIFO ids)"))
+    if name == "q8-gemv-7b-ffn":
+        return Q8Workload(name, 4096, 11008, 1, seed,
+                          describe=("Q8_0 matrix-vector product at the Llama-2-7B FFN up "
+                                    "projection, W 11008 x 4096 (50.7 MB BlockQ8), one activation "
+                                    "row, Infinity Cache flushed per launch"))
+    if name == "q8-matmul-110m-b32":
+        return Q8Workload(name, 768, 2048, 32, seed,
+                          describe=("Q8_0 matrix product at the Llama-2-110M FFN up projection, "
+                                    "W 2048 x 768 (1.77 MB BlockQ8), 32 activation rows, "
+                                    "Infinity Cache flushed per launch"))
     raise ValueError(name)
 
 
 WORKLOADS = ["decode-b64-ctx4096", "decode-single-110m", "decode-b32-mixed",
-             "decode-prefix-shared", "prefill-b8-12x64"]
+             "decode-prefix-shared", "prefill-b8-12x64", "q8-gemv-7b-ffn", "q8-matmul-110m-b32"]
 
 
 def kernel_name(w) -> str:
+    if hasattr(w, "kernel"):
+        return w.kernel()
     if w.bound == "hbm":
         # <head_dim, query heads per workgroup, non-temporal K/V loads>: the
         # library streams K/V unless pages are shared or a KV head has several
@@ -430,7 +526,7 @@ def main():
     launch_ms = [a.elapsed_time(b) for ev in events for a, b in ev]
     kernel_ms = float(np.mean(launch_ms))
     w.check()
-    assert w.pool.take_device_errors() == 0
+    assert (w.device_errors() if hasattr(w, "device_errors") else w.pool.take_device_errors()) == 0
 
     work = w.work_per_launch()
     if w.flush:
@@ -459,8 +555,9 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": w.describe, "batch": w.B, "n_heads": w.H, "n_kv_heads": w.Hkv,
-                   "head_dim": w.hd, "pool_pages": w.pages, "parallelism": "single GPU"},
+        "config": (w.config() if hasattr(w, "config") else
+                   {"workload": w.describe, "batch": w.B, "n_heads": w.H, "n_kv_heads": w.Hkv,
+                    "head_dim": w.hd, "pool_pages": w.pages, "parallelism": "single GPU"}),
         "tokens_per_s": round(w.tokens_per_step() / (ms_per_step * 1e-3), 1),
         "roofline": {
             "bound": w.bound,
