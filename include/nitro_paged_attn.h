@@ -223,6 +223,45 @@ int nitro_rope_kv_append_prefill(nitro_kvpool* pool, int32_t layer, float* q, fl
 int nitro_q8_matmul(const void* w, const float* x, float* out, int32_t batch, int32_t n,
                     int32_t d, int32_t semantics, void* stream);
 
+/* ------------------------ transformer step (model) -------------------------
+ * The forward passes of src/model_q8.cpp around the attention path, on the
+ * device: embedding, per layer rms_norm -> wq/wk/wv (Q8) -> RoPE + KV append
+ * -> paged attention -> wo -> residual -> rms_norm -> w1, w3 -> SwiGLU -> w2
+ * -> residual, then the final rms_norm and the fp32 classifier (wcls = the
+ * embedding table, src/Server_Inference.cpp:69).
+ *
+ * nitro_model_create takes the reference's model file as bytes
+ * (src/Server_Inference.cpp:45-69, written by scripts/quantize.py): a header
+ * of 7 int32 {dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size,
+ * seq_len}, then token_embedding_table f32, rms_att f32, wq wk wv wo Q8,
+ * rms_ffn f32, w1 w2 w3 Q8, rms_final f32, freq_cis_real, freq_cis_imag f32.
+ * The weights are copied to the device; the caller may free the blob.  The
+ * pool used with a model must have n_layers layers and kv_dim =
+ * n_kv_heads * dim / n_heads.
+ *
+ * semantics selects the Q8 product (NITRO_Q8_*): forward_decode_batch and
+ * forward_prefill_chunk compute their Q8 products with matmul_bulk
+ * (NITRO_Q8_LAST_BLOCK reproduces them), forward_paged with matmul
+ * (NITRO_Q8_FULL_ROWS).  The classifier is fp32 in both. */
+typedef struct nitro_model nitro_model;
+int nitro_model_create(const void* blob, uint64_t bytes, nitro_model** out);
+int nitro_model_destroy(nitro_model* model);
+/* config[7] = the header fields, in file order. */
+int nitro_model_config(const nitro_model* model, int32_t* config);
+/* forward_decode_batch (src/model_q8.cpp:571-694), forward_paged (:244-368)
+ * with batch = 1: tokens[batch] (host), one per sequence of the uploaded
+ * decode batch (nitro_decode_batch_upload, positions = the slots written
+ * now; the caller has already run the host bookkeeping of
+ * Sequence::allocate_next_token).  Writes logits[batch][vocab_size] (device). */
+int nitro_forward_decode_batch(nitro_model* model, nitro_kvpool* pool, const int32_t* tokens,
+                               int32_t batch, float* logits, int32_t semantics, void* stream);
+/* forward_prefill_chunk (src/model_q8.cpp:424-557) for every chunk of the
+ * uploaded prefill batch: tokens[total_rows] (host, chunks packed in batch
+ * order).  Writes logits[chunks][vocab_size] (device) for the last token of
+ * each chunk. */
+int nitro_forward_prefill(nitro_model* model, nitro_kvpool* pool, const int32_t* tokens,
+                          int32_t total_rows, float* logits, int32_t semantics, void* stream);
+
 /* ------------------------------ checks ------------------------------------
  * Kernels re-check every page id they dereference against the pool size and
  * skip (and record) any outside it instead of faulting.  This reads and

@@ -90,6 +90,11 @@ SIGNATURES = {
     "nitro_rope_kv_append_prefill": [_vp, _i32, _fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32,
                                      _vp],
     "nitro_q8_matmul": [_vp, _fp, _fp, _i32, _i32, _i32, _i32, _vp],
+    "nitro_model_create": [_vp, ctypes.c_uint64, ctypes.POINTER(_vp)],
+    "nitro_model_destroy": [_vp],
+    "nitro_model_config": [_vp, _i32p],
+    "nitro_forward_decode_batch": [_vp, _vp, _i32p, _i32, _fp, _i32, _vp],
+    "nitro_forward_prefill": [_vp, _vp, _i32p, _i32, _fp, _i32, _vp],
     "nitro_kvpool_take_device_errors": [_vp, _i32p],
 }
 _RESTYPES = {

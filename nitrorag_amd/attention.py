@@ -128,6 +128,7 @@ class KVPool:
                s.ctypes.data_as(N._i32p), n.ctypes.data_as(N._i32p), s.size, t.shape[1],
                _stream_ptr(stream))
         self.prefill_rows = int(n.sum())
+        self.prefill_chunks = int(n.size)
 
     def kv_append_prefill(self, layer: int, k, v, stream=None) -> None:
         self._need(k, self.prefill_rows * self.kv_dim, "k")

@@ -24,8 +24,9 @@ LIB = os.path.join(HERE, "libnitro_paged_attn.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("NITRO_OFFLOAD_ARCH", "gfx950")
-DEVICE_SOURCES = ["paged_attn_decode.hip", "paged_attn_prefill.hip", "kv_append.hip", "q8_matmul.hip"]
-HIP_HOST_SOURCES = ["capi_device.cpp"]
+DEVICE_SOURCES = ["paged_attn_decode.hip", "paged_attn_prefill.hip", "kv_append.hip", "q8_matmul.hip",
+                  "model_kernels.hip"]
+HIP_HOST_SOURCES = ["capi_device.cpp", "model.cpp"]
 HOST_SOURCES = ["paged_memory.cpp", "capi_host.cpp"]
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"-I{INCLUDE}", f"-I{CSRC}", "-Wall"]

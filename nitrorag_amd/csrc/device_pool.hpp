@@ -166,6 +166,17 @@ hipError_t launch_kv_append_decode(float* k_pool, float* v_pool, const float* k,
 // selects the reference's matmul_bulk semantics.
 hipError_t launch_q8_matmul(const void* w, const float* x, float* out, int batch, int n, int d,
                             bool last_block_only, hipStream_t stream);
+// Row-wise model kernels and the fp32 classifier product (model_kernels.hip).
+hipError_t launch_embed_rows(const float* table, const int32_t* tokens, float* x, int rows, int dim,
+                             int vocab, int32_t* bad_tokens, hipStream_t stream);
+hipError_t launch_add_rmsnorm(float* x, const float* delta, const float* weight, float* out, int rows,
+                              int dim, hipStream_t stream);
+hipError_t launch_gather_last_rows(const float* x, const float* ffn, const int32_t* row_off,
+                                  const int32_t* len, float* last, int chunks, int dim,
+                                  hipStream_t stream);
+hipError_t launch_swiglu(float* hb, const float* hb2, size_t n, hipStream_t stream);
+hipError_t launch_f32_matmul(const float* w, const float* x, float* out, int batch, int n, int d,
+                             hipStream_t stream);
 hipError_t launch_rope_kv_append(float* k_pool, float* v_pool, float* q, float* k, const float* v,
                                  const float* freq_real, const float* freq_imag,
                                  const int32_t* tables, const int32_t* positions,

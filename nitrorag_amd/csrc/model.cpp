@@ -1,0 +1,257 @@
+// The transformer step around the attention path: device weights in the
+// reference's on-disk layout and the forward passes of src/model_q8.cpp
+// (forward_decode_batch :571-694, forward_prefill_chunk :424-557,
+// forward_paged :244-368) composed from this library's kernels.  Declared in
+// include/nitro_paged_attn.h.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "capi_common.hpp"
+#include "device_pool.hpp"
+#include "nitro_paged_attn.h"
+
+using namespace nitro;
+
+struct nitro_model {
+    int32_t dim = 0, hidden = 0, n_layers = 0, n_heads = 0, n_kv_heads = 0, vocab = 0, seq_len = 0;
+    int32_t head_size = 0, kv_dim = 0;
+    uint8_t* weights = nullptr;  // the file's sections after the 28-byte header
+    size_t weight_bytes = 0;
+    // section offsets (bytes) within `weights`, src/Server_Inference.cpp:52-69
+    size_t o_emb = 0, o_rms_att = 0, o_wq = 0, o_wk = 0, o_wv = 0, o_wo = 0, o_rms_ffn = 0;
+    size_t o_w1 = 0, o_w2 = 0, o_w3 = 0, o_rms_final = 0, o_freq_real = 0, o_freq_imag = 0;
+    DeviceBuffer<float> x, xb, attn, proj, ffn, q, k, v, hb, hb2, last;
+    DeviceBuffer<int32_t> tokens;
+    Staging staging;
+
+    const float* f32(size_t off) const { return reinterpret_cast<const float*>(weights + off); }
+    const uint8_t* q8(size_t off, int layer, size_t rows, size_t cols) const {
+        return weights + off + (size_t)layer * rows * (cols / 32) * 36;
+    }
+};
+
+namespace {
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+void q8(const nitro_model* m, size_t off, int layer, int d, int n, const float* in, float* out,
+        int rows, int semantics, hipStream_t s) {
+    hip_check(launch_q8_matmul(m->q8(off, layer, d, n), in, out, rows, n, d,
+                               semantics == NITRO_Q8_LAST_BLOCK, s),
+              "q8_matmul launch");
+}
+
+void reserve_rows(nitro_model* m, int rows) {
+    const size_t r = (size_t)rows;
+    m->x.reserve(r * m->dim);
+    m->xb.reserve(r * m->dim);
+    m->attn.reserve(r * m->dim);
+    m->proj.reserve(r * m->dim);
+    m->ffn.reserve(r * m->dim);
+    m->q.reserve(r * m->dim);
+    m->k.reserve(r * m->kv_dim);
+    m->v.reserve(r * m->kv_dim);
+    m->hb.reserve(r * m->hidden);
+    m->hb2.reserve(r * m->hidden);
+    m->tokens.reserve(r);
+}
+
+void check_model_pool(const nitro_model* m, const nitro_kvpool* pool) {
+    require(m != nullptr, ERR_INVALID_ARGUMENT, "null model");
+    require(pool != nullptr, ERR_INVALID_ARGUMENT, "null pool");
+    require(pool->num_layers == m->n_layers && pool->kv_dim == m->kv_dim, ERR_INVALID_ARGUMENT,
+            "pool layers / kv_dim do not match the model");
+}
+
+void upload_tokens(nitro_model* m, const int32_t* tokens, int rows, hipStream_t s) {
+    require(tokens != nullptr, ERR_INVALID_ARGUMENT, "null tokens");
+    for (int i = 0; i < rows; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->vocab)
+            throw Error(ERR_INVALID_ARGUMENT, "token id " + std::to_string(tokens[i]) + " outside the vocabulary");
+    int32_t* h = m->staging.acquire(rows);
+    std::memcpy(h, tokens, sizeof(int32_t) * rows);
+    m->staging.copy(m->tokens.ptr, h, rows, s);
+    m->staging.finish(s);
+}
+
+// The layer loop shared by the decode and prefill forwards: after it, x holds
+// the residual stream and `ffn` the last layer's FFN output (not yet added).
+template <typename Attend>
+void layers(nitro_model* m, nitro_kvpool* pool, int rows, int semantics, hipStream_t s, Attend attend) {
+    const int dim = m->dim, kv = m->kv_dim, hid = m->hidden;
+    hip_check(launch_embed_rows(m->f32(m->o_emb), m->tokens.ptr, m->x.ptr, rows, dim, m->vocab,
+                                pool->bad_pages.ptr, s),
+              "embed launch");
+    for (int l = 0; l < m->n_layers; l++) {
+        // x += previous layer's FFN output; xb = rms_norm(x) (src/model_q8.cpp:586-589)
+        hip_check(launch_add_rmsnorm(m->x.ptr, l ? m->ffn.ptr : nullptr,
+                                     m->f32(m->o_rms_att) + (size_t)l * dim, m->xb.ptr, rows, dim, s),
+                  "rmsnorm launch");
+        q8(m, m->o_wq, l, dim, dim, m->xb.ptr, m->q.ptr, rows, semantics, s);   // :590
+        q8(m, m->o_wk, l, kv, dim, m->xb.ptr, m->k.ptr, rows, semantics, s);    // :591
+        q8(m, m->o_wv, l, kv, dim, m->xb.ptr, m->v.ptr, rows, semantics, s);    // :592
+        attend(l);  // RoPE + KV append + attention -> m->attn (:594-662)
+        q8(m, m->o_wo, l, dim, dim, m->attn.ptr, m->proj.ptr, rows, semantics, s);  // :663
+        // x += wo . attn; xb = rms_norm(x) (:664-669)
+        hip_check(launch_add_rmsnorm(m->x.ptr, m->proj.ptr, m->f32(m->o_rms_ffn) + (size_t)l * dim,
+                                     m->xb.ptr, rows, dim, s),
+                  "rmsnorm launch");
+        q8(m, m->o_w1, l, hid, dim, m->xb.ptr, m->hb.ptr, rows, semantics, s);   // :670
+        q8(m, m->o_w3, l, hid, dim, m->xb.ptr, m->hb2.ptr, rows, semantics, s);  // :671
+        hip_check(launch_swiglu(m->hb.ptr, m->hb2.ptr, (size_t)rows * hid, s), "swiglu launch");
+        q8(m, m->o_w2, l, dim, hid, m->hb.ptr, m->ffn.ptr, rows, semantics, s);  // :682
+    }
+}
+
+size_t q8_bytes(size_t rows, size_t cols) { return rows * (cols / 32) * 36; }
+
+}  // namespace
+
+extern "C" {
+
+int nitro_model_create(const void* blob, uint64_t bytes, nitro_model** out) {
+    return guarded([&] {
+        require(out != nullptr, ERR_INVALID_ARGUMENT, "null output pointer");
+        *out = nullptr;
+        require(blob != nullptr && bytes >= 28, ERR_INVALID_ARGUMENT, "model blob shorter than its header");
+        int32_t h[7];
+        std::memcpy(h, blob, sizeof(h));
+        nitro_model* m = new nitro_model();
+        try {
+            m->dim = h[0];
+            m->hidden = h[1];
+            m->n_layers = h[2];
+            m->n_heads = h[3];
+            m->n_kv_heads = h[4];
+            m->vocab = h[5];
+            m->seq_len = h[6];
+            require(m->dim > 0 && m->hidden > 0 && m->n_layers > 0 && m->n_heads > 0 &&
+                        m->n_kv_heads > 0 && m->vocab > 0 && m->seq_len > 0,
+                    ERR_INVALID_ARGUMENT, "header fields must be positive");
+            require(m->dim % m->n_heads == 0 && m->n_heads % m->n_kv_heads == 0, ERR_UNSUPPORTED,
+                    "dim must split into heads and heads into KV groups");
+            m->head_size = m->dim / m->n_heads;
+            m->kv_dim = m->n_kv_heads * m->head_size;
+            require(supported_head_dim(m->head_size), ERR_UNSUPPORTED, "head_size must be 32, 64, 128 or 256");
+            require(m->dim % 64 == 0 && m->hidden % 32 == 0 && m->kv_dim % 32 == 0, ERR_UNSUPPORTED,
+                    "dim must be a multiple of 64, hidden_dim and kv_dim of 32");
+            const size_t L = m->n_layers, D = m->dim, Hd = m->hidden, KV = m->kv_dim, V = m->vocab;
+            size_t o = 0;
+            m->o_emb = o;        o += V * D * 4;
+            m->o_rms_att = o;    o += L * D * 4;
+            m->o_wq = o;         o += L * q8_bytes(D, D);
+            m->o_wk = o;         o += L * q8_bytes(KV, D);
+            m->o_wv = o;         o += L * q8_bytes(KV, D);
+            m->o_wo = o;         o += L * q8_bytes(D, D);
+            m->o_rms_ffn = o;    o += L * D * 4;
+            m->o_w1 = o;         o += L * q8_bytes(Hd, D);
+            m->o_w2 = o;         o += L * q8_bytes(D, Hd);
+            m->o_w3 = o;         o += L * q8_bytes(Hd, D);
+            m->o_rms_final = o;  o += D * 4;
+            m->o_freq_real = o;  o += (size_t)m->seq_len * m->head_size / 2 * 4;
+            m->o_freq_imag = o;  o += (size_t)m->seq_len * m->head_size / 2 * 4;
+            if (bytes < 28 + o)
+                throw Error(ERR_INVALID_ARGUMENT, "model blob holds " + std::to_string(bytes) +
+                                                      " bytes; its header needs " + std::to_string(28 + o));
+            m->weight_bytes = o;
+            hip_check(hipMalloc((void**)&m->weights, o), "hipMalloc(weights)");
+            hip_check(hipMemcpy(m->weights, static_cast<const uint8_t*>(blob) + 28, o, hipMemcpyHostToDevice),
+                      "hipMemcpy(weights)");
+        } catch (...) {
+            if (m->weights) (void)hipFree(m->weights);
+            delete m;
+            throw;
+        }
+        *out = m;
+    });
+}
+
+int nitro_model_destroy(nitro_model* m) {
+    if (!m) return NITRO_OK;
+    return guarded([&] {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(m->weights);
+        delete m;
+    });
+}
+
+int nitro_model_config(const nitro_model* m, int32_t* cfg) {
+    return guarded([&] {
+        require(m != nullptr && cfg != nullptr, ERR_INVALID_ARGUMENT, "null pointer");
+        const int32_t v[7] = {m->dim, m->hidden, m->n_layers, m->n_heads, m->n_kv_heads, m->vocab, m->seq_len};
+        std::memcpy(cfg, v, sizeof(v));
+    });
+}
+
+int nitro_forward_decode_batch(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int32_t batch,
+                               float* logits, int32_t semantics, void* stream) {
+    return guarded([&] {
+        check_model_pool(m, pool);
+        require(logits != nullptr, ERR_INVALID_ARGUMENT, "null logits");
+        require(semantics == NITRO_Q8_FULL_ROWS || semantics == NITRO_Q8_LAST_BLOCK, ERR_INVALID_ARGUMENT,
+                "unknown Q8 semantics");
+        require(pool->decode.batch > 0, ERR_NO_BATCH, "no decode batch uploaded");
+        require(batch == pool->decode.batch, ERR_INVALID_ARGUMENT,
+                "batch differs from the uploaded decode batch");
+        hipStream_t s = as_stream(stream);
+        reserve_rows(m, batch);
+        upload_tokens(m, tokens, batch, s);
+        layers(m, pool, batch, semantics, s, [&](int l) {
+            require(nitro_rope_kv_append(pool, l, m->q.ptr, m->k.ptr, m->v.ptr, m->f32(m->o_freq_real),
+                                         m->f32(m->o_freq_imag), m->seq_len, m->n_heads, m->n_kv_heads,
+                                         m->head_size, stream) == NITRO_OK,
+                    ERR_INVALID_ARGUMENT, nitro_last_error());
+            require(nitro_paged_attn_decode(pool, l, m->q.ptr, m->attn.ptr, m->n_heads, m->n_kv_heads,
+                                            m->head_size, stream) == NITRO_OK,
+                    ERR_INVALID_ARGUMENT, nitro_last_error());
+        });
+        // x += FFN output; x = rms_norm(x) in place; logits = wcls . x (:687-692)
+        hip_check(launch_add_rmsnorm(m->x.ptr, m->ffn.ptr, m->f32(m->o_rms_final), m->x.ptr, batch, m->dim, s),
+                  "rmsnorm launch");
+        hip_check(launch_f32_matmul(m->f32(m->o_emb), m->x.ptr, logits, batch, m->dim, m->vocab, s),
+                  "classifier launch");
+        pool->last_stream = s;
+    });
+}
+
+int nitro_forward_prefill(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int32_t total_rows,
+                          float* logits, int32_t semantics, void* stream) {
+    return guarded([&] {
+        check_model_pool(m, pool);
+        require(logits != nullptr, ERR_INVALID_ARGUMENT, "null logits");
+        require(semantics == NITRO_Q8_FULL_ROWS || semantics == NITRO_Q8_LAST_BLOCK, ERR_INVALID_ARGUMENT,
+                "unknown Q8 semantics");
+        const PrefillBatch& p = pool->prefill;
+        require(p.batch > 0, ERR_NO_BATCH, "no prefill batch uploaded");
+        require(total_rows == p.total_rows, ERR_INVALID_ARGUMENT,
+                "total_rows differs from the uploaded prefill batch");
+        hipStream_t s = as_stream(stream);
+        reserve_rows(m, total_rows);
+        m->last.reserve((size_t)p.batch * m->dim);
+        upload_tokens(m, tokens, total_rows, s);
+        layers(m, pool, total_rows, semantics, s, [&](int l) {
+            require(nitro_rope_kv_append_prefill(pool, l, m->q.ptr, m->k.ptr, m->v.ptr, m->f32(m->o_freq_real),
+                                                 m->f32(m->o_freq_imag), m->seq_len, m->n_heads,
+                                                 m->n_kv_heads, m->head_size, stream) == NITRO_OK,
+                    ERR_INVALID_ARGUMENT, nitro_last_error());
+            require(nitro_paged_attn_prefill(pool, l, m->q.ptr, m->attn.ptr, m->n_heads, m->n_kv_heads,
+                                             m->head_size, stream) == NITRO_OK,
+                    ERR_INVALID_ARGUMENT, nitro_last_error());
+        });
+        // Each chunk's last token: x += FFN output; rms_norm; logits = wcls . x (:553-555)
+        hip_check(launch_gather_last_rows(m->x.ptr, m->ffn.ptr, p.d_row_off.ptr, p.d_len.ptr, m->last.ptr,
+                                          p.batch, m->dim, s),
+                  "gather launch");
+        hip_check(launch_add_rmsnorm(m->last.ptr, nullptr, m->f32(m->o_rms_final), m->last.ptr, p.batch,
+                                     m->dim, s),
+                  "rmsnorm launch");
+        hip_check(launch_f32_matmul(m->f32(m->o_emb), m->last.ptr, logits, p.batch, m->dim, m->vocab, s),
+                  "classifier launch");
+        pool->last_stream = s;
+    });
+}
+
+}  // extern "C"

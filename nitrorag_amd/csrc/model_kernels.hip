@@ -1,0 +1,301 @@
+// Row-wise kernels of the transformer step around attention for gfx950, and
+// the fp32 matrix product of the classifier.  Each follows the reference's
+// formula (src/model_q8.cpp); reductions run in parallel, so sums differ from
+// the reference's sequential order by fp32 rounding only.
+//  - embed_rows: x[r] = token_embedding_table[tokens[r]] (:573-580, :432-436)
+//  - add_rmsnorm: x[r] += delta[r] (optional), then
+//      out[r] = weight * (x[r] / sqrtf(mean(x[r]^2) + 1e-5))  (rms_norm, :128-140)
+//  - swiglu: hb = hb * (1 / (1 + expf(-hb))) * hb2  (:672-680, :536-544)
+//  - f32_matmul: out[b][i] = sum_k w[i][k] * x[b][k], w fp32 [d][n]
+//      (matmul :80-90 and matmul_bulk :370-380, float overloads: the
+//      classifier wcls), VALU for up to 4 rows, fp32 MFMA above.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "device_pool.hpp"
+
+namespace nitro {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int ROW_THREADS = 256;
+
+__global__ __launch_bounds__(ROW_THREADS) void embed_rows_kernel(const float* __restrict__ table,
+                                                                 const int32_t* __restrict__ tokens,
+                                                                 float* __restrict__ x, int dim,
+                                                                 int vocab, int32_t* bad_tokens) {
+    const int r = blockIdx.x;
+    int t = tokens[r];
+    if ((unsigned)t >= (unsigned)vocab) {
+        if (threadIdx.x == 0) atomicAdd(bad_tokens, 1);
+        t = 0;  // defined result; the count reports the bad id
+    }
+    const float4* src = reinterpret_cast<const float4*>(table + (size_t)t * dim);
+    float4* dst = reinterpret_cast<float4*>(x + (size_t)r * dim);
+    for (int i = threadIdx.x; i < dim / 4; i += ROW_THREADS) dst[i] = src[i];
+}
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < ROW_THREADS / 64; w++) s += red[w];
+    return s;
+}
+
+// One workgroup per row; x, delta, out are [rows][dim] (out may alias x).
+__global__ __launch_bounds__(ROW_THREADS) void add_rmsnorm_kernel(float* x,
+                                                                  const float* __restrict__ delta,
+                                                                  const float* __restrict__ weight,
+                                                                  float* out, int dim) {
+    __shared__ float red[ROW_THREADS / 64];
+    float* xr = x + (size_t)blockIdx.x * dim;
+    const float* dr = delta ? delta + (size_t)blockIdx.x * dim : nullptr;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < dim; i += ROW_THREADS) {
+        float v = xr[i];
+        if (dr) {
+            v += dr[i];
+            xr[i] = v;
+        }
+        ss = fmaf(v, v, ss);
+    }
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + 1e-5f);
+    float* orow = out + (size_t)blockIdx.x * dim;
+    for (int i = threadIdx.x; i < dim; i += ROW_THREADS) orow[i] = weight[i] * (inv * xr[i]);
+}
+
+// last[b] = x[r] + ffn[r] for the last row r = row_off[b] + len[b] - 1 of chunk b.
+__global__ __launch_bounds__(ROW_THREADS) void gather_last_rows_kernel(const float* __restrict__ x,
+                                                                       const float* __restrict__ ffn,
+                                                                       const int32_t* __restrict__ row_off,
+                                                                       const int32_t* __restrict__ len,
+                                                                       float* __restrict__ last, int dim) {
+    const int b = blockIdx.x;
+    const size_t r = (size_t)(row_off[b] + len[b] - 1);
+    for (int i = threadIdx.x; i < dim; i += ROW_THREADS)
+        last[(size_t)b * dim + i] = x[r * dim + i] + ffn[r * dim + i];
+}
+
+__global__ __launch_bounds__(ROW_THREADS) void swiglu_kernel(float* __restrict__ hb,
+                                                             const float* __restrict__ hb2, size_t n) {
+    const size_t i = (size_t)blockIdx.x * ROW_THREADS + threadIdx.x;
+    if (i >= n) return;
+    float v = hb[i];
+    v *= 1.0f / (1.0f + expf(-v));
+    hb[i] = v * hb2[i];
+}
+
+// fp32 rows of w: lane (r = l%16, g = l/16) takes k = 64*chunk + 16*g .. +15
+// of row row0 + r (64 contiguous bytes); same lane layout as the Q8 kernels.
+constexpr int F32_WAVES = 8;
+constexpr int F32_UNROLL = 2;
+constexpr int F32_SLAB = F32_WAVES * F32_UNROLL * 64;
+
+__device__ __forceinline__ float sum_over_rows(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Up to NB activation rows on the VALU; n % 64 == 0.
+template <int NB>
+__global__ __launch_bounds__(64 * F32_WAVES) void f32_gemv_kernel(const float* __restrict__ w,
+                                                                   const float* __restrict__ x,
+                                                                   float* __restrict__ out, int n, int d) {
+    __shared__ __attribute__((aligned(16))) float xs[NB][F32_SLAB];
+    __shared__ float red[F32_WAVES][NB][16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int row0 = blockIdx.x * 16;
+    const float* wrow = w + (size_t)min(row0 + r, d - 1) * n;
+    float acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[b] = 0.0f;
+    for (int slab = 0; slab < n; slab += F32_SLAB) {
+        const int k0 = slab + wave * F32_UNROLL * 64 + 16 * g;
+        float4 wv[F32_UNROLL][4];
+#pragma unroll
+        for (int u = 0; u < F32_UNROLL; u++) {
+            const int k = k0 + 64 * u;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                wv[u][i] = k < n ? reinterpret_cast<const float4*>(wrow + k)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        const int slab_len = min(F32_SLAB, n - slab);
+        __syncthreads();
+        for (int i = threadIdx.x; i < NB * (slab_len / 4); i += 64 * F32_WAVES) {
+            const int b = i / (slab_len / 4), f = i - b * (slab_len / 4);
+            *reinterpret_cast<float4*>(&xs[b][4 * f]) = reinterpret_cast<const float4*>(x + (size_t)b * n + slab)[f];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < F32_UNROLL; u++) {
+            const int k = k0 + 64 * u;
+            if (k >= n) continue;
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                const float4* xp = reinterpret_cast<const float4*>(&xs[b][k - slab]);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 v = xp[i];
+                    acc[b] = fmaf(wv[u][i].x, v.x, acc[b]);
+                    acc[b] = fmaf(wv[u][i].y, v.y, acc[b]);
+                    acc[b] = fmaf(wv[u][i].z, v.z, acc[b]);
+                    acc[b] = fmaf(wv[u][i].w, v.w, acc[b]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[b] = sum_over_rows(acc[b]);
+    if (g == 0) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) red[wave][b][r] = acc[b];
+    }
+    __syncthreads();
+    if (threadIdx.x >= NB * 16) return;
+    const int b = threadIdx.x / 16, rr = threadIdx.x % 16;
+    if (row0 + rr >= d) return;
+    float s = 0.0f;
+#pragma unroll
+    for (int v = 0; v < F32_WAVES; v++) s += red[v][b][rr];
+    out[(size_t)b * d + row0 + rr] = s;
+}
+
+// More rows on fp32 MFMA: out^T[16 rows][16 batch] per wave, 4 waves split k
+// by 64-k chunks; lane (r, g) feeds w[row0+r][64c + 16g + m] and
+// x[b][64c + 16g + m] to instruction m.
+constexpr int F32M_WAVES = 4;
+constexpr int F32M_BTILES = 4;
+
+__global__ __launch_bounds__(64 * F32M_WAVES) void f32_matmul_mfma_kernel(const float* __restrict__ w,
+                                                                          const float* __restrict__ x,
+                                                                          float* __restrict__ out,
+                                                                          int batch, int n, int d) {
+    __shared__ f32x4 red[F32M_WAVES - 1][F32M_BTILES][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int row0 = blockIdx.x * 16;
+    const int b0 = blockIdx.y * 16 * F32M_BTILES;
+    const int btiles = min(F32M_BTILES, (batch - b0 + 15) / 16);
+    const float* wrow = w + (size_t)min(row0 + r, d - 1) * n;
+    f32x4 acc[F32M_BTILES];
+#pragma unroll
+    for (int t = 0; t < F32M_BTILES; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nchunk = n / 64;
+    for (int ch = wave; ch < nchunk; ch += F32M_WAVES) {
+        const int k = 64 * ch + 16 * g;
+        float wv[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 v = reinterpret_cast<const float4*>(wrow + k)[i];
+            wv[4 * i] = v.x;
+            wv[4 * i + 1] = v.y;
+            wv[4 * i + 2] = v.z;
+            wv[4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int t = 0; t < F32M_BTILES; t++) {
+            if (t >= btiles) break;  // uniform
+            const int bb = b0 + 16 * t + r;
+            float xv[16];
+            if (bb < batch) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 v = reinterpret_cast<const float4*>(x + (size_t)bb * n + k)[i];
+                    xv[4 * i] = v.x;
+                    xv[4 * i + 1] = v.y;
+                    xv[4 * i + 2] = v.z;
+                    xv[4 * i + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < 16; m++) xv[m] = 0.0f;
+            }
+#pragma unroll
+            for (int m = 0; m < 16; m++)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[m], xv[m], acc[t], 0, 0, 0);
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int t = 0; t < F32M_BTILES; t++)
+            if (t < btiles) red[wave - 1][t][lane] = acc[t];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int t = 0; t < F32M_BTILES; t++) {
+        if (t >= btiles) break;
+        f32x4 s = acc[t];
+#pragma unroll
+        for (int v = 0; v < F32M_WAVES - 1; v++) s += red[v][t][lane];
+        const int bb = b0 + 16 * t + (lane & 15);
+        if (bb >= batch) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int row = row0 + 4 * (lane >> 4) + j;
+            if (row < d) out[(size_t)bb * d + row] = s[j];
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_embed_rows(const float* table, const int32_t* tokens, float* x, int rows, int dim,
+                             int vocab, int32_t* bad_tokens, hipStream_t stream) {
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(rows), dim3(ROW_THREADS), 0, stream, table, tokens, x,
+                       dim, vocab, bad_tokens);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rmsnorm(float* x, const float* delta, const float* weight, float* out, int rows,
+                              int dim, hipStream_t stream) {
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(ROW_THREADS), 0, stream, x, delta, weight,
+                       out, dim);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_last_rows(const float* x, const float* ffn, const int32_t* row_off,
+                                  const int32_t* len, float* last, int chunks, int dim,
+                                  hipStream_t stream) {
+    hipLaunchKernelGGL(gather_last_rows_kernel, dim3(chunks), dim3(ROW_THREADS), 0, stream, x, ffn,
+                       row_off, len, last, dim);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(float* hb, const float* hb2, size_t n, hipStream_t stream) {
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + ROW_THREADS - 1) / ROW_THREADS)),
+                       dim3(ROW_THREADS), 0, stream, hb, hb2, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_f32_matmul(const float* w, const float* x, float* out, int batch, int n, int d,
+                             hipStream_t stream) {
+    if (n % 64 != 0) return hipErrorInvalidValue;
+    if (batch <= 4) {
+        const dim3 grid((unsigned)((d + 15) / 16)), block(64 * F32_WAVES);
+        switch (batch) {
+            case 1: hipLaunchKernelGGL(f32_gemv_kernel<1>, grid, block, 0, stream, w, x, out, n, d); break;
+            case 2: hipLaunchKernelGGL(f32_gemv_kernel<2>, grid, block, 0, stream, w, x, out, n, d); break;
+            case 3: hipLaunchKernelGGL(f32_gemv_kernel<3>, grid, block, 0, stream, w, x, out, n, d); break;
+            default: hipLaunchKernelGGL(f32_gemv_kernel<4>, grid, block, 0, stream, w, x, out, n, d); break;
+        }
+        return hipGetLastError();
+    }
+    const dim3 grid((unsigned)((d + 15) / 16), (unsigned)((batch + 16 * F32M_BTILES - 1) / (16 * F32M_BTILES)));
+    hipLaunchKernelGGL(f32_matmul_mfma_kernel, grid, dim3(64 * F32M_WAVES), 0, stream, w, x, out, batch,
+                       n, d);
+    return hipGetLastError();
+}
+
+}  // namespace nitro

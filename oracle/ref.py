@@ -35,6 +35,11 @@ def lib() -> ctypes.CDLL:
         L.ref_hash_block_state.argtypes = [u64, _i32p, ci]
         L.ref_hash_block_state.restype = u64
         L.ref_set_threads.argtypes = [ci]
+        L.ref_model_create.argtypes = [ci, ci, ci, ci, ci, ci, ci, ci, ci, ci, u64]
+        L.ref_model_create.restype = vp
+        L.ref_model_serialize.argtypes = [vp, ctypes.POINTER(ctypes.c_uint8), u64]
+        L.ref_model_serialize.restype = u64
+        L.ref_read_logits.argtypes = [vp, ci, _f32p]
         L.ref_q8_matmul.argtypes = [_f32p, _f32p, vp, ci, ci]
         L.ref_q8_matmul.restype = None
         L.ref_q8_matmul_bulk.argtypes = [_f32p, _f32p, vp, ci, ci, ci]
@@ -101,6 +106,35 @@ class RefWorld:
         self.seq_len, self.max_rows = seq_len, max_rows
         self.dim = n_heads * head_dim
         self.kv_dim = n_kv_heads * head_dim
+
+    @classmethod
+    def random_model(cls, n_heads, n_kv_heads, head_dim, n_layers, vocab, seq_len, hidden_dim,
+                     total_blocks, max_rows=64, max_seqs=8, seed=1, threads=1):
+        """A world whose model has every weight random (ref_model_create): for
+        logits-level golden vectors of the forward passes."""
+        self = cls.__new__(cls)
+        L = lib()
+        L.ref_set_threads(threads)
+        self.h = L.ref_model_create(n_heads, n_kv_heads, head_dim, n_layers, vocab, seq_len,
+                                    hidden_dim, total_blocks, max_rows, max_seqs, seed)
+        self.n_heads, self.n_kv_heads, self.head_dim = n_heads, n_kv_heads, head_dim
+        self.n_layers, self.total_blocks, self.max_seqs = n_layers, total_blocks, max_seqs
+        self.seq_len, self.max_rows, self.vocab = seq_len, max_rows, vocab
+        self.dim = n_heads * head_dim
+        self.kv_dim = n_kv_heads * head_dim
+        return self
+
+    def serialize(self) -> np.ndarray:
+        """The model in the reference's file layout (src/Server_Inference.cpp:45-69)."""
+        n = lib().ref_model_serialize(self.h, None, 0)
+        out = np.zeros(n, dtype=np.uint8)
+        assert lib().ref_model_serialize(self.h, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), n) == n
+        return out
+
+    def logits(self, rows) -> np.ndarray:
+        out = np.zeros((rows, self.vocab), dtype=np.float32)
+        assert lib().ref_read_logits(self.h, rows, out.ctypes.data_as(_f32p)) == 0
+        return out
 
     def close(self):
         if self.h:

@@ -116,12 +116,34 @@ void ref_q8_matmul_bulk(float* out, const float* x, const void* w, int batch, in
 // A tiny Llama-shaped model around a KVBlock_Manager/PrefixCacheManager pair.
 // dim and kv_dim must be multiples of 32 (Q8 blocks); RoPE tables are the
 // identity rotation so K/V rows in the pool are exactly the computed k/v.
+static void* build_world(int n_heads, int n_kv_heads, int head_size, int n_layers, int vocab,
+                         int seq_len, int hidden_dim, int total_blocks, int max_rows, int max_seqs,
+                         uint64_t seed, bool random_model);
+
 void* ref_world_create(int n_heads, int n_kv_heads, int head_size, int n_layers, int vocab,
                        int seq_len, int total_blocks, int max_rows, int max_seqs, uint64_t seed) {
+    return build_world(n_heads, n_kv_heads, head_size, n_layers, vocab, seq_len, 32, total_blocks,
+                       max_rows, max_seqs, seed, false);
+}
+
+// A tiny model with every weight random (embedding U[-1,1), rms weights
+// U[0.5,1.5), Q8 matrices with random int8 and per-block scales), and the
+// usual RoPE tables (angle pos * 10000^(-2i/head_size), i < head_size/2) —
+// for logits-level golden vectors of the forward passes.
+void* ref_model_create(int n_heads, int n_kv_heads, int head_size, int n_layers, int vocab,
+                       int seq_len, int hidden_dim, int total_blocks, int max_rows, int max_seqs,
+                       uint64_t seed) {
+    return build_world(n_heads, n_kv_heads, head_size, n_layers, vocab, seq_len, hidden_dim,
+                       total_blocks, max_rows, max_seqs, seed, true);
+}
+
+static void* build_world(int n_heads, int n_kv_heads, int head_size, int n_layers, int vocab,
+                         int seq_len, int hidden_dim, int total_blocks, int max_rows, int max_seqs,
+                         uint64_t seed, bool random_model) {
     World* W = new World();
     Config_Transformer& c = W->c;
     c.dim = n_heads * head_size;
-    c.hidden_dim = 32;
+    c.hidden_dim = hidden_dim;
     c.n_layers = n_layers;
     c.n_heads = n_heads;
     c.n_kv_heads = n_kv_heads;
@@ -152,6 +174,29 @@ void* ref_world_create(int n_heads, int n_kv_heads, int head_size, int n_layers,
     fill_q8(W->w1, n_layers * c.hidden_dim, c.dim, rng, 1.0f / 64);
     fill_q8(W->w3, n_layers * c.hidden_dim, c.dim, rng, 1.0f / 64);
     fill_q8(W->w2, n_layers * c.dim, c.hidden_dim, rng, 0.0f);
+    if (random_model) {
+        for (auto& x : W->rms1) x = 1.0f + 0.5f * uniform_pm1(rng);
+        for (auto& x : W->rms2) x = 1.0f + 0.5f * uniform_pm1(rng);
+        for (auto& x : W->rms3) x = 1.0f + 0.5f * uniform_pm1(rng);
+        auto rand_q8 = [&](std::vector<BlockQ8>& m, int rows, int cols) {
+            fill_q8(m, rows, cols, rng, 1.0f);
+            const float base = 1.0f / (127.0f * std::sqrt((float)cols));
+            for (auto& b : m) b.scale = base * (1.0f + 0.5f * uniform_pm1(rng));
+        };
+        rand_q8(W->wq, n_layers * c.dim, c.dim);
+        rand_q8(W->wk, n_layers * W->kv_dim, c.dim);
+        rand_q8(W->wv, n_layers * W->kv_dim, c.dim);
+        rand_q8(W->wo, n_layers * c.dim, c.dim);
+        rand_q8(W->w1, n_layers * c.hidden_dim, c.dim);
+        rand_q8(W->w3, n_layers * c.hidden_dim, c.dim);
+        rand_q8(W->w2, n_layers * c.dim, c.hidden_dim);
+        for (int pos = 0; pos < seq_len; pos++)
+            for (int i = 0; i < head_size / 2; i++) {
+                const double ang = pos * std::pow(10000.0, -2.0 * i / head_size);
+                W->fcr[(size_t)pos * (head_size / 2) + i] = (float)std::cos(ang);
+                W->fci[(size_t)pos * (head_size / 2) + i] = (float)std::sin(ang);
+            }
+    }
     Transformer_Weights& w = W->w;
     w.token_embedding_table = W->emb.data();
     w.rms_attn_weights = W->rms1.data();
@@ -186,6 +231,44 @@ void* ref_world_create(int n_heads, int n_kv_heads, int head_size, int n_layers,
     W->cache = new PrefixCacheManager(*W->mem, total_blocks);
     W->reqs.assign(max_seqs, nullptr);
     return W;
+}
+
+// Writes the model in the reference's file layout (src/Server_Inference.cpp:45-69):
+// 7 int32 header fields, then the weight sections in load order.  Returns the
+// byte count; writes only when cap is large enough.
+uint64_t ref_model_serialize(void* p, uint8_t* out, uint64_t cap) {
+    World* W = (World*)p;
+    const Config_Transformer& c = W->c;
+    std::vector<uint8_t> b;
+    auto put = [&](const void* src, size_t n) {
+        const uint8_t* s = (const uint8_t*)src;
+        b.insert(b.end(), s, s + n);
+    };
+    const int32_t h[7] = {c.dim, c.hidden_dim, c.n_layers, c.n_heads, c.n_kv_heads, c.vocab_size, c.seq_len};
+    put(h, sizeof(h));
+    put(W->emb.data(), W->emb.size() * 4);
+    put(W->rms1.data(), W->rms1.size() * 4);
+    put(W->wq.data(), W->wq.size() * sizeof(BlockQ8));
+    put(W->wk.data(), W->wk.size() * sizeof(BlockQ8));
+    put(W->wv.data(), W->wv.size() * sizeof(BlockQ8));
+    put(W->wo.data(), W->wo.size() * sizeof(BlockQ8));
+    put(W->rms2.data(), W->rms2.size() * 4);
+    put(W->w1.data(), W->w1.size() * sizeof(BlockQ8));
+    put(W->w2.data(), W->w2.size() * sizeof(BlockQ8));
+    put(W->w3.data(), W->w3.size() * sizeof(BlockQ8));
+    put(W->rms3.data(), W->rms3.size() * 4);
+    put(W->fcr.data(), W->fcr.size() * 4);
+    put(W->fci.data(), W->fci.size() * 4);
+    if (b.size() <= cap) std::memcpy(out, b.data(), b.size());
+    return b.size();
+}
+
+// Copies rows [0, rows) of s->logits (rows x vocab_size).
+int ref_read_logits(void* p, int rows, float* out) {
+    World* W = (World*)p;
+    if (rows > W->max_rows) return 1;
+    std::memcpy(out, W->s.logits, sizeof(float) * (size_t)rows * W->c.vocab_size);
+    return 0;
 }
 
 void ref_world_destroy(void* p) {

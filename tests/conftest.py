@@ -49,3 +49,12 @@ def golden_q8():
     return {name: (m, {k.split("/", 1)[1]: arrays[k] for k in arrays.files
                        if k.startswith(name + "/")})
             for name, m in meta.items()}
+
+
+@pytest.fixture(scope="session")
+def golden_model():
+    blob = np.fromfile(os.path.join(GOLDEN, "model_tiny.bin"), dtype=np.uint8)
+    with open(os.path.join(GOLDEN, "model_forward.json")) as f:
+        meta = json.load(f)
+    arrays = np.load(os.path.join(GOLDEN, "model_forward.npz"))
+    return blob, meta, {k: arrays[k] for k in arrays.files}

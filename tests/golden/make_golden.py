@@ -24,6 +24,10 @@ Writes, next to this script:
   q8_matmul.json + q8_matmul.npz
                              the reference's matmul and matmul_bulk (BlockQ8) on
                              packed Q8 matrices and fp32 activations
+  model_tiny.bin + model_forward.json + model_forward.npz
+                             a tiny random model in the reference's file layout and
+                             the logits of forward_prefill_chunk / forward_paged /
+                             forward_decode_batch over a scripted session
 """
 from __future__ import annotations
 
@@ -486,6 +490,49 @@ def make_q8():
     return meta, arrays
 
 
+MODEL = dict(n_heads=4, n_kv_heads=2, head_dim=32, n_layers=2, vocab=160, seq_len=128,
+             hidden_dim=96, total_blocks=48)
+
+
+def make_model():
+    """Logits of the reference's forward passes on a tiny random model
+    (ref_model_create), over a script that mixes forward_prefill_chunk (fresh
+    and continued chunks), forward_paged and forward_decode_batch, one
+    reference thread (forward_decode_batch allocates inside an OpenMP loop).
+    Returns (model file bytes, meta, arrays)."""
+    W = ref.RefWorld.random_model(**MODEL, max_rows=64, max_seqs=4, seed=4242, threads=1)
+    blob = W.serialize()
+    rng = np.random.default_rng(4343)
+    V = MODEL["vocab"]
+    toks = lambda n: rng.integers(0, V, size=n).astype(np.int32)
+    for slot in range(3):
+        W.op(pm.OP_SEQ_NEW, slot)
+    script = [("prefill", [0], toks(37)), ("prefill", [1], toks(20)), ("prefill", [1], toks(13))]
+    script += [("paged", [2], toks(1)) for _ in range(5)]
+    script += [("decode", [0, 1], toks(2)) for _ in range(3)]
+    script += [("decode", [0, 1, 2], toks(3)) for _ in range(2)]
+    script += [("prefill", [2], toks(11)), ("decode", [2, 0], toks(2))]
+    meta, arrays = [], {}
+    for i, (kind, slots, t) in enumerate(script):
+        if kind == "prefill":
+            start = W.prefill_chunk(slots[0], t)
+            lg = W.logits(1)
+            meta.append(dict(kind=kind, slots=slots, start=start))
+        elif kind == "paged":
+            pos = W.forward_paged(slots[0], int(t[0]))
+            lg = W.logits(1)
+            meta.append(dict(kind=kind, slots=slots, pos=pos))
+        else:
+            pos = W.decode_batch(slots, t)
+            lg = W.logits(len(slots))
+            meta.append(dict(kind=kind, slots=slots, pos=[int(p) for p in pos]))
+        arrays[f"{i}/tokens"] = t
+        arrays[f"{i}/logits"] = lg
+    tables = {str(slot): W.block_table(slot).tolist() for slot in range(3)}
+    W.close()
+    return blob, dict(model=MODEL, script=meta, final_tables=tables), arrays
+
+
 def main():
     if not ref.available():
         sys.exit("oracle/_ref/libnitro_ref.so is missing: run `make -C oracle ref` first")
@@ -501,8 +548,14 @@ def main():
     with open(os.path.join(HERE, "q8_matmul.json"), "w") as f:
         json.dump(q8_meta, f, indent=1)
     np.savez_compressed(os.path.join(HERE, "q8_matmul.npz"), **q8_arrays)
+    blob, m_meta, m_arrays = make_model()
+    blob.tofile(os.path.join(HERE, "model_tiny.bin"))
+    with open(os.path.join(HERE, "model_forward.json"), "w") as f:
+        json.dump(m_meta, f, indent=1)
+    np.savez_compressed(os.path.join(HERE, "model_forward.npz"), **m_arrays)
     for fn in ("fnv.json", "block_manager_traces.json", "attention.json", "attention.npz",
-               "q8_matmul.json", "q8_matmul.npz"):
+               "q8_matmul.json", "q8_matmul.npz", "model_tiny.bin", "model_forward.json",
+               "model_forward.npz"):
         print(fn, os.path.getsize(os.path.join(HERE, fn)))
 
 

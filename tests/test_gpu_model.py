@@ -1,0 +1,120 @@
+"""GPU parity of the transformer step (nitro_forward_decode_batch /
+nitro_forward_prefill over a model loaded from the reference's file layout)
+against logits recorded from the reference's own forward_prefill_chunk,
+forward_paged and forward_decode_batch on a tiny random model.
+
+The host bookkeeping (BlockManager / Sequence) replays the same script, so
+positions and block tables must come out identical.  Logits bar: |gpu - ref|
+<= 2e-3 + 1e-3*|ref| (logits reach |80|; every product and reduction of two
+layers runs in a different fp32 order)."""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_ATOL, LOGIT_RTOL = 2e-3, 1e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    import nitrorag_amd  # noqa: F401
+    yield
+    torch.cuda.synchronize()
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def check_logits(got, want, what):
+    err = np.abs(got - want)
+    bound = LOGIT_ATOL + LOGIT_RTOL * np.abs(want)
+    worst = np.unravel_index(np.argmax(err - bound), err.shape)
+    assert np.all(err <= bound), (f"{what}: |gpu-ref| {err[worst]:.3g} > {bound[worst]:.3g} at {worst} "
+                                  f"(gpu {got[worst]:.6g}, ref {want[worst]:.6g})")
+    assert np.array_equal(got.argmax(axis=1), want.argmax(axis=1)), what
+
+
+def test_model_config_round_trip(golden_model):
+    import nitrorag_amd as na
+
+    blob, meta, _ = golden_model
+    m = na.Model(blob)
+    cfg = meta["model"]
+    assert m.config == dict(dim=cfg["n_heads"] * cfg["head_dim"], hidden_dim=cfg["hidden_dim"],
+                            n_layers=cfg["n_layers"], n_heads=cfg["n_heads"],
+                            n_kv_heads=cfg["n_kv_heads"], vocab_size=cfg["vocab"], seq_len=cfg["seq_len"])
+
+
+def test_forward_passes_match_reference_golden(golden_model):
+    import torch
+
+    import nitrorag_amd as na
+    from nitrorag_amd.model import FULL_ROWS, LAST_BLOCK
+
+    blob, meta, arrays = golden_model
+    cfg = meta["model"]
+    model = na.Model(blob)
+    pool = na.KVPool(cfg["total_blocks"], cfg["n_layers"], model.kv_dim)
+    bm = na.BlockManager(cfg["total_blocks"])
+    seqs = {slot: na.Sequence(slot) for slot in range(3)}
+    for i, op in enumerate(meta["script"]):
+        toks = arrays[f"{i}/tokens"]
+        want = arrays[f"{i}/logits"]
+        slots = op["slots"]
+        say(f"step {i}: {op['kind']} slots {slots}")
+        if op["kind"] == "prefill":
+            s = seqs[slots[0]]
+            start = s.logical_token_count
+            assert start == op["start"]
+            for t in toks:  # src/model_q8.cpp:428-430
+                s.allocate_next_token(int(t), bm)
+            pool.upload_prefill_batch(na.pack_block_tables([s]), [start], [len(toks)])
+            got = model.forward_prefill(pool, toks, semantics=LAST_BLOCK)
+        else:
+            batch = [seqs[x] for x in slots]
+            pos = [s.logical_token_count for s in batch]
+            assert pos == ([op["pos"]] if op["kind"] == "paged" else op["pos"])
+            for s, t in zip(batch, toks):  # in batch order (one reference thread)
+                s.allocate_next_token(int(t), bm)
+            pool.upload_decode_batch(na.pack_block_tables(batch), pos)
+            sem = FULL_ROWS if op["kind"] == "paged" else LAST_BLOCK
+            got = model.forward_decode_batch(pool, toks, semantics=sem)
+        torch.cuda.synchronize()
+        check_logits(got.cpu().numpy(), want, f"step {i} ({op['kind']})")
+    assert pool.take_device_errors() == 0
+    for slot, table in meta["final_tables"].items():
+        assert seqs[int(slot)].block_table == table
+
+
+def test_model_argument_errors(golden_model):
+    import torch
+
+    import nitrorag_amd as na
+
+    blob, meta, _ = golden_model
+    with pytest.raises(na.NitroError):
+        na.Model(blob[:-4])  # truncated file
+    model = na.Model(blob)
+    cfg = meta["model"]
+    pool = na.KVPool(cfg["total_blocks"], cfg["n_layers"], model.kv_dim)
+    with pytest.raises(na.NitroError) as e:
+        model.forward_decode_batch(pool, [1])  # no batch uploaded
+    assert e.value.status == na._native.NO_BATCH
+    bm = na.BlockManager(cfg["total_blocks"])
+    s = na.Sequence(0)
+    s.allocate_next_token(1, bm)
+    pool.upload_decode_batch(na.pack_block_tables([s]), [0])
+    with pytest.raises(na.NitroError):
+        model.forward_decode_batch(pool, [cfg["vocab"]])  # token outside the vocabulary
+    wrong = na.KVPool(cfg["total_blocks"], cfg["n_layers"] + 1, model.kv_dim)
+    wrong.upload_decode_batch(na.pack_block_tables([s]), [0])
+    with pytest.raises(na.NitroError):
+        model.forward_decode_batch(wrong, [1])  # pool geometry differs from the model
+    torch.cuda.synchronize()
