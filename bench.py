@@ -32,6 +32,7 @@ Other workloads (survey configs and the next rows, measured for the design notes
                          fresh pages then attended causally; FLOPs = sum 2*H*hd*L(L+1)
   q8-gemv-7b-ffn         Q8_0 product, W 11008 x 4096 BlockQ8, 1 activation row
   q8-matmul-110m-b32     Q8_0 product, W 2048 x 768 BlockQ8, 32 activation rows
+  model-110m-decode-b32  one decode step of a 110M-shaped Q8 model, B=32 at context 512
 The three small decode workloads fit in the 256 MB Infinity Cache, so a 1 GiB
 buffer is read before every timed launch and only the launch itself is timed
 (events).
@@ -378,6 +379,112 @@ class Q8Workload:
         return {}
 
 
+class ModelDecodeWorkload:
+    """One decode step of the whole model (nitro_forward_decode_batch, full-row
+    Q8 products): embedding, n_layers x (rms_norm, wq/wk/wv, RoPE + KV append,
+    paged attention, wo, residual, rms_norm, w1/w3, SwiGLU, w2, residual), final
+    rms_norm and the fp32 classifier, for B sequences at context ctx.  Synthetic
+    model file in the reference's layout (nitrorag_amd.model.synthetic_model_file).
+    Algorithmic bytes per step: every weight once + K/V rows read by attention +
+    K/V rows written + activations in/out (logits)."""
+
+    bound = "hbm"
+    flush = False
+
+    def __init__(self, name, cfg, B, ctx, seed, describe):
+        self.name, self.cfg, self.B, self.ctx, self.seed, self.describe = name, cfg, B, ctx, seed, describe
+        dim, hid, L, H, Hkv, V, S = cfg
+        self.H, self.Hkv, self.hd, self.L, self.V = H, Hkv, dim // H, L, V
+        self.kv_dim = Hkv * (dim // H)
+        self.pages = B * ((ctx + 15) // 16) + 16
+        self.tables = seeded_tables(np.full(B, ctx), self.pages, seed)
+        self.positions = np.full(B, ctx - 1, np.int32)
+
+    def setup(self, dev, g):
+        import torch
+
+        import nitrorag_amd as na
+        from nitrorag_amd.model import synthetic_model_file
+
+        self.blob = synthetic_model_file(*self.cfg, seed=self.seed)
+        self.model = na.Model(self.blob)
+        shape = (self.pages, self.L, 16, self.kv_dim)
+        self.k = torch.randn(shape, device=dev, generator=g)
+        self.v = torch.randn(shape, device=dev, generator=g)
+        self.pool = na.KVPool.wrap(self.k, self.v)
+        self.pool.upload_decode_batch(self.tables, self.positions)
+        self.tokens = np.random.default_rng(self.seed).integers(0, self.V, self.B).astype(np.int32)
+        self.logits = torch.empty((self.B, self.V), device=dev)
+
+    def step(self, stream, events=None):
+        from nitrorag_amd.model import FULL_ROWS
+
+        if events is not None:
+            events[0][0].record(stream)
+        self.model.forward_decode_batch(self.pool, self.tokens, self.logits, FULL_ROWS, stream)
+        if events is not None:
+            events[0][1].record(stream)
+
+    def launches_per_step(self):
+        return 1
+
+    def work_per_launch(self):
+        dim, hid, L, H, Hkv, V, S = self.cfg
+        q8 = lambda r, c: r * (c // 32) * 36
+        weights = (V * dim * 4 + L * (q8(dim, dim) * 2 + q8(self.kv_dim, dim) * 2 + q8(hid, dim) * 2
+                                      + q8(dim, hid) + 2 * dim * 4) + dim * 4)
+        kv = L * self.B * self.ctx * self.kv_dim * 8 + L * self.B * self.kv_dim * 8
+        return int(weights + kv + self.B * V * 4)
+
+    def tokens_per_step(self):
+        return self.B
+
+    def kernel(self):
+        return "forward_decode_batch step (all kernels)"
+
+    def config(self):
+        dim, hid, L, H, Hkv, V, S = self.cfg
+        return {"workload": self.describe, "batch": self.B, "context": self.ctx, "dim": dim,
+                "hidden_dim": hid, "n_layers": L, "n_heads": H, "n_kv_heads": Hkv, "vocab": V,
+                "parallelism": "single GPU"}
+
+    def check(self):
+        import torch
+
+        assert torch.isfinite(self.logits).all().item(), "non-finite logits"
+
+    def cpu_baseline(self, seconds, sample):
+        """The oracle's composed forward_paged-style step (full-row matmul, the
+        oracle attention) for `sample` of the sequences, their pages copied out."""
+        import torch
+
+        from oracle import attn
+        from oracle import model as om
+
+        rows = min(sample, self.B)
+        ora = om.OracleModel(self.blob)
+        n_pages = self.tables.shape[1]
+        idx = torch.from_numpy(self.tables[:rows].reshape(-1).astype(np.int64)).to(self.k.device)
+        kh = self.k.index_select(0, idx).cpu().numpy()
+        vh = self.v.index_select(0, idx).cpu().numpy()
+        local = np.arange(rows * n_pages, dtype=np.int32).reshape(rows, n_pages)
+        pos = self.positions[:rows]
+        toks = self.tokens[:rows]
+        per_rep, reps, el = time_cpu(lambda: ora.forward_decode_batch(kh, vh, local, pos, toks, bulk=False),
+                                     seconds)
+        return {"value": round(rows / per_rep, 2), "unit": "tokens/s", "cores": attn.max_threads(),
+                "kind": "port",
+                "sample": (f"{rows} of the {self.B} sequences of this workload, one decode step of "
+                           f"the oracle's composed forward (src/model_q8.cpp:571-694 with full-row "
+                           f"matmul), {reps} reps in {el:.1f} s")}
+
+    def device_errors(self):
+        return self.pool.take_device_errors()
+
+    def extra(self, kernel_s):
+        return {}
+
+
 def prefix_shared_workload(seed):
     """48 sequences: 512 shared prefix tokens (32 pages via FNV-1a prefix-cache hits),
     private suffixes ~ U[64,512], then one decode token each."""
@@ -433,6 +540,12 @@ def make_workload(name, seed):
         return PrefillWorkload(name, 8, 12, 12, 64, rng.integers(128, 1025, size=8), seed,
                                describe=("causal prefill, B=8 prompts, lengths ~ U[128,1024], "
                                          "12 heads x 64, fresh 16-token pages (LIFO ids)"))
+    if name == "model-110m-decode-b32":
+        return ModelDecodeWorkload(name, (768, 2048, 12, 12, 12, 32000, 1024), 32, 512, seed,
+                                   describe=("one decode step of a Llama-2-110M-shaped model "
+                                             "(dim 768, hidden 2048, 12 layers, 12 heads x 64, "
+                                             "vocab 32000, Q8_0 weights, synthetic), B=32 sequences "
+                                             "at context 512, full-row Q8 products"))
     if name == "q8-gemv-7b-ffn":
         return Q8Workload(name, 4096, 11008, 1, seed,
                           describe=("Q8_0 matrix-vector product at the Llama-2-7B FFN up "
@@ -447,7 +560,8 @@ def make_workload(name, seed):
 
 
 WORKLOADS = ["decode-b64-ctx4096", "decode-single-110m", "decode-b32-mixed",
-             "decode-prefix-shared", "prefill-b8-12x64", "q8-gemv-7b-ffn", "q8-matmul-110m-b32"]
+             "decode-prefix-shared", "prefill-b8-12x64", "q8-gemv-7b-ffn", "q8-matmul-110m-b32",
+             "model-110m-decode-b32"]
 
 
 def kernel_name(w) -> str:

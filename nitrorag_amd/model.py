@@ -79,3 +79,44 @@ class Model:
         N.call("nitro_forward_prefill", self._h, pool.handle, t.ctypes.data_as(N._i32p), t.size,
                _dev(logits, "logits"), semantics, _stream_ptr(stream))
         return logits
+
+
+def synthetic_model_file(dim: int, hidden_dim: int, n_layers: int, n_heads: int, n_kv_heads: int,
+                         vocab_size: int, seq_len: int, seed: int = 0) -> np.ndarray:
+    """A model file in the reference's layout (src/Server_Inference.cpp:45-69)
+    with synthetic weights: embedding U[-1,1), rms weights U[0.5,1.5), Q8
+    matrices of random int8 with per-block scales ~ 1/(127*sqrt(cols)) (unit
+    scale activations), and RoPE tables cos/sin(pos * 10000^(-2i/head_size)).
+    For benchmarks and tests where no trained checkpoint is available."""
+    rng = np.random.default_rng(seed)
+    head = dim // n_heads
+    kv_dim = n_kv_heads * head
+    parts = [np.array([dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len],
+                      np.int32).view(np.uint8)]
+
+    def f32(a):
+        parts.append(np.ascontiguousarray(a, dtype=np.float32).view(np.uint8).reshape(-1))
+
+    def q8(rows, cols):
+        nb = cols // 32
+        blocks = np.empty((n_layers * rows, nb, 36), np.uint8)
+        scale = (1.0 / (127.0 * np.sqrt(cols))) * (1.0 + 0.5 * rng.uniform(-1, 1, (n_layers * rows, nb, 1)))
+        blocks[:, :, :4] = scale.astype(np.float32).view(np.uint8)
+        blocks[:, :, 4:] = rng.integers(-127, 128, (n_layers * rows, nb, 32), dtype=np.int8).view(np.uint8)
+        parts.append(blocks.reshape(-1))
+
+    f32(rng.uniform(-1, 1, (vocab_size, dim)))
+    f32(rng.uniform(0.5, 1.5, (n_layers, dim)))
+    q8(dim, dim)
+    q8(kv_dim, dim)
+    q8(kv_dim, dim)
+    q8(dim, dim)
+    f32(rng.uniform(0.5, 1.5, (n_layers, dim)))
+    q8(hidden_dim, dim)
+    q8(dim, hidden_dim)
+    q8(hidden_dim, dim)
+    f32(rng.uniform(0.5, 1.5, dim))
+    ang = np.arange(seq_len)[:, None] * 10000.0 ** (-2.0 * np.arange(head // 2) / head)[None, :]
+    f32(np.cos(ang))
+    f32(np.sin(ang))
+    return np.concatenate(parts)

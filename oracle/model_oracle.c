@@ -7,6 +7,7 @@
 #include "model_oracle.h"
 
 #include <immintrin.h>
+#include <math.h>
 #include <omp.h>
 #include <string.h>
 
@@ -71,6 +72,49 @@ void oracle_q8_matmul_bulk(float* out, const float* x, const uint8_t* w, int bat
                 for (int c = 0; c < 4; c++) sum = _mm256_fmadd_ps(wf[c], _mm256_loadu_ps(xr + 8 * c), sum);
                 out[(size_t)b * d + i] = hsum8(sum);
             }
+        }
+    }
+}
+
+/* src/model_q8.cpp:128-140 */
+void oracle_rms_norm(float* out, const float* x, const float* weight, int size) {
+    float ss = 0.0f;
+    for (int i = 0; i < size; i++) ss += x[i] * x[i];
+    ss /= size;
+    ss += 1e-5f;
+    ss = 1.0f / sqrtf(ss);
+    for (int i = 0; i < size; i++) out[i] = weight[i] * (ss * x[i]);
+}
+
+/* src/model_q8.cpp:672-680 (forward_decode_batch's form; forward_paged and
+ * forward_prefill_chunk multiply by hb2 in a second statement, same value) */
+void oracle_swiglu(float* hb, const float* hb2, int n) {
+    for (int i = 0; i < n; i++) {
+        float val = hb[i];
+        val *= (1.0f / (1.0f + expf(-val)));
+        hb[i] = val * hb2[i];
+    }
+}
+
+/* src/model_q8.cpp:80-90 (matmul, float weights) */
+void oracle_f32_matmul(float* out, const float* x, const float* w, int n, int d, int n_threads) {
+#pragma omp parallel for num_threads(n_threads)
+    for (int i = 0; i < d; i++) {
+        float val = 0.0f;
+        for (int j = 0; j < n; j++) val += w[(size_t)i * n + j] * x[j];
+        out[i] = val;
+    }
+}
+
+/* src/model_q8.cpp:370-380 (matmul_bulk, float weights) */
+void oracle_f32_matmul_bulk(float* out, const float* x, const float* w, int batch, int n, int d,
+                            int n_threads) {
+#pragma omp parallel for collapse(2) num_threads(n_threads)
+    for (int b = 0; b < batch; b++) {
+        for (int i = 0; i < d; i++) {
+            float val = 0.0f;
+            for (int j = 0; j < n; j++) val += x[(size_t)b * n + j] * w[(size_t)i * n + j];
+            out[(size_t)b * d + i] = val;
         }
     }
 }

@@ -12,6 +12,10 @@
  *                          fp64 closed form sum_k float(q)*scale*x
  *   oracle_q8_matmul_bulk  reference build golden vectors (matmul_bulk,
  *                          bit-exact), closed form "last block only"
+ *   oracle_rms_norm, oracle_swiglu, oracle_f32_matmul(_bulk)
+ *                          reference build golden logits of forward_paged /
+ *                          forward_decode_batch / forward_prefill_chunk through
+ *                          oracle/model.py's forward passes; fp64 closed forms
  */
 #ifndef NITRO_MODEL_ORACLE_H
 #define NITRO_MODEL_ORACLE_H
@@ -28,6 +32,15 @@ extern "C" {
 void oracle_q8_matmul(float* out, const float* x, const uint8_t* w, int n, int d, int n_threads);
 void oracle_q8_matmul_bulk(float* out, const float* x, const uint8_t* w, int batch, int n, int d,
                            int n_threads);
+
+/* src/model_q8.cpp:128-140 */
+void oracle_rms_norm(float* out, const float* x, const float* weight, int size);
+/* src/model_q8.cpp:672-680 over n values: hb = silu(hb) * hb2 */
+void oracle_swiglu(float* hb, const float* hb2, int n);
+/* src/model_q8.cpp:80-90 (matmul, float) and :370-380 (matmul_bulk, float) */
+void oracle_f32_matmul(float* out, const float* x, const float* w, int n, int d, int n_threads);
+void oracle_f32_matmul_bulk(float* out, const float* x, const float* w, int batch, int n, int d,
+                            int n_threads);
 
 #ifdef __cplusplus
 }

@@ -118,3 +118,56 @@ def test_model_argument_errors(golden_model):
     with pytest.raises(na.NitroError):
         model.forward_decode_batch(wrong, [1])  # pool geometry differs from the model
     torch.cuda.synchronize()
+
+
+MODELS = {
+    # name: (dim, hidden, layers, heads, kv heads, vocab, seq_len)
+    "mha_hd64_l3": (256, 512, 3, 4, 4, 1000, 256),
+    "gqa_hd128_l2": (512, 1024, 2, 4, 2, 700, 200),
+    "gqa_hd32_l2": (128, 256, 2, 4, 1, 300, 300),
+}
+
+
+@pytest.mark.parametrize("name", sorted(MODELS))
+def test_forward_vs_oracle_on_synthetic_models(name):
+    """A synthetic model file through both: the GPU forward passes against the
+    oracle's composed restatement (prefill chunks, then batched decode with
+    both Q8 semantics), same host bookkeeping."""
+    import torch
+
+    import nitrorag_amd as na
+    from nitrorag_amd.model import FULL_ROWS, LAST_BLOCK, synthetic_model_file
+    from oracle import model as om
+
+    dim, hid, L, H, Hkv, V, S = MODELS[name]
+    say(f"synthetic model {name}")
+    blob = synthetic_model_file(dim, hid, L, H, Hkv, V, S, seed=len(name))
+    model, ora = na.Model(blob), om.OracleModel(blob)
+    pages = 64
+    pool = na.KVPool(pages, L, model.kv_dim)
+    k = np.zeros((pages, L, 16, model.kv_dim), np.float32)
+    v = np.zeros_like(k)
+    bm = na.BlockManager(pages)
+    rng = np.random.default_rng(5)
+    seqs = [na.Sequence(i) for i in range(3)]
+    for s, n in zip(seqs, (70, 33, 5)):  # prefill each prompt as one chunk
+        toks = rng.integers(0, V, n).astype(np.int32)
+        start = s.logical_token_count
+        for t in toks:
+            s.allocate_next_token(int(t), bm)
+        pool.upload_prefill_batch(na.pack_block_tables([s]), [start], [n])
+        got = model.forward_prefill(pool, toks, semantics=LAST_BLOCK).cpu().numpy()
+        want = ora.forward_prefill_chunk(k, v, na.pack_block_tables([s])[0], start, toks)[None, :]
+        check_logits(got, want, f"{name} prefill {n}")
+    for step, sem in enumerate([LAST_BLOCK, FULL_ROWS, LAST_BLOCK]):
+        toks = rng.integers(0, V, 3).astype(np.int32)
+        pos = [s.logical_token_count for s in seqs]
+        for s, t in zip(seqs, toks):
+            s.allocate_next_token(int(t), bm)
+        tables = na.pack_block_tables(seqs)
+        pool.upload_decode_batch(tables, pos)
+        got = model.forward_decode_batch(pool, toks, semantics=sem).cpu().numpy()
+        want = ora.forward_decode_batch(k, v, tables, pos, toks, bulk=sem == LAST_BLOCK)
+        check_logits(got, want, f"{name} decode step {step}")
+    torch.cuda.synchronize()
+    assert pool.take_device_errors() == 0

@@ -82,3 +82,60 @@ def test_q8_oracle_matches_live_reference():
         want = np.stack([ref.q8_matmul(w, x[b], n, d) for b in range(B)])
         assert np.array_equal(om.q8_matmul(w, x, n, d), want)
         assert np.array_equal(om.q8_matmul_bulk(w, x, n, d), ref.q8_matmul_bulk(w, x, n, d))
+
+
+def replay_oracle_forward(blob, meta, arrays):
+    """Drive oracle.model.OracleModel through the recorded script with this
+    library's host bookkeeping; yields (step, logits, want)."""
+    import nitrorag_amd as na
+
+    M = om.OracleModel(blob)
+    cfg = meta["model"]
+    k = np.zeros((cfg["total_blocks"], cfg["n_layers"], 16, M.kv_dim), np.float32)
+    v = np.zeros_like(k)
+    bm = na.BlockManager(cfg["total_blocks"])
+    seqs = {s: na.Sequence(s) for s in range(3)}
+    for i, op in enumerate(meta["script"]):
+        t = arrays[f"{i}/tokens"]
+        slots = op["slots"]
+        if op["kind"] == "prefill":
+            s = seqs[slots[0]]
+            start = s.logical_token_count
+            for tok in t:
+                s.allocate_next_token(int(tok), bm)
+            got = M.forward_prefill_chunk(k, v, na.pack_block_tables([s])[0], start, t)[None, :]
+        else:
+            batch = [seqs[x] for x in slots]
+            pos = [s.logical_token_count for s in batch]
+            for s, tok in zip(batch, t):
+                s.allocate_next_token(int(tok), bm)
+            got = M.forward_decode_batch(k, v, na.pack_block_tables(batch), pos, t,
+                                         bulk=op["kind"] != "paged")
+        yield i, got, arrays[f"{i}/logits"]
+
+
+def test_oracle_forward_matches_reference_golden_logits(golden_model):
+    """The oracle's composed forward passes against the reference build's
+    logits: bit-exact or within fp32 rounding (|logits| reach ~80)."""
+    blob, meta, arrays = golden_model
+    exact = 0
+    for i, got, want in replay_oracle_forward(blob, meta, arrays):
+        np.testing.assert_allclose(got, want, rtol=1e-6, atol=2e-5, err_msg=f"step {i}")
+        exact += np.array_equal(got, want)
+    assert exact >= 3  # the first steps (no accumulated rounding) are bit-exact
+
+
+def test_model_pieces_closed_form():
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((3, 256)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    x64 = x.astype(np.float64)
+    want = w * x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-5)
+    np.testing.assert_allclose(om.rms_norm(x, w), want, rtol=2e-6, atol=1e-6)
+    hb, hb2 = x[0] * 4, x[1]
+    np.testing.assert_allclose(om.swiglu(hb, hb2), hb / (1 + np.exp(-hb.astype(np.float64))) * hb2,
+                               rtol=2e-6, atol=1e-6)
+    W = rng.standard_normal((40, 256)).astype(np.float32)
+    for bulk in (False, True):
+        np.testing.assert_allclose(om.f32_matmul(W, x, bulk), x64 @ W.T.astype(np.float64),
+                                   rtol=1e-5, atol=1e-5)
