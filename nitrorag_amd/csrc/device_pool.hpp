@@ -166,6 +166,12 @@ hipError_t launch_kv_append_decode(float* k_pool, float* v_pool, const float* k,
 // selects the reference's matmul_bulk semantics.
 hipError_t launch_q8_matmul(const void* w, const float* x, float* out, int batch, int n, int d,
                             bool last_block_only, hipStream_t stream);
+// Three matrices sharing x and n (wq/wk/wv): out[m] = x . w[m]^T, [batch][d[m]].
+hipError_t launch_q8_matmul3(const void* const* w, const float* x, float* const* out, const int* d,
+                             int batch, int n, bool last_block_only, hipStream_t stream);
+// hb = silu(x . w1^T) * (x . w3^T), [batch][hidden] (src/model_q8.cpp:670-680).
+hipError_t launch_q8_swiglu(const void* w1, const void* w3, const float* x, float* hb, int batch, int n,
+                            int hidden, bool last_block_only, hipStream_t stream);
 // Row-wise model kernels and the fp32 classifier product (model_kernels.hip).
 hipError_t launch_embed_rows(const float* table, const int32_t* tokens, float* x, int rows, int dim,
                              int vocab, int32_t* bad_tokens, hipStream_t stream);

@@ -23,7 +23,7 @@ struct nitro_model {
     // section offsets (bytes) within `weights`, src/Server_Inference.cpp:52-69
     size_t o_emb = 0, o_rms_att = 0, o_wq = 0, o_wk = 0, o_wv = 0, o_wo = 0, o_rms_ffn = 0;
     size_t o_w1 = 0, o_w2 = 0, o_w3 = 0, o_rms_final = 0, o_freq_real = 0, o_freq_imag = 0;
-    DeviceBuffer<float> x, xb, attn, proj, ffn, q, k, v, hb, hb2, last;
+    DeviceBuffer<float> x, xb, attn, proj, ffn, q, k, v, hb, last;
     DeviceBuffer<int32_t> tokens;
     Staging staging;
 
@@ -55,7 +55,6 @@ void reserve_rows(nitro_model* m, int rows) {
     m->k.reserve(r * m->kv_dim);
     m->v.reserve(r * m->kv_dim);
     m->hb.reserve(r * m->hidden);
-    m->hb2.reserve(r * m->hidden);
     m->tokens.reserve(r);
 }
 
@@ -90,18 +89,23 @@ void layers(nitro_model* m, nitro_kvpool* pool, int rows, int semantics, hipStre
         hip_check(launch_add_rmsnorm(m->x.ptr, l ? m->ffn.ptr : nullptr,
                                      m->f32(m->o_rms_att) + (size_t)l * dim, m->xb.ptr, rows, dim, s),
                   "rmsnorm launch");
-        q8(m, m->o_wq, l, dim, dim, m->xb.ptr, m->q.ptr, rows, semantics, s);   // :590
-        q8(m, m->o_wk, l, kv, dim, m->xb.ptr, m->k.ptr, rows, semantics, s);    // :591
-        q8(m, m->o_wv, l, kv, dim, m->xb.ptr, m->v.ptr, rows, semantics, s);    // :592
+        // q, k, v = wq.xb, wk.xb, wv.xb in one launch (:590-592)
+        const void* wqkv[3] = {m->q8(m->o_wq, l, dim, dim), m->q8(m->o_wk, l, kv, dim),
+                               m->q8(m->o_wv, l, kv, dim)};
+        float* qkv[3] = {m->q.ptr, m->k.ptr, m->v.ptr};
+        const int dqkv[3] = {dim, kv, kv};
+        hip_check(launch_q8_matmul3(wqkv, m->xb.ptr, qkv, dqkv, rows, dim, semantics == NITRO_Q8_LAST_BLOCK, s),
+                  "q8_matmul3 launch");
         attend(l);  // RoPE + KV append + attention -> m->attn (:594-662)
         q8(m, m->o_wo, l, dim, dim, m->attn.ptr, m->proj.ptr, rows, semantics, s);  // :663
         // x += wo . attn; xb = rms_norm(x) (:664-669)
         hip_check(launch_add_rmsnorm(m->x.ptr, m->proj.ptr, m->f32(m->o_rms_ffn) + (size_t)l * dim,
                                      m->xb.ptr, rows, dim, s),
                   "rmsnorm launch");
-        q8(m, m->o_w1, l, hid, dim, m->xb.ptr, m->hb.ptr, rows, semantics, s);   // :670
-        q8(m, m->o_w3, l, hid, dim, m->xb.ptr, m->hb2.ptr, rows, semantics, s);  // :671
-        hip_check(launch_swiglu(m->hb.ptr, m->hb2.ptr, (size_t)rows * hid, s), "swiglu launch");
+        // hb = silu(w1.xb) * (w3.xb) in one launch (:670-680)
+        hip_check(launch_q8_swiglu(m->q8(m->o_w1, l, hid, dim), m->q8(m->o_w3, l, hid, dim), m->xb.ptr,
+                                   m->hb.ptr, rows, dim, hid, semantics == NITRO_Q8_LAST_BLOCK, s),
+                  "q8_swiglu launch");
         q8(m, m->o_w2, l, dim, hid, m->hb.ptr, m->ffn.ptr, rows, semantics, s);  // :682
     }
 }

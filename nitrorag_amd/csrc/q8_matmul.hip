@@ -23,12 +23,20 @@
 // round-robin and add their partial tiles through LDS.  Batches of more than
 // 16 rows reuse the dequantised weights for every 16-row batch tile.
 //
+// A launch may cover a group of up to 3 matrices with the same input x and
+// n (wq/wk/wv; w1/w3): a workgroup computes the same 16 rows of each member
+// (members with fewer rows skip the upper tiles), and for the w1/w3 pair the
+// epilogue applies SwiGLU, hb = silu(w1.x) * (w3.x) (src/model_q8.cpp:672-680),
+// so the hidden activations are written once.
+//
 // Batches of 1..4 rows use a VALU form of the same lane layout (q8_gemv):
 // each lane forms the dot products of its 16 weights with x directly, the
 // four lane groups of a row are summed with gfx950's row-swap permutes and
 // the waves through LDS.  Both kernels issue the weight loads of Q8_UNROLL
 // chunks before using any, so enough HBM reads are in flight per wave.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 #include "device_pool.hpp"
 
@@ -75,12 +83,22 @@ __device__ __forceinline__ float dequant(uint32_t q4, int j, float scale) {
     return (float)(int)(int8_t)(q4 >> (8 * j)) * scale;
 }
 
-template <bool LAST_BLOCK_ONLY>
-__global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(const uint8_t* __restrict__ w,
-                                                                   const float* __restrict__ x,
-                                                                   float* __restrict__ out,
-                                                                   int batch, int n, int d) {
-    __shared__ f32x4 red[Q8_WAVES - 1][Q8_MAX_BTILES][64];
+}  // namespace
+
+// Up to 3 matrices sharing x (same n); out[m] is [batch][d[m]].
+struct Q8Group {
+    const uint8_t* w[3];
+    float* out[3];
+    int d[3];
+};
+
+namespace {
+
+template <int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY>
+__global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, const float* __restrict__ x,
+                                                                   int batch, int n) {
+    constexpr int U = NMAT == 1 ? Q8_UNROLL : 2;  // chunks in flight per wave
+    __shared__ f32x4 red[Q8_WAVES - 1][NMAT][Q8_MAX_BTILES][64];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int r = lane & 15;
@@ -90,58 +108,75 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(const uint8_t*
     const int btiles = min(Q8_MAX_BTILES, (batch - b0 + 15) / 16);
     const int nb = n / Q8_BLOCK;
     const int nchunk = (nb + 1) / 2;
-    const uint8_t* wrow = w + (size_t)min(row0 + r, d - 1) * nb * Q8_BLOCK_BYTES;
-
-    f32x4 acc[Q8_MAX_BTILES];
+    const uint8_t* wrow[NMAT];
+    bool act[NMAT];  // uniform: this tile has rows of member m
 #pragma unroll
-    for (int t = 0; t < Q8_MAX_BTILES; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < NMAT; m++) {
+        act[m] = row0 < grp.d[m];
+        wrow[m] = grp.w[m] + (size_t)min(row0 + r, grp.d[m] - 1) * nb * Q8_BLOCK_BYTES;
+    }
+
+    f32x4 acc[NMAT][Q8_MAX_BTILES];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int t = 0; t < Q8_MAX_BTILES; t++) acc[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int first = LAST_BLOCK_ONLY ? nchunk - 1 : 0;
-    // Wave w takes chunks first + (round*Q8_WAVES + w)*Q8_UNROLL + u.
-    for (int base = first + wave * Q8_UNROLL; base < nchunk; base += Q8_WAVES * Q8_UNROLL) {
-        Q8Slice sl[Q8_UNROLL];
+    // Wave w takes chunks first + (round*Q8_WAVES + w)*U + u.
+    for (int base = first + wave * U; base < nchunk; base += Q8_WAVES * U) {
+        Q8Slice sl[U][NMAT];
 #pragma unroll
-        for (int u = 0; u < Q8_UNROLL; u++) {
+        for (int u = 0; u < U; u++) {
             const int blk = 2 * (base + u) + (g >> 1);
             const bool valid = base + u < nchunk && blk < nb && (!LAST_BLOCK_ONLY || blk == nb - 1);
-            sl[u] = load_slice(wrow, blk, g & 1, valid);
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) sl[u][m] = load_slice(wrow[m], blk, g & 1, valid && act[m]);
         }
+        // Per batch tile, the x operands of all U chunks are loaded together
+        // (one round trip), then the chunks' MFMAs run.
 #pragma unroll
-        for (int u = 0; u < Q8_UNROLL; u++) {
-            if (base + u >= nchunk) break;  // uniform
-            const int blk = 2 * (base + u) + (g >> 1);
-            const bool valid = blk < nb && (!LAST_BLOCK_ONLY || blk == nb - 1);
-            float wv[16];
+        for (int t = 0; t < Q8_MAX_BTILES; t++) {
+            if (t >= btiles) break;  // uniform
+            const int bb = b0 + t * 16 + r;  // batch row this lane feeds (B operand column)
+            float xv[U][16];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                wv[j] = dequant(sl[u].q[0], j, sl[u].scale);
-                wv[4 + j] = dequant(sl[u].q[1], j, sl[u].scale);
-                wv[8 + j] = dequant(sl[u].q[2], j, sl[u].scale);
-                wv[12 + j] = dequant(sl[u].q[3], j, sl[u].scale);
+            for (int u = 0; u < U; u++) {
+                const int blk = 2 * (base + u) + (g >> 1);
+                const bool valid = base + u < nchunk && blk < nb && (!LAST_BLOCK_ONLY || blk == nb - 1);
+                if (valid && bb < batch) {
+                    const float4* xp = reinterpret_cast<const float4*>(
+                        x + (size_t)bb * n + blk * Q8_BLOCK + 16 * (g & 1));
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float4 v = xp[i];
+                        xv[u][4 * i] = v.x;
+                        xv[u][4 * i + 1] = v.y;
+                        xv[u][4 * i + 2] = v.z;
+                        xv[u][4 * i + 3] = v.w;
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 16; q++) xv[u][q] = 0.0f;
+                }
             }
-            const int k0 = blk * Q8_BLOCK + 16 * (g & 1);
 #pragma unroll
-            for (int t = 0; t < Q8_MAX_BTILES; t++) {
-                if (t < btiles) {  // uniform
-                    const int bb = b0 + t * 16 + r;  // batch row this lane feeds (B operand column)
-                    float xv[16];
-                    if (valid && bb < batch) {
-                        const float4* xp = reinterpret_cast<const float4*>(x + (size_t)bb * n + k0);
+            for (int u = 0; u < U; u++) {
+                if (base + u >= nchunk) break;  // uniform
 #pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            const float4 v = xp[i];
-                            xv[4 * i] = v.x;
-                            xv[4 * i + 1] = v.y;
-                            xv[4 * i + 2] = v.z;
-                            xv[4 * i + 3] = v.w;
-                        }
-                    } else {
+                for (int m = 0; m < NMAT; m++) {
+                    if (!act[m]) continue;  // uniform
+                    float wv[16];
 #pragma unroll
-                        for (int m = 0; m < 16; m++) xv[m] = 0.0f;
+                    for (int jj = 0; jj < 4; jj++) {
+                        wv[jj] = dequant(sl[u][m].q[0], jj, sl[u][m].scale);
+                        wv[4 + jj] = dequant(sl[u][m].q[1], jj, sl[u][m].scale);
+                        wv[8 + jj] = dequant(sl[u][m].q[2], jj, sl[u][m].scale);
+                        wv[12 + jj] = dequant(sl[u][m].q[3], jj, sl[u][m].scale);
                     }
 #pragma unroll
-                    for (int m = 0; m < 16; m++)
-                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[m], xv[m], acc[t], 0, 0, 0);
+                    for (int q = 0; q < 16; q++)
+                        acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[q], xv[u][q], acc[m][t], 0, 0, 0);
                 }
             }
         }
@@ -151,44 +186,60 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(const uint8_t*
     // out^T[row0 + 4*(l/16) + j][b0 + 16t + l%16], j = 0..3.
     if (wave > 0) {
 #pragma unroll
-        for (int t = 0; t < Q8_MAX_BTILES; t++)
-            if (t < btiles) red[wave - 1][t][lane] = acc[t];
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int t = 0; t < Q8_MAX_BTILES; t++)
+                if (t < btiles) red[wave - 1][m][t][lane] = acc[m][t];
     }
     __syncthreads();
     if (wave > 0) return;
 #pragma unroll
     for (int t = 0; t < Q8_MAX_BTILES; t++) {
         if (t >= btiles) break;
-        f32x4 s = acc[t];
+        f32x4 s[NMAT];
 #pragma unroll
-        for (int v = 0; v < Q8_WAVES - 1; v++) s += red[v][t][lane];
+        for (int m = 0; m < NMAT; m++) {
+            s[m] = acc[m][t];
+#pragma unroll
+            for (int v = 0; v < Q8_WAVES - 1; v++) s[m] += red[v][m][t][lane];
+        }
         const int bb = b0 + t * 16 + (lane & 15);
         if (bb >= batch) continue;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int row = row0 + 4 * (lane >> 4) + j;
-            if (row < d) out[(size_t)bb * d + row] = s[j];
+            if constexpr (SWIGLU) {
+                if (row < grp.d[0]) {
+                    float h = s[0][j];
+                    h *= 1.0f / (1.0f + expf(-h));
+                    grp.out[0][(size_t)bb * grp.d[0] + row] = h * s[1][j];
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < NMAT; m++)
+                    if (row < grp.d[m]) grp.out[m][(size_t)bb * grp.d[m] + row] = s[m][j];
+            }
         }
     }
 }
 
 // Batches of 1..NB rows on the VALU: lane (r, g) dots its 16 weights of row
 // row0 + r with x[b] at the same 16 k for every b.  A workgroup of
-// GEMV_WAVES waves owns 16 rows; per slab of GEMV_WAVES*Q8_UNROLL chunks
-// (2048 k) each wave first issues the weight loads of its Q8_UNROLL chunks,
-// then the workgroup stages the slab of x in LDS (lanes of a lane group read
-// the same x, which LDS broadcasts), and then the waves compute.  The 4 lane
-// groups are summed with row-swap permutes and the waves through LDS in a
-// fixed order (results are repeatable bit for bit).
+// GEMV_WAVES waves owns 16 rows (of each group member); per slab of
+// GEMV_WAVES*U chunks (2048 k for one matrix) each wave first issues the
+// weight loads of its U chunks, then the workgroup stages the slab of x in
+// LDS (lanes of a lane group read the same x, which LDS broadcasts), and then
+// the waves compute.  The 4 lane groups are summed with row-swap permutes and
+// the waves through LDS in a fixed order (results are repeatable bit for bit).
 constexpr int GEMV_WAVES = 8;
-constexpr int GEMV_SLAB = GEMV_WAVES * Q8_UNROLL * 64;  // k per slab
 
-template <int NB, bool LAST_BLOCK_ONLY>
-__global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(const uint8_t* __restrict__ w,
-                                                                   const float* __restrict__ x,
-                                                                   float* __restrict__ out, int n, int d) {
-    __shared__ __attribute__((aligned(16))) float xs[NB][GEMV_SLAB];
-    __shared__ float red[GEMV_WAVES][NB][16];
+template <int NB, int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY>
+__global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, const float* __restrict__ x,
+                                                                   int n) {
+    constexpr int U = NMAT == 1 ? Q8_UNROLL : 2;  // chunks in flight per wave
+    constexpr int SLAB = GEMV_WAVES * U * 64;     // k per slab
+    __shared__ __attribute__((aligned(16))) float xs[NB][SLAB];
+    __shared__ float red[GEMV_WAVES][NMAT][NB][16];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int r = lane & 15;
@@ -196,24 +247,33 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(const uint8_t*
     const int row0 = blockIdx.x * 16;
     const int nb = n / Q8_BLOCK;
     const int nchunk = (nb + 1) / 2;
-    const uint8_t* wrow = w + (size_t)min(row0 + r, d - 1) * nb * Q8_BLOCK_BYTES;
-
-    float acc[NB];
+    const uint8_t* wrow[NMAT];
+    bool act[NMAT];
 #pragma unroll
-    for (int b = 0; b < NB; b++) acc[b] = 0.0f;
+    for (int m = 0; m < NMAT; m++) {
+        act[m] = row0 < grp.d[m];
+        wrow[m] = grp.w[m] + (size_t)min(row0 + r, grp.d[m] - 1) * nb * Q8_BLOCK_BYTES;
+    }
+
+    float acc[NMAT][NB];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int b = 0; b < NB; b++) acc[m][b] = 0.0f;
 
     // In the last-block form only the final chunk matters: one slab holding it.
     const int k_begin = LAST_BLOCK_ONLY ? (nchunk - 1) * 64 : 0;
-    for (int slab = k_begin; slab < n; slab += GEMV_SLAB) {
-        const int c0 = slab / 64 + wave * Q8_UNROLL;  // this wave's first chunk
-        Q8Slice sl[Q8_UNROLL];
+    for (int slab = k_begin; slab < n; slab += SLAB) {
+        const int c0 = slab / 64 + wave * U;  // this wave's first chunk
+        Q8Slice sl[U][NMAT];
 #pragma unroll
-        for (int u = 0; u < Q8_UNROLL; u++) {
+        for (int u = 0; u < U; u++) {
             const int blk = 2 * (c0 + u) + (g >> 1);
             const bool valid = c0 + u < nchunk && blk < nb && (!LAST_BLOCK_ONLY || blk == nb - 1);
-            sl[u] = load_slice(wrow, blk, g & 1, valid);
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) sl[u][m] = load_slice(wrow[m], blk, g & 1, valid && act[m]);
         }
-        const int slab_len = min(GEMV_SLAB, n - slab);  // multiple of 32
+        const int slab_len = min(SLAB, n - slab);  // multiple of 32
         __syncthreads();  // previous slab's x reads are done
         for (int i = threadIdx.x; i < NB * (slab_len / 4); i += 64 * GEMV_WAVES) {
             const int b = i / (slab_len / 4), f = i - b * (slab_len / 4);
@@ -222,79 +282,129 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(const uint8_t*
         }
         __syncthreads();
 #pragma unroll
-        for (int u = 0; u < Q8_UNROLL; u++) {
+        for (int u = 0; u < U; u++) {
             const int blk = 2 * (c0 + u) + (g >> 1);
             const bool valid = c0 + u < nchunk && blk < nb && (!LAST_BLOCK_ONLY || blk == nb - 1);
             if (!valid) continue;  // no cross-lane work inside the chunk loop
             const int kl = blk * Q8_BLOCK + 16 * (g & 1) - slab;  // k within the slab
-            float wv[16];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                wv[j] = dequant(sl[u].q[0], j, sl[u].scale);
-                wv[4 + j] = dequant(sl[u].q[1], j, sl[u].scale);
-                wv[8 + j] = dequant(sl[u].q[2], j, sl[u].scale);
-                wv[12 + j] = dequant(sl[u].q[3], j, sl[u].scale);
-            }
+            for (int m = 0; m < NMAT; m++) {
+                if (!act[m]) continue;
+                float wv[16];
 #pragma unroll
-            for (int b = 0; b < NB; b++) {
-                const float4* xp = reinterpret_cast<const float4*>(&xs[b][kl]);
+                for (int jj = 0; jj < 4; jj++) {
+                    wv[jj] = dequant(sl[u][m].q[0], jj, sl[u][m].scale);
+                    wv[4 + jj] = dequant(sl[u][m].q[1], jj, sl[u][m].scale);
+                    wv[8 + jj] = dequant(sl[u][m].q[2], jj, sl[u][m].scale);
+                    wv[12 + jj] = dequant(sl[u][m].q[3], jj, sl[u][m].scale);
+                }
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float4 v = xp[i];
-                    acc[b] = fmaf(wv[4 * i], v.x, acc[b]);
-                    acc[b] = fmaf(wv[4 * i + 1], v.y, acc[b]);
-                    acc[b] = fmaf(wv[4 * i + 2], v.z, acc[b]);
-                    acc[b] = fmaf(wv[4 * i + 3], v.w, acc[b]);
+                for (int b = 0; b < NB; b++) {
+                    const float4* xp = reinterpret_cast<const float4*>(&xs[b][kl]);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 v = xp[q];
+                        acc[m][b] = fmaf(wv[4 * q], v.x, acc[m][b]);
+                        acc[m][b] = fmaf(wv[4 * q + 1], v.y, acc[m][b]);
+                        acc[m][b] = fmaf(wv[4 * q + 2], v.z, acc[m][b]);
+                        acc[m][b] = fmaf(wv[4 * q + 3], v.w, acc[m][b]);
+                    }
                 }
             }
         }
     }
 #pragma unroll
-    for (int b = 0; b < NB; b++) acc[b] = sum_over_rows(acc[b]);  // lanes r, r+16, r+32, r+48
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int b = 0; b < NB; b++) acc[m][b] = sum_over_rows(acc[m][b]);  // lanes r, r+16, r+32, r+48
     if (g == 0) {
 #pragma unroll
-        for (int b = 0; b < NB; b++) red[wave][b][r] = acc[b];
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int b = 0; b < NB; b++) red[wave][m][b][r] = acc[m][b];
     }
     __syncthreads();
     if (threadIdx.x >= NB * 16) return;
     const int b = threadIdx.x / 16, rr = threadIdx.x % 16;
-    if (row0 + rr >= d) return;
-    float sum = 0.0f;
+    const int row = row0 + rr;
+    float sum[NMAT];
 #pragma unroll
-    for (int v = 0; v < GEMV_WAVES; v++) sum += red[v][b][rr];
-    out[(size_t)b * d + row0 + rr] = sum;
+    for (int m = 0; m < NMAT; m++) {
+        sum[m] = 0.0f;
+#pragma unroll
+        for (int v = 0; v < GEMV_WAVES; v++) sum[m] += red[v][m][b][rr];
+    }
+    if constexpr (SWIGLU) {
+        if (row < grp.d[0]) {
+            float h = sum[0];
+            h *= 1.0f / (1.0f + expf(-h));
+            grp.out[0][(size_t)b * grp.d[0] + row] = h * sum[1];
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+            if (row < grp.d[m]) grp.out[m][(size_t)b * grp.d[m] + row] = sum[m];
+    }
 }
 
-template <int NB>
-static void launch_gemv(const uint8_t* w, const float* x, float* out, int n, int d, bool last,
-                        hipStream_t stream) {
-    const dim3 grid((unsigned)((d + 15) / 16)), block(64 * GEMV_WAVES);
+template <int NB, int NMAT, bool SWIGLU>
+static void launch_gemv(const Q8Group& grp, const float* x, int n, int dmax, bool last, hipStream_t stream) {
+    const dim3 grid((unsigned)((dmax + 15) / 16)), block(64 * GEMV_WAVES);
     if (last)
-        hipLaunchKernelGGL((q8_gemv_kernel<NB, true>), grid, block, 0, stream, w, x, out, n, d);
+        hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, true>), grid, block, 0, stream, grp, x, n);
     else
-        hipLaunchKernelGGL((q8_gemv_kernel<NB, false>), grid, block, 0, stream, w, x, out, n, d);
+        hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, false>), grid, block, 0, stream, grp, x, n);
+}
+
+template <int NMAT, bool SWIGLU>
+static void launch_group(const Q8Group& grp, const float* x, int batch, int n, int dmax, bool last,
+                         hipStream_t stream) {
+    if (batch <= Q8_GEMV_MAX_BATCH) {
+        switch (batch) {
+            case 1: launch_gemv<1, NMAT, SWIGLU>(grp, x, n, dmax, last, stream); break;
+            case 2: launch_gemv<2, NMAT, SWIGLU>(grp, x, n, dmax, last, stream); break;
+            case 3: launch_gemv<3, NMAT, SWIGLU>(grp, x, n, dmax, last, stream); break;
+            default: launch_gemv<4, NMAT, SWIGLU>(grp, x, n, dmax, last, stream); break;
+        }
+        return;
+    }
+    const dim3 grid((unsigned)((dmax + 15) / 16),
+                    (unsigned)((batch + 16 * Q8_MAX_BTILES - 1) / (16 * Q8_MAX_BTILES)));
+    const dim3 block(64 * Q8_WAVES);
+    if (last)
+        hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, true>), grid, block, 0, stream, grp, x, batch, n);
+    else
+        hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, false>), grid, block, 0, stream, grp, x, batch, n);
 }
 
 }  // namespace
 
 hipError_t launch_q8_matmul(const void* w, const float* x, float* out, int batch, int n, int d,
                             bool last_block_only, hipStream_t stream) {
-    const dim3 grid((unsigned)((d + 15) / 16), (unsigned)((batch + 16 * Q8_MAX_BTILES - 1) / (16 * Q8_MAX_BTILES)));
-    const dim3 block(64 * Q8_WAVES);
-    const uint8_t* wb = static_cast<const uint8_t*>(w);
-    if (batch <= Q8_GEMV_MAX_BATCH) {
-        switch (batch) {
-            case 1: launch_gemv<1>(wb, x, out, n, d, last_block_only, stream); break;
-            case 2: launch_gemv<2>(wb, x, out, n, d, last_block_only, stream); break;
-            case 3: launch_gemv<3>(wb, x, out, n, d, last_block_only, stream); break;
-            default: launch_gemv<4>(wb, x, out, n, d, last_block_only, stream); break;
-        }
-        return hipGetLastError();
+    Q8Group grp{{static_cast<const uint8_t*>(w), nullptr, nullptr}, {out, nullptr, nullptr}, {d, 0, 0}};
+    launch_group<1, false>(grp, x, batch, n, d, last_block_only, stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_matmul3(const void* const* w, const float* x, float* const* out, const int* d,
+                             int batch, int n, bool last_block_only, hipStream_t stream) {
+    Q8Group grp{};
+    for (int m = 0; m < 3; m++) {
+        grp.w[m] = static_cast<const uint8_t*>(w[m]);
+        grp.out[m] = out[m];
+        grp.d[m] = d[m];
     }
-    if (last_block_only)
-        hipLaunchKernelGGL(q8_matmul_kernel<true>, grid, block, 0, stream, wb, x, out, batch, n, d);
-    else
-        hipLaunchKernelGGL(q8_matmul_kernel<false>, grid, block, 0, stream, wb, x, out, batch, n, d);
+    const int dmax = std::max(d[0], std::max(d[1], d[2]));
+    launch_group<3, false>(grp, x, batch, n, dmax, last_block_only, stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_swiglu(const void* w1, const void* w3, const float* x, float* hb, int batch, int n,
+                            int hidden, bool last_block_only, hipStream_t stream) {
+    Q8Group grp{{static_cast<const uint8_t*>(w1), static_cast<const uint8_t*>(w3), nullptr},
+                {hb, nullptr, nullptr},
+                {hidden, hidden, 0}};
+    launch_group<2, true>(grp, x, batch, n, hidden, last_block_only, stream);
     return hipGetLastError();
 }
 
