@@ -104,6 +104,24 @@ def q8_matmul_bulk(w: np.ndarray, x: np.ndarray, n: int, d: int, n_threads: int 
     return out
 
 
+def scale_residual_outputs(blob: np.ndarray, factor: float) -> np.ndarray:
+    """A copy of a model file (src/Server_Inference.cpp:45-69) with the block
+    scales of wo and w2 multiplied by `factor` — what the reference driver's
+    random model with out_scale=factor holds (exact for powers of two)."""
+    b = np.array(blob, dtype=np.uint8, copy=True)
+    D, Hd, L, H, Hkv, V, S = (int(v) for v in b[:28].view(np.int32))
+    KV = D // H * Hkv
+    q8b = lambda rows, cols: rows * (cols // Q8_BLOCK) * Q8_BLOCK_BYTES
+    o_wo = 28 + V * D * 4 + L * D * 4 + L * (q8b(D, D) + 2 * q8b(KV, D))
+    o_w2 = o_wo + L * q8b(D, D) + L * D * 4 + L * q8b(Hd, D)
+    for off, nbytes in ((o_wo, L * q8b(D, D)), (o_w2, L * q8b(D, Hd))):
+        blocks = b[off:off + nbytes].reshape(-1, Q8_BLOCK_BYTES)
+        sc = blocks[:, :4].copy().view(np.float32) * np.float32(factor)
+        blocks[:, :4] = sc.view(np.uint8).reshape(-1, 4)
+        b[off:off + nbytes] = blocks.reshape(-1)
+    return b
+
+
 def _p(a: np.ndarray):
     assert a.dtype == np.float32 and a.flags.c_contiguous
     return a.ctypes.data_as(_f32p)

@@ -35,7 +35,7 @@ def lib() -> ctypes.CDLL:
         L.ref_hash_block_state.argtypes = [u64, _i32p, ci]
         L.ref_hash_block_state.restype = u64
         L.ref_set_threads.argtypes = [ci]
-        L.ref_model_create.argtypes = [ci, ci, ci, ci, ci, ci, ci, ci, ci, ci, u64]
+        L.ref_model_create.argtypes = [ci, ci, ci, ci, ci, ci, ci, ci, ci, ci, u64, ctypes.c_float]
         L.ref_model_create.restype = vp
         L.ref_model_serialize.argtypes = [vp, ctypes.POINTER(ctypes.c_uint8), u64]
         L.ref_model_serialize.restype = u64
@@ -61,6 +61,11 @@ def lib() -> ctypes.CDLL:
         L.ref_read_contiguous_cache.argtypes = [vp, _f32p, _f32p]
         L.ref_write_contiguous_cache.argtypes = [vp, _f32p, _f32p]
         L.ref_block_table.argtypes = [vp, ci, _i32p, ci]
+        L.ref_sched_create.argtypes = [vp, ci]
+        L.ref_sched_add.argtypes = [vp, ci, _i32p, ci]
+        L.ref_sched_active.argtypes = [vp]
+        L.ref_sched_step.argtypes = [vp]
+        L.ref_sched_state.argtypes = [vp, _i32p, ci]
         _lib = L
     return _lib
 
@@ -109,14 +114,16 @@ class RefWorld:
 
     @classmethod
     def random_model(cls, n_heads, n_kv_heads, head_dim, n_layers, vocab, seq_len, hidden_dim,
-                     total_blocks, max_rows=64, max_seqs=8, seed=1, threads=1):
+                     total_blocks, max_rows=64, max_seqs=8, seed=1, threads=1, out_scale=1.0):
         """A world whose model has every weight random (ref_model_create): for
-        logits-level golden vectors of the forward passes."""
+        logits-level golden vectors of the forward passes.  out_scale > 1
+        strengthens wo and w2 so the layers, not the token's own embedding,
+        decide the argmax."""
         self = cls.__new__(cls)
         L = lib()
         L.ref_set_threads(threads)
         self.h = L.ref_model_create(n_heads, n_kv_heads, head_dim, n_layers, vocab, seq_len,
-                                    hidden_dim, total_blocks, max_rows, max_seqs, seed)
+                                    hidden_dim, total_blocks, max_rows, max_seqs, seed, out_scale)
         self.n_heads, self.n_kv_heads, self.head_dim = n_heads, n_kv_heads, head_dim
         self.n_layers, self.total_blocks, self.max_seqs = n_layers, total_blocks, max_seqs
         self.seq_len, self.max_rows, self.vocab = seq_len, max_rows, vocab
@@ -167,6 +174,28 @@ class RefWorld:
         n = lib().ref_snapshot(self.h, buf.ctypes.data_as(_i32p), cap)
         assert n >= 0
         return pm.decode_snapshot(buf[:n], self.total_blocks, self.max_seqs)
+
+    # ---- Continuous_Scheduler (src/pagedMemory.hpp:287-399) ---------------
+    def sched_create(self, max_tokens_per_batch=256):
+        assert lib().ref_sched_create(self.h, max_tokens_per_batch) == 0
+
+    def sched_add(self, req_id, prompt):
+        t = np.ascontiguousarray(prompt, dtype=np.int32)
+        assert lib().ref_sched_add(self.h, req_id, t.ctypes.data_as(_i32p), t.size) == 0
+
+    def sched_active(self) -> bool:
+        return lib().ref_sched_active(self.h) != 0
+
+    def sched_step(self) -> int:
+        """0, or 1 when the reference called exit() (pool exhausted)."""
+        return int(lib().ref_sched_step(self.h))
+
+    def sched_state(self) -> np.ndarray:
+        cap = 1 << 16
+        buf = np.zeros(cap, dtype=np.int32)
+        n = lib().ref_sched_state(self.h, buf.ctypes.data_as(_i32p), cap)
+        assert n >= 0
+        return buf[:n].copy()
 
     def block_table(self, slot) -> np.ndarray:
         buf = np.zeros(4096, dtype=np.int32)

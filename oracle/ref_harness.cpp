@@ -74,6 +74,8 @@ struct World {
     std::vector<BlockQ8> wq, wk, wv, wo, w1, w2, w3;
     int kv_dim = 0, head_size = 0, max_rows = 0, total_blocks = 0;
     std::vector<float> key_cache, value_cache;
+    Continuous_Scheduler* sched = nullptr;
+    std::vector<Request*> sched_reqs;  // in the order they were added
 };
 
 void fill_q8(std::vector<BlockQ8>& m, int rows, int cols, uint64_t& rng, float scale) {
@@ -118,28 +120,31 @@ void ref_q8_matmul_bulk(float* out, const float* x, const void* w, int batch, in
 // identity rotation so K/V rows in the pool are exactly the computed k/v.
 static void* build_world(int n_heads, int n_kv_heads, int head_size, int n_layers, int vocab,
                          int seq_len, int hidden_dim, int total_blocks, int max_rows, int max_seqs,
-                         uint64_t seed, bool random_model);
+                         uint64_t seed, bool random_model, float out_scale);
 
 void* ref_world_create(int n_heads, int n_kv_heads, int head_size, int n_layers, int vocab,
                        int seq_len, int total_blocks, int max_rows, int max_seqs, uint64_t seed) {
     return build_world(n_heads, n_kv_heads, head_size, n_layers, vocab, seq_len, 32, total_blocks,
-                       max_rows, max_seqs, seed, false);
+                       max_rows, max_seqs, seed, false, 1.0f);
 }
 
 // A tiny model with every weight random (embedding U[-1,1), rms weights
 // U[0.5,1.5), Q8 matrices with random int8 and per-block scales), and the
 // usual RoPE tables (angle pos * 10000^(-2i/head_size), i < head_size/2) —
-// for logits-level golden vectors of the forward passes.
+// for logits-level golden vectors of the forward passes.  out_scale multiplies
+// the scales of wo and w2 (the two products added to the residual stream):
+// above 1 the layers outweigh the token's own embedding in the tied
+// classifier, so the argmax depends on the attention context.
 void* ref_model_create(int n_heads, int n_kv_heads, int head_size, int n_layers, int vocab,
                        int seq_len, int hidden_dim, int total_blocks, int max_rows, int max_seqs,
-                       uint64_t seed) {
+                       uint64_t seed, float out_scale) {
     return build_world(n_heads, n_kv_heads, head_size, n_layers, vocab, seq_len, hidden_dim,
-                       total_blocks, max_rows, max_seqs, seed, true);
+                       total_blocks, max_rows, max_seqs, seed, true, out_scale);
 }
 
 static void* build_world(int n_heads, int n_kv_heads, int head_size, int n_layers, int vocab,
                          int seq_len, int hidden_dim, int total_blocks, int max_rows, int max_seqs,
-                         uint64_t seed, bool random_model) {
+                         uint64_t seed, bool random_model, float out_scale) {
     World* W = new World();
     Config_Transformer& c = W->c;
     c.dim = n_heads * head_size;
@@ -190,6 +195,8 @@ static void* build_world(int n_heads, int n_kv_heads, int head_size, int n_layer
         rand_q8(W->w1, n_layers * c.hidden_dim, c.dim);
         rand_q8(W->w3, n_layers * c.hidden_dim, c.dim);
         rand_q8(W->w2, n_layers * c.dim, c.hidden_dim);
+        for (auto& b : W->wo) b.scale *= out_scale;
+        for (auto& b : W->w2) b.scale *= out_scale;
         for (int pos = 0; pos < seq_len; pos++)
             for (int i = 0; i < head_size / 2; i++) {
                 const double ang = pos * std::pow(10000.0, -2.0 * i / head_size);
@@ -274,6 +281,8 @@ int ref_read_logits(void* p, int rows, float* out) {
 void ref_world_destroy(void* p) {
     World* W = (World*)p;
     for (auto* r : W->reqs) delete r;
+    for (auto* r : W->sched_reqs) delete r;
+    delete W->sched;
     delete W->cache;
     delete W->mem;
     RunState& s = W->s;
@@ -498,6 +507,78 @@ int ref_write_contiguous_cache(void* p, const float* key_cache, const float* val
     std::memcpy(W->key_cache.data(), key_cache, sizeof(float) * W->key_cache.size());
     std::memcpy(W->value_cache.data(), value_cache, sizeof(float) * W->value_cache.size());
     return 0;
+}
+
+// ---- Continuous_Scheduler (src/pagedMemory.hpp:287-399) -------------------
+// One scheduler over the world's model, block manager and prefix cache.  The
+// budget member max_tokens_per_batch (256 in the reference) may be set so
+// small models exercise chunked prefill; everything else is the reference's.
+
+int ref_sched_create(void* p, int max_tokens_per_batch) {
+    World* W = (World*)p;
+    if (W->sched) return 1;
+    W->sched = new Continuous_Scheduler();
+    W->sched->max_tokens_per_batch = max_tokens_per_batch;
+    return 0;
+}
+
+int ref_sched_add(void* p, int req_id, const int* prompt, int n) {
+    World* W = (World*)p;
+    if (!W->sched || n <= 0) return 1;
+    Request* r = new Request(req_id, std::vector<int>(prompt, prompt + n));
+    W->sched_reqs.push_back(r);
+    W->sched->add_request(r);
+    return 0;
+}
+
+int ref_sched_active(void* p) { return ((World*)p)->sched->has_active_requests() ? 1 : 0; }
+
+// Returns 0, or 1 when the reference called exit() (pool exhausted).
+int ref_sched_step(void* p) {
+    World* W = (World*)p;
+    try {
+        W->sched->step(&W->c, &W->w, &W->s, *W->mem, *W->cache);
+    } catch (const RefExit&) {
+        return 1;
+    }
+    return 0;
+}
+
+// Serialises the scheduler into an int32 stream:
+//   [n, running_batch ids...] [n, waiting_queue ids front->back...] [n_requests]
+//   then per request, in the order added: [req_id, prefill_idx, is_prefill_done,
+//   is_finished, next_token_to_process, |generated|, generated...,
+//   logical_token_count, hash lo, hash hi, |buffer|, buffer..., |table|, table...].
+// Returns the word count (negated when cap is too small).
+int ref_sched_state(void* p, int32_t* buf, int cap) {
+    World* W = (World*)p;
+    std::vector<int32_t> o;
+    o.push_back((int32_t)W->sched->running_batch.size());
+    for (Request* r : W->sched->running_batch) o.push_back(r->req_id);
+    std::queue<Request*> q = W->sched->waiting_queue;
+    o.push_back((int32_t)q.size());
+    for (; !q.empty(); q.pop()) o.push_back(q.front()->req_id);
+    o.push_back((int32_t)W->sched_reqs.size());
+    for (Request* r : W->sched_reqs) {
+        o.push_back(r->req_id);
+        o.push_back(r->prefill_idx);
+        o.push_back(r->is_prefill_done ? 1 : 0);
+        o.push_back(r->is_finished ? 1 : 0);
+        o.push_back(r->next_token_to_process);
+        o.push_back((int32_t)r->generated_tokens.size());
+        for (int t : r->generated_tokens) o.push_back(t);
+        const Sequence& q2 = r->seq;
+        o.push_back(q2.logical_token_count);
+        o.push_back((int32_t)(uint32_t)(q2.current_hash & 0xffffffffu));
+        o.push_back((int32_t)(uint32_t)(q2.current_hash >> 32));
+        o.push_back((int32_t)q2.token_buffer.size());
+        for (int t : q2.token_buffer) o.push_back(t);
+        o.push_back((int32_t)q2.block_table.size());
+        for (int t : q2.block_table) o.push_back(t);
+    }
+    if ((int)o.size() > cap) return -(int)o.size();
+    std::memcpy(buf, o.data(), o.size() * sizeof(int32_t));
+    return (int)o.size();
 }
 
 int ref_block_table(void* p, int slot, int* out, int cap) {

@@ -28,6 +28,11 @@ Writes, next to this script:
                              a tiny random model in the reference's file layout and
                              the logits of forward_prefill_chunk / forward_paged /
                              forward_decode_batch over a scripted session
+  sched_traces.json + sched_traces.npz
+                             steps of the reference's Continuous_Scheduler over the tiny
+                             model with wo/w2 scaled by 64: scheduler state and
+                             block-manager snapshot words per step, and the top logits
+                             of the rows each step left behind
 """
 from __future__ import annotations
 
@@ -533,6 +538,128 @@ def make_model():
     return blob, dict(model=MODEL, script=meta, final_tables=tables), arrays
 
 
+# Scheduler scenarios over the tiny model with wo/w2 scaled by SCHED_OUT_SCALE
+# (so the layers, not the token's own embedding, decide the argmax).  Each is
+# (name, total_blocks, max_tokens_per_batch, {step: [(req_id, prompt_len or
+# prompt source)]}); prompts are drawn from SCHED_PROMPT_SEED.
+SCHED_OUT_SCALE = 64.0
+SCHED_PROMPT_SEED = 9
+SCHED_TOP = 16
+
+
+def sched_scenarios():
+    rng = np.random.default_rng(SCHED_PROMPT_SEED)
+    V = MODEL["vocab"]
+    tok = lambda n: [int(t) for t in rng.integers(0, V, n)]
+    shared = tok(40)
+    s = [("shared_prompt", 48, 256, {0: [(i, shared) for i in range(5)]})]
+    s.append(("chunked", 48, 24, {0: [(0, tok(70)), (1, tok(33))], 3: [(2, tok(50))],
+                                  6: [(3, tok(5))]}))
+    s.append(("budget_exhausted", 48, 3, {0: [(0, tok(20)), (1, tok(9)), (2, tok(5)),
+                                              (3, tok(7))]}))
+    p = tok(32)
+    s.append(("full_hit", 48, 256, {0: [(0, p)], 2: [(1, p), (2, p + tok(5))], 4: [(3, p[:16])]}))
+    s.append(("eviction", 16, 256, {0: [(0, tok(40)), (1, tok(40))], 10: [(2, tok(40))],
+                                    22: [(3, tok(40))], 25: [(4, tok(40))], 30: [(5, tok(24))]}))
+    return s
+
+
+def make_sched():
+    """Steps of the reference's Continuous_Scheduler (src/pagedMemory.hpp:287-399)
+    over the tiny model, one reference thread.  Per step: the scheduler state
+    words (ref_sched_state), the block-manager snapshot words (ref_snapshot),
+    and the largest SCHED_TOP logits (value, index) of every row the step left
+    in s->logits: the decode rows when a decode batch ran, else the prefill
+    chunk's last row.  The same steps replayed by the oracle scheduler on the
+    oracle model must agree, and every argmax decision must win by a margin
+    well above fp32 rounding (checked here, so the fixture is robust)."""
+    from oracle import scheduler as sc
+    from oracle.model import OracleModel, scale_residual_outputs
+
+    meta, arrays = [], {}
+    min_gap = np.inf
+    for name, total, budget, arrivals in sched_scenarios():
+        W = ref.RefWorld.random_model(**dict(MODEL, total_blocks=total), max_rows=256, max_seqs=0,
+                                      seed=4242, threads=1, out_scale=SCHED_OUT_SCALE)
+        blob = W.serialize()
+        base = np.fromfile(os.path.join(HERE, "model_tiny.bin"), dtype=np.uint8)
+        assert np.array_equal(blob, scale_residual_outputs(base, SCHED_OUT_SCALE))
+        W.sched_create(budget)
+        mem = pm.KVBlockManager(total)
+        cache = pm.PrefixCacheManager(mem, total)
+        S = sc.ContinuousScheduler(mem, cache, budget)
+        fwd = sc.OracleForward(OracleModel(blob), total)
+        states, bms, tops_v, tops_i, rows, kinds = [], [], [], [], [], []
+        t, last = 0, max(arrivals)
+        evicted = False
+        while True:
+            for rid, prompt in arrivals.get(t, []):
+                W.sched_add(rid, prompt)
+                S.add_request(sc.Request(rid, prompt))
+            if not W.sched_active() and t >= last:
+                assert not S.has_active_requests()
+                break
+            cached_before = set(cache.reverse_map)
+            assert W.sched_step() == 0, (name, t)
+            p = S.step(fwd)
+            evicted |= bool(cached_before - set(cache.reverse_map))
+            st = W.sched_state()
+            assert st.tolist() == S.state_words(), (name, t)
+            snap = W.snapshot()
+            bm_words = _snapshot_words(W)
+            states.append(st)
+            bms.append(bm_words)
+            if p.decode_reqs:
+                lg = W.logits(len(p.decode_reqs))
+                np.testing.assert_allclose(lg, fwd.decode_logits, atol=1e-3, rtol=1e-4)
+                kinds.append(1)
+            elif p.prefill_req is not None:
+                lg = W.logits(1)
+                np.testing.assert_allclose(lg[0], fwd.prefill_logits, atol=1e-3, rtol=1e-4)
+                kinds.append(2)
+            else:
+                lg = np.zeros((0, MODEL["vocab"]), np.float32)
+                kinds.append(0)
+            decided = list(fwd.decode_logits) if fwd.decode_logits is not None else []
+            if p.prefill_req is not None and p.prefill_req.is_prefill_done:
+                decided.append(fwd.prefill_logits)
+            for row in decided:
+                srt = np.sort(row)[::-1]
+                min_gap = min(min_gap, srt[0] - srt[1], srt[0])
+            idx = np.argsort(-lg, axis=1, kind="stable")[:, :SCHED_TOP].astype(np.int32)
+            tops_i.append(idx)
+            tops_v.append(np.take_along_axis(lg, idx, axis=1))
+            rows.append(len(lg))
+            assert snap["free_list"] == list(mem.free_list), (name, t)
+            t += 1
+        if name == "eviction":
+            assert evicted, "eviction scenario never evicted"
+        W.close()
+        off = lambda parts: np.cumsum([0] + [len(x) for x in parts]).astype(np.int64)
+        arrays[f"{name}/state"] = np.concatenate(states).astype(np.int32)
+        arrays[f"{name}/state_off"] = off(states)
+        arrays[f"{name}/bm"] = np.concatenate(bms).astype(np.int32)
+        arrays[f"{name}/bm_off"] = off(bms)
+        arrays[f"{name}/top_val"] = np.concatenate(tops_v).astype(np.float32)
+        arrays[f"{name}/top_idx"] = np.concatenate(tops_i).astype(np.int32)
+        arrays[f"{name}/rows"] = np.asarray(rows, np.int32)
+        arrays[f"{name}/kind"] = np.asarray(kinds, np.int32)
+        meta.append(dict(name=name, total_blocks=total, max_tokens_per_batch=budget, steps=t,
+                         arrivals={str(k): [[rid, list(pr)] for rid, pr in v]
+                                   for k, v in arrivals.items()}))
+    assert min_gap > 0.05, f"an argmax decision wins by only {min_gap}"
+    return dict(model=MODEL, seed=4242, out_scale=SCHED_OUT_SCALE, max_generated=20,
+                top=SCHED_TOP, min_gap=float(min_gap), scenarios=meta), arrays
+
+
+def _snapshot_words(W) -> np.ndarray:
+    cap = 1 << 20
+    buf = np.zeros(cap, dtype=np.int32)
+    n = ref.lib().ref_snapshot(W.h, buf.ctypes.data_as(ref._i32p), cap)
+    assert n >= 0
+    return buf[:n].copy()
+
+
 def main():
     if not ref.available():
         sys.exit("oracle/_ref/libnitro_ref.so is missing: run `make -C oracle ref` first")
@@ -553,9 +680,13 @@ def main():
     with open(os.path.join(HERE, "model_forward.json"), "w") as f:
         json.dump(m_meta, f, indent=1)
     np.savez_compressed(os.path.join(HERE, "model_forward.npz"), **m_arrays)
+    s_meta, s_arrays = make_sched()
+    with open(os.path.join(HERE, "sched_traces.json"), "w") as f:
+        json.dump(s_meta, f, separators=(",", ":"))
+    np.savez_compressed(os.path.join(HERE, "sched_traces.npz"), **s_arrays)
     for fn in ("fnv.json", "block_manager_traces.json", "attention.json", "attention.npz",
                "q8_matmul.json", "q8_matmul.npz", "model_tiny.bin", "model_forward.json",
-               "model_forward.npz"):
+               "model_forward.npz", "sched_traces.json", "sched_traces.npz"):
         print(fn, os.path.getsize(os.path.join(HERE, fn)))
 
 
