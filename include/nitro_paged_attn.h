@@ -262,6 +262,65 @@ int nitro_forward_decode_batch(nitro_model* model, nitro_kvpool* pool, const int
 int nitro_forward_prefill(nitro_model* model, nitro_kvpool* pool, const int32_t* tokens,
                           int32_t total_rows, float* logits, int32_t semantics, void* stream);
 
+/* ======================== continuous scheduler ============================
+ * Request + Continuous_Scheduler (src/pagedMemory.hpp:287-399) over a
+ * block manager the caller keeps alive.  max_tokens_per_batch is the
+ * reference's token budget per step (256 there); max_generated is its finish
+ * length (20, hard-coded at :393).  Block ids, prefix-cache state, chunking
+ * and finish decisions come out exactly as the reference's.  A step either
+ * runs on the device (nitro_sched_step) or is split for a caller-supplied
+ * forward: nitro_sched_plan, the caller's forwards, nitro_sched_commit.
+ * After an error from plan or step (e.g. NITRO_ERR_OUT_OF_PAGES, where the
+ * reference calls exit(1)) the scheduler must only be destroyed. */
+typedef struct nitro_scheduler nitro_scheduler;
+int nitro_sched_create(nitro_block_manager* bm, int32_t max_tokens_per_batch, int32_t max_generated,
+                       nitro_scheduler** out);
+int nitro_sched_destroy(nitro_scheduler* sched);
+/* new Request(req_id, prompt) + add_request (:309-312); n > 0, ids unique. */
+int nitro_sched_add_request(nitro_scheduler* sched, int32_t req_id, const int32_t* prompt, int32_t n);
+int nitro_sched_has_active_requests(const nitro_scheduler* sched, int32_t* active); /* :313-315 */
+/* step (:316-378) up to its two forward calls, including the
+ * allocate_next_token loops those forwards begin with (src/model_q8.cpp:
+ * 428-430, then :578-582 in batch order).  prefill[4] = {request id or -1,
+ * chunk length, start position, 1 if the chunk completes the prompt}; the
+ * chunk is prompt[start, start + length).  The decode rows (running order)
+ * go to decode_ids / decode_tokens / decode_positions (cap entries each, at
+ * least the running batch's size; any may be NULL), their count to *n_decode. */
+int nitro_sched_plan(nitro_scheduler* sched, int32_t* prefill, int32_t* decode_ids,
+                     int32_t* decode_tokens, int32_t* decode_positions, int32_t cap,
+                     int32_t* n_decode);
+/* step (:380-397) after the forwards: argmax tokens of the prefill chunk
+ * (used when it completed its prompt) and of the n decode rows. */
+int nitro_sched_commit(nitro_scheduler* sched, int32_t prefill_token, const int32_t* decode_tokens,
+                       int32_t n);
+/* One whole step on the device: plan, then ONE forward over the prefill
+ * chunk's rows and the decode rows together (each weight matrix is read once
+ * for both; forward_prefill_chunk + forward_decode_batch, src/model_q8.cpp:
+ * 424-557 and 571-694), the reference's argmax (:559-569) on the device,
+ * the tokens back to the host, commit.  Block tables live on the device
+ * (one row per request, rows updated with the pages each step adds).  The
+ * first call binds the scheduler to `pool` (pages must cover the block
+ * manager's); later calls must pass the same pool.  Synchronises `stream`. */
+int nitro_sched_step(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* pool,
+                     int32_t semantics, void* stream);
+/* Logits rows the last nitro_sched_step computed (host copy, rows x
+ * vocab_size): the prefill chunk's last row first when it completed its
+ * prompt, then the decode rows.  *rows receives their count. */
+int nitro_sched_last_logits(const nitro_scheduler* sched, float* logits, int32_t cap_rows,
+                            int32_t* rows);
+/* Scheduler state as int32 words: [n, running ids] [n, waiting ids] [n requests],
+ * then per request in the order added: id, prefill_idx, is_prefill_done,
+ * is_finished, next_token_to_process, [n, generated], logical_token_count,
+ * current_hash lo, hi, [n, token buffer], [n, block table]. */
+int nitro_sched_state(const nitro_scheduler* sched, int32_t* words, int32_t cap, int32_t* n);
+int nitro_sched_generated(const nitro_scheduler* sched, int32_t req_id, int32_t* tokens, int32_t cap,
+                          int32_t* n);
+/* status[6] = {prefill_idx, is_prefill_done, is_finished, next_token_to_process,
+ * generated count, logical_token_count}. */
+int nitro_sched_request_status(const nitro_scheduler* sched, int32_t req_id, int32_t* status);
+/* Forgets a finished request that a later step has released. */
+int nitro_sched_drop_request(nitro_scheduler* sched, int32_t req_id);
+
 /* ------------------------------ checks ------------------------------------
  * Kernels re-check every page id they dereference against the pool size and
  * skip (and record) any outside it instead of faulting.  This reads and

@@ -12,5 +12,6 @@ from ._native import NitroError, lib  # noqa: F401
 from .attention import KVPool  # noqa: F401
 from .model import Model  # noqa: F401
 from .q8 import q8_matmul  # noqa: F401
+from .scheduler import ContinuousScheduler  # noqa: F401
 from .paged_memory import (BLOCK_SIZE, FNV_OFFSET_BASIS, BlockManager, Sequence,  # noqa: F401
                            hash_block_state, pack_block_tables)

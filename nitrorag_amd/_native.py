@@ -95,6 +95,18 @@ SIGNATURES = {
     "nitro_model_config": [_vp, _i32p],
     "nitro_forward_decode_batch": [_vp, _vp, _i32p, _i32, _fp, _i32, _vp],
     "nitro_forward_prefill": [_vp, _vp, _i32p, _i32, _fp, _i32, _vp],
+    "nitro_sched_create": [_vp, _i32, _i32, ctypes.POINTER(_vp)],
+    "nitro_sched_destroy": [_vp],
+    "nitro_sched_add_request": [_vp, _i32, _i32p, _i32],
+    "nitro_sched_has_active_requests": [_vp, _i32p],
+    "nitro_sched_plan": [_vp, _i32p, _i32p, _i32p, _i32p, _i32, _i32p],
+    "nitro_sched_commit": [_vp, _i32, _i32p, _i32],
+    "nitro_sched_step": [_vp, _vp, _vp, _i32, _vp],
+    "nitro_sched_last_logits": [_vp, ctypes.POINTER(ctypes.c_float), _i32, _i32p],
+    "nitro_sched_state": [_vp, _i32p, _i32, _i32p],
+    "nitro_sched_generated": [_vp, _i32, _i32p, _i32, _i32p],
+    "nitro_sched_request_status": [_vp, _i32, _i32p],
+    "nitro_sched_drop_request": [_vp, _i32],
     "nitro_kvpool_take_device_errors": [_vp, _i32p],
 }
 _RESTYPES = {

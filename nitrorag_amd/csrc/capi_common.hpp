@@ -37,3 +37,14 @@ inline void require(bool ok, Status s, const char* msg) {
 }
 
 }  // namespace nitro
+
+// The bookkeeping handles of the C ABI (opaque to callers).
+struct nitro_block_manager {
+    explicit nitro_block_manager(int n) : bm(n) {}
+    nitro::BlockManager bm;
+};
+
+struct nitro_sequence {
+    explicit nitro_sequence(int id) : seq(id) {}
+    nitro::Sequence seq;
+};

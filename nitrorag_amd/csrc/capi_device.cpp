@@ -85,6 +85,26 @@ int env_int(const char* name, int fallback) {
 
 }  // namespace
 
+namespace nitro {
+
+void set_device_decode_batch(nitro_kvpool* pool, int batch, int max_pages, const int32_t* positions,
+                             bool shared_pages, int32_t** tables, int32_t** device_positions) {
+    require_pool(pool);
+    require(batch > 0 && max_pages > 0, ERR_INVALID_ARGUMENT, "batch and max_pages must be positive");
+    DecodeBatch& d = pool->decode;
+    d.batch = 0;
+    d.tables.reserve((size_t)batch * max_pages);
+    d.pos.reserve(batch);
+    d.positions.assign(positions, positions + batch);
+    d.shared_pages = shared_pages;
+    d.batch = batch;
+    d.max_pages = max_pages;
+    *tables = d.tables.ptr;
+    *device_positions = d.pos.ptr;
+}
+
+}  // namespace nitro
+
 extern "C" {
 
 static int make_pool(float* k, float* v, bool owned, int32_t num_pages, int32_t num_layers,

@@ -6,16 +6,6 @@
 #include "nitro_paged_attn.h"
 #include "paged_memory.hpp"
 
-struct nitro_block_manager {
-    explicit nitro_block_manager(int n) : bm(n) {}
-    nitro::BlockManager bm;
-};
-
-struct nitro_sequence {
-    explicit nitro_sequence(int id) : seq(id) {}
-    nitro::Sequence seq;
-};
-
 namespace nitro {
 namespace {
 thread_local std::string g_last_error;

@@ -110,6 +110,8 @@ struct PrefillBatch {
 
 }  // namespace nitro
 
+struct nitro_model;
+
 struct nitro_kvpool {
     float* k = nullptr;
     float* v = nullptr;
@@ -195,6 +197,13 @@ hipError_t launch_kv_scatter_rows(float* k_pool, float* v_pool, const float* k, 
                                   int64_t layer_off, int num_pages, int32_t* bad_pages,
                                   hipStream_t stream);
 
+// Continuous-scheduler step (scheduler_kernels.hip): resident block-table
+// rows -> this step's decode tables, and the reference's argmax per row.
+hipError_t launch_sched_tables(int32_t* store, int row_stride, const int32_t* desc, const int32_t* other,
+                               int n_other, int32_t* tables, int32_t* positions, int batch, int max_pages,
+                               hipStream_t stream);
+hipError_t launch_argmax_rows(const float* logits, int32_t* next, int rows, int vocab, hipStream_t stream);
+
 struct PrefillLaunch {
     const float* q;
     float* out;
@@ -214,5 +223,25 @@ struct PrefillLaunch {
 // Query rows per prefill work item.
 int prefill_block_m(int head_dim);
 hipError_t launch_paged_attn_prefill(const PrefillLaunch& a, hipStream_t stream);
+
+}  // namespace nitro
+
+namespace nitro {
+
+// Makes pool->decode a batch whose tables [batch][max_pages] and positions
+// the caller writes on the device (stream-ordered before the next launch);
+// positions is the host copy (launch geometry).  Returns the device arrays.
+void set_device_decode_batch(nitro_kvpool* pool, int batch, int max_pages, const int32_t* positions,
+                             bool shared_pages, int32_t** tables, int32_t** device_positions);
+
+// One forward over prefill rows [0, prefill_rows) (the one-sequence batch in
+// pool->prefill) and decode rows [prefill_rows, prefill_rows + decode_rows)
+// (pool->decode), tokens on the device.  Logits and argmax go out for the
+// decode rows, preceded by the prefill chunk's last row when prefill_logits.
+void forward_mixed(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int prefill_rows,
+                   int decode_rows, bool prefill_logits, float* logits, int32_t* next, int semantics,
+                   hipStream_t stream);
+// Dimensions the scheduler needs: {dim, vocab, seq_len, n_layers, kv_dim}.
+void model_dims(const nitro_model* m, int32_t* dims);
 
 }  // namespace nitro

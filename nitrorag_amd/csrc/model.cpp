@@ -79,9 +79,10 @@ void upload_tokens(nitro_model* m, const int32_t* tokens, int rows, hipStream_t 
 // The layer loop shared by the decode and prefill forwards: after it, x holds
 // the residual stream and `ffn` the last layer's FFN output (not yet added).
 template <typename Attend>
-void layers(nitro_model* m, nitro_kvpool* pool, int rows, int semantics, hipStream_t s, Attend attend) {
+void layers(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int rows, int semantics, hipStream_t s,
+            Attend attend) {
     const int dim = m->dim, kv = m->kv_dim, hid = m->hidden;
-    hip_check(launch_embed_rows(m->f32(m->o_emb), m->tokens.ptr, m->x.ptr, rows, dim, m->vocab,
+    hip_check(launch_embed_rows(m->f32(m->o_emb), tokens, m->x.ptr, rows, dim, m->vocab,
                                 pool->bad_pages.ptr, s),
               "embed launch");
     for (int l = 0; l < m->n_layers; l++) {
@@ -113,6 +114,68 @@ void layers(nitro_model* m, nitro_kvpool* pool, int rows, int semantics, hipStre
 size_t q8_bytes(size_t rows, size_t cols) { return rows * (cols / 32) * 36; }
 
 }  // namespace
+
+namespace nitro {
+
+void model_dims(const nitro_model* m, int32_t* dims) {
+    dims[0] = m->dim;
+    dims[1] = m->vocab;
+    dims[2] = m->seq_len;
+    dims[3] = m->n_layers;
+    dims[4] = m->kv_dim;
+}
+
+void forward_mixed(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int P, int B,
+                   bool prefill_logits, float* logits, int32_t* next, int semantics, hipStream_t s) {
+    check_model_pool(m, pool);
+    require(P >= 0 && B >= 0 && P + B > 0, ERR_INVALID_ARGUMENT, "no rows");
+    require(!prefill_logits || P > 0, ERR_INVALID_ARGUMENT, "prefill logits without prefill rows");
+    require(P == 0 || (pool->prefill.batch == 1 && pool->prefill.total_rows == P), ERR_NO_BATCH,
+            "the prefill rows differ from the uploaded one-sequence prefill batch");
+    require(B == 0 || pool->decode.batch == B, ERR_NO_BATCH, "the decode rows differ from the decode batch");
+    const size_t dim = m->dim, kv = m->kv_dim;
+    void* stream = s;
+    reserve_rows(m, P + B);
+    layers(m, pool, tokens, P + B, semantics, s, [&](int l) {
+        // forward_prefill_chunk's RoPE, KV append and causal attention for
+        // rows [0, P) (src/model_q8.cpp:447-530), forward_decode_batch's for
+        // the rest (:594-662)
+        if (P > 0) {
+            require(nitro_rope_kv_append_prefill(pool, l, m->q.ptr, m->k.ptr, m->v.ptr, m->f32(m->o_freq_real),
+                                                 m->f32(m->o_freq_imag), m->seq_len, m->n_heads,
+                                                 m->n_kv_heads, m->head_size, stream) == NITRO_OK,
+                    ERR_INVALID_ARGUMENT, nitro_last_error());
+            require(nitro_paged_attn_prefill(pool, l, m->q.ptr, m->attn.ptr, m->n_heads, m->n_kv_heads,
+                                             m->head_size, stream) == NITRO_OK,
+                    ERR_INVALID_ARGUMENT, nitro_last_error());
+        }
+        if (B > 0) {
+            float* q = m->q.ptr + P * dim;
+            require(nitro_rope_kv_append(pool, l, q, m->k.ptr + P * kv, m->v.ptr + P * kv,
+                                         m->f32(m->o_freq_real), m->f32(m->o_freq_imag), m->seq_len,
+                                         m->n_heads, m->n_kv_heads, m->head_size, stream) == NITRO_OK,
+                    ERR_INVALID_ARGUMENT, nitro_last_error());
+            require(nitro_paged_attn_decode(pool, l, q, m->attn.ptr + P * dim, m->n_heads, m->n_kv_heads,
+                                            m->head_size, stream) == NITRO_OK,
+                    ERR_INVALID_ARGUMENT, nitro_last_error());
+        }
+    });
+    // The rows whose logits are used are contiguous: the chunk's last row
+    // (when it completes its prompt) and the decode rows.  x += FFN output;
+    // rms_norm; logits = wcls . x (:553-555, :687-692); argmax (:559-569).
+    const int first = prefill_logits ? P - 1 : P;
+    const int out_rows = P + B - first;
+    if (out_rows == 0) return;
+    float* x = m->x.ptr + first * dim;
+    hip_check(launch_add_rmsnorm(x, m->ffn.ptr + first * dim, m->f32(m->o_rms_final), x, out_rows, m->dim, s),
+              "rmsnorm launch");
+    hip_check(launch_f32_matmul(m->f32(m->o_emb), x, logits, out_rows, m->dim, m->vocab, s),
+              "classifier launch");
+    hip_check(launch_argmax_rows(logits, next, out_rows, m->vocab, s), "argmax launch");
+    pool->last_stream = s;
+}
+
+}  // namespace nitro
 
 extern "C" {
 
@@ -203,7 +266,7 @@ int nitro_forward_decode_batch(nitro_model* m, nitro_kvpool* pool, const int32_t
         hipStream_t s = as_stream(stream);
         reserve_rows(m, batch);
         upload_tokens(m, tokens, batch, s);
-        layers(m, pool, batch, semantics, s, [&](int l) {
+        layers(m, pool, m->tokens.ptr, batch, semantics, s, [&](int l) {
             require(nitro_rope_kv_append(pool, l, m->q.ptr, m->k.ptr, m->v.ptr, m->f32(m->o_freq_real),
                                          m->f32(m->o_freq_imag), m->seq_len, m->n_heads, m->n_kv_heads,
                                          m->head_size, stream) == NITRO_OK,
@@ -236,7 +299,7 @@ int nitro_forward_prefill(nitro_model* m, nitro_kvpool* pool, const int32_t* tok
         reserve_rows(m, total_rows);
         m->last.reserve((size_t)p.batch * m->dim);
         upload_tokens(m, tokens, total_rows, s);
-        layers(m, pool, total_rows, semantics, s, [&](int l) {
+        layers(m, pool, m->tokens.ptr, total_rows, semantics, s, [&](int l) {
             require(nitro_rope_kv_append_prefill(pool, l, m->q.ptr, m->k.ptr, m->v.ptr, m->f32(m->o_freq_real),
                                                  m->f32(m->o_freq_imag), m->seq_len, m->n_heads,
                                                  m->n_kv_heads, m->head_size, stream) == NITRO_OK,

@@ -1,0 +1,263 @@
+// Device half of the continuous scheduler: nitro_sched_step and
+// nitro_sched_last_logits (declared in include/nitro_paged_attn.h).
+//
+// One step = the host plan (scheduler.cpp), one upload of the step's small
+// inputs, one forward over the prefill chunk's rows and the decode rows
+// together, the argmax on the device, a read-back of one token per row, the
+// host commit.  Block tables stay on the device: every request that holds
+// pages owns a row of `store` (row_stride = pages of a full sequence) that
+// receives only the entries its sequence gained this step; the decode
+// kernels' dense [batch][max_pages] tables are written from those rows on
+// the device (launch_sched_tables).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "capi_common.hpp"
+#include "device_pool.hpp"
+#include "nitro_paged_attn.h"
+#include "scheduler.hpp"
+
+namespace nitro {
+
+struct SchedDevice {
+    nitro_kvpool* pool = nullptr;
+    nitro_model* model = nullptr;
+    int device = 0;
+    int row_stride = 0;                 // pages per resident row
+    int rows = 0;                       // resident rows allocated
+    std::vector<int> free_rows;         // LIFO
+    DeviceBuffer<int32_t> store;        // [rows][row_stride]
+    DeviceBuffer<int32_t> step_in;      // tokens, decode descriptors, other entries
+    DeviceBuffer<float> logits;         // [out_rows][vocab]
+    DeviceBuffer<int32_t> next;         // [out_rows]
+    Staging staging;
+    int32_t* readback = nullptr;        // pinned, next tokens
+    size_t readback_count = 0;
+    int last_rows = 0;
+    int vocab = 0;
+    std::vector<uint32_t> page_mark;    // shared-page scan stamps
+    uint32_t stamp = 0;
+
+    ~SchedDevice() {
+        if (readback) (void)hipHostFree(readback);
+    }
+
+    int take_row(hipStream_t s) {
+        if (free_rows.empty()) grow(std::max(16, 2 * rows), s);
+        const int r = free_rows.back();
+        free_rows.pop_back();
+        return r;
+    }
+
+    void grow(int n, hipStream_t s) {
+        DeviceBuffer<int32_t> bigger;
+        bigger.reserve((size_t)n * row_stride);
+        if (rows > 0)
+            hip_check(hipMemcpyAsync(bigger.ptr, store.ptr, sizeof(int32_t) * (size_t)rows * row_stride,
+                                     hipMemcpyDeviceToDevice, s),
+                      "hipMemcpyAsync(resident tables)");
+        hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        std::swap(store.ptr, bigger.ptr);
+        std::swap(store.count, bigger.count);
+        for (int r = n - 1; r >= rows; r--) free_rows.push_back(r);
+        rows = n;
+    }
+};
+
+namespace {
+
+void free_device(SchedDevice* d) { delete d; }
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// True when some page appears in more than one decode row's table (prefix
+// sharing): the decode kernel then keeps its K/V loads cacheable.
+bool rows_share_pages(SchedDevice& d, const StepPlan& p, int num_pages) {
+    if ((int)d.page_mark.size() < num_pages) d.page_mark.assign(num_pages, 0);
+    if (++d.stamp == 0) {
+        std::fill(d.page_mark.begin(), d.page_mark.end(), 0);
+        d.stamp = 1;
+    }
+    for (const Request* r : p.decode)
+        for (int32_t page : r->seq.block_table) {
+            if (d.page_mark[page] == d.stamp) return true;
+            d.page_mark[page] = d.stamp;
+        }
+    return false;
+}
+
+// Refuses, before any state changes, a step the model could not run: a
+// position at or past seq_len, a token outside the vocabulary.
+void check_step_fits(const ContinuousScheduler& h, int seq_len, int vocab) {
+    for (const Request* r : h.running()) {
+        if (r->is_finished) continue;
+        if (r->seq.logical_token_count >= seq_len)
+            throw Error(ERR_INVALID_ARGUMENT, "request " + std::to_string(r->req_id) +
+                                                  " would decode at position " +
+                                                  std::to_string(r->seq.logical_token_count) +
+                                                  ", past the model's seq_len");
+        if (r->next_token_to_process < 0 || r->next_token_to_process >= vocab)
+            throw Error(ERR_INVALID_ARGUMENT, "token outside the vocabulary");
+    }
+    if (const Request* r = h.waiting_head()) {
+        if ((int)r->prompt_tokens.size() > seq_len)
+            throw Error(ERR_INVALID_ARGUMENT, "request " + std::to_string(r->req_id) +
+                                                  " has a prompt longer than the model's seq_len");
+        for (int32_t t : r->prompt_tokens)
+            if (t < 0 || t >= vocab) throw Error(ERR_INVALID_ARGUMENT, "prompt token outside the vocabulary");
+    }
+}
+
+}  // namespace
+}  // namespace nitro
+
+using namespace nitro;
+
+extern "C" {
+
+int nitro_sched_step(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* pool, int32_t semantics,
+                     void* stream) {
+    return guarded([&] {
+        require(sched != nullptr && model != nullptr && pool != nullptr, ERR_INVALID_ARGUMENT, "null handle");
+        require(semantics == NITRO_Q8_FULL_ROWS || semantics == NITRO_Q8_LAST_BLOCK, ERR_INVALID_ARGUMENT,
+                "unknown Q8 semantics");
+        ContinuousScheduler& h = sched->host;
+        int32_t dims[5];
+        model_dims(model, dims);
+        const int vocab = dims[1], seq_len = dims[2];
+        require(pool->num_layers == dims[3] && pool->kv_dim == dims[4], ERR_INVALID_ARGUMENT,
+                "pool layers / kv_dim do not match the model");
+        require(h.block_manager().mem.total_blocks() <= pool->num_pages, ERR_INVALID_ARGUMENT,
+                "the block manager has more pages than the pool");
+        hipStream_t s = as_stream(stream);
+        if (!sched->dev) {
+            auto* d = new SchedDevice();
+            d->pool = pool;
+            d->model = model;
+            d->row_stride = (seq_len + BLOCK_SIZE - 1) / BLOCK_SIZE;
+            d->vocab = vocab;
+            hip_check(hipGetDevice(&d->device), "hipGetDevice");
+            sched->dev = d;
+            sched->dev_free = free_device;
+        }
+        SchedDevice& d = *sched->dev;
+        require(d.pool == pool && d.model == model, ERR_INVALID_ARGUMENT,
+                "a scheduler steps one model over one pool (those of its first step)");
+        check_step_fits(h, seq_len, vocab);
+
+        const StepPlan& p = h.plan();
+        // From here on a failure leaves the step planned: the scheduler can
+        // only be destroyed (as after the reference's exit).
+        for (Request* r : p.released) {
+            if (r->slot >= 0) d.free_rows.push_back(r->slot);
+            r->slot = -1;
+            r->pages_on_device = 0;
+        }
+        const int P = (int)p.prefill_tokens.size(), B = (int)p.decode.size();
+        // New table entries: a decode row's single new page travels in its
+        // descriptor, the rest in the `other` list.
+        std::vector<int32_t> desc(4 * (size_t)B), other;
+        for (int b = 0; b < B; b++) {
+            Request* r = p.decode[b];
+            if (r->slot < 0) r->slot = d.take_row(s);
+            const int n = (int)r->seq.block_table.size();
+            require(n - r->pages_on_device <= 1 && n <= d.row_stride, ERR_BAD_BLOCK_TABLE,
+                    "a decode row gained more than one page");
+            desc[4 * b] = r->slot;
+            desc[4 * b + 1] = p.decode_positions[b];
+            desc[4 * b + 2] = n > r->pages_on_device ? r->pages_on_device : -1;
+            desc[4 * b + 3] = n > r->pages_on_device ? r->seq.block_table[n - 1] : 0;
+            r->pages_on_device = n;
+        }
+        for (Request* r : p.grown) {
+            if (std::find(p.decode.begin(), p.decode.end(), r) != p.decode.end()) continue;
+            if (r->slot < 0) r->slot = d.take_row(s);
+            const int n = (int)r->seq.block_table.size();
+            require(n <= d.row_stride, ERR_BAD_BLOCK_TABLE, "a block table is longer than seq_len allows");
+            for (int j = r->pages_on_device; j < n; j++) {
+                other.push_back(r->slot * d.row_stride + j);
+                other.push_back(r->seq.block_table[j]);
+            }
+            r->pages_on_device = n;
+        }
+        const int n_other = (int)other.size() / 2;
+        const int out_rows = B + (p.prefill_finishes ? 1 : 0);
+        d.last_rows = 0;
+        if (P + B == 0 && n_other == 0) {
+            h.commit(0, nullptr, 0);
+            return;
+        }
+
+        // One upload: tokens (prefill rows, then decode rows), descriptors, other entries.
+        const size_t n_in = (size_t)P + B + desc.size() + other.size();
+        d.step_in.reserve(n_in);
+        int32_t* hin = d.staging.acquire(n_in);
+        std::copy(p.prefill_tokens.begin(), p.prefill_tokens.end(), hin);
+        std::copy(p.decode_tokens.begin(), p.decode_tokens.end(), hin + P);
+        std::copy(desc.begin(), desc.end(), hin + P + B);
+        std::copy(other.begin(), other.end(), hin + P + B + desc.size());
+        d.staging.copy(d.step_in.ptr, hin, n_in, s);
+        d.staging.finish(s);
+        const int32_t* d_tokens = d.step_in.ptr;
+        const int32_t* d_desc = d.step_in.ptr + P + B;
+        const int32_t* d_other = d_desc + desc.size();
+
+        int32_t* d_tables = nullptr;
+        int32_t* d_positions = nullptr;
+        int max_pages = 1;
+        if (B > 0) {
+            for (int b = 0; b < B; b++) max_pages = std::max(max_pages, p.decode_positions[b] / BLOCK_SIZE + 1);
+            set_device_decode_batch(pool, B, max_pages, p.decode_positions.data(),
+                                    rows_share_pages(d, p, pool->num_pages), &d_tables, &d_positions);
+        }
+        hip_check(launch_sched_tables(d.store.ptr, d.row_stride, d_desc, d_other, n_other, d_tables,
+                                      d_positions, B, max_pages, s),
+                  "sched_tables launch");
+        if (P > 0) {
+            const std::vector<int32_t>& t = p.prefill->seq.block_table;
+            const int32_t start = p.prefill_start, len = P;
+            require(nitro_prefill_batch_upload(pool, t.data(), &start, &len, 1, (int32_t)t.size(), stream) ==
+                        NITRO_OK,
+                    ERR_INVALID_ARGUMENT, nitro_last_error());
+        }
+        if (P + B > 0) {
+            d.logits.reserve((size_t)std::max(out_rows, 1) * vocab);
+            d.next.reserve(std::max(out_rows, 1));
+            forward_mixed(model, pool, d_tokens, P, B, p.prefill_finishes, d.logits.ptr, d.next.ptr, semantics, s);
+        }
+        if ((size_t)out_rows > d.readback_count) {
+            if (d.readback) hip_check(hipHostFree(d.readback), "hipHostFree");
+            d.readback = nullptr;
+            d.readback_count = 0;
+            hip_check(hipHostMalloc((void**)&d.readback, sizeof(int32_t) * out_rows), "hipHostMalloc");
+            d.readback_count = out_rows;
+        }
+        if (out_rows > 0)
+            hip_check(hipMemcpyAsync(d.readback, d.next.ptr, sizeof(int32_t) * out_rows, hipMemcpyDeviceToHost, s),
+                      "hipMemcpyAsync(next tokens)");
+        hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        pool->last_stream = s;
+        d.last_rows = out_rows;
+        const int first = p.prefill_finishes ? 1 : 0;
+        h.commit(first ? d.readback[0] : 0, d.readback + first, B);
+    });
+}
+
+int nitro_sched_last_logits(const nitro_scheduler* sched, float* logits, int32_t cap_rows, int32_t* rows) {
+    return guarded([&] {
+        require(sched != nullptr && rows != nullptr, ERR_INVALID_ARGUMENT, "null pointer");
+        const SchedDevice* d = sched->dev;
+        *rows = d ? d->last_rows : 0;
+        if (!d || d->last_rows == 0 || logits == nullptr) return;
+        require(cap_rows >= d->last_rows, ERR_INVALID_ARGUMENT, "output buffer too small (rows in *rows)");
+        hip_check(hipMemcpy(logits, d->logits.ptr, sizeof(float) * (size_t)d->last_rows * d->vocab,
+                            hipMemcpyDeviceToHost),
+                  "hipMemcpy(logits)");
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,109 @@
+"""GPU parity of the continuous scheduler's device step (nitro_sched_step: host
+plan, one forward over the prefill chunk's rows and the decode rows together
+over device-resident block tables, argmax on the device, commit) against the
+reference's own Continuous_Scheduler (src/pagedMemory.hpp:287-399) stepping
+the same tiny model, recorded in tests/golden/sched_traces.*.
+
+Every step must leave the reference's scheduler state word for word — which
+includes every token the device argmax chose (the fixture's decisions win by
+at least 0.16, far above fp32 rounding) — and the logits the reference left
+behind must match within |gpu - ref| <= 2e-3 + 1e-3*|ref| on the recorded
+top entries of each row."""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_ATOL, LOGIT_RTOL = 2e-3, 1e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    import nitrorag_amd  # noqa: F401
+    yield
+    torch.cuda.synchronize()
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def test_scheduler_steps_match_reference(golden_sched, golden_model):
+    import nitrorag_amd as na
+    from nitrorag_amd.q8 import LAST_BLOCK
+    from oracle import scheduler as sc
+    from oracle.model import scale_residual_outputs
+
+    meta, traces = golden_sched
+    blob, _, _ = golden_model
+    model = na.Model(scale_residual_outputs(blob, meta["out_scale"]))
+    for tr in traces:
+        say(f"scheduler scenario {tr.name}: {tr.steps} steps, {tr.total_blocks} pages, "
+            f"budget {tr.budget}")
+        pool = na.KVPool(tr.total_blocks, model.n_layers, model.kv_dim)
+        bm = na.BlockManager(tr.total_blocks)
+        S = na.ContinuousScheduler(bm, tr.budget, meta["max_generated"])
+        last = max(tr.arrivals)
+        t = 0
+        while True:
+            for rid, prompt in tr.arrivals.get(t, []):
+                S.add_request(rid, prompt)
+            if not S.has_active_requests() and t >= last:
+                break
+            before = sc.decode_state(S.state_words())
+            S.step(model, pool, LAST_BLOCK)
+            got = S.state_words()
+            assert got == tr.state(t), (tr.name, t, sc.decode_state(got), sc.decode_state(tr.state(t)))
+            lg = S.last_logits()
+            idx, val = tr.top(t)
+            after = sc.decode_state(got)
+            finished_prefill = any(r["done"] and not b["done"] and r["generated"]
+                                   for r, b in zip(after["requests"], before["requests"]))
+            if tr.kind(t) == 1:
+                rows = lg[1:] if finished_prefill else lg
+            elif tr.kind(t) == 2 and finished_prefill:
+                rows = lg
+            else:
+                rows = None
+            if rows is not None:
+                assert rows.shape[0] == idx.shape[0], (tr.name, t)
+                g = np.take_along_axis(rows, idx, axis=1)
+                bound = LOGIT_ATOL + LOGIT_RTOL * np.abs(val)
+                assert np.all(np.abs(g - val) <= bound), (tr.name, t, np.abs(g - val).max())
+            t += 1
+        assert t == tr.steps
+        assert pool.take_device_errors() == 0
+        S.close()
+        pool.close()
+
+
+def test_scheduler_refuses_positions_past_seq_len(golden_model):
+    """A step that would decode at seq_len is refused before any state changes."""
+    import nitrorag_amd as na
+    from nitrorag_amd.q8 import LAST_BLOCK
+
+    blob, meta, _ = golden_model
+    model = na.Model(blob)
+    seq_len = model.config["seq_len"]
+    pool = na.KVPool(16, model.n_layers, model.kv_dim)
+    bm = na.BlockManager(16)
+    S = na.ContinuousScheduler(bm, 256, 1000)
+    S.add_request(0, [1] * (seq_len + 1))
+    words = S.state_words()
+    with pytest.raises(na.NitroError):
+        S.step(model, pool, LAST_BLOCK)
+    assert S.state_words() == words
+    S2 = na.ContinuousScheduler(bm, 256, 1000)
+    S2.add_request(1, [2] * (seq_len - 1))
+    S2.step(model, pool, LAST_BLOCK)      # prefill to seq_len - 1 tokens
+    S2.step(model, pool, LAST_BLOCK)      # decodes at position seq_len - 1
+    words = S2.state_words()
+    with pytest.raises(na.NitroError):
+        S2.step(model, pool, LAST_BLOCK)  # position seq_len: refused
+    assert S2.state_words() == words
