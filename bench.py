@@ -485,6 +485,157 @@ class ModelDecodeWorkload:
         return {}
 
 
+class ServeWorkload:
+    """The reference's continuous-batching experiment (src/model_q8.cpp:864-908)
+    on the device scheduler (nitro_sched_step): `users` requests with the same
+    256-token prompt (token 263) submitted together, token budget 256 per
+    step, 20 generated tokens each, an 8000-page pool, stepped until every
+    request has finished; Llama-2-110M-shaped synthetic model, the
+    reference's Q8 products (matmul_bulk semantics).  One bench step = one
+    whole run; value = users * 20 / run time (aggregate tokens/s, the
+    reference's figure), plus the average time to first token.  Algorithmic
+    bytes per run: per scheduler step, the weights the step needs once (the
+    fp32 classifier, norms, and the last BlockQ8 of every Q8 row, all that
+    matmul_bulk reads) + the K/V rows its attention reads and writes + logits."""
+
+    bound = "hbm"
+    flush = False
+    PROMPT, TOKEN, GEN, BUDGET, PAGES = 256, 263, 20, 256, 8000
+
+    def __init__(self, name, users, seed, describe):
+        self.name, self.users, self.seed, self.describe = name, users, seed, describe
+        self.cfg = (768, 2048, 12, 12, 12, 32000, 1024)
+        dim, hid, L, H, Hkv, V, S = self.cfg
+        self.kv_dim, self.L, self.V = Hkv * (dim // H), L, V
+        self.ttft_ms = []
+
+    def setup(self, dev, g):
+        import nitrorag_amd as na
+        from nitrorag_amd.model import synthetic_model_file
+
+        self.blob = synthetic_model_file(*self.cfg, seed=self.seed)
+        self.model = na.Model(self.blob)
+        self.pool = na.KVPool(self.PAGES, self.L, self.kv_dim)
+        self.prompt = [self.TOKEN] * self.PROMPT
+        self.sched_steps, self.run_bytes = self._schedule_shape()
+
+    def _schedule_shape(self):
+        """Host-only dry run of the same schedule (its shape does not depend
+        on the tokens): scheduler steps per run and algorithmic bytes."""
+        import nitrorag_amd as na
+
+        dim, hid, L, H, Hkv, V, S = self.cfg
+        q8 = lambda r, c: r * 36  # matmul_bulk keeps the last BlockQ8 of each row only
+        weights = (V * dim * 4 + L * (q8(dim, dim) * 2 + q8(self.kv_dim, dim) * 2 + q8(hid, dim) * 2
+                                      + q8(dim, hid) + 2 * dim * 4) + dim * 4)
+        row = L * self.kv_dim * 4 * 2  # one K and one V row over all layers
+        bm = na.BlockManager(self.PAGES)
+        sch = na.ContinuousScheduler(bm, self.BUDGET, self.GEN)
+        for u in range(self.users):
+            sch.add_request(u, self.prompt)
+        steps, total = 0, 0
+        while sch.has_active_requests():
+            p = sch.plan()
+            rows = len(p.decode_ids) + p.prefill_length
+            if rows:
+                total += weights
+                total += sum(pos + 1 for pos in p.decode_positions) * row  # decode reads
+                total += (p.prefill_start + p.prefill_length) * row * (1 if p.prefill_length else 0)
+                total += rows * row + (len(p.decode_ids) + p.prefill_finishes) * V * 4
+            sch.commit(1 if p.prefill_finishes else 0, [1] * len(p.decode_ids))
+            steps += 1
+        sch.close()
+        return steps, total
+
+    def step(self, stream, events=None):
+        import nitrorag_amd as na
+        from nitrorag_amd.q8 import LAST_BLOCK
+
+        bm = na.BlockManager(self.PAGES)
+        sch = na.ContinuousScheduler(bm, self.BUDGET, self.GEN)
+        if events is not None:
+            events[0][0].record(stream)
+        t0 = time.perf_counter()
+        for u in range(self.users):
+            sch.add_request(u, self.prompt)
+        waiting = set(range(self.users))
+        ttft = []
+        while sch.has_active_requests():
+            sch.step(self.model, self.pool, LAST_BLOCK, stream)
+            for u in list(waiting):
+                if sch.request_status(u)["is_prefill_done"]:
+                    ttft.append((time.perf_counter() - t0) * 1e3)
+                    waiting.discard(u)
+        if events is not None:
+            events[0][1].record(stream)
+        self.ttft_ms.append(float(np.mean(ttft)))
+        self.generated = sum(len(sch.generated(u)) for u in range(self.users))
+        sch.close()
+
+    def launches_per_step(self):
+        return 1
+
+    def work_per_launch(self):
+        return int(self.run_bytes)
+
+    def tokens_per_step(self):
+        return self.users * self.GEN
+
+    def kernel(self):
+        return "continuous-scheduler run (all kernels, host plan/commit between steps)"
+
+    def config(self):
+        dim, hid, L, H, Hkv, V, S = self.cfg
+        return {"workload": self.describe, "users": self.users, "prompt_tokens": self.PROMPT,
+                "generated_per_user": self.GEN, "token_budget": self.BUDGET, "pool_pages": self.PAGES,
+                "dim": dim, "hidden_dim": hid, "n_layers": L, "n_heads": H, "vocab": V,
+                "parallelism": "single GPU"}
+
+    def check(self):
+        assert self.generated == self.users * self.GEN, self.generated
+
+    def device_errors(self):
+        return self.pool.take_device_errors()
+
+    def headline(self, ms_per_step):
+        return {"metric": f"{self.name} aggregate tokens/s", "unit": "tokens/s",
+                "value": round(self.users * self.GEN / (ms_per_step * 1e-3), 1)}
+
+    def extra(self, kernel_s):
+        return {"avg_ttft_ms": round(float(np.mean(self.ttft_ms[-5:])), 3),
+                "scheduler_steps_per_run": self.sched_steps}
+
+    def cpu_baseline(self, seconds, sample):
+        """The reference's own scheduler and forward passes (oracle/_ref, built
+        from its sources) on the same experiment with `sample` users (at most
+        16: with more, two of its OpenMP threads allocate pages at once in
+        forward_decode_batch, src/model_q8.cpp:578-582, a data race)."""
+        from oracle import ref
+
+        if not ref.available():
+            return None
+        users = min(sample, 16, self.users)
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        dim, hid, L, H, Hkv, V, S = self.cfg
+        W = ref.RefWorld.random_model(H, Hkv, dim // H, L, V, S, hid, self.PAGES, max_rows=512,
+                                      max_seqs=0, seed=self.seed & 0xffffffff, threads=threads)
+        W.sched_create(self.BUDGET)
+        t0 = time.perf_counter()
+        for u in range(users):
+            W.sched_add(u, self.prompt)
+        steps = 0
+        while W.sched_active():
+            assert W.sched_step() == 0
+            steps += 1
+        el = time.perf_counter() - t0
+        W.close()
+        return {"value": round(users * self.GEN / el, 2), "unit": "tokens/s", "cores": threads,
+                "kind": "reference",
+                "sample": (f"{users} users of this experiment through the reference's "
+                           f"Continuous_Scheduler and forward passes ({steps} steps, {el:.1f} s, "
+                           f"random 110M-shaped weights)")}
+
+
 def prefix_shared_workload(seed):
     """48 sequences: 512 shared prefix tokens (32 pages via FNV-1a prefix-cache hits),
     private suffixes ~ U[64,512], then one decode token each."""
@@ -546,6 +697,13 @@ def make_workload(name, seed):
                                              "(dim 768, hidden 2048, 12 layers, 12 heads x 64, "
                                              "vocab 32000, Q8_0 weights, synthetic), B=32 sequences "
                                              "at context 512, full-row Q8 products"))
+    if name.startswith("serve-110m-u"):
+        users = int(name.rsplit("u", 1)[1])
+        return ServeWorkload(name, users, seed,
+                             describe=(f"continuous batching: {users} users x 256-token shared "
+                                       f"prompt, 20 generated tokens each, token budget 256, "
+                                       f"8000-page pool, Llama-2-110M-shaped Q8_0 model "
+                                       f"(synthetic), reference Q8 semantics"))
     if name == "q8-gemv-7b-ffn":
         return Q8Workload(name, 4096, 11008, 1, seed,
                           describe=("Q8_0 matrix-vector product at the Llama-2-7B FFN up "
@@ -561,7 +719,8 @@ def make_workload(name, seed):
 
 WORKLOADS = ["decode-b64-ctx4096", "decode-single-110m", "decode-b32-mixed",
              "decode-prefix-shared", "prefill-b8-12x64", "q8-gemv-7b-ffn", "q8-matmul-110m-b32",
-             "model-110m-decode-b32"]
+             "model-110m-decode-b32", "serve-110m-u1", "serve-110m-u4", "serve-110m-u8",
+             "serve-110m-u16", "serve-110m-u32"]
 
 
 def kernel_name(w) -> str:
@@ -686,6 +845,8 @@ def main():
         },
         "cpu_baseline": None,
     }
+    if hasattr(w, "headline"):
+        line.update(w.headline(ms_per_step))
     line.update(w.extra(kernel_s))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = w.cpu_baseline(args.cpu_seconds, args.cpu_sample)

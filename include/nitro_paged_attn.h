@@ -308,6 +308,10 @@ int nitro_sched_step(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* p
  * prompt, then the decode rows.  *rows receives their count. */
 int nitro_sched_last_logits(const nitro_scheduler* sched, float* logits, int32_t cap_rows,
                             int32_t* rows);
+/* argmax (src/model_q8.cpp:559-569) of each of `rows` rows of logits
+ * (device, rows x vocab) into out (device, rows int32): the first index of the
+ * largest value above 0.0, 0 when no value exceeds 0.0; NaN never wins. */
+int nitro_argmax(const float* logits, int32_t rows, int32_t vocab, int32_t* out, void* stream);
 /* Scheduler state as int32 words: [n, running ids] [n, waiting ids] [n requests],
  * then per request in the order added: id, prefill_idx, is_prefill_done,
  * is_finished, next_token_to_process, [n, generated], logical_token_count,

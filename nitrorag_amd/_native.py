@@ -103,6 +103,7 @@ SIGNATURES = {
     "nitro_sched_commit": [_vp, _i32, _i32p, _i32],
     "nitro_sched_step": [_vp, _vp, _vp, _i32, _vp],
     "nitro_sched_last_logits": [_vp, ctypes.POINTER(ctypes.c_float), _i32, _i32p],
+    "nitro_argmax": [_fp, _i32, _i32, _fp, _vp],
     "nitro_sched_state": [_vp, _i32p, _i32, _i32p],
     "nitro_sched_generated": [_vp, _i32, _i32p, _i32, _i32p],
     "nitro_sched_request_status": [_vp, _i32, _i32p],

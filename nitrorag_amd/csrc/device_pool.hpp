@@ -200,8 +200,8 @@ hipError_t launch_kv_scatter_rows(float* k_pool, float* v_pool, const float* k, 
 // Continuous-scheduler step (scheduler_kernels.hip): resident block-table
 // rows -> this step's decode tables, and the reference's argmax per row.
 hipError_t launch_sched_tables(int32_t* store, int row_stride, const int32_t* desc, const int32_t* other,
-                               int n_other, int32_t* tables, int32_t* positions, int batch, int max_pages,
-                               hipStream_t stream);
+                               int n_other, const int32_t* chunk_table, int32_t* tables, int32_t* positions,
+                               int batch, int max_pages, hipStream_t stream);
 hipError_t launch_argmax_rows(const float* logits, int32_t* next, int rows, int vocab, hipStream_t stream);
 
 struct PrefillLaunch {
@@ -234,13 +234,16 @@ namespace nitro {
 void set_device_decode_batch(nitro_kvpool* pool, int batch, int max_pages, const int32_t* positions,
                              bool shared_pages, int32_t** tables, int32_t** device_positions);
 
-// One forward over prefill rows [0, prefill_rows) (the one-sequence batch in
-// pool->prefill) and decode rows [prefill_rows, prefill_rows + decode_rows)
-// (pool->decode), tokens on the device.  Logits and argmax go out for the
+// One forward over prefill rows [0, prefill_rows) and decode rows
+// [prefill_rows, prefill_rows + decode_rows), tokens on the device.  With
+// prefill_as_decode the decode batch in pool->decode holds every row (a
+// chunk row is a decode row at its own position over the chunk's table);
+// otherwise the prefill rows are the one-sequence batch in pool->prefill and
+// pool->decode holds the decode rows.  Logits and argmax go out for the
 // decode rows, preceded by the prefill chunk's last row when prefill_logits.
 void forward_mixed(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int prefill_rows,
-                   int decode_rows, bool prefill_logits, float* logits, int32_t* next, int semantics,
-                   hipStream_t stream);
+                   int decode_rows, bool prefill_as_decode, bool prefill_logits, float* logits,
+                   int32_t* next, int semantics, hipStream_t stream);
 // Dimensions the scheduler needs: {dim, vocab, seq_len, n_layers, kv_dim}.
 void model_dims(const nitro_model* m, int32_t* dims);
 

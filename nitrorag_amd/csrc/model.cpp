@@ -126,17 +126,36 @@ void model_dims(const nitro_model* m, int32_t* dims) {
 }
 
 void forward_mixed(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int P, int B,
-                   bool prefill_logits, float* logits, int32_t* next, int semantics, hipStream_t s) {
+                   bool prefill_as_decode, bool prefill_logits, float* logits, int32_t* next, int semantics,
+                   hipStream_t s) {
     check_model_pool(m, pool);
     require(P >= 0 && B >= 0 && P + B > 0, ERR_INVALID_ARGUMENT, "no rows");
     require(!prefill_logits || P > 0, ERR_INVALID_ARGUMENT, "prefill logits without prefill rows");
-    require(P == 0 || (pool->prefill.batch == 1 && pool->prefill.total_rows == P), ERR_NO_BATCH,
-            "the prefill rows differ from the uploaded one-sequence prefill batch");
-    require(B == 0 || pool->decode.batch == B, ERR_NO_BATCH, "the decode rows differ from the decode batch");
+    if (prefill_as_decode) {
+        require(pool->decode.batch == P + B, ERR_NO_BATCH, "the rows differ from the decode batch");
+    } else {
+        require(P == 0 || (pool->prefill.batch == 1 && pool->prefill.total_rows == P), ERR_NO_BATCH,
+                "the prefill rows differ from the uploaded one-sequence prefill batch");
+        require(B == 0 || pool->decode.batch == B, ERR_NO_BATCH, "the decode rows differ from the decode batch");
+    }
     const size_t dim = m->dim, kv = m->kv_dim;
     void* stream = s;
     reserve_rows(m, P + B);
     layers(m, pool, tokens, P + B, semantics, s, [&](int l) {
+        if (prefill_as_decode) {
+            // every row attends its own prefix (keys 0..position): RoPE + KV
+            // append of all rows, then one decode-attention launch; a chunk
+            // row at position p sees the same keys as in forward_prefill_chunk
+            // (src/model_q8.cpp:493-530)
+            require(nitro_rope_kv_append(pool, l, m->q.ptr, m->k.ptr, m->v.ptr, m->f32(m->o_freq_real),
+                                         m->f32(m->o_freq_imag), m->seq_len, m->n_heads, m->n_kv_heads,
+                                         m->head_size, stream) == NITRO_OK,
+                    ERR_INVALID_ARGUMENT, nitro_last_error());
+            require(nitro_paged_attn_decode(pool, l, m->q.ptr, m->attn.ptr, m->n_heads, m->n_kv_heads,
+                                            m->head_size, stream) == NITRO_OK,
+                    ERR_INVALID_ARGUMENT, nitro_last_error());
+            return;
+        }
         // forward_prefill_chunk's RoPE, KV append and causal attention for
         // rows [0, P) (src/model_q8.cpp:447-530), forward_decode_batch's for
         // the rest (:594-662)

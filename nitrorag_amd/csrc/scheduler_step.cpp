@@ -70,6 +70,9 @@ struct SchedDevice {
 
 namespace {
 
+// Prefill chunks of at most this many rows run as rows of the decode batch.
+constexpr int PREFILL_AS_DECODE_MAX_ROWS = 32;
+
 void free_device(SchedDevice* d) { delete d; }
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
@@ -158,19 +161,34 @@ int nitro_sched_step(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* p
             r->pages_on_device = 0;
         }
         const int P = (int)p.prefill_tokens.size(), B = (int)p.decode.size();
+        // A short chunk rides in the decode batch: each of its rows is a decode
+        // row at its own position over the chunk's table (one RoPE/append and
+        // one attention launch per layer for all rows).  Long chunks keep the
+        // prefill kernel, which reads each K/V page once for many query rows.
+        const bool chunk_rows = P > 0 && P <= PREFILL_AS_DECODE_MAX_ROWS;
+        const int R = (chunk_rows ? P : 0) + B;  // rows of the decode batch
         // New table entries: a decode row's single new page travels in its
         // descriptor, the rest in the `other` list.
-        std::vector<int32_t> desc(4 * (size_t)B), other;
+        std::vector<int32_t> desc(4 * (size_t)R), other;
+        std::vector<int32_t> positions(R);
+        const int c0 = chunk_rows ? P : 0;  // first request row in the batch
+        for (int i = 0; i < c0; i++) {
+            desc[4 * i] = -1;
+            desc[4 * i + 1] = positions[i] = p.prefill_start + i;
+            desc[4 * i + 2] = -1;
+            desc[4 * i + 3] = 0;
+        }
         for (int b = 0; b < B; b++) {
             Request* r = p.decode[b];
             if (r->slot < 0) r->slot = d.take_row(s);
             const int n = (int)r->seq.block_table.size();
             require(n - r->pages_on_device <= 1 && n <= d.row_stride, ERR_BAD_BLOCK_TABLE,
                     "a decode row gained more than one page");
-            desc[4 * b] = r->slot;
-            desc[4 * b + 1] = p.decode_positions[b];
-            desc[4 * b + 2] = n > r->pages_on_device ? r->pages_on_device : -1;
-            desc[4 * b + 3] = n > r->pages_on_device ? r->seq.block_table[n - 1] : 0;
+            int32_t* e = &desc[4 * (size_t)(c0 + b)];
+            e[0] = r->slot;
+            e[1] = positions[c0 + b] = p.decode_positions[b];
+            e[2] = n > r->pages_on_device ? r->pages_on_device : -1;
+            e[3] = n > r->pages_on_device ? r->seq.block_table[n - 1] : 0;
             r->pages_on_device = n;
         }
         for (Request* r : p.grown) {
@@ -191,33 +209,40 @@ int nitro_sched_step(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* p
             h.commit(0, nullptr, 0);
             return;
         }
+        const std::vector<int32_t> no_table;
+        const std::vector<int32_t>& chunk_table = chunk_rows ? p.prefill->seq.block_table : no_table;
 
-        // One upload: tokens (prefill rows, then decode rows), descriptors, other entries.
-        const size_t n_in = (size_t)P + B + desc.size() + other.size();
+        // One upload: tokens (prefill rows, then decode rows), descriptors,
+        // other entries, the chunk's table.
+        const size_t n_in = (size_t)P + B + desc.size() + other.size() + chunk_table.size();
         d.step_in.reserve(n_in);
         int32_t* hin = d.staging.acquire(n_in);
-        std::copy(p.prefill_tokens.begin(), p.prefill_tokens.end(), hin);
-        std::copy(p.decode_tokens.begin(), p.decode_tokens.end(), hin + P);
-        std::copy(desc.begin(), desc.end(), hin + P + B);
-        std::copy(other.begin(), other.end(), hin + P + B + desc.size());
+        int32_t* w = hin;
+        w = std::copy(p.prefill_tokens.begin(), p.prefill_tokens.end(), w);
+        w = std::copy(p.decode_tokens.begin(), p.decode_tokens.end(), w);
+        w = std::copy(desc.begin(), desc.end(), w);
+        w = std::copy(other.begin(), other.end(), w);
+        std::copy(chunk_table.begin(), chunk_table.end(), w);
         d.staging.copy(d.step_in.ptr, hin, n_in, s);
         d.staging.finish(s);
         const int32_t* d_tokens = d.step_in.ptr;
         const int32_t* d_desc = d.step_in.ptr + P + B;
         const int32_t* d_other = d_desc + desc.size();
+        const int32_t* d_chunk_table = d_other + other.size();
 
         int32_t* d_tables = nullptr;
         int32_t* d_positions = nullptr;
         int max_pages = 1;
-        if (B > 0) {
-            for (int b = 0; b < B; b++) max_pages = std::max(max_pages, p.decode_positions[b] / BLOCK_SIZE + 1);
-            set_device_decode_batch(pool, B, max_pages, p.decode_positions.data(),
-                                    rows_share_pages(d, p, pool->num_pages), &d_tables, &d_positions);
+        if (R > 0) {
+            for (int i = 0; i < R; i++) max_pages = std::max(max_pages, positions[i] / BLOCK_SIZE + 1);
+            // chunk rows read one table (and may share prefix hits with decode rows)
+            const bool shared = c0 > 0 || rows_share_pages(d, p, pool->num_pages);
+            set_device_decode_batch(pool, R, max_pages, positions.data(), shared, &d_tables, &d_positions);
         }
-        hip_check(launch_sched_tables(d.store.ptr, d.row_stride, d_desc, d_other, n_other, d_tables,
-                                      d_positions, B, max_pages, s),
+        hip_check(launch_sched_tables(d.store.ptr, d.row_stride, d_desc, d_other, n_other, d_chunk_table,
+                                      d_tables, d_positions, R, max_pages, s),
                   "sched_tables launch");
-        if (P > 0) {
+        if (P > 0 && !chunk_rows) {
             const std::vector<int32_t>& t = p.prefill->seq.block_table;
             const int32_t start = p.prefill_start, len = P;
             require(nitro_prefill_batch_upload(pool, t.data(), &start, &len, 1, (int32_t)t.size(), stream) ==
@@ -227,7 +252,8 @@ int nitro_sched_step(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* p
         if (P + B > 0) {
             d.logits.reserve((size_t)std::max(out_rows, 1) * vocab);
             d.next.reserve(std::max(out_rows, 1));
-            forward_mixed(model, pool, d_tokens, P, B, p.prefill_finishes, d.logits.ptr, d.next.ptr, semantics, s);
+            forward_mixed(model, pool, d_tokens, P, B, chunk_rows, p.prefill_finishes, d.logits.ptr, d.next.ptr,
+                          semantics, s);
         }
         if ((size_t)out_rows > d.readback_count) {
             if (d.readback) hip_check(hipHostFree(d.readback), "hipHostFree");
@@ -244,6 +270,14 @@ int nitro_sched_step(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* p
         d.last_rows = out_rows;
         const int first = p.prefill_finishes ? 1 : 0;
         h.commit(first ? d.readback[0] : 0, d.readback + first, B);
+    });
+}
+
+int nitro_argmax(const float* logits, int32_t rows, int32_t vocab, int32_t* out, void* stream) {
+    return guarded([&] {
+        require(logits != nullptr && out != nullptr, ERR_INVALID_ARGUMENT, "null pointer");
+        require(rows >= 0 && vocab > 0, ERR_INVALID_ARGUMENT, "rows must be >= 0 and vocab > 0");
+        hip_check(launch_argmax_rows(logits, out, rows, vocab, as_stream(stream)), "argmax launch");
     });
 }
 

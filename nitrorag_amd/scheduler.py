@@ -15,6 +15,24 @@ from .attention import _stream_ptr
 from .q8 import LAST_BLOCK
 
 
+def argmax(logits, out=None, stream=None):
+    """argmax (src/model_q8.cpp:559-569) of each row of a [rows][vocab] fp32
+    GPU tensor: the first index of the largest value above 0.0, 0 when none
+    exceeds 0.0.  Returns an int32 GPU tensor [rows]."""
+    import torch
+
+    from .attention import _dev
+
+    rows, vocab = logits.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int32, device=logits.device)
+    if out.dtype != torch.int32 or out.device.type != "cuda" or not out.is_contiguous() or out.numel() < rows:
+        raise TypeError("out must be a contiguous int32 GPU tensor with one entry per row")
+    N.call("nitro_argmax", _dev(logits, "logits"), rows, vocab, ctypes.c_void_p(out.data_ptr()),
+           _stream_ptr(stream))
+    return out
+
+
 @dataclass
 class StepPlan:
     """The two forward calls of one step: the prefill chunk (request id,

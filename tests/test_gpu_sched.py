@@ -107,3 +107,30 @@ def test_scheduler_refuses_positions_past_seq_len(golden_model):
     with pytest.raises(na.NitroError):
         S2.step(model, pool, LAST_BLOCK)  # position seq_len: refused
     assert S2.state_words() == words
+
+
+def test_device_argmax_quirks():
+    """nitro_argmax on hand-made rows against the oracle's restatement of the
+    reference's argmax (src/model_q8.cpp:559-569): all values <= 0 -> 0,
+    first of equal maxima, NaN never wins; rows of odd length take the
+    scalar path."""
+    import torch
+
+    from nitrorag_amd.scheduler import argmax
+    from oracle import scheduler as sc
+
+    rng = np.random.default_rng(5)
+    for vocab in (32000, 160, 1001, 7):
+        rows = rng.standard_normal((9, vocab)).astype(np.float32)
+        rows[1] = -np.abs(rows[1])                       # nothing above 0
+        rows[2] = 0.0
+        rows[3, :] = -1.0
+        rows[3, [vocab // 3, vocab - 1]] = 5.0           # equal maxima
+        rows[4, vocab - 1] = 100.0                        # maximum in the last entry
+        rows[5, ::2] = np.nan
+        rows[5, 1 % vocab] = 50.0
+        rows[6] = np.abs(rows[6]) * 1e-30                 # tiny positives
+        rows[7, :] = 2.0                                  # all equal -> 0
+        got = argmax(torch.from_numpy(rows).cuda()).cpu().numpy()
+        want = [sc.argmax(r) for r in rows]
+        assert got.tolist() == want, (vocab, got.tolist(), want)
