@@ -164,19 +164,40 @@ hipError_t launch_kv_append_decode(float* k_pool, float* v_pool, const float* k,
                                    int max_pages, int kv_dim, int64_t page_stride,
                                    int64_t layer_off, int num_pages, int32_t* bad_pages,
                                    hipStream_t stream);
+// rms_norm folded into a Q8 product's input (weight == nullptr: none): the
+// product reads the raw residual stream x and uses weight[k] * (inv * x[b][k])
+// with inv = 1 / sqrtf(sum_p ss[p * ss_stride + b] / n + 1e-5).
+struct Q8Norm {
+    const float* weight = nullptr;
+    const float* ss = nullptr;
+    int nparts = 0, ss_stride = 0;
+};
+// Residual epilogue of a Q8 product into x: x += product, and per 16-row
+// tile p of the output the sum of squares of each batch row's new entries
+// goes to ss[p * ss_stride + b].
+struct Q8Resid {
+    float* ss = nullptr;
+    int ss_stride = 0;
+};
 // Q8_0 matrix product (rows of BlockQ8, fp32 activations); last_block_only
 // selects the reference's matmul_bulk semantics.
 hipError_t launch_q8_matmul(const void* w, const float* x, float* out, int batch, int n, int d,
                             bool last_block_only, hipStream_t stream);
+// x[b] += w . in[b] ([batch][d], in place) with the squares of the new x
+// rows summed per 16 outputs into ss (ceil(d/16) partials per row, stride batch).
+hipError_t launch_q8_residual(const void* w, const float* in, float* x, float* ss, int batch, int n, int d,
+                              bool last_block_only, hipStream_t stream);
 // Three matrices sharing x and n (wq/wk/wv): out[m] = x . w[m]^T, [batch][d[m]].
 hipError_t launch_q8_matmul3(const void* const* w, const float* x, float* const* out, const int* d,
-                             int batch, int n, bool last_block_only, hipStream_t stream);
+                             int batch, int n, bool last_block_only, const Q8Norm& norm, hipStream_t stream);
 // hb = silu(x . w1^T) * (x . w3^T), [batch][hidden] (src/model_q8.cpp:670-680).
 hipError_t launch_q8_swiglu(const void* w1, const void* w3, const float* x, float* hb, int batch, int n,
-                            int hidden, bool last_block_only, hipStream_t stream);
+                            int hidden, bool last_block_only, const Q8Norm& norm, hipStream_t stream);
 // Row-wise model kernels and the fp32 classifier product (model_kernels.hip).
+// x[r] = table[tokens[r]]; with ss, ss[r] = the row's sum of squares (one
+// partial per row for a following Q8Norm).
 hipError_t launch_embed_rows(const float* table, const int32_t* tokens, float* x, int rows, int dim,
-                             int vocab, int32_t* bad_tokens, hipStream_t stream);
+                             int vocab, int32_t* bad_tokens, float* ss, hipStream_t stream);
 hipError_t launch_add_rmsnorm(float* x, const float* delta, const float* weight, float* out, int rows,
                               int dim, hipStream_t stream);
 hipError_t launch_gather_last_rows(const float* x, const float* ffn, const int32_t* row_off,

@@ -23,7 +23,7 @@ struct nitro_model {
     // section offsets (bytes) within `weights`, src/Server_Inference.cpp:52-69
     size_t o_emb = 0, o_rms_att = 0, o_wq = 0, o_wk = 0, o_wv = 0, o_wo = 0, o_rms_ffn = 0;
     size_t o_w1 = 0, o_w2 = 0, o_w3 = 0, o_rms_final = 0, o_freq_real = 0, o_freq_imag = 0;
-    DeviceBuffer<float> x, xb, attn, proj, ffn, q, k, v, hb, last;
+    DeviceBuffer<float> x, attn, q, k, v, hb, last, ss;
     DeviceBuffer<int32_t> tokens;
     Staging staging;
 
@@ -37,20 +37,11 @@ namespace {
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-void q8(const nitro_model* m, size_t off, int layer, int d, int n, const float* in, float* out,
-        int rows, int semantics, hipStream_t s) {
-    hip_check(launch_q8_matmul(m->q8(off, layer, d, n), in, out, rows, n, d,
-                               semantics == NITRO_Q8_LAST_BLOCK, s),
-              "q8_matmul launch");
-}
-
 void reserve_rows(nitro_model* m, int rows) {
     const size_t r = (size_t)rows;
     m->x.reserve(r * m->dim);
-    m->xb.reserve(r * m->dim);
     m->attn.reserve(r * m->dim);
-    m->proj.reserve(r * m->dim);
-    m->ffn.reserve(r * m->dim);
+    m->ss.reserve(r * (size_t)((m->dim + 15) / 16));
     m->q.reserve(r * m->dim);
     m->k.reserve(r * m->kv_dim);
     m->v.reserve(r * m->kv_dim);
@@ -76,38 +67,43 @@ void upload_tokens(nitro_model* m, const int32_t* tokens, int rows, hipStream_t 
     m->staging.finish(s);
 }
 
-// The layer loop shared by the decode and prefill forwards: after it, x holds
-// the residual stream and `ffn` the last layer's FFN output (not yet added).
+// The layer loop shared by the decode, prefill and mixed forwards.  x is the
+// residual stream; rms_norm is folded into the products that read it (wq/wk/wv
+// and w1/w3 take rms_norm(x, rms_att / rms_ffn) as input), and wo and w2 add
+// their products into x in place, leaving per row the partial sums of
+// squares the next norm needs in `ss` (src/model_q8.cpp:584-684).  After it x
+// holds the final residual stream.
 template <typename Attend>
 void layers(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int rows, int semantics, hipStream_t s,
             Attend attend) {
     const int dim = m->dim, kv = m->kv_dim, hid = m->hidden;
-    hip_check(launch_embed_rows(m->f32(m->o_emb), tokens, m->x.ptr, rows, dim, m->vocab,
-                                pool->bad_pages.ptr, s),
+    const bool last = semantics == NITRO_Q8_LAST_BLOCK;
+    const int parts = (dim + 15) / 16;  // partials per row left by wo / w2
+    hip_check(launch_embed_rows(m->f32(m->o_emb), tokens, m->x.ptr, rows, dim, m->vocab, pool->bad_pages.ptr,
+                                m->ss.ptr, s),
               "embed launch");
     for (int l = 0; l < m->n_layers; l++) {
-        // x += previous layer's FFN output; xb = rms_norm(x) (src/model_q8.cpp:586-589)
-        hip_check(launch_add_rmsnorm(m->x.ptr, l ? m->ffn.ptr : nullptr,
-                                     m->f32(m->o_rms_att) + (size_t)l * dim, m->xb.ptr, rows, dim, s),
-                  "rmsnorm launch");
-        // q, k, v = wq.xb, wk.xb, wv.xb in one launch (:590-592)
+        // q, k, v = wq/wk/wv . rms_norm(x, rms_att) in one launch (:586-592)
+        const Q8Norm att{m->f32(m->o_rms_att) + (size_t)l * dim, m->ss.ptr, l ? parts : 1, rows};
         const void* wqkv[3] = {m->q8(m->o_wq, l, dim, dim), m->q8(m->o_wk, l, kv, dim),
                                m->q8(m->o_wv, l, kv, dim)};
         float* qkv[3] = {m->q.ptr, m->k.ptr, m->v.ptr};
         const int dqkv[3] = {dim, kv, kv};
-        hip_check(launch_q8_matmul3(wqkv, m->xb.ptr, qkv, dqkv, rows, dim, semantics == NITRO_Q8_LAST_BLOCK, s),
-                  "q8_matmul3 launch");
+        hip_check(launch_q8_matmul3(wqkv, m->x.ptr, qkv, dqkv, rows, dim, last, att, s), "q8_matmul3 launch");
         attend(l);  // RoPE + KV append + attention -> m->attn (:594-662)
-        q8(m, m->o_wo, l, dim, dim, m->attn.ptr, m->proj.ptr, rows, semantics, s);  // :663
-        // x += wo . attn; xb = rms_norm(x) (:664-669)
-        hip_check(launch_add_rmsnorm(m->x.ptr, m->proj.ptr, m->f32(m->o_rms_ffn) + (size_t)l * dim,
-                                     m->xb.ptr, rows, dim, s),
-                  "rmsnorm launch");
-        // hb = silu(w1.xb) * (w3.xb) in one launch (:670-680)
-        hip_check(launch_q8_swiglu(m->q8(m->o_w1, l, hid, dim), m->q8(m->o_w3, l, hid, dim), m->xb.ptr,
-                                   m->hb.ptr, rows, dim, hid, semantics == NITRO_Q8_LAST_BLOCK, s),
+        // x += wo . attn (:663-666)
+        hip_check(launch_q8_residual(m->q8(m->o_wo, l, dim, dim), m->attn.ptr, m->x.ptr, m->ss.ptr, rows, dim,
+                                     dim, last, s),
+                  "q8 wo launch");
+        // hb = silu(w1 . xb) * (w3 . xb), xb = rms_norm(x, rms_ffn), one launch (:667-680)
+        const Q8Norm ffn{m->f32(m->o_rms_ffn) + (size_t)l * dim, m->ss.ptr, parts, rows};
+        hip_check(launch_q8_swiglu(m->q8(m->o_w1, l, hid, dim), m->q8(m->o_w3, l, hid, dim), m->x.ptr,
+                                   m->hb.ptr, rows, dim, hid, last, ffn, s),
                   "q8_swiglu launch");
-        q8(m, m->o_w2, l, dim, hid, m->hb.ptr, m->ffn.ptr, rows, semantics, s);  // :682
+        // x += w2 . hb (:682-684)
+        hip_check(launch_q8_residual(m->q8(m->o_w2, l, dim, hid), m->hb.ptr, m->x.ptr, m->ss.ptr, rows, hid,
+                                     dim, last, s),
+                  "q8 w2 launch");
     }
 }
 
@@ -180,14 +176,13 @@ void forward_mixed(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, in
         }
     });
     // The rows whose logits are used are contiguous: the chunk's last row
-    // (when it completes its prompt) and the decode rows.  x += FFN output;
-    // rms_norm; logits = wcls . x (:553-555, :687-692); argmax (:559-569).
+    // (when it completes its prompt) and the decode rows.  rms_norm; logits =
+    // wcls . x (:553-555, :687-692); argmax (:559-569).
     const int first = prefill_logits ? P - 1 : P;
     const int out_rows = P + B - first;
     if (out_rows == 0) return;
     float* x = m->x.ptr + first * dim;
-    hip_check(launch_add_rmsnorm(x, m->ffn.ptr + first * dim, m->f32(m->o_rms_final), x, out_rows, m->dim, s),
-              "rmsnorm launch");
+    hip_check(launch_add_rmsnorm(x, nullptr, m->f32(m->o_rms_final), x, out_rows, m->dim, s), "rmsnorm launch");
     hip_check(launch_f32_matmul(m->f32(m->o_emb), x, logits, out_rows, m->dim, m->vocab, s),
               "classifier launch");
     hip_check(launch_argmax_rows(logits, next, out_rows, m->vocab, s), "argmax launch");
@@ -294,8 +289,8 @@ int nitro_forward_decode_batch(nitro_model* m, nitro_kvpool* pool, const int32_t
                                             m->head_size, stream) == NITRO_OK,
                     ERR_INVALID_ARGUMENT, nitro_last_error());
         });
-        // x += FFN output; x = rms_norm(x) in place; logits = wcls . x (:687-692)
-        hip_check(launch_add_rmsnorm(m->x.ptr, m->ffn.ptr, m->f32(m->o_rms_final), m->x.ptr, batch, m->dim, s),
+        // x = rms_norm(x) in place; logits = wcls . x (:687-692)
+        hip_check(launch_add_rmsnorm(m->x.ptr, nullptr, m->f32(m->o_rms_final), m->x.ptr, batch, m->dim, s),
                   "rmsnorm launch");
         hip_check(launch_f32_matmul(m->f32(m->o_emb), m->x.ptr, logits, batch, m->dim, m->vocab, s),
                   "classifier launch");
@@ -327,8 +322,8 @@ int nitro_forward_prefill(nitro_model* m, nitro_kvpool* pool, const int32_t* tok
                                              m->head_size, stream) == NITRO_OK,
                     ERR_INVALID_ARGUMENT, nitro_last_error());
         });
-        // Each chunk's last token: x += FFN output; rms_norm; logits = wcls . x (:553-555)
-        hip_check(launch_gather_last_rows(m->x.ptr, m->ffn.ptr, p.d_row_off.ptr, p.d_len.ptr, m->last.ptr,
+        // Each chunk's last token: rms_norm; logits = wcls . x (:553-555)
+        hip_check(launch_gather_last_rows(m->x.ptr, nullptr, p.d_row_off.ptr, p.d_len.ptr, m->last.ptr,
                                           p.batch, m->dim, s),
                   "gather launch");
         hip_check(launch_add_rmsnorm(m->last.ptr, nullptr, m->f32(m->o_rms_final), m->last.ptr, p.batch,

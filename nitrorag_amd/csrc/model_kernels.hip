@@ -22,21 +22,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int ROW_THREADS = 256;
 
-__global__ __launch_bounds__(ROW_THREADS) void embed_rows_kernel(const float* __restrict__ table,
-                                                                 const int32_t* __restrict__ tokens,
-                                                                 float* __restrict__ x, int dim,
-                                                                 int vocab, int32_t* bad_tokens) {
-    const int r = blockIdx.x;
-    int t = tokens[r];
-    if ((unsigned)t >= (unsigned)vocab) {
-        if (threadIdx.x == 0) atomicAdd(bad_tokens, 1);
-        t = 0;  // defined result; the count reports the bad id
-    }
-    const float4* src = reinterpret_cast<const float4*>(table + (size_t)t * dim);
-    float4* dst = reinterpret_cast<float4*>(x + (size_t)r * dim);
-    for (int i = threadIdx.x; i < dim / 4; i += ROW_THREADS) dst[i] = src[i];
-}
-
 __device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
     for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m);
@@ -47,6 +32,32 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
     for (int w = 0; w < ROW_THREADS / 64; w++) s += red[w];
     return s;
+}
+
+__global__ __launch_bounds__(ROW_THREADS) void embed_rows_kernel(const float* __restrict__ table,
+                                                                 const int32_t* __restrict__ tokens,
+                                                                 float* __restrict__ x, int dim,
+                                                                 int vocab, int32_t* bad_tokens,
+                                                                 float* __restrict__ ss) {
+    __shared__ float red[ROW_THREADS / 64];
+    const int r = blockIdx.x;
+    int t = tokens[r];
+    if ((unsigned)t >= (unsigned)vocab) {
+        if (threadIdx.x == 0) atomicAdd(bad_tokens, 1);
+        t = 0;  // defined result; the count reports the bad id
+    }
+    const float4* src = reinterpret_cast<const float4*>(table + (size_t)t * dim);
+    float4* dst = reinterpret_cast<float4*>(x + (size_t)r * dim);
+    float sq = 0.0f;
+    for (int i = threadIdx.x; i < dim / 4; i += ROW_THREADS) {
+        const float4 v = src[i];
+        dst[i] = v;
+        sq = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, sq))));
+    }
+    if (ss) {  // uniform
+        sq = block_sum(sq, red);
+        if (threadIdx.x == 0) ss[r] = sq;
+    }
 }
 
 // One workgroup per row; x, delta, out are [rows][dim] (out may alias x).
@@ -72,7 +83,7 @@ __global__ __launch_bounds__(ROW_THREADS) void add_rmsnorm_kernel(float* x,
     for (int i = threadIdx.x; i < dim; i += ROW_THREADS) orow[i] = weight[i] * (inv * xr[i]);
 }
 
-// last[b] = x[r] + ffn[r] for the last row r = row_off[b] + len[b] - 1 of chunk b.
+// last[b] = x[r] (+ ffn[r] when given) for the last row r = row_off[b] + len[b] - 1 of chunk b.
 __global__ __launch_bounds__(ROW_THREADS) void gather_last_rows_kernel(const float* __restrict__ x,
                                                                        const float* __restrict__ ffn,
                                                                        const int32_t* __restrict__ row_off,
@@ -81,7 +92,7 @@ __global__ __launch_bounds__(ROW_THREADS) void gather_last_rows_kernel(const flo
     const int b = blockIdx.x;
     const size_t r = (size_t)(row_off[b] + len[b] - 1);
     for (int i = threadIdx.x; i < dim; i += ROW_THREADS)
-        last[(size_t)b * dim + i] = x[r * dim + i] + ffn[r * dim + i];
+        last[(size_t)b * dim + i] = ffn ? x[r * dim + i] + ffn[r * dim + i] : x[r * dim + i];
 }
 
 __global__ __launch_bounds__(ROW_THREADS) void swiglu_kernel(float* __restrict__ hb,
@@ -252,9 +263,9 @@ __global__ __launch_bounds__(64 * F32M_WAVES) void f32_matmul_mfma_kernel(const 
 }  // namespace
 
 hipError_t launch_embed_rows(const float* table, const int32_t* tokens, float* x, int rows, int dim,
-                             int vocab, int32_t* bad_tokens, hipStream_t stream) {
+                             int vocab, int32_t* bad_tokens, float* ss, hipStream_t stream) {
     hipLaunchKernelGGL(embed_rows_kernel, dim3(rows), dim3(ROW_THREADS), 0, stream, table, tokens, x,
-                       dim, vocab, bad_tokens);
+                       dim, vocab, bad_tokens, ss);
     return hipGetLastError();
 }
 

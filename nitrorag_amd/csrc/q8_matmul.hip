@@ -29,6 +29,16 @@
 // epilogue applies SwiGLU, hb = silu(w1.x) * (w3.x) (src/model_q8.cpp:672-680),
 // so the hidden activations are written once.
 //
+// The layer's rms_norm and residual adds live in these launches too:
+//  - NORM (the wq/wk/wv and w1/w3 groups): x is the raw residual stream and
+//    the input is rms_norm(x, weight) (src/model_q8.cpp:128-140): each x the
+//    kernel loads becomes weight[k] * (inv * x[b][k]), inv = 1 / sqrtf(ss / n
+//    + 1e-5), ss the sum of the row's partial sums of squares (written by
+//    the launch that last changed x), added in a fixed order;
+//  - RESID (wo, w2): the product is added into x in place and, per 16-row
+//    output tile, the squares of each batch row's 16 new entries are summed
+//    into one partial (tile p of row b at ss[p * ss_stride + b]).
+//
 // Batches of 1..4 rows use a VALU form of the same lane layout (q8_gemv):
 // each lane forms the dot products of its 16 weights with x directly, the
 // four lane groups of a row are summed with gfx950's row-swap permutes and
@@ -83,6 +93,26 @@ __device__ __forceinline__ float dequant(uint32_t q4, int j, float scale) {
     return (float)(int)(int8_t)(q4 >> (8 * j)) * scale;
 }
 
+// Partials first, first + step, ... of batch row b, added in that order; the
+// loads of 16 partials are issued before any is added (one round trip for a
+// row of up to 16 * step partials).
+__device__ __forceinline__ float partial_sum(const Q8Norm& nm, int b, int first, int step) {
+    float s = 0.0f;
+    for (int p0 = first; p0 < nm.nparts; p0 += 16 * step) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int p = p0 + i * step;
+            v[i] = p < nm.nparts ? nm.ss[(size_t)p * nm.ss_stride + b] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) s += v[i];
+    }
+    return s;
+}
+
+__device__ __forceinline__ float inv_rms(float ss, int n) { return 1.0f / sqrtf(ss / (float)n + 1e-5f); }
+
 }  // namespace
 
 // Up to 3 matrices sharing x (same n); out[m] is [batch][d[m]].
@@ -94,11 +124,12 @@ struct Q8Group {
 
 namespace {
 
-template <int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY>
+template <int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY, bool NORM, bool RESID>
 __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, const float* __restrict__ x,
-                                                                   int batch, int n) {
+                                                                   int batch, int n, Q8Norm nm, Q8Resid resid) {
     constexpr int U = NMAT == 1 ? Q8_UNROLL : 2;  // chunks in flight per wave
     __shared__ f32x4 red[Q8_WAVES - 1][NMAT][Q8_MAX_BTILES][64];
+    __shared__ float norm_s[NORM ? Q8_WAVES * 64 : 1];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int r = lane & 15;
@@ -108,6 +139,19 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
     const int btiles = min(Q8_MAX_BTILES, (batch - b0 + 15) / 16);
     const int nb = n / Q8_BLOCK;
     const int nchunk = (nb + 1) / 2;
+    if constexpr (NORM) {
+        // thread (row j = tid % 64, class c = tid / 64) adds partials c, c + 4, ...;
+        // then row j's four class sums are added in order: norm_s[j] = inv_rms
+        const int j = threadIdx.x & 63, c = threadIdx.x >> 6;
+        norm_s[c * 64 + j] = b0 + j < batch ? partial_sum(nm, b0 + j, c, Q8_WAVES) : 0.0f;
+        __syncthreads();
+        float ss = 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < Q8_WAVES; cc++) ss += norm_s[cc * 64 + lane];
+        __syncthreads();
+        if (wave == 0) norm_s[lane] = inv_rms(ss, n);
+        __syncthreads();
+    }
     const uint8_t* wrow[NMAT];
     bool act[NMAT];  // uniform: this tile has rows of member m
 #pragma unroll
@@ -145,8 +189,8 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
                 const int blk = 2 * (base + u) + (g >> 1);
                 const bool valid = base + u < nchunk && blk < nb && (!LAST_BLOCK_ONLY || blk == nb - 1);
                 if (valid && bb < batch) {
-                    const float4* xp = reinterpret_cast<const float4*>(
-                        x + (size_t)bb * n + blk * Q8_BLOCK + 16 * (g & 1));
+                    const int k0 = blk * Q8_BLOCK + 16 * (g & 1);
+                    const float4* xp = reinterpret_cast<const float4*>(x + (size_t)bb * n + k0);
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const float4 v = xp[i];
@@ -154,6 +198,18 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
                         xv[u][4 * i + 1] = v.y;
                         xv[u][4 * i + 2] = v.z;
                         xv[u][4 * i + 3] = v.w;
+                    }
+                    if constexpr (NORM) {
+                        const float inv = norm_s[t * 16 + r];
+                        const float4* wp = reinterpret_cast<const float4*>(nm.weight + k0);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const float4 w = wp[i];
+                            xv[u][4 * i] = w.x * (inv * xv[u][4 * i]);
+                            xv[u][4 * i + 1] = w.y * (inv * xv[u][4 * i + 1]);
+                            xv[u][4 * i + 2] = w.z * (inv * xv[u][4 * i + 2]);
+                            xv[u][4 * i + 3] = w.w * (inv * xv[u][4 * i + 3]);
+                        }
                     }
                 } else {
 #pragma unroll
@@ -195,7 +251,7 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
     if (wave > 0) return;
 #pragma unroll
     for (int t = 0; t < Q8_MAX_BTILES; t++) {
-        if (t >= btiles) break;
+        if (t >= btiles) break;  // uniform
         f32x4 s[NMAT];
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
@@ -204,20 +260,38 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
             for (int v = 0; v < Q8_WAVES - 1; v++) s[m] += red[v][m][t][lane];
         }
         const int bb = b0 + t * 16 + (lane & 15);
-        if (bb >= batch) continue;
+        if constexpr (RESID) {
+            // x[bb][row] += product; the squares of the tile's 16 new entries
+            // of row bb are summed over the four lane groups (rows 4*(l/16) + j)
+            float ssq = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int row = row0 + 4 * (lane >> 4) + j;
-            if constexpr (SWIGLU) {
-                if (row < grp.d[0]) {
-                    float h = s[0][j];
-                    h *= 1.0f / (1.0f + expf(-h));
-                    grp.out[0][(size_t)bb * grp.d[0] + row] = h * s[1][j];
+            for (int j = 0; j < 4; j++) {
+                const int row = row0 + 4 * (lane >> 4) + j;
+                if (bb < batch && row < grp.d[0]) {
+                    float* xe = grp.out[0] + (size_t)bb * grp.d[0] + row;
+                    const float v = *xe + s[0][j];
+                    *xe = v;
+                    ssq = fmaf(v, v, ssq);
                 }
-            } else {
+            }
+            ssq = sum_over_rows(ssq);
+            if (lane < 16 && bb < batch) resid.ss[(size_t)blockIdx.x * resid.ss_stride + bb] = ssq;
+        } else {
+            if (bb >= batch) continue;
 #pragma unroll
-                for (int m = 0; m < NMAT; m++)
-                    if (row < grp.d[m]) grp.out[m][(size_t)bb * grp.d[m] + row] = s[m][j];
+            for (int j = 0; j < 4; j++) {
+                const int row = row0 + 4 * (lane >> 4) + j;
+                if constexpr (SWIGLU) {
+                    if (row < grp.d[0]) {
+                        float h = s[0][j];
+                        h *= 1.0f / (1.0f + expf(-h));
+                        grp.out[0][(size_t)bb * grp.d[0] + row] = h * s[1][j];
+                    }
+                } else {
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++)
+                        if (row < grp.d[m]) grp.out[m][(size_t)bb * grp.d[m] + row] = s[m][j];
+                }
             }
         }
     }
@@ -228,18 +302,20 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
 // GEMV_WAVES waves owns 16 rows (of each group member); per slab of
 // GEMV_WAVES*U chunks (2048 k for one matrix) each wave first issues the
 // weight loads of its U chunks, then the workgroup stages the slab of x in
-// LDS (lanes of a lane group read the same x, which LDS broadcasts), and then
-// the waves compute.  The 4 lane groups are summed with row-swap permutes and
-// the waves through LDS in a fixed order (results are repeatable bit for bit).
+// LDS (lanes of a lane group read the same x, which LDS broadcasts; NORM
+// applies rms_norm while staging), and then the waves compute.  The 4 lane
+// groups are summed with row-swap permutes and the waves through LDS in a
+// fixed order (results are repeatable bit for bit).
 constexpr int GEMV_WAVES = 8;
 
-template <int NB, int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY>
+template <int NB, int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY, bool NORM, bool RESID>
 __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, const float* __restrict__ x,
-                                                                   int n) {
+                                                                   int n, Q8Norm nm, Q8Resid resid) {
     constexpr int U = NMAT == 1 ? Q8_UNROLL : 2;  // chunks in flight per wave
     constexpr int SLAB = GEMV_WAVES * U * 64;     // k per slab
     __shared__ __attribute__((aligned(16))) float xs[NB][SLAB];
     __shared__ float red[GEMV_WAVES][NMAT][NB][16];
+    __shared__ float inv_s[NB];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int r = lane & 15;
@@ -247,6 +323,17 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, c
     const int row0 = blockIdx.x * 16;
     const int nb = n / Q8_BLOCK;
     const int nchunk = (nb + 1) / 2;
+    if constexpr (NORM) {
+        // wave b < NB: lane i adds row b's partials i, i + 64, ...; then the
+        // 64 lane sums are added (ordered before use by the barrier ahead of
+        // the first slab's staging)
+        if (wave < NB) {
+            float v = partial_sum(nm, wave, lane, 64);
+#pragma unroll
+            for (int msk = 32; msk > 0; msk >>= 1) v += __shfl_xor(v, msk);
+            if (lane == 0) inv_s[wave] = inv_rms(v, n);
+        }
+    }
     const uint8_t* wrow[NMAT];
     bool act[NMAT];
 #pragma unroll
@@ -275,11 +362,17 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, c
         }
         const int slab_len = min(SLAB, n - slab);  // multiple of 32
         __syncthreads();  // previous slab's x reads are done
-        for (int i = threadIdx.x; i < NB * (slab_len / 4); i += 64 * GEMV_WAVES) {
-            const int b = i / (slab_len / 4), f = i - b * (slab_len / 4);
-            *reinterpret_cast<float4*>(&xs[b][4 * f]) =
-                reinterpret_cast<const float4*>(x + (size_t)b * n + slab)[f];
-        }
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+            for (int f = threadIdx.x; f < slab_len / 4; f += 64 * GEMV_WAVES) {
+                float4 v = reinterpret_cast<const float4*>(x + (size_t)b * n + slab)[f];
+                if constexpr (NORM) {
+                    const float inv = inv_s[b];
+                    const float4 w = reinterpret_cast<const float4*>(nm.weight + slab)[f];
+                    v = make_float4(w.x * (inv * v.x), w.y * (inv * v.y), w.z * (inv * v.z), w.w * (inv * v.w));
+                }
+                *reinterpret_cast<float4*>(&xs[b][4 * f]) = v;
+            }
         __syncthreads();
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -334,7 +427,19 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, c
 #pragma unroll
         for (int v = 0; v < GEMV_WAVES; v++) sum[m] += red[v][m][b][rr];
     }
-    if constexpr (SWIGLU) {
+    if constexpr (RESID) {
+        // x[b][row] += product; the 16 lanes of batch row b add their squares
+        float ssq = 0.0f;
+        if (row < grp.d[0]) {
+            float* xe = grp.out[0] + (size_t)b * grp.d[0] + row;
+            const float v = *xe + sum[0];
+            *xe = v;
+            ssq = v * v;
+        }
+#pragma unroll
+        for (int msk = 8; msk > 0; msk >>= 1) ssq += __shfl_xor(ssq, msk, 16);
+        if (rr == 0) resid.ss[(size_t)blockIdx.x * resid.ss_stride + b] = ssq;
+    } else if constexpr (SWIGLU) {
         if (row < grp.d[0]) {
             float h = sum[0];
             h *= 1.0f / (1.0f + expf(-h));
@@ -347,24 +452,27 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, c
     }
 }
 
-template <int NB, int NMAT, bool SWIGLU>
-static void launch_gemv(const Q8Group& grp, const float* x, int n, int dmax, bool last, hipStream_t stream) {
+template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID>
+void launch_gemv(const Q8Group& grp, const float* x, int n, int dmax, bool last, const Q8Norm& nm,
+                 const Q8Resid& rs, hipStream_t stream) {
     const dim3 grid((unsigned)((dmax + 15) / 16)), block(64 * GEMV_WAVES);
     if (last)
-        hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, true>), grid, block, 0, stream, grp, x, n);
+        hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, true, NORM, RESID>), grid, block, 0, stream, grp, x,
+                           n, nm, rs);
     else
-        hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, false>), grid, block, 0, stream, grp, x, n);
+        hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, false, NORM, RESID>), grid, block, 0, stream, grp,
+                           x, n, nm, rs);
 }
 
-template <int NMAT, bool SWIGLU>
-static void launch_group(const Q8Group& grp, const float* x, int batch, int n, int dmax, bool last,
-                         hipStream_t stream) {
+template <int NMAT, bool SWIGLU, bool NORM, bool RESID>
+void launch_group(const Q8Group& grp, const float* x, int batch, int n, int dmax, bool last, const Q8Norm& nm,
+                  const Q8Resid& rs, hipStream_t stream) {
     if (batch <= Q8_GEMV_MAX_BATCH) {
         switch (batch) {
-            case 1: launch_gemv<1, NMAT, SWIGLU>(grp, x, n, dmax, last, stream); break;
-            case 2: launch_gemv<2, NMAT, SWIGLU>(grp, x, n, dmax, last, stream); break;
-            case 3: launch_gemv<3, NMAT, SWIGLU>(grp, x, n, dmax, last, stream); break;
-            default: launch_gemv<4, NMAT, SWIGLU>(grp, x, n, dmax, last, stream); break;
+            case 1: launch_gemv<1, NMAT, SWIGLU, NORM, RESID>(grp, x, n, dmax, last, nm, rs, stream); break;
+            case 2: launch_gemv<2, NMAT, SWIGLU, NORM, RESID>(grp, x, n, dmax, last, nm, rs, stream); break;
+            case 3: launch_gemv<3, NMAT, SWIGLU, NORM, RESID>(grp, x, n, dmax, last, nm, rs, stream); break;
+            default: launch_gemv<4, NMAT, SWIGLU, NORM, RESID>(grp, x, n, dmax, last, nm, rs, stream); break;
         }
         return;
     }
@@ -372,9 +480,11 @@ static void launch_group(const Q8Group& grp, const float* x, int batch, int n, i
                     (unsigned)((batch + 16 * Q8_MAX_BTILES - 1) / (16 * Q8_MAX_BTILES)));
     const dim3 block(64 * Q8_WAVES);
     if (last)
-        hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, true>), grid, block, 0, stream, grp, x, batch, n);
+        hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, true, NORM, RESID>), grid, block, 0, stream, grp, x,
+                           batch, n, nm, rs);
     else
-        hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, false>), grid, block, 0, stream, grp, x, batch, n);
+        hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, false, NORM, RESID>), grid, block, 0, stream, grp, x,
+                           batch, n, nm, rs);
 }
 
 }  // namespace
@@ -382,12 +492,20 @@ static void launch_group(const Q8Group& grp, const float* x, int batch, int n, i
 hipError_t launch_q8_matmul(const void* w, const float* x, float* out, int batch, int n, int d,
                             bool last_block_only, hipStream_t stream) {
     Q8Group grp{{static_cast<const uint8_t*>(w), nullptr, nullptr}, {out, nullptr, nullptr}, {d, 0, 0}};
-    launch_group<1, false>(grp, x, batch, n, d, last_block_only, stream);
+    launch_group<1, false, false, false>(grp, x, batch, n, d, last_block_only, Q8Norm{}, Q8Resid{}, stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_residual(const void* w, const float* in, float* x, float* ss, int batch, int n, int d,
+                              bool last_block_only, hipStream_t stream) {
+    Q8Group grp{{static_cast<const uint8_t*>(w), nullptr, nullptr}, {x, nullptr, nullptr}, {d, 0, 0}};
+    launch_group<1, false, false, true>(grp, in, batch, n, d, last_block_only, Q8Norm{}, Q8Resid{ss, batch},
+                                        stream);
     return hipGetLastError();
 }
 
 hipError_t launch_q8_matmul3(const void* const* w, const float* x, float* const* out, const int* d,
-                             int batch, int n, bool last_block_only, hipStream_t stream) {
+                             int batch, int n, bool last_block_only, const Q8Norm& nm, hipStream_t stream) {
     Q8Group grp{};
     for (int m = 0; m < 3; m++) {
         grp.w[m] = static_cast<const uint8_t*>(w[m]);
@@ -395,16 +513,22 @@ hipError_t launch_q8_matmul3(const void* const* w, const float* x, float* const*
         grp.d[m] = d[m];
     }
     const int dmax = std::max(d[0], std::max(d[1], d[2]));
-    launch_group<3, false>(grp, x, batch, n, dmax, last_block_only, stream);
+    if (nm.weight)
+        launch_group<3, false, true, false>(grp, x, batch, n, dmax, last_block_only, nm, Q8Resid{}, stream);
+    else
+        launch_group<3, false, false, false>(grp, x, batch, n, dmax, last_block_only, nm, Q8Resid{}, stream);
     return hipGetLastError();
 }
 
 hipError_t launch_q8_swiglu(const void* w1, const void* w3, const float* x, float* hb, int batch, int n,
-                            int hidden, bool last_block_only, hipStream_t stream) {
+                            int hidden, bool last_block_only, const Q8Norm& nm, hipStream_t stream) {
     Q8Group grp{{static_cast<const uint8_t*>(w1), static_cast<const uint8_t*>(w3), nullptr},
                 {hb, nullptr, nullptr},
                 {hidden, hidden, 0}};
-    launch_group<2, true>(grp, x, batch, n, hidden, last_block_only, stream);
+    if (nm.weight)
+        launch_group<2, true, true, false>(grp, x, batch, n, hidden, last_block_only, nm, Q8Resid{}, stream);
+    else
+        launch_group<2, true, false, false>(grp, x, batch, n, hidden, last_block_only, nm, Q8Resid{}, stream);
     return hipGetLastError();
 }
 
