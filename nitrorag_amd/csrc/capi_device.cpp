@@ -88,13 +88,16 @@ int env_int(const char* name, int fallback) {
 namespace nitro {
 
 void set_device_decode_batch(nitro_kvpool* pool, int batch, int max_pages, const int32_t* positions,
-                             bool shared_pages, int32_t** tables, int32_t** device_positions) {
+                             bool shared_pages, int32_t** tables, int32_t** device_positions,
+                             int32_t** device_slots) {
     require_pool(pool);
     require(batch > 0 && max_pages > 0, ERR_INVALID_ARGUMENT, "batch and max_pages must be positive");
     DecodeBatch& d = pool->decode;
     d.batch = 0;
     d.tables.reserve((size_t)batch * max_pages);
     d.pos.reserve(batch);
+    d.slots.reserve(batch);
+    *device_slots = d.slots.ptr;
     d.positions.assign(positions, positions + batch);
     d.shared_pages = shared_pages;
     d.batch = batch;
@@ -204,13 +207,18 @@ int nitro_decode_batch_upload(nitro_kvpool* pool, const int32_t* tables, const i
         d.batch = 0;  // invalid until the copies are issued
         d.tables.reserve(nt);
         d.pos.reserve(batch);
+        d.slots.reserve(batch);
         hipStream_t s = as_stream(stream);
         Staging& st = pool->decode_staging;
-        int32_t* h = st.acquire(nt + batch);
+        int32_t* h = st.acquire(nt + 2 * (size_t)batch);
         std::memcpy(h, tables, nt * sizeof(int32_t));
         std::memcpy(h + nt, positions, batch * sizeof(int32_t));
+        for (int b = 0; b < batch; b++)  // where each row's K/V goes (the fused RoPE/append reads it)
+            h[nt + batch + b] = tables[(size_t)b * max_pages + positions[b] / BLOCK_SIZE] * BLOCK_SIZE +
+                                positions[b] % BLOCK_SIZE;
         st.copy(d.tables.ptr, h, nt, s);
         st.copy(d.pos.ptr, h + nt, batch, s);
+        st.copy(d.slots.ptr, h + nt + batch, batch, s);
         st.finish(s);
         d.positions.assign(positions, positions + batch);
         d.shared_pages = any_page_shared(pool, d, tables, positions, batch, max_pages);

@@ -94,6 +94,7 @@ struct DecodeBatch {
     std::vector<uint32_t> page_mark; // per pool page: upload stamp (shared-page scan)
     uint32_t stamp = 0;
     DeviceBuffer<int32_t> tables, pos;
+    DeviceBuffer<int32_t> slots;     // per row: page * 16 + position % 16 (where its K/V row goes)
 };
 
 struct PrefillBatch {
@@ -179,6 +180,26 @@ struct Q8Resid {
     float* ss = nullptr;
     int ss_stride = 0;
 };
+// RoPE and the K/V append folded into the wq/wk/wv product's epilogue
+// (src/model_q8.cpp:594-617, 447-470): q and k are rotated with
+// freq_real/imag[pos] of their batch row, q goes to its buffer, k and v
+// straight into the pools at the row's slot (page * 16 + position % 16).
+// Rows below `split` take position / slot from pos[0] / slot[0], the others
+// from pos[1] / slot[1] at (row - split).  Page ids outside the pool are
+// skipped and counted in bad_pages.
+struct Q8Rope {
+    const float* freq_real = nullptr;
+    const float* freq_imag = nullptr;
+    int head_dim = 0;
+    float* k_pool = nullptr;
+    float* v_pool = nullptr;
+    int64_t page_stride = 0, layer_off = 0;
+    int num_pages = 0;
+    int32_t* bad_pages = nullptr;
+    const int32_t* pos[2] = {nullptr, nullptr};
+    const int32_t* slot[2] = {nullptr, nullptr};
+    int split = 0;
+};
 // Q8_0 matrix product (rows of BlockQ8, fp32 activations); last_block_only
 // selects the reference's matmul_bulk semantics.
 hipError_t launch_q8_matmul(const void* w, const float* x, float* out, int batch, int n, int d,
@@ -187,9 +208,11 @@ hipError_t launch_q8_matmul(const void* w, const float* x, float* out, int batch
 // rows summed per 16 outputs into ss (ceil(d/16) partials per row, stride batch).
 hipError_t launch_q8_residual(const void* w, const float* in, float* x, float* ss, int batch, int n, int d,
                               bool last_block_only, hipStream_t stream);
-// Three matrices sharing x and n (wq/wk/wv): out[m] = x . w[m]^T, [batch][d[m]].
-hipError_t launch_q8_matmul3(const void* const* w, const float* x, float* const* out, const int* d,
-                             int batch, int n, bool last_block_only, const Q8Norm& norm, hipStream_t stream);
+// wq/wk/wv sharing x and n: q = wq . rms_norm(x), k, v likewise, with the
+// RoPE + K/V-append epilogue: q written to out_q [batch][dim], k and v to the
+// pools (d = {dim, kv_dim, kv_dim}).
+hipError_t launch_q8_qkv(const void* const* w, const float* x, float* out_q, const int* d, int batch, int n,
+                         bool last_block_only, const Q8Norm& norm, const Q8Rope& rope, hipStream_t stream);
 // hb = silu(x . w1^T) * (x . w3^T), [batch][hidden] (src/model_q8.cpp:670-680).
 hipError_t launch_q8_swiglu(const void* w1, const void* w3, const float* x, float* hb, int batch, int n,
                             int hidden, bool last_block_only, const Q8Norm& norm, hipStream_t stream);
@@ -222,7 +245,7 @@ hipError_t launch_kv_scatter_rows(float* k_pool, float* v_pool, const float* k, 
 // rows -> this step's decode tables, and the reference's argmax per row.
 hipError_t launch_sched_tables(int32_t* store, int row_stride, const int32_t* desc, const int32_t* other,
                                int n_other, const int32_t* chunk_table, int32_t* tables, int32_t* positions,
-                               int batch, int max_pages, hipStream_t stream);
+                               int32_t* slots, int batch, int max_pages, hipStream_t stream);
 hipError_t launch_argmax_rows(const float* logits, int32_t* next, int rows, int vocab, hipStream_t stream);
 
 struct PrefillLaunch {
@@ -253,7 +276,8 @@ namespace nitro {
 // the caller writes on the device (stream-ordered before the next launch);
 // positions is the host copy (launch geometry).  Returns the device arrays.
 void set_device_decode_batch(nitro_kvpool* pool, int batch, int max_pages, const int32_t* positions,
-                             bool shared_pages, int32_t** tables, int32_t** device_positions);
+                             bool shared_pages, int32_t** tables, int32_t** device_positions,
+                             int32_t** device_slots);
 
 // One forward over prefill rows [0, prefill_rows) and decode rows
 // [prefill_rows, prefill_rows + decode_rows), tokens on the device.  With

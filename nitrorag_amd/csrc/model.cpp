@@ -5,6 +5,7 @@
 // include/nitro_paged_attn.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -23,7 +24,7 @@ struct nitro_model {
     // section offsets (bytes) within `weights`, src/Server_Inference.cpp:52-69
     size_t o_emb = 0, o_rms_att = 0, o_wq = 0, o_wk = 0, o_wv = 0, o_wo = 0, o_rms_ffn = 0;
     size_t o_w1 = 0, o_w2 = 0, o_w3 = 0, o_rms_final = 0, o_freq_real = 0, o_freq_imag = 0;
-    DeviceBuffer<float> x, attn, q, k, v, hb, last, ss;
+    DeviceBuffer<float> x, attn, q, hb, last, ss;
     DeviceBuffer<int32_t> tokens;
     Staging staging;
 
@@ -43,8 +44,6 @@ void reserve_rows(nitro_model* m, int rows) {
     m->attn.reserve(r * m->dim);
     m->ss.reserve(r * (size_t)((m->dim + 15) / 16));
     m->q.reserve(r * m->dim);
-    m->k.reserve(r * m->kv_dim);
-    m->v.reserve(r * m->kv_dim);
     m->hb.reserve(r * m->hidden);
     m->tokens.reserve(r);
 }
@@ -74,8 +73,8 @@ void upload_tokens(nitro_model* m, const int32_t* tokens, int rows, hipStream_t 
 // squares the next norm needs in `ss` (src/model_q8.cpp:584-684).  After it x
 // holds the final residual stream.
 template <typename Attend>
-void layers(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int rows, int semantics, hipStream_t s,
-            Attend attend) {
+void layers(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int rows, int semantics, Q8Rope rope,
+            hipStream_t s, Attend attend) {
     const int dim = m->dim, kv = m->kv_dim, hid = m->hidden;
     const bool last = semantics == NITRO_Q8_LAST_BLOCK;
     const int parts = (dim + 15) / 16;  // partials per row left by wo / w2
@@ -83,14 +82,15 @@ void layers(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int rows,
                                 m->ss.ptr, s),
               "embed launch");
     for (int l = 0; l < m->n_layers; l++) {
-        // q, k, v = wq/wk/wv . rms_norm(x, rms_att) in one launch (:586-592)
+        // q, k, v = wq/wk/wv . rms_norm(x, rms_att) in one launch, RoPE on q and
+        // k, k and v appended to the pools (:586-617)
         const Q8Norm att{m->f32(m->o_rms_att) + (size_t)l * dim, m->ss.ptr, l ? parts : 1, rows};
         const void* wqkv[3] = {m->q8(m->o_wq, l, dim, dim), m->q8(m->o_wk, l, kv, dim),
                                m->q8(m->o_wv, l, kv, dim)};
-        float* qkv[3] = {m->q.ptr, m->k.ptr, m->v.ptr};
         const int dqkv[3] = {dim, kv, kv};
-        hip_check(launch_q8_matmul3(wqkv, m->x.ptr, qkv, dqkv, rows, dim, last, att, s), "q8_matmul3 launch");
-        attend(l);  // RoPE + KV append + attention -> m->attn (:594-662)
+        rope.layer_off = pool->layer_offset(l);
+        hip_check(launch_q8_qkv(wqkv, m->x.ptr, m->q.ptr, dqkv, rows, dim, last, att, rope, s), "q8_qkv launch");
+        attend(l);  // attention over the pools -> m->attn (:618-662)
         // x += wo . attn (:663-666)
         hip_check(launch_q8_residual(m->q8(m->o_wo, l, dim, dim), m->attn.ptr, m->x.ptr, m->ss.ptr, rows, dim,
                                      dim, last, s),
@@ -108,6 +108,38 @@ void layers(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int rows,
 }
 
 size_t q8_bytes(size_t rows, size_t cols) { return rows * (cols / 32) * 36; }
+
+// RoPE / K-V append arguments of a forward: rows below `split` take position
+// and slot from (pos_a, slot_a), the rest from (pos_b, slot_b).
+Q8Rope rope_args(const nitro_model* m, nitro_kvpool* pool, const int32_t* pos_a, const int32_t* slot_a,
+                 int split, const int32_t* pos_b, const int32_t* slot_b) {
+    Q8Rope r;
+    r.freq_real = m->f32(m->o_freq_real);
+    r.freq_imag = m->f32(m->o_freq_imag);
+    r.head_dim = m->head_size;
+    r.k_pool = pool->k;
+    r.v_pool = pool->v;
+    r.page_stride = pool->page_stride();
+    r.num_pages = pool->num_pages;
+    r.bad_pages = pool->bad_pages.ptr;
+    r.pos[0] = pos_a;
+    r.slot[0] = slot_a;
+    r.pos[1] = pos_b;
+    r.slot[1] = slot_b;
+    r.split = split;
+    return r;
+}
+
+void check_positions(const nitro_model* m, int max_pos) {
+    if (max_pos >= m->seq_len)
+        throw Error(ERR_INVALID_ARGUMENT, "position " + std::to_string(max_pos) + " is outside the model's seq_len");
+}
+
+int max_of(const std::vector<int32_t>& v) {
+    int r = 0;
+    for (int x : v) r = std::max(r, (int)x);
+    return r;
+}
 
 }  // namespace
 
@@ -134,46 +166,38 @@ void forward_mixed(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, in
                 "the prefill rows differ from the uploaded one-sequence prefill batch");
         require(B == 0 || pool->decode.batch == B, ERR_NO_BATCH, "the decode rows differ from the decode batch");
     }
-    const size_t dim = m->dim, kv = m->kv_dim;
+    const size_t dim = m->dim;
     void* stream = s;
+    const DecodeBatch& d = pool->decode;
+    const PrefillBatch& pf = pool->prefill;
+    if (prefill_as_decode || B > 0) check_positions(m, max_of(d.positions));
+    if (!prefill_as_decode && P > 0) check_positions(m, pf.max_pos);
+    // every row's RoPE position and K/V slot: the decode batch's, or the
+    // prefill batch's for rows [0, P) when those go through the prefill kernel
+    const Q8Rope rope = prefill_as_decode || P == 0
+                            ? rope_args(m, pool, d.pos.ptr, d.slots.ptr, P + B, nullptr, nullptr)
+                            : rope_args(m, pool, pf.row_pos.ptr, pf.slots.ptr, P, d.pos.ptr, d.slots.ptr);
     reserve_rows(m, P + B);
-    layers(m, pool, tokens, P + B, semantics, s, [&](int l) {
+    layers(m, pool, tokens, P + B, semantics, rope, s, [&](int l) {
         if (prefill_as_decode) {
-            // every row attends its own prefix (keys 0..position): RoPE + KV
-            // append of all rows, then one decode-attention launch; a chunk
-            // row at position p sees the same keys as in forward_prefill_chunk
-            // (src/model_q8.cpp:493-530)
-            require(nitro_rope_kv_append(pool, l, m->q.ptr, m->k.ptr, m->v.ptr, m->f32(m->o_freq_real),
-                                         m->f32(m->o_freq_imag), m->seq_len, m->n_heads, m->n_kv_heads,
-                                         m->head_size, stream) == NITRO_OK,
-                    ERR_INVALID_ARGUMENT, nitro_last_error());
+            // every row attends its own prefix (keys 0..position) in one
+            // decode-attention launch; a chunk row at position p sees the same
+            // keys as in forward_prefill_chunk (src/model_q8.cpp:493-530)
             require(nitro_paged_attn_decode(pool, l, m->q.ptr, m->attn.ptr, m->n_heads, m->n_kv_heads,
                                             m->head_size, stream) == NITRO_OK,
                     ERR_INVALID_ARGUMENT, nitro_last_error());
             return;
         }
-        // forward_prefill_chunk's RoPE, KV append and causal attention for
-        // rows [0, P) (src/model_q8.cpp:447-530), forward_decode_batch's for
-        // the rest (:594-662)
-        if (P > 0) {
-            require(nitro_rope_kv_append_prefill(pool, l, m->q.ptr, m->k.ptr, m->v.ptr, m->f32(m->o_freq_real),
-                                                 m->f32(m->o_freq_imag), m->seq_len, m->n_heads,
-                                                 m->n_kv_heads, m->head_size, stream) == NITRO_OK,
-                    ERR_INVALID_ARGUMENT, nitro_last_error());
+        // forward_prefill_chunk's causal attention for rows [0, P)
+        // (src/model_q8.cpp:471-530), forward_decode_batch's for the rest (:618-662)
+        if (P > 0)
             require(nitro_paged_attn_prefill(pool, l, m->q.ptr, m->attn.ptr, m->n_heads, m->n_kv_heads,
                                              m->head_size, stream) == NITRO_OK,
                     ERR_INVALID_ARGUMENT, nitro_last_error());
-        }
-        if (B > 0) {
-            float* q = m->q.ptr + P * dim;
-            require(nitro_rope_kv_append(pool, l, q, m->k.ptr + P * kv, m->v.ptr + P * kv,
-                                         m->f32(m->o_freq_real), m->f32(m->o_freq_imag), m->seq_len,
-                                         m->n_heads, m->n_kv_heads, m->head_size, stream) == NITRO_OK,
+        if (B > 0)
+            require(nitro_paged_attn_decode(pool, l, m->q.ptr + P * dim, m->attn.ptr + P * dim, m->n_heads,
+                                            m->n_kv_heads, m->head_size, stream) == NITRO_OK,
                     ERR_INVALID_ARGUMENT, nitro_last_error());
-            require(nitro_paged_attn_decode(pool, l, q, m->attn.ptr + P * dim, m->n_heads, m->n_kv_heads,
-                                            m->head_size, stream) == NITRO_OK,
-                    ERR_INVALID_ARGUMENT, nitro_last_error());
-        }
     });
     // The rows whose logits are used are contiguous: the chunk's last row
     // (when it completes its prompt) and the decode rows.  rms_norm; logits =
@@ -278,13 +302,12 @@ int nitro_forward_decode_batch(nitro_model* m, nitro_kvpool* pool, const int32_t
         require(batch == pool->decode.batch, ERR_INVALID_ARGUMENT,
                 "batch differs from the uploaded decode batch");
         hipStream_t s = as_stream(stream);
+        const DecodeBatch& d = pool->decode;
+        check_positions(m, max_of(d.positions));
         reserve_rows(m, batch);
         upload_tokens(m, tokens, batch, s);
-        layers(m, pool, m->tokens.ptr, batch, semantics, s, [&](int l) {
-            require(nitro_rope_kv_append(pool, l, m->q.ptr, m->k.ptr, m->v.ptr, m->f32(m->o_freq_real),
-                                         m->f32(m->o_freq_imag), m->seq_len, m->n_heads, m->n_kv_heads,
-                                         m->head_size, stream) == NITRO_OK,
-                    ERR_INVALID_ARGUMENT, nitro_last_error());
+        const Q8Rope rope = rope_args(m, pool, d.pos.ptr, d.slots.ptr, batch, nullptr, nullptr);
+        layers(m, pool, m->tokens.ptr, batch, semantics, rope, s, [&](int l) {
             require(nitro_paged_attn_decode(pool, l, m->q.ptr, m->attn.ptr, m->n_heads, m->n_kv_heads,
                                             m->head_size, stream) == NITRO_OK,
                     ERR_INVALID_ARGUMENT, nitro_last_error());
@@ -313,11 +336,9 @@ int nitro_forward_prefill(nitro_model* m, nitro_kvpool* pool, const int32_t* tok
         reserve_rows(m, total_rows);
         m->last.reserve((size_t)p.batch * m->dim);
         upload_tokens(m, tokens, total_rows, s);
-        layers(m, pool, m->tokens.ptr, total_rows, semantics, s, [&](int l) {
-            require(nitro_rope_kv_append_prefill(pool, l, m->q.ptr, m->k.ptr, m->v.ptr, m->f32(m->o_freq_real),
-                                                 m->f32(m->o_freq_imag), m->seq_len, m->n_heads,
-                                                 m->n_kv_heads, m->head_size, stream) == NITRO_OK,
-                    ERR_INVALID_ARGUMENT, nitro_last_error());
+        check_positions(m, p.max_pos);
+        const Q8Rope rope = rope_args(m, pool, p.row_pos.ptr, p.slots.ptr, total_rows, nullptr, nullptr);
+        layers(m, pool, m->tokens.ptr, total_rows, semantics, rope, s, [&](int l) {
             require(nitro_paged_attn_prefill(pool, l, m->q.ptr, m->attn.ptr, m->n_heads, m->n_kv_heads,
                                              m->head_size, stream) == NITRO_OK,
                     ERR_INVALID_ARGUMENT, nitro_last_error());

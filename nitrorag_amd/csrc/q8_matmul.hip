@@ -113,6 +113,33 @@ __device__ __forceinline__ float partial_sum(const Q8Norm& nm, int b, int first,
 
 __device__ __forceinline__ float inv_rms(float ss, int n) { return 1.0f / sqrtf(ss / (float)n + 1e-5f); }
 
+// Where batch row b's K/V goes and the position it rotates with.
+struct RopeRow {
+    int pos, page, in_page;
+    bool page_ok;
+};
+
+__device__ __forceinline__ RopeRow rope_row(const Q8Rope& rp, int b) {
+    const int w = b < rp.split ? 0 : 1;
+    const int i = w ? b - rp.split : b;
+    RopeRow r;
+    r.pos = rp.pos[w][i];
+    const int slot = rp.slot[w][i];
+    r.page = slot >> 4;
+    r.in_page = slot & 15;
+    r.page_ok = r.page >= 0 && r.page < rp.num_pages;
+    return r;
+}
+
+// (x, y) rotated by the angle of pair f of position pos: the reference's
+// (x*fcr - y*fci, x*fci + y*fcr) (src/model_q8.cpp:600-612).
+__device__ __forceinline__ float2 rotate_pair(const Q8Rope& rp, int pos, int feature, float x, float y) {
+    const int f = (feature % rp.head_dim) >> 1;
+    const float c = rp.freq_real[(size_t)pos * (rp.head_dim >> 1) + f];
+    const float sn = rp.freq_imag[(size_t)pos * (rp.head_dim >> 1) + f];
+    return make_float2(x * c - y * sn, x * sn + y * c);
+}
+
 }  // namespace
 
 // Up to 3 matrices sharing x (same n); out[m] is [batch][d[m]].
@@ -124,9 +151,10 @@ struct Q8Group {
 
 namespace {
 
-template <int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY, bool NORM, bool RESID>
+template <int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY, bool NORM, bool RESID, bool ROPE>
 __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, const float* __restrict__ x,
-                                                                   int batch, int n, Q8Norm nm, Q8Resid resid) {
+                                                                   int batch, int n, Q8Norm nm, Q8Resid resid,
+                                                                   Q8Rope rope) {
     constexpr int U = NMAT == 1 ? Q8_UNROLL : 2;  // chunks in flight per wave
     __shared__ f32x4 red[Q8_WAVES - 1][NMAT][Q8_MAX_BTILES][64];
     __shared__ float norm_s[NORM ? Q8_WAVES * 64 : 1];
@@ -260,6 +288,30 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
             for (int v = 0; v < Q8_WAVES - 1; v++) s[m] += red[v][m][t][lane];
         }
         const int bb = b0 + t * 16 + (lane & 15);
+        if constexpr (ROPE) {
+            // q, k, v for features f0..f0+3 of row bb: two RoPE pairs
+            if (bb >= batch) continue;
+            const RopeRow rr = rope_row(rope, bb);
+            const int f0 = row0 + 4 * (lane >> 4);
+            if (f0 < grp.d[0]) {
+                const float2 a = rotate_pair(rope, rr.pos, f0, s[0][0], s[0][1]);
+                const float2 c = rotate_pair(rope, rr.pos, f0 + 2, s[0][2], s[0][3]);
+                *reinterpret_cast<float4*>(grp.out[0] + (size_t)bb * grp.d[0] + f0) = make_float4(a.x, a.y, c.x, c.y);
+            }
+            if (f0 < grp.d[1]) {
+                if (rr.page_ok) {
+                    const size_t o = (size_t)rr.page * rope.page_stride + rope.layer_off +
+                                     (size_t)rr.in_page * grp.d[1] + f0;
+                    const float2 a = rotate_pair(rope, rr.pos, f0, s[1][0], s[1][1]);
+                    const float2 c = rotate_pair(rope, rr.pos, f0 + 2, s[1][2], s[1][3]);
+                    *reinterpret_cast<float4*>(rope.k_pool + o) = make_float4(a.x, a.y, c.x, c.y);
+                    *reinterpret_cast<float4*>(rope.v_pool + o) = make_float4(s[2][0], s[2][1], s[2][2], s[2][3]);
+                } else if (f0 == 0) {
+                    atomicAdd(rope.bad_pages, 1);  // once per row: the lane holding feature 0
+                }
+            }
+            continue;
+        }
         if constexpr (RESID) {
             // x[bb][row] += product; the squares of the tile's 16 new entries
             // of row bb are summed over the four lane groups (rows 4*(l/16) + j)
@@ -308,9 +360,9 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
 // fixed order (results are repeatable bit for bit).
 constexpr int GEMV_WAVES = 8;
 
-template <int NB, int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY, bool NORM, bool RESID>
+template <int NB, int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY, bool NORM, bool RESID, bool ROPE>
 __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, const float* __restrict__ x,
-                                                                   int n, Q8Norm nm, Q8Resid resid) {
+                                                                   int n, Q8Norm nm, Q8Resid resid, Q8Rope rope) {
     constexpr int U = NMAT == 1 ? Q8_UNROLL : 2;  // chunks in flight per wave
     constexpr int SLAB = GEMV_WAVES * U * 64;     // k per slab
     __shared__ __attribute__((aligned(16))) float xs[NB][SLAB];
@@ -427,6 +479,27 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, c
 #pragma unroll
         for (int v = 0; v < GEMV_WAVES; v++) sum[m] += red[v][m][b][rr];
     }
+    if constexpr (ROPE) {
+        // RoPE pairs are features (row, row ^ 1): adjacent lanes of the group
+        const float q_o = __shfl_xor(sum[0], 1), k_o = __shfl_xor(sum[1], 1);
+        const RopeRow rp = rope_row(rope, b);
+        const bool odd = rr & 1;
+        const int fe = row & ~1;
+        const float2 qr = rotate_pair(rope, rp.pos, fe, odd ? q_o : sum[0], odd ? sum[0] : q_o);
+        const float2 kr = rotate_pair(rope, rp.pos, fe, odd ? k_o : sum[1], odd ? sum[1] : k_o);
+        if (row < grp.d[0]) grp.out[0][(size_t)b * grp.d[0] + row] = odd ? qr.y : qr.x;
+        if (row < grp.d[1]) {
+            if (rp.page_ok) {
+                const size_t o = (size_t)rp.page * rope.page_stride + rope.layer_off +
+                                 (size_t)rp.in_page * grp.d[1] + row;
+                rope.k_pool[o] = odd ? kr.y : kr.x;
+                rope.v_pool[o] = sum[2];
+            } else if (row == 0) {
+                atomicAdd(rope.bad_pages, 1);  // once per row
+            }
+        }
+        return;
+    }
     if constexpr (RESID) {
         // x[b][row] += product; the 16 lanes of batch row b add their squares
         float ssq = 0.0f;
@@ -452,27 +525,27 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, c
     }
 }
 
-template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID>
+template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
 void launch_gemv(const Q8Group& grp, const float* x, int n, int dmax, bool last, const Q8Norm& nm,
-                 const Q8Resid& rs, hipStream_t stream) {
+                 const Q8Resid& rs, const Q8Rope& rp, hipStream_t stream) {
     const dim3 grid((unsigned)((dmax + 15) / 16)), block(64 * GEMV_WAVES);
     if (last)
-        hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, true, NORM, RESID>), grid, block, 0, stream, grp, x,
-                           n, nm, rs);
+        hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, true, NORM, RESID, ROPE>), grid, block, 0, stream,
+                           grp, x, n, nm, rs, rp);
     else
-        hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, false, NORM, RESID>), grid, block, 0, stream, grp,
-                           x, n, nm, rs);
+        hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, false, NORM, RESID, ROPE>), grid, block, 0, stream,
+                           grp, x, n, nm, rs, rp);
 }
 
-template <int NMAT, bool SWIGLU, bool NORM, bool RESID>
+template <int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE = false>
 void launch_group(const Q8Group& grp, const float* x, int batch, int n, int dmax, bool last, const Q8Norm& nm,
-                  const Q8Resid& rs, hipStream_t stream) {
+                  const Q8Resid& rs, hipStream_t stream, const Q8Rope& rp = Q8Rope{}) {
     if (batch <= Q8_GEMV_MAX_BATCH) {
         switch (batch) {
-            case 1: launch_gemv<1, NMAT, SWIGLU, NORM, RESID>(grp, x, n, dmax, last, nm, rs, stream); break;
-            case 2: launch_gemv<2, NMAT, SWIGLU, NORM, RESID>(grp, x, n, dmax, last, nm, rs, stream); break;
-            case 3: launch_gemv<3, NMAT, SWIGLU, NORM, RESID>(grp, x, n, dmax, last, nm, rs, stream); break;
-            default: launch_gemv<4, NMAT, SWIGLU, NORM, RESID>(grp, x, n, dmax, last, nm, rs, stream); break;
+            case 1: launch_gemv<1, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, last, nm, rs, rp, stream); break;
+            case 2: launch_gemv<2, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, last, nm, rs, rp, stream); break;
+            case 3: launch_gemv<3, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, last, nm, rs, rp, stream); break;
+            default: launch_gemv<4, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, last, nm, rs, rp, stream); break;
         }
         return;
     }
@@ -480,11 +553,11 @@ void launch_group(const Q8Group& grp, const float* x, int batch, int n, int dmax
                     (unsigned)((batch + 16 * Q8_MAX_BTILES - 1) / (16 * Q8_MAX_BTILES)));
     const dim3 block(64 * Q8_WAVES);
     if (last)
-        hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, true, NORM, RESID>), grid, block, 0, stream, grp, x,
-                           batch, n, nm, rs);
+        hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, true, NORM, RESID, ROPE>), grid, block, 0, stream, grp,
+                           x, batch, n, nm, rs, rp);
     else
-        hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, false, NORM, RESID>), grid, block, 0, stream, grp, x,
-                           batch, n, nm, rs);
+        hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, false, NORM, RESID, ROPE>), grid, block, 0, stream, grp,
+                           x, batch, n, nm, rs, rp);
 }
 
 }  // namespace
@@ -504,19 +577,17 @@ hipError_t launch_q8_residual(const void* w, const float* in, float* x, float* s
     return hipGetLastError();
 }
 
-hipError_t launch_q8_matmul3(const void* const* w, const float* x, float* const* out, const int* d,
-                             int batch, int n, bool last_block_only, const Q8Norm& nm, hipStream_t stream) {
+hipError_t launch_q8_qkv(const void* const* w, const float* x, float* out_q, const int* d, int batch, int n,
+                         bool last_block_only, const Q8Norm& nm, const Q8Rope& rope, hipStream_t stream) {
+    if (!nm.weight || !rope.freq_real || d[1] != d[2] || d[0] % 32 || d[1] % 32) return hipErrorInvalidValue;
     Q8Group grp{};
     for (int m = 0; m < 3; m++) {
         grp.w[m] = static_cast<const uint8_t*>(w[m]);
-        grp.out[m] = out[m];
         grp.d[m] = d[m];
     }
-    const int dmax = std::max(d[0], std::max(d[1], d[2]));
-    if (nm.weight)
-        launch_group<3, false, true, false>(grp, x, batch, n, dmax, last_block_only, nm, Q8Resid{}, stream);
-    else
-        launch_group<3, false, false, false>(grp, x, batch, n, dmax, last_block_only, nm, Q8Resid{}, stream);
+    grp.out[0] = out_q;  // k and v go to the pools
+    const int dmax = std::max(d[0], d[1]);
+    launch_group<3, false, true, false, true>(grp, x, batch, n, dmax, last_block_only, nm, Q8Resid{}, stream, rope);
     return hipGetLastError();
 }
 
@@ -525,10 +596,8 @@ hipError_t launch_q8_swiglu(const void* w1, const void* w3, const float* x, floa
     Q8Group grp{{static_cast<const uint8_t*>(w1), static_cast<const uint8_t*>(w3), nullptr},
                 {hb, nullptr, nullptr},
                 {hidden, hidden, 0}};
-    if (nm.weight)
-        launch_group<2, true, true, false>(grp, x, batch, n, hidden, last_block_only, nm, Q8Resid{}, stream);
-    else
-        launch_group<2, true, false, false>(grp, x, batch, n, hidden, last_block_only, nm, Q8Resid{}, stream);
+    if (!nm.weight) return hipErrorInvalidValue;
+    launch_group<2, true, true, false>(grp, x, batch, n, hidden, last_block_only, nm, Q8Resid{}, stream);
     return hipGetLastError();
 }
 

@@ -22,13 +22,15 @@ constexpr int SCHED_THREADS = 256;
 // new index or -1, new page}.  A request's row (slot >= 0) records its new
 // page in the resident row; a prefill-chunk row (slot -1) reads the chunk's
 // uploaded table instead.  Either writes tables[b][0, max_pages) (entries
-// past the position's page are 0) and positions[b].  Workgroup `batch`
+// past the position's page are 0), positions[b] and slots[b] = page * 16 +
+// position % 16 (where the row's K/V goes).  Workgroup `batch`
 // (present when n_other > 0) stores the new entries of requests that are
 // not decode rows; no row of this launch reads those.
 __global__ __launch_bounds__(SCHED_THREADS) void sched_tables_kernel(
     int32_t* __restrict__ store, int row_stride, const int32_t* __restrict__ desc,
     const int32_t* __restrict__ other, int n_other, const int32_t* __restrict__ chunk_table,
-    int32_t* __restrict__ tables, int32_t* __restrict__ positions, int batch, int max_pages) {
+    int32_t* __restrict__ tables, int32_t* __restrict__ positions, int32_t* __restrict__ slots, int batch,
+    int max_pages) {
     const int b = blockIdx.x;
     if (b == batch) {
         for (int i = threadIdx.x; i < n_other; i += SCHED_THREADS) store[other[2 * i]] = other[2 * i + 1];
@@ -39,6 +41,8 @@ __global__ __launch_bounds__(SCHED_THREADS) void sched_tables_kernel(
     if (threadIdx.x == 0) {
         if (slot >= 0 && new_idx >= 0) store[(size_t)slot * row_stride + new_idx] = new_page;
         positions[b] = pos;
+        const int j = pos >> 4;  // the row's own page: new this step, or already resident
+        slots[b] = ((j == new_idx) ? new_page : row[j]) * 16 + (pos & 15);
     }
     const int pages = (pos >> 4) + 1;
     int32_t* out = tables + (size_t)b * max_pages;
@@ -114,11 +118,11 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void argmax_rows_kernel(const float
 
 hipError_t launch_sched_tables(int32_t* store, int row_stride, const int32_t* desc, const int32_t* other,
                                int n_other, const int32_t* chunk_table, int32_t* tables, int32_t* positions,
-                               int batch, int max_pages, hipStream_t stream) {
+                               int32_t* slots, int batch, int max_pages, hipStream_t stream) {
     const int groups = batch + (n_other > 0 ? 1 : 0);
     if (groups == 0) return hipSuccess;
     hipLaunchKernelGGL(sched_tables_kernel, dim3(groups), dim3(SCHED_THREADS), 0, stream, store, row_stride,
-                       desc, other, n_other, chunk_table, tables, positions, batch, max_pages);
+                       desc, other, n_other, chunk_table, tables, positions, slots, batch, max_pages);
     return hipGetLastError();
 }
 

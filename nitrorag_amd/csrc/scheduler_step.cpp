@@ -232,15 +232,17 @@ int nitro_sched_step(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* p
 
         int32_t* d_tables = nullptr;
         int32_t* d_positions = nullptr;
+        int32_t* d_slots = nullptr;
         int max_pages = 1;
         if (R > 0) {
             for (int i = 0; i < R; i++) max_pages = std::max(max_pages, positions[i] / BLOCK_SIZE + 1);
             // chunk rows read one table (and may share prefix hits with decode rows)
             const bool shared = c0 > 0 || rows_share_pages(d, p, pool->num_pages);
-            set_device_decode_batch(pool, R, max_pages, positions.data(), shared, &d_tables, &d_positions);
+            set_device_decode_batch(pool, R, max_pages, positions.data(), shared, &d_tables, &d_positions,
+                                    &d_slots);
         }
         hip_check(launch_sched_tables(d.store.ptr, d.row_stride, d_desc, d_other, n_other, d_chunk_table,
-                                      d_tables, d_positions, R, max_pages, s),
+                                      d_tables, d_positions, d_slots, R, max_pages, s),
                   "sched_tables launch");
         if (P > 0 && !chunk_rows) {
             const std::vector<int32_t>& t = p.prefill->seq.block_table;
