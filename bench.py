@@ -704,6 +704,13 @@ def make_workload(name, seed):
                                        f"prompt, 20 generated tokens each, token budget 256, "
                                        f"8000-page pool, Llama-2-110M-shaped Q8_0 model "
                                        f"(synthetic), reference Q8 semantics"))
+    if name.startswith("model-7b-decode-b"):
+        B = int(name.rsplit("b", 1)[1])
+        return ModelDecodeWorkload(name, (4096, 11008, 32, 32, 32, 32000, 4096), B, 1024, seed,
+                                   describe=(f"one decode step of a Llama-2-7B-shaped model (dim 4096, "
+                                             f"hidden 11008, 32 layers, 32 heads x 128, vocab 32000, "
+                                             f"Q8_0 weights, synthetic), B={B} sequences at context 1024, "
+                                             f"full-row Q8 products"))
     if name == "q8-gemv-7b-ffn":
         return Q8Workload(name, 4096, 11008, 1, seed,
                           describe=("Q8_0 matrix-vector product at the Llama-2-7B FFN up "
@@ -719,7 +726,7 @@ def make_workload(name, seed):
 
 WORKLOADS = ["decode-b64-ctx4096", "decode-single-110m", "decode-b32-mixed",
              "decode-prefix-shared", "prefill-b8-12x64", "q8-gemv-7b-ffn", "q8-matmul-110m-b32",
-             "model-110m-decode-b32", "serve-110m-u1", "serve-110m-u4", "serve-110m-u8",
+             "model-110m-decode-b32", "model-7b-decode-b1", "model-7b-decode-b8", "serve-110m-u1", "serve-110m-u4", "serve-110m-u8",
              "serve-110m-u16", "serve-110m-u32"]
 
 

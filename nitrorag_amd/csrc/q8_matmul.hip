@@ -47,6 +47,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "device_pool.hpp"
 
@@ -79,6 +80,17 @@ __device__ __forceinline__ Q8Slice load_slice(const uint8_t* wrow, int blk, int 
         s.q[2] = qp[2];
         s.q[3] = qp[3];
     }
+    return s;
+}
+
+// load_slice without a branch: an invalid slice reads block 0 of the row
+// (always in bounds) and gets scale 0, so every lane issues the same loads
+// and the waits before use count exactly the loads that are needed.
+__device__ __forceinline__ Q8Slice load_slice_always(const uint8_t* wrow, int blk, int half, bool valid) {
+    const uint8_t* bp = wrow + (size_t)(valid ? blk : 0) * 36;
+    const uint32_t* qp = reinterpret_cast<const uint32_t*>(bp + 4 + 16 * half);
+    Q8Slice s{{qp[0], qp[1], qp[2], qp[3]}, *reinterpret_cast<const float*>(bp)};
+    if (!valid) s.scale = 0.0f;
     return s;
 }
 
@@ -360,10 +372,14 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
 // fixed order (results are repeatable bit for bit).
 constexpr int GEMV_WAVES = 8;
 
+#ifndef NITRO_GEMV_UNROLL
+#define NITRO_GEMV_UNROLL 8
+#endif
 template <int NB, int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY, bool NORM, bool RESID, bool ROPE>
 __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, const float* __restrict__ x,
                                                                    int n, Q8Norm nm, Q8Resid resid, Q8Rope rope) {
-    constexpr int U = NMAT == 1 ? Q8_UNROLL : 2;  // chunks in flight per wave
+    // chunks in flight per wave: a slab covers 4096 k of one matrix (2048 of a group)
+    constexpr int U = NMAT == 1 ? NITRO_GEMV_UNROLL : NITRO_GEMV_UNROLL / 2;
     constexpr int SLAB = GEMV_WAVES * U * 64;     // k per slab
     __shared__ __attribute__((aligned(16))) float xs[NB][SLAB];
     __shared__ float red[GEMV_WAVES][NMAT][NB][16];
@@ -525,9 +541,255 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, c
     }
 }
 
+// Batches of 1..NB rows over long rows (full-row products, n >= 2048),
+// weights streamed row by row.  A tile is 16R output rows: four row sets of
+// four row groups of R rows.  A wave owns one row group of each set and half
+// of the k range (chunks of 1024 k = 32 blocks, the two halves interleaved);
+// lane l takes half l%2 of block 32*chunk + l/2 of each row, so one load
+// instruction covers 32 consecutive blocks of a row (1152 contiguous bytes).
+// A wave's work items (row set, chunk) run in order across the tile and on
+// into its next tile (workgroups loop over tiles when the tiles outnumber
+// ROWDOT_MAX_GROUPS), each item's weights loaded while the previous item is
+// used, in two register sets that alternate.  x (with rms_norm)
+// is read per item.  After a row set's last chunk the 64 lanes of each row
+// are summed with a fixed butterfly into LDS; at the tile's end the two k
+// halves are added in a fixed order and the epilogue (SwiGLU, RoPE + K/V
+// append, residual) runs on the sums in LDS.
+template <int NB, int NMAT>
+constexpr int rowdot_rows() {
+    return NMAT == 1 ? 4 : NMAT == 2 ? 2 : (NB <= 2 ? 2 : 1);
+}
+constexpr int ROWDOT_SETS = 1;
+
+template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
+__global__ __launch_bounds__(512) void q8_rowdot_kernel(Q8Group grp, const float* __restrict__ x, int n,
+                                                         int ntiles, Q8Norm nm, Q8Resid resid, Q8Rope rope) {
+    constexpr int R = rowdot_rows<NB, NMAT>();
+    constexpr int TROWS = ROWDOT_SETS * 4 * R;  // output rows per tile
+    __shared__ float red[2][NMAT][TROWS][NB];
+    __shared__ float inv_s[NB];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int kh = wave & 1;   // k half
+    const int rg = wave >> 1;  // row group within each set
+    const int nb = n / Q8_BLOCK;
+    const int nchunks = (nb + 31) / 32;
+    const int per_set = (nchunks - kh + 1) / 2;  // chunks kh, kh + 2, ... (>= 1: n >= 2048)
+    const int items = ROWDOT_SETS * per_set;
+    // rows of item e of `tile`; e == items is the first item of the next tile
+    auto item_rows = [&](int tile, int e, int& row_base, int& c) {
+        if (e >= items) {
+            tile += gridDim.x;
+            e = 0;
+        }
+        const int set = e / per_set;
+        c = kh + 2 * (e - set * per_set);
+        row_base = tile < ntiles ? tile * TROWS + (set * 4 + rg) * R : INT32_MAX / 2;
+    };
+    auto load_item = [&](Q8Slice (&sl)[NMAT][R], int tile, int e) {
+        int row_base, c;
+        item_rows(tile, e, row_base, c);
+        const int blk = 32 * c + (lane >> 1);
+        const bool valid = blk < nb;
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int row = row_base + r;
+                const uint8_t* wr = grp.w[m] + (size_t)min(row, grp.d[m] - 1) * nb * Q8_BLOCK_BYTES;
+                sl[m][r] = load_slice_always(wr, blk, lane & 1, valid && row < grp.d[m]);
+            }
+    };
+    auto load_x = [&](float (&xv)[NB][16], int e) {
+        const int set = e / per_set;
+        const int c = kh + 2 * (e - set * per_set);
+        const int blk = 32 * c + (lane >> 1);
+        // an invalid lane reads x[b][0..16) (in bounds); its weights are 0
+        const int k0 = blk < nb ? blk * Q8_BLOCK + 16 * (lane & 1) : 0;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const float4* xp = reinterpret_cast<const float4*>(x + (size_t)b * n + k0);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 v = xp[q];
+                xv[b][4 * q] = v.x;
+                xv[b][4 * q + 1] = v.y;
+                xv[b][4 * q + 2] = v.z;
+                xv[b][4 * q + 3] = v.w;
+            }
+            if constexpr (NORM) {
+                const float inv = inv_s[b];
+                const float4* wp = reinterpret_cast<const float4*>(nm.weight + k0);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 w = wp[q];
+                    xv[b][4 * q] = w.x * (inv * xv[b][4 * q]);
+                    xv[b][4 * q + 1] = w.y * (inv * xv[b][4 * q + 1]);
+                    xv[b][4 * q + 2] = w.z * (inv * xv[b][4 * q + 2]);
+                    xv[b][4 * q + 3] = w.w * (inv * xv[b][4 * q + 3]);
+                }
+            }
+        }
+    };
+    float acc[NMAT][R][NB];
+    auto clear = [&] {
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int b = 0; b < NB; b++) acc[m][r][b] = 0.0f;
+    };
+    // x of item e, then the next item's weights into `next`, then e's products
+    // with `now`; after a row set's last chunk, its row sums go to LDS.
+    auto step = [&](const Q8Slice (&now)[NMAT][R], Q8Slice (&next)[NMAT][R], int tile, int e) {
+        float xv[NB][16];
+        load_x(xv, e);
+        load_item(next, tile, e + 1);
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float wv[16];
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    wv[jj] = dequant(now[m][r].q[0], jj, now[m][r].scale);
+                    wv[4 + jj] = dequant(now[m][r].q[1], jj, now[m][r].scale);
+                    wv[8 + jj] = dequant(now[m][r].q[2], jj, now[m][r].scale);
+                    wv[12 + jj] = dequant(now[m][r].q[3], jj, now[m][r].scale);
+                }
+#pragma unroll
+                for (int b = 0; b < NB; b++)
+#pragma unroll
+                    for (int q = 0; q < 16; q++) acc[m][r][b] = fmaf(wv[q], xv[b][q], acc[m][r][b]);
+            }
+        const int set = e / per_set;
+        if (e - set * per_set == per_set - 1) {  // the set's last chunk (wave-uniform)
+#pragma unroll
+            for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                for (int r = 0; r < R; r++)
+#pragma unroll
+                    for (int b = 0; b < NB; b++) {
+                        float v = acc[m][r][b];
+#pragma unroll
+                        for (int msk = 32; msk > 0; msk >>= 1) v += __shfl_xor(v, msk);
+                        if (lane == 0) red[kh][m][(set * 4 + rg) * R + r][b] = v;
+                    }
+            clear();
+        }
+    };
+    Q8Slice sa[NMAT][R], sb[NMAT][R];
+    load_item(sa, blockIdx.x, 0);
+    if constexpr (NORM) {
+        // wave b < NB adds row b's partials (lane i takes i, i + 64, ...)
+        if (wave < NB) {
+            float v = partial_sum(nm, wave, lane, 64);
+#pragma unroll
+            for (int msk = 32; msk > 0; msk >>= 1) v += __shfl_xor(v, msk);
+            if (lane == 0) inv_s[wave] = inv_rms(v, n);
+        }
+        __syncthreads();
+    }
+    clear();
+    // Items alternate between the two register sets; a tile with an odd item
+    // count hands the next tile's first item over in the other set.
+    auto run_tile = [&](auto& first, auto& second, int tile) {
+        int e = 0;
+        for (; e + 1 < items; e += 2) {
+            step(first, second, tile, e);
+            step(second, first, tile, e + 1);
+        }
+        if (e < items) step(first, second, tile, e);
+    };
+    bool flipped = false;
+    for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        if (!flipped)
+            run_tile(sa, sb, tile);
+        else
+            run_tile(sb, sa, tile);
+        flipped ^= (items & 1) != 0;
+        __syncthreads();
+        for (int t = threadIdx.x; t < NB * TROWS; t += 512) {
+            const int b = t / TROWS, i = t % TROWS;
+            const int row = tile * TROWS + i;
+            float sum[NMAT];
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) sum[m] = red[0][m][i][b] + red[1][m][i][b];
+            if constexpr (ROPE) {
+                // RoPE pairs are rows (i, i ^ 1) of the tile
+                const float q_o = red[0][0][i ^ 1][b] + red[1][0][i ^ 1][b];
+                const float k_o = red[0][1][i ^ 1][b] + red[1][1][i ^ 1][b];
+                const RopeRow rp = rope_row(rope, b);
+                const bool odd = i & 1;
+                const int fe = row & ~1;
+                const float2 qr = rotate_pair(rope, rp.pos, fe, odd ? q_o : sum[0], odd ? sum[0] : q_o);
+                const float2 kr = rotate_pair(rope, rp.pos, fe, odd ? k_o : sum[1], odd ? sum[1] : k_o);
+                if (row < grp.d[0]) grp.out[0][(size_t)b * grp.d[0] + row] = odd ? qr.y : qr.x;
+                if (row < grp.d[1]) {
+                    if (rp.page_ok) {
+                        const size_t o = (size_t)rp.page * rope.page_stride + rope.layer_off +
+                                         (size_t)rp.in_page * grp.d[1] + row;
+                        rope.k_pool[o] = odd ? kr.y : kr.x;
+                        rope.v_pool[o] = sum[2];
+                    } else if (row == 0) {
+                        atomicAdd(rope.bad_pages, 1);  // once per row
+                    }
+                }
+            } else if constexpr (RESID) {
+                static_assert(!RESID || TROWS % 16 == 0, "residual partials are per 16 rows");
+                // x[b][row] += product; each 16 threads (16 rows of batch row b) add their squares
+                float ssq = 0.0f;
+                if (row < grp.d[0]) {
+                    float* xe = grp.out[0] + (size_t)b * grp.d[0] + row;
+                    const float v = *xe + sum[0];
+                    *xe = v;
+                    ssq = v * v;
+                }
+#pragma unroll
+                for (int msk = 8; msk > 0; msk >>= 1) ssq += __shfl_xor(ssq, msk, 16);
+                if ((i & 15) == 0 && row < grp.d[0]) resid.ss[(size_t)(row >> 4) * resid.ss_stride + b] = ssq;
+            } else if constexpr (SWIGLU) {
+                if (row < grp.d[0]) {
+                    float h = sum[0];
+                    h *= 1.0f / (1.0f + expf(-h));
+                    grp.out[0][(size_t)b * grp.d[0] + row] = h * sum[1];
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < NMAT; m++)
+                    if (row < grp.d[m]) grp.out[m][(size_t)b * grp.d[m] + row] = sum[m];
+            }
+        }
+        __syncthreads();  // red is reused by the next tile
+    }
+}
+
+// Row streaming pays off once a row has at least two 1024-k chunks (both k
+// halves busy).  Tiles are small (4R rows), so there are enough of them to
+// fill the GPU; past ROWDOT_MAX_GROUPS the workgroups loop over tiles.
+constexpr int ROWDOT_MIN_N = 2048;
+constexpr int ROWDOT_MAX_GROUPS = 1024;
+
+bool use_rowdot() {
+    static const bool on = [] {
+        const char* e = getenv("NITRO_Q8_GEMV");
+        return !(e && e[0] == 's');  // "s": the slab kernel (comparison runs)
+    }();
+    return on;
+}
+
 template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
 void launch_gemv(const Q8Group& grp, const float* x, int n, int dmax, bool last, const Q8Norm& nm,
                  const Q8Resid& rs, const Q8Rope& rp, hipStream_t stream) {
+    if (!last && n >= ROWDOT_MIN_N && use_rowdot()) {
+        constexpr int ROWS = ROWDOT_SETS * 4 * rowdot_rows<NB, NMAT>();
+        const int ntiles = (dmax + ROWS - 1) / ROWS;
+        const dim3 grid((unsigned)std::min(ntiles, ROWDOT_MAX_GROUPS)), block(512);
+        hipLaunchKernelGGL((q8_rowdot_kernel<NB, NMAT, SWIGLU, NORM, RESID, ROPE>), grid, block, 0, stream, grp, x,
+                           n, ntiles, nm, rs, rp);
+        return;
+    }
     const dim3 grid((unsigned)((dmax + 15) / 16)), block(64 * GEMV_WAVES);
     if (last)
         hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, true, NORM, RESID, ROPE>), grid, block, 0, stream,

@@ -85,27 +85,40 @@ def synthetic_model_file(dim: int, hidden_dim: int, n_layers: int, n_heads: int,
                          vocab_size: int, seq_len: int, seed: int = 0) -> np.ndarray:
     """A model file in the reference's layout (src/Server_Inference.cpp:45-69)
     with synthetic weights: embedding U[-1,1), rms weights U[0.5,1.5), Q8
-    matrices of random int8 with per-block scales ~ 1/(127*sqrt(cols)) (unit
-    scale activations), and RoPE tables cos/sin(pos * 10000^(-2i/head_size)).
-    For benchmarks and tests where no trained checkpoint is available."""
+    matrices of random int8 in [-127, 127] with per-block scales ~
+    1/(127*sqrt(cols)) (unit scale activations), and RoPE tables
+    cos/sin(pos * 10000^(-2i/head_size)).  For benchmarks and tests where no
+    trained checkpoint is available; written straight into one buffer so a
+    7B-shaped file (7.3 GB) takes seconds."""
     rng = np.random.default_rng(seed)
     head = dim // n_heads
     kv_dim = n_kv_heads * head
-    parts = [np.array([dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len],
-                      np.int32).view(np.uint8)]
+    q8n = lambda rows, cols: n_layers * rows * (cols // 32) * 36
+    total = (28 + 4 * (vocab_size * dim + 2 * n_layers * dim + dim + seq_len * head)
+             + 2 * q8n(dim, dim) + 2 * q8n(kv_dim, dim) + 2 * q8n(hidden_dim, dim) + q8n(dim, hidden_dim))
+    out = np.empty(total, np.uint8)
+    off = 0
+
+    def put(b):
+        nonlocal off
+        out[off:off + b.size] = b
+        off += b.size
 
     def f32(a):
-        parts.append(np.ascontiguousarray(a, dtype=np.float32).view(np.uint8).reshape(-1))
+        put(np.ascontiguousarray(a, dtype=np.float32).view(np.uint8).reshape(-1))
 
     def q8(rows, cols):
+        nonlocal off
         nb = cols // 32
-        blocks = np.empty((n_layers * rows, nb, 36), np.uint8)
+        blocks = out[off:off + q8n(rows, cols)].reshape(n_layers * rows, nb, 36)
         scale = (1.0 / (127.0 * np.sqrt(cols))) * (1.0 + 0.5 * rng.uniform(-1, 1, (n_layers * rows, nb, 1)))
         blocks[:, :, :4] = scale.astype(np.float32).view(np.uint8)
-        blocks[:, :, 4:] = rng.integers(-127, 128, (n_layers * rows, nb, 32), dtype=np.int8).view(np.uint8)
-        parts.append(blocks.reshape(-1))
+        q = rng.bit_generator.random_raw(n_layers * rows * nb * 4).view(np.int8).reshape(n_layers * rows, nb, 32)
+        blocks[:, :, 4:] = np.maximum(q, -127).view(np.uint8)
+        off += blocks.size
 
-    f32(rng.uniform(-1, 1, (vocab_size, dim)))
+    put(np.array([dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len], np.int32).view(np.uint8))
+    f32(rng.random((vocab_size, dim), dtype=np.float32) * 2.0 - 1.0)
     f32(rng.uniform(0.5, 1.5, (n_layers, dim)))
     q8(dim, dim)
     q8(kv_dim, dim)
@@ -119,4 +132,5 @@ def synthetic_model_file(dim: int, hidden_dim: int, n_layers: int, n_heads: int,
     ang = np.arange(seq_len)[:, None] * 10000.0 ** (-2.0 * np.arange(head // 2) / head)[None, :]
     f32(np.cos(ang))
     f32(np.sin(ang))
-    return np.concatenate(parts)
+    assert off == total
+    return out

@@ -125,6 +125,9 @@ MODELS = {
     "mha_hd64_l3": (256, 512, 3, 4, 4, 1000, 256),
     "gqa_hd128_l2": (512, 1024, 2, 4, 2, 700, 200),
     "gqa_hd32_l2": (128, 256, 2, 4, 1, 300, 300),
+    # rows of >= 2048 k: the row-streaming products with rms_norm, RoPE + K/V
+    # append, SwiGLU and residual epilogues (3 decode rows)
+    "gqa_hd128_wide_l1": (2048, 2304, 1, 16, 4, 500, 128),
 }
 
 

@@ -55,6 +55,10 @@ SHAPES = [
     # tiles of 16 (1, 15, 16, 17, 64, 65), rows not a multiple of 16, odd blocks per row
     (768, 768, 1), (768, 2048, 3), (2048, 768, 16), (768, 768, 17), (2048, 768, 64),
     (768, 200, 65), (96, 40, 100), (32, 7, 5), (4096, 48, 2),
+    # rows of >= 2048 k with 1-4 activation rows take the row-streaming kernel:
+    # 1024-k chunks split over two k halves (odd and even chunk counts), tiles
+    # of 16 rows not filling the matrix, more tiles than workgroups
+    (2048, 40, 1), (2304, 96, 2), (11008, 64, 3), (4096, 4100, 4), (4128, 16400, 1),
 ]
 
 
