@@ -325,6 +325,37 @@ int nitro_sched_request_status(const nitro_scheduler* sched, int32_t req_id, int
 /* Forgets a finished request that a later step has released. */
 int nitro_sched_drop_request(nitro_scheduler* sched, int32_t req_id);
 
+/* ============================== NitroRPC ==================================
+ * The wire format of src/NitroRPC.hpp, host byte order (little-endian here):
+ * an int vector is its int32 count then the int32 values (send_ints /
+ * recv_ints, :39-56); a structured query is uint64 subset_mask, float32
+ * range_min, float32 range_max, then dim float32 (recv_structured_query,
+ * :58-67).  The encoders report the byte count in *bytes (and write when
+ * `out` holds it); the decoder reports count and bytes consumed.  The fd
+ * functions are send_all / recv_all (:19-37) over a connected socket. */
+int nitro_rpc_encode_ints(const int32_t* data, int32_t n, uint8_t* out, uint64_t cap, uint64_t* bytes);
+int nitro_rpc_decode_ints(const uint8_t* buf, uint64_t len, int32_t* out, int32_t cap, int32_t* n,
+                          uint64_t* consumed);
+int nitro_rpc_encode_structured_query(uint64_t subset_mask, float range_min, float range_max, const float* vec,
+                                      int32_t dim, uint8_t* out, uint64_t cap, uint64_t* bytes);
+int nitro_rpc_send_ints(int32_t fd, const int32_t* data, int32_t n);                 /* :39-46 */
+int nitro_rpc_recv_ints(int32_t fd, int32_t* out, int32_t cap, int32_t* n);           /* :48-56 */
+int nitro_rpc_recv_structured_query(int32_t fd, int32_t dim, uint64_t* subset_mask, float* range_min,
+                                    float* range_max, float* vec);                   /* :58-67 */
+
+/* The serving loop of src/Server_Inference.cpp:86-112 over connections the
+ * caller has accepted: nitro_server_accept_fd reads the prompt (an int
+ * vector of at most max_prompt_tokens) and adds it as request 0, 1, 2, ...
+ * (req_counter, :27-34); each nitro_server_step runs one nitro_sched_step,
+ * sends every request's new tokens as bare int32 values and closes the
+ * connections of finished requests.  *active = has_active_requests. */
+typedef struct nitro_server nitro_server;
+int nitro_server_create(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* pool, int32_t semantics,
+                        int32_t max_prompt_tokens, nitro_server** out);
+int nitro_server_destroy(nitro_server* server); /* closes connections still open */
+int nitro_server_accept_fd(nitro_server* server, int32_t fd, int32_t* req_id);
+int nitro_server_step(nitro_server* server, void* stream, int32_t* active);
+
 /* ------------------------------ checks ------------------------------------
  * Kernels re-check every page id they dereference against the pool size and
  * skip (and record) any outside it instead of faulting.  This reads and

@@ -108,6 +108,18 @@ SIGNATURES = {
     "nitro_sched_generated": [_vp, _i32, _i32p, _i32, _i32p],
     "nitro_sched_request_status": [_vp, _i32, _i32p],
     "nitro_sched_drop_request": [_vp, _i32],
+    "nitro_rpc_encode_ints": [_i32p, _i32, ctypes.POINTER(ctypes.c_uint8), _u64, _u64p],
+    "nitro_rpc_decode_ints": [ctypes.POINTER(ctypes.c_uint8), _u64, _i32p, _i32, _i32p, _u64p],
+    "nitro_rpc_encode_structured_query": [_u64, ctypes.c_float, ctypes.c_float, ctypes.POINTER(ctypes.c_float),
+                                          _i32, ctypes.POINTER(ctypes.c_uint8), _u64, _u64p],
+    "nitro_rpc_send_ints": [_i32, _i32p, _i32],
+    "nitro_rpc_recv_ints": [_i32, _i32p, _i32, _i32p],
+    "nitro_rpc_recv_structured_query": [_i32, _i32, _u64p, ctypes.POINTER(ctypes.c_float),
+                                        ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)],
+    "nitro_server_create": [_vp, _vp, _vp, _i32, _i32, ctypes.POINTER(_vp)],
+    "nitro_server_destroy": [_vp],
+    "nitro_server_accept_fd": [_vp, _i32, _i32p],
+    "nitro_server_step": [_vp, _vp, _i32p],
     "nitro_kvpool_take_device_errors": [_vp, _i32p],
 }
 _RESTYPES = {

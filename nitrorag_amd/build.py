@@ -27,7 +27,7 @@ ARCH = os.environ.get("NITRO_OFFLOAD_ARCH", "gfx950")
 DEVICE_SOURCES = ["paged_attn_decode.hip", "paged_attn_prefill.hip", "kv_append.hip", "q8_matmul.hip",
                   "model_kernels.hip", "scheduler_kernels.hip"]
 HIP_HOST_SOURCES = ["capi_device.cpp", "model.cpp", "scheduler_step.cpp"]
-HOST_SOURCES = ["paged_memory.cpp", "capi_host.cpp", "scheduler.cpp"]
+HOST_SOURCES = ["paged_memory.cpp", "capi_host.cpp", "scheduler.cpp", "rpc.cpp"]
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"-I{INCLUDE}", f"-I{CSRC}", "-Wall"]
 # Code object v5: loadable by the HIP runtime torch bundles (ROCm 7.0) as well

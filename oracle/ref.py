@@ -61,6 +61,9 @@ def lib() -> ctypes.CDLL:
         L.ref_read_contiguous_cache.argtypes = [vp, _f32p, _f32p]
         L.ref_write_contiguous_cache.argtypes = [vp, _f32p, _f32p]
         L.ref_block_table.argtypes = [vp, ci, _i32p, ci]
+        L.ref_rpc_send_ints.argtypes = [ci, _i32p, ci]
+        L.ref_rpc_recv_ints.argtypes = [ci, _i32p, ci]
+        L.ref_rpc_recv_structured_query.argtypes = [ci, ci, ctypes.POINTER(ctypes.c_uint64), _f32p, _f32p, _f32p]
         L.ref_sched_create.argtypes = [vp, ci]
         L.ref_sched_add.argtypes = [vp, ci, _i32p, ci]
         L.ref_sched_active.argtypes = [vp]

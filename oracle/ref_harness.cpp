@@ -5,9 +5,10 @@
 // under the reference checkout, with the reference's flags.  Nothing from the
 // reference is copied here: this file only instantiates the reference's types
 // and calls its functions so that tests/golden/make_golden.py can record
-// golden vectors (block-manager traces, prefix-cache state, and attention
+// golden vectors (block-manager traces, prefix-cache state, attention
 // outputs of forward_decode_batch / forward_paged / forward_prefill_chunk /
-// forward) and so that CPU tests can cross-check the oracle live.
+// forward, scheduler steps, NitroRPC messages) and so that CPU tests can
+// cross-check the oracle live.
 //
 // Attention outputs are observed through s->xb2 = wo . xb with wo the Q8
 // identity.  forward_paged and forward use the full-row Q8 matmul, so all of
@@ -49,6 +50,7 @@ struct RefExit {
 #define private public
 #include "model_q8.cpp"
 #undef private
+#include "NitroRPC.hpp"
 #undef exit
 
 namespace {
@@ -579,6 +581,29 @@ int ref_sched_state(void* p, int32_t* buf, int cap) {
     if ((int)o.size() > cap) return -(int)o.size();
     std::memcpy(buf, o.data(), o.size() * sizeof(int32_t));
     return (int)o.size();
+}
+
+// ---- NitroRPC (src/NitroRPC.hpp), over a connected socket ----------------
+int ref_rpc_send_ints(int fd, const int* data, int n) {
+    return NitroRPC::send_ints(fd, std::vector<int>(data, data + n)) ? 0 : 1;
+}
+
+// Returns the count received (or -1 on failure); copies at most cap values.
+int ref_rpc_recv_ints(int fd, int* out, int cap) {
+    std::vector<int> v;
+    if (!NitroRPC::recv_ints(fd, v)) return -1;
+    for (int i = 0; i < (int)v.size() && i < cap; i++) out[i] = v[i];
+    return (int)v.size();
+}
+
+int ref_rpc_recv_structured_query(int fd, int dim, uint64_t* mask, float* lo, float* hi, float* vec) {
+    StructuredQuery q;
+    if (!NitroRPC::recv_structured_query(fd, q, dim)) return 1;
+    *mask = q.subset_mask;
+    *lo = q.range_min;
+    *hi = q.range_max;
+    for (int i = 0; i < dim; i++) vec[i] = q.vec[i];
+    return 0;
 }
 
 int ref_block_table(void* p, int slot, int* out, int cap) {

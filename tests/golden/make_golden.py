@@ -28,6 +28,8 @@ Writes, next to this script:
                              a tiny random model in the reference's file layout and
                              the logits of forward_prefill_chunk / forward_paged /
                              forward_decode_batch over a scripted session
+  rpc.json                   the reference's NitroRPC send_ints bytes and recv_ints /
+                             recv_structured_query decodes over socket pairs
   sched_traces.json + sched_traces.npz
                              steps of the reference's Continuous_Scheduler over the tiny
                              model with wo/w2 scaled by 64: scheduler state and
@@ -660,6 +662,78 @@ def _snapshot_words(W) -> np.ndarray:
     return buf[:n].copy()
 
 
+def make_rpc():
+    """The reference's NitroRPC (src/NitroRPC.hpp) over UNIX socket pairs: the
+    bytes send_ints puts on the wire for a set of int vectors, and what
+    recv_ints / recv_structured_query decode from hand-made messages
+    (including a message cut short, which the reference reports as failure)."""
+    import ctypes
+    import socket
+
+    L = ref.lib()
+    rng = np.random.default_rng(99)
+    out = []
+
+    def drain(sock):
+        sock.setblocking(False)
+        data = b""
+        while True:
+            try:
+                chunk = sock.recv(1 << 16)
+            except BlockingIOError:
+                break
+            if not chunk:
+                break
+            data += chunk
+        return data
+
+    vectors = [[], [7], [1, 2, 3], [-1, 2**31 - 1, -2**31, 0],
+               [int(v) for v in rng.integers(-2**31, 2**31, 300)]]
+    for vals in vectors:
+        a, b = socket.socketpair()
+        arr = np.asarray(vals, np.int32)
+        assert L.ref_rpc_send_ints(a.fileno(), arr.ctypes.data_as(ref._i32p), arr.size) == 0
+        wire = drain(b)
+        a.close(), b.close()
+        out.append(dict(kind="send_ints", values=vals, wire=wire.hex()))
+    for vals in vectors[1:]:
+        a, b = socket.socketpair()
+        msg = np.asarray([len(vals)] + vals, np.int32).tobytes()
+        b.sendall(msg)
+        buf = np.zeros(max(1, len(vals)), np.int32)
+        n = L.ref_rpc_recv_ints(a.fileno(), buf.ctypes.data_as(ref._i32p), buf.size)
+        a.close(), b.close()
+        out.append(dict(kind="recv_ints", wire=msg.hex(), count=int(n), values=buf[:max(n, 0)].tolist()))
+    # a message cut short: count 5, two values, then the peer closes
+    a, b = socket.socketpair()
+    msg = np.asarray([5, 10, 20], np.int32).tobytes()
+    b.sendall(msg)
+    b.close()
+    buf = np.zeros(8, np.int32)
+    n = L.ref_rpc_recv_ints(a.fileno(), buf.ctypes.data_as(ref._i32p), buf.size)
+    a.close()
+    out.append(dict(kind="recv_ints_truncated", wire=msg.hex(), count=int(n)))
+    for dim, seed in ((8, 1), (0, 2), (33, 3)):
+        r = np.random.default_rng(seed)
+        mask = int(r.integers(0, 2**63)) * 2 + 1
+        lo, hi = np.float32(r.standard_normal()), np.float32(r.standard_normal())
+        vec = r.standard_normal(dim).astype(np.float32)
+        msg = (np.uint64(mask).tobytes() + lo.tobytes() + hi.tobytes() + vec.tobytes())
+        a, b = socket.socketpair()
+        b.sendall(msg)
+        m = ctypes.c_uint64()
+        flo, fhi = ctypes.c_float(), ctypes.c_float()
+        got = np.zeros(max(dim, 1), np.float32)
+        st = L.ref_rpc_recv_structured_query(a.fileno(), dim, ctypes.byref(m), ctypes.byref(flo),
+                                             ctypes.byref(fhi), got.ctypes.data_as(ref._f32p))
+        a.close(), b.close()
+        assert st == 0
+        out.append(dict(kind="recv_structured_query", dim=dim, wire=msg.hex(), subset_mask=int(m.value),
+                        range_min=float(flo.value), range_max=float(fhi.value),
+                        vec=got[:dim].astype(np.float64).tolist()))
+    return out
+
+
 def main():
     if not ref.available():
         sys.exit("oracle/_ref/libnitro_ref.so is missing: run `make -C oracle ref` first")
@@ -680,13 +754,15 @@ def main():
     with open(os.path.join(HERE, "model_forward.json"), "w") as f:
         json.dump(m_meta, f, indent=1)
     np.savez_compressed(os.path.join(HERE, "model_forward.npz"), **m_arrays)
+    with open(os.path.join(HERE, "rpc.json"), "w") as f:
+        json.dump(make_rpc(), f, indent=0)
     s_meta, s_arrays = make_sched()
     with open(os.path.join(HERE, "sched_traces.json"), "w") as f:
         json.dump(s_meta, f, separators=(",", ":"))
     np.savez_compressed(os.path.join(HERE, "sched_traces.npz"), **s_arrays)
     for fn in ("fnv.json", "block_manager_traces.json", "attention.json", "attention.npz",
                "q8_matmul.json", "q8_matmul.npz", "model_tiny.bin", "model_forward.json",
-               "model_forward.npz", "sched_traces.json", "sched_traces.npz"):
+               "model_forward.npz", "sched_traces.json", "sched_traces.npz", "rpc.json"):
         print(fn, os.path.getsize(os.path.join(HERE, fn)))
 
 
