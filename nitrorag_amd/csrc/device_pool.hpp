@@ -200,6 +200,18 @@ struct Q8Rope {
     const int32_t* slot[2] = {nullptr, nullptr};
     int split = 0;
 };
+// A Q8_0 matrix in the matrix-core tile layout: a record per (16-row tile,
+// 32-k block) of 576 bytes, the 16 rows' block scales (floats) and then 64
+// runs of 8 int8, run c holding weights 8*(c/16)..+8 of the block of row
+// c%16 (one 8-byte load per lane of a wave is one 512-byte read); a tile's
+// records in block order, tiles in row order; rows past d are zero.
+// Products over more than 4 activation rows read this copy when given one.
+struct Q8Tiled {
+    const void* w[3] = {nullptr, nullptr, nullptr};
+};
+inline size_t q8_tiled_bytes(size_t d, size_t n) { return (d + 15) / 16 * (n / 32) * 576; }
+// tiled = the tile layout of w (rows of BlockQ8, d x n)
+hipError_t launch_q8_tile(const void* w, void* tiled, int d, int n, hipStream_t stream);
 // Q8_0 matrix product (rows of BlockQ8, fp32 activations); last_block_only
 // selects the reference's matmul_bulk semantics.
 hipError_t launch_q8_matmul(const void* w, const float* x, float* out, int batch, int n, int d,
@@ -207,15 +219,17 @@ hipError_t launch_q8_matmul(const void* w, const float* x, float* out, int batch
 // x[b] += w . in[b] ([batch][d], in place) with the squares of the new x
 // rows summed per 16 outputs into ss (ceil(d/16) partials per row, stride batch).
 hipError_t launch_q8_residual(const void* w, const float* in, float* x, float* ss, int batch, int n, int d,
-                              bool last_block_only, hipStream_t stream);
+                              bool last_block_only, hipStream_t stream, const void* w_tiled = nullptr);
 // wq/wk/wv sharing x and n: q = wq . rms_norm(x), k, v likewise, with the
 // RoPE + K/V-append epilogue: q written to out_q [batch][dim], k and v to the
 // pools (d = {dim, kv_dim, kv_dim}).
 hipError_t launch_q8_qkv(const void* const* w, const float* x, float* out_q, const int* d, int batch, int n,
-                         bool last_block_only, const Q8Norm& norm, const Q8Rope& rope, hipStream_t stream);
+                         bool last_block_only, const Q8Norm& norm, const Q8Rope& rope, hipStream_t stream,
+                         const Q8Tiled& tiled = Q8Tiled{});
 // hb = silu(x . w1^T) * (x . w3^T), [batch][hidden] (src/model_q8.cpp:670-680).
 hipError_t launch_q8_swiglu(const void* w1, const void* w3, const float* x, float* hb, int batch, int n,
-                            int hidden, bool last_block_only, const Q8Norm& norm, hipStream_t stream);
+                            int hidden, bool last_block_only, const Q8Norm& norm, hipStream_t stream,
+                            const Q8Tiled& tiled = Q8Tiled{});
 // Row-wise model kernels and the fp32 classifier product (model_kernels.hip).
 // x[r] = table[tokens[r]]; with ss, ss[r] = the row's sum of squares (one
 // partial per row for a following Q8Norm).

@@ -24,6 +24,11 @@ struct nitro_model {
     // section offsets (bytes) within `weights`, src/Server_Inference.cpp:52-69
     size_t o_emb = 0, o_rms_att = 0, o_wq = 0, o_wk = 0, o_wv = 0, o_wo = 0, o_rms_ffn = 0;
     size_t o_w1 = 0, o_w2 = 0, o_w3 = 0, o_rms_final = 0, o_freq_real = 0, o_freq_imag = 0;
+    // the seven Q8 matrices again in the matrix-core tile layout (Q8Tiled),
+    // each section holding every layer (rows are multiples of 16, so no tile
+    // spans two layers); read by the products over more than 4 rows
+    uint8_t* tiled = nullptr;
+    size_t t_wq = 0, t_wk = 0, t_wv = 0, t_wo = 0, t_w1 = 0, t_w2 = 0, t_w3 = 0;
     DeviceBuffer<float> x, attn, q, hb, last, ss;
     DeviceBuffer<int32_t> tokens;
     Staging staging;
@@ -31,6 +36,9 @@ struct nitro_model {
     const float* f32(size_t off) const { return reinterpret_cast<const float*>(weights + off); }
     const uint8_t* q8(size_t off, int layer, size_t rows, size_t cols) const {
         return weights + off + (size_t)layer * rows * (cols / 32) * 36;
+    }
+    const uint8_t* q8t(size_t off, int layer, size_t rows, size_t cols) const {
+        return tiled + off + (size_t)layer * q8_tiled_bytes(rows, cols);
     }
 };
 
@@ -87,22 +95,30 @@ void layers(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int rows,
         const Q8Norm att{m->f32(m->o_rms_att) + (size_t)l * dim, m->ss.ptr, l ? parts : 1, rows};
         const void* wqkv[3] = {m->q8(m->o_wq, l, dim, dim), m->q8(m->o_wk, l, kv, dim),
                                m->q8(m->o_wv, l, kv, dim)};
+        Q8Tiled tqkv;
+        tqkv.w[0] = m->q8t(m->t_wq, l, dim, dim);
+        tqkv.w[1] = m->q8t(m->t_wk, l, kv, dim);
+        tqkv.w[2] = m->q8t(m->t_wv, l, kv, dim);
         const int dqkv[3] = {dim, kv, kv};
         rope.layer_off = pool->layer_offset(l);
-        hip_check(launch_q8_qkv(wqkv, m->x.ptr, m->q.ptr, dqkv, rows, dim, last, att, rope, s), "q8_qkv launch");
+        hip_check(launch_q8_qkv(wqkv, m->x.ptr, m->q.ptr, dqkv, rows, dim, last, att, rope, s, tqkv),
+                  "q8_qkv launch");
         attend(l);  // attention over the pools -> m->attn (:618-662)
         // x += wo . attn (:663-666)
         hip_check(launch_q8_residual(m->q8(m->o_wo, l, dim, dim), m->attn.ptr, m->x.ptr, m->ss.ptr, rows, dim,
-                                     dim, last, s),
+                                     dim, last, s, m->q8t(m->t_wo, l, dim, dim)),
                   "q8 wo launch");
         // hb = silu(w1 . xb) * (w3 . xb), xb = rms_norm(x, rms_ffn), one launch (:667-680)
         const Q8Norm ffn{m->f32(m->o_rms_ffn) + (size_t)l * dim, m->ss.ptr, parts, rows};
+        Q8Tiled t13;
+        t13.w[0] = m->q8t(m->t_w1, l, hid, dim);
+        t13.w[1] = m->q8t(m->t_w3, l, hid, dim);
         hip_check(launch_q8_swiglu(m->q8(m->o_w1, l, hid, dim), m->q8(m->o_w3, l, hid, dim), m->x.ptr,
-                                   m->hb.ptr, rows, dim, hid, last, ffn, s),
+                                   m->hb.ptr, rows, dim, hid, last, ffn, s, t13),
                   "q8_swiglu launch");
         // x += w2 . hb (:682-684)
         hip_check(launch_q8_residual(m->q8(m->o_w2, l, dim, hid), m->hb.ptr, m->x.ptr, m->ss.ptr, rows, hid,
-                                     dim, last, s),
+                                     dim, last, s, m->q8t(m->t_w2, l, dim, hid)),
                   "q8 w2 launch");
     }
 }
@@ -265,7 +281,25 @@ int nitro_model_create(const void* blob, uint64_t bytes, nitro_model** out) {
             hip_check(hipMalloc((void**)&m->weights, o), "hipMalloc(weights)");
             hip_check(hipMemcpy(m->weights, static_cast<const uint8_t*>(blob) + 28, o, hipMemcpyHostToDevice),
                       "hipMemcpy(weights)");
+            // the tile-layout copies, all layers of a matrix in one pass
+            struct Mat {
+                size_t src, *dst, rows, cols;
+            } mats[7] = {{m->o_wq, &m->t_wq, D, D},   {m->o_wk, &m->t_wk, KV, D}, {m->o_wv, &m->t_wv, KV, D},
+                         {m->o_wo, &m->t_wo, D, D},   {m->o_w1, &m->t_w1, Hd, D}, {m->o_w2, &m->t_w2, D, Hd},
+                         {m->o_w3, &m->t_w3, Hd, D}};
+            size_t t = 0;
+            for (Mat& mt : mats) {
+                *mt.dst = t;
+                t += L * q8_tiled_bytes(mt.rows, mt.cols);
+            }
+            hip_check(hipMalloc((void**)&m->tiled, t), "hipMalloc(tiled weights)");
+            for (const Mat& mt : mats)
+                hip_check(launch_q8_tile(m->weights + mt.src, m->tiled + *mt.dst, (int)(L * mt.rows), (int)mt.cols,
+                                         nullptr),
+                          "q8 tile launch");
+            hip_check(hipDeviceSynchronize(), "q8 tile");
         } catch (...) {
+            if (m->tiled) (void)hipFree(m->tiled);
             if (m->weights) (void)hipFree(m->weights);
             delete m;
             throw;
@@ -279,6 +313,7 @@ int nitro_model_destroy(nitro_model* m) {
     return guarded([&] {
         (void)hipDeviceSynchronize();
         (void)hipFree(m->weights);
+        (void)hipFree(m->tiled);
         delete m;
     });
 }

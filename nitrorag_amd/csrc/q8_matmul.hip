@@ -154,11 +154,13 @@ __device__ __forceinline__ float2 rotate_pair(const Q8Rope& rp, int pos, int fea
 
 }  // namespace
 
-// Up to 3 matrices sharing x (same n); out[m] is [batch][d[m]].
+// Up to 3 matrices sharing x (same n); out[m] is [batch][d[m]]; wt[m] the
+// same matrix in the tile layout (or null).
 struct Q8Group {
     const uint8_t* w[3];
     float* out[3];
     int d[3];
+    const uint8_t* wt[3];
 };
 
 namespace {
@@ -541,6 +543,56 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, c
     }
 }
 
+// The epilogue of one output element, out[b][row] of each group member, for
+// kernels that hold finished sums one element per thread: `pair` holds the
+// q and k sums of row row ^ 1 (RoPE pairs).  RESID: the 16 threads of rows
+// 16p..16p+15 of batch row b must be 16 consecutive lanes (ordered by row)
+// and call this together; they add their squares into partial p of row b.
+template <int NMAT, bool SWIGLU, bool RESID, bool ROPE>
+__device__ __forceinline__ void store_row_sums(const Q8Group& grp, const Q8Resid& resid, const Q8Rope& rope, int b,
+                                               int row, const float (&sum)[NMAT], const float (&pair)[2]) {
+    if constexpr (ROPE) {
+        const RopeRow rp = rope_row(rope, b);
+        const bool odd = row & 1;
+        const int fe = row & ~1;
+        const float2 qr = rotate_pair(rope, rp.pos, fe, odd ? pair[0] : sum[0], odd ? sum[0] : pair[0]);
+        const float2 kr = rotate_pair(rope, rp.pos, fe, odd ? pair[1] : sum[1], odd ? sum[1] : pair[1]);
+        if (row < grp.d[0]) grp.out[0][(size_t)b * grp.d[0] + row] = odd ? qr.y : qr.x;
+        if (row < grp.d[1]) {
+            if (rp.page_ok) {
+                const size_t o = (size_t)rp.page * rope.page_stride + rope.layer_off +
+                                 (size_t)rp.in_page * grp.d[1] + row;
+                rope.k_pool[o] = odd ? kr.y : kr.x;
+                rope.v_pool[o] = sum[2];
+            } else if (row == 0) {
+                atomicAdd(rope.bad_pages, 1);  // once per row
+            }
+        }
+    } else if constexpr (RESID) {
+        // x[b][row] += product; the 16 threads of the row group add their squares
+        float ssq = 0.0f;
+        if (row < grp.d[0]) {
+            float* xe = grp.out[0] + (size_t)b * grp.d[0] + row;
+            const float v = *xe + sum[0];
+            *xe = v;
+            ssq = v * v;
+        }
+#pragma unroll
+        for (int msk = 8; msk > 0; msk >>= 1) ssq += __shfl_xor(ssq, msk, 16);
+        if ((row & 15) == 0 && row < grp.d[0]) resid.ss[(size_t)(row >> 4) * resid.ss_stride + b] = ssq;
+    } else if constexpr (SWIGLU) {
+        if (row < grp.d[0]) {
+            float h = sum[0];
+            h *= 1.0f / (1.0f + expf(-h));
+            grp.out[0][(size_t)b * grp.d[0] + row] = h * sum[1];
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+            if (row < grp.d[m]) grp.out[m][(size_t)b * grp.d[m] + row] = sum[m];
+    }
+}
+
 // Batches of 1..NB rows over long rows (full-row products, n >= 2048),
 // weights streamed row by row.  A tile is 16R output rows: four row sets of
 // four row groups of R rows.  A wave owns one row group of each set and half
@@ -713,56 +765,286 @@ __global__ __launch_bounds__(512) void q8_rowdot_kernel(Q8Group grp, const float
         for (int t = threadIdx.x; t < NB * TROWS; t += 512) {
             const int b = t / TROWS, i = t % TROWS;
             const int row = tile * TROWS + i;
-            float sum[NMAT];
+            float sum[NMAT], pair[2] = {0.0f, 0.0f};
 #pragma unroll
             for (int m = 0; m < NMAT; m++) sum[m] = red[0][m][i][b] + red[1][m][i][b];
             if constexpr (ROPE) {
                 // RoPE pairs are rows (i, i ^ 1) of the tile
-                const float q_o = red[0][0][i ^ 1][b] + red[1][0][i ^ 1][b];
-                const float k_o = red[0][1][i ^ 1][b] + red[1][1][i ^ 1][b];
-                const RopeRow rp = rope_row(rope, b);
-                const bool odd = i & 1;
-                const int fe = row & ~1;
-                const float2 qr = rotate_pair(rope, rp.pos, fe, odd ? q_o : sum[0], odd ? sum[0] : q_o);
-                const float2 kr = rotate_pair(rope, rp.pos, fe, odd ? k_o : sum[1], odd ? sum[1] : k_o);
-                if (row < grp.d[0]) grp.out[0][(size_t)b * grp.d[0] + row] = odd ? qr.y : qr.x;
-                if (row < grp.d[1]) {
-                    if (rp.page_ok) {
-                        const size_t o = (size_t)rp.page * rope.page_stride + rope.layer_off +
-                                         (size_t)rp.in_page * grp.d[1] + row;
-                        rope.k_pool[o] = odd ? kr.y : kr.x;
-                        rope.v_pool[o] = sum[2];
-                    } else if (row == 0) {
-                        atomicAdd(rope.bad_pages, 1);  // once per row
-                    }
-                }
-            } else if constexpr (RESID) {
-                static_assert(!RESID || TROWS % 16 == 0, "residual partials are per 16 rows");
-                // x[b][row] += product; each 16 threads (16 rows of batch row b) add their squares
-                float ssq = 0.0f;
-                if (row < grp.d[0]) {
-                    float* xe = grp.out[0] + (size_t)b * grp.d[0] + row;
-                    const float v = *xe + sum[0];
-                    *xe = v;
-                    ssq = v * v;
-                }
-#pragma unroll
-                for (int msk = 8; msk > 0; msk >>= 1) ssq += __shfl_xor(ssq, msk, 16);
-                if ((i & 15) == 0 && row < grp.d[0]) resid.ss[(size_t)(row >> 4) * resid.ss_stride + b] = ssq;
-            } else if constexpr (SWIGLU) {
-                if (row < grp.d[0]) {
-                    float h = sum[0];
-                    h *= 1.0f / (1.0f + expf(-h));
-                    grp.out[0][(size_t)b * grp.d[0] + row] = h * sum[1];
-                }
-            } else {
-#pragma unroll
-                for (int m = 0; m < NMAT; m++)
-                    if (row < grp.d[m]) grp.out[m][(size_t)b * grp.d[m] + row] = sum[m];
+                pair[0] = red[0][0][i ^ 1][b] + red[1][0][i ^ 1][b];
+                pair[1] = red[0][1][i ^ 1][b] + red[1][1][i ^ 1][b];
             }
+            static_assert(!RESID || TROWS % 16 == 0, "residual partials are per 16 rows");
+            store_row_sums<NMAT, SWIGLU, RESID, ROPE>(grp, resid, rope, b, row, sum, pair);
         }
         __syncthreads();  // red is reused by the next tile
     }
+}
+
+// Batches of more than 4 rows (full-row products) on the bf16 matrix cores
+// at fp32 accuracy.  An int8 weight is exact in bf16, and an fp32 activation
+// is the exact sum of three bf16 numbers: hi = its upper 16 bits, mid = the
+// upper 16 bits of the remainder and lo = what is left (each step keeps 8
+// significant bits; 24 in all).  Each product q * part is exact in the fp32
+// accumulator, so three v_mfma_f32_16x16x32_bf16 (lo, mid, hi; 32 k = one
+// block each) give the block's sum sum_k q[k] * x[k] with fp32 accumulation,
+// which is then scaled: acc += scale * sum (the reference scales each weight
+// before the product, src/model_q8.cpp:106-112; the two agree to fp32
+// rounding).  Per instruction, A = x parts (lane l: batch row l%16, k =
+// 8*(l/16) + i of the block) and B = the block's weights (lane l: weight row
+// l%16, bytes 4 + 8*(l/16) .. +8 of its 36), so the accumulator leaves lane l
+// holding out[batch 4*(l/16) + j][row l%16] and every lane scales by the
+// scale of its own row.
+//
+// A workgroup owns 16 rows of each group member and 16 or 32 batch rows (BT
+// tiles of 16; larger batches add workgroups along y); MMA_WAVES waves take the rows' blocks U at a time,
+// round-robin.  A wave's rounds are pipelined: it loads a round's x (an L2
+// read) and then issues the next round's weight loads before computing, so
+// one round of weights is always in flight behind the one in use (the x
+// loads go first because a wait covers every older load).  At the end the
+// waves' tiles are added through LDS in a fixed wave order, one thread per
+// (member, batch row, row), and the shared epilogue runs.
+constexpr int MMA_WAVES = 16;
+constexpr int MMA_TILE_STRIDE = 20;  // floats per batch row of a staged tile (stores hit 64 distinct banks)
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Elements (a, b) as a bf16 pair: the upper 16 bits of each (a truncation,
+// exact where a and b have at most 8 significant bits).
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+    // bytes 2, 3 of a then bytes 2, 3 of b (v_perm_b32: bytes 0-3 are the
+    // second operand, 4-7 the first)
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
+
+__device__ __forceinline__ float q8_value(uint32_t w, int j) { return (float)(int)(int8_t)(w >> (8 * j)); }
+
+// Eight int8 weights (two words, k order) as bf16.
+__device__ __forceinline__ bf16x8 q8_bf16(uint32_t w0, uint32_t w1) {
+    u32x4 r;
+    r[0] = bf16_pair(q8_value(w0, 0), q8_value(w0, 1));
+    r[1] = bf16_pair(q8_value(w0, 2), q8_value(w0, 3));
+    r[2] = bf16_pair(q8_value(w1, 0), q8_value(w1, 1));
+    r[3] = bf16_pair(q8_value(w1, 2), q8_value(w1, 3));
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+__device__ __forceinline__ float upper16(float v) { return __uint_as_float(__float_as_uint(v) & 0xffff0000u); }
+
+// v = hi + mid + lo exactly (v finite and not below 2^-102 in magnitude
+// unless zero: each part keeps 8 significant bits of what is left).
+__device__ __forceinline__ void split3(const float (&v)[8], bf16x8& hi, bf16x8& mid, bf16x8& lo) {
+    u32x4 h, m, l;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const float a = v[2 * p], b = v[2 * p + 1];
+        const float ar = a - upper16(a), br = b - upper16(b);
+        const float al = ar - upper16(ar), bl = br - upper16(br);
+        h[p] = bf16_pair(a, b);
+        m[p] = bf16_pair(ar, br);
+        l[p] = bf16_pair(al, bl);
+    }
+    hi = __builtin_bit_cast(bf16x8, h);
+    mid = __builtin_bit_cast(bf16x8, m);
+    lo = __builtin_bit_cast(bf16x8, l);
+}
+
+// Blocks per wave per round: two rounds of weights and x stay within the 128
+// registers of 16 waves per CU.
+template <int NMAT, int BT>
+constexpr int mma_unroll() {
+    return BT == 1 ? (NMAT == 3 ? 1 : 2) : 1;
+}
+constexpr int MMA_MAX_BT = 2;       // batch tiles per workgroup (more rows: more workgroups along y)
+constexpr int MMA_NORM_MAX_N = 8192;  // rms weights staged in LDS (larger n: the fp32 kernel)
+
+// One round of a wave: weights and x of U blocks.
+template <int NMAT, int BT, int U>
+struct MmaRound {
+    uint32_t q[U][NMAT][2];
+    float scale[U][NMAT];
+    float x[BT][U][8];
+};
+
+template <int NMAT, int BT, bool TILED, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
+__global__ __launch_bounds__(64 * MMA_WAVES) void q8_mma_kernel(Q8Group grp, const float* __restrict__ x, int batch,
+                                                                int n, Q8Norm nm, Q8Resid resid, Q8Rope rope) {
+    constexpr int U = mma_unroll<NMAT, BT>();
+    constexpr int STRIDE = MMA_WAVES * U;  // blocks per round of the workgroup
+    __shared__ float red[MMA_WAVES][NMAT][16 * MMA_TILE_STRIDE];
+    __shared__ float norm_s[NORM ? MMA_WAVES * 64 : 1];
+    __shared__ float norm_w[NORM ? MMA_NORM_MAX_N : 1];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int row0 = blockIdx.x * 16;
+    const int b0 = blockIdx.y * 16 * BT;
+    const int nb = n / Q8_BLOCK;
+    if constexpr (NORM) {
+        // thread (row j = tid % 64, class c = tid / 64) adds partials c, c + 16, ...;
+        // row j's class sums are then added in class order: norm_s[j] = inv_rms
+        const int j = threadIdx.x & 63, c = threadIdx.x >> 6;
+        norm_s[c * 64 + j] = j < 16 * BT && b0 + j < batch ? partial_sum(nm, b0 + j, c, MMA_WAVES) : 0.0f;
+        for (int k = threadIdx.x; k < n; k += 64 * MMA_WAVES) norm_w[k] = nm.weight[k];
+        __syncthreads();
+        float ss = 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < MMA_WAVES; cc++) ss += norm_s[cc * 64 + lane];
+        __syncthreads();
+        if (wave == 0) norm_s[lane] = inv_rms(ss, n);
+        __syncthreads();
+    }
+    // Lanes past the batch read the last batch row and rows past a member's
+    // end read its last row (finite values, never stored); blocks past the
+    // row read the last block with scale 0.
+    // (32-bit offsets from the uniform bases: the launcher keeps each matrix
+    // and x under 2^32 bytes).  Block blk of this lane: its 8 weights at
+    // qoff + blk * BSTEP, its row's scale at soff + blk * BSTEP.
+    constexpr uint32_t BSTEP = TILED ? 576 : Q8_BLOCK_BYTES;
+    const uint8_t* wbase[NMAT];
+    uint32_t qoff[NMAT], soff[NMAT];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+        if constexpr (TILED) {
+            const uint32_t rec = (uint32_t)min((int)blockIdx.x, (grp.d[m] + 15) / 16 - 1) * nb * 576;
+            wbase[m] = grp.wt[m];
+            qoff[m] = rec + 64 + 8 * lane;
+            soff[m] = rec + 4 * r;
+        } else {
+            const uint32_t row = (uint32_t)min(row0 + r, grp.d[m] - 1) * nb * Q8_BLOCK_BYTES;
+            wbase[m] = grp.w[m];
+            qoff[m] = row + 4 + 8 * g;
+            soff[m] = row;
+        }
+    }
+    uint32_t xrow[BT];
+#pragma unroll
+    for (int t = 0; t < BT; t++) xrow[t] = (uint32_t)min(b0 + t * 16 + r, batch - 1) * n + 8 * g;
+    f32x4 acc[NMAT][BT];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int t = 0; t < BT; t++) acc[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+
+    using Round = MmaRound<NMAT, BT, U>;
+    auto load_round = [&](Round& R, int base) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const bool valid = base + u < nb;
+            const int blk = valid ? base + u : nb - 1;
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                const uint2 q = *reinterpret_cast<const uint2*>(wbase[m] + (qoff[m] + (uint32_t)blk * BSTEP));
+                R.q[u][m][0] = q.x;
+                R.q[u][m][1] = q.y;
+                const float sc = *reinterpret_cast<const float*>(wbase[m] + (soff[m] + (uint32_t)blk * BSTEP));
+                R.scale[u][m] = valid ? sc : 0.0f;
+            }
+#pragma unroll
+            for (int t = 0; t < BT; t++) {
+                const float4 a = *reinterpret_cast<const float4*>(x + (xrow[t] + blk * Q8_BLOCK));
+                const float4 c = *reinterpret_cast<const float4*>(x + (xrow[t] + blk * Q8_BLOCK + 4));
+                R.x[t][u][0] = a.x, R.x[t][u][1] = a.y, R.x[t][u][2] = a.z, R.x[t][u][3] = a.w;
+                R.x[t][u][4] = c.x, R.x[t][u][5] = c.y, R.x[t][u][6] = c.z, R.x[t][u][7] = c.w;
+            }
+        }
+    };
+    // per block: its weights as bf16, then per batch tile the split x and
+    // NMAT independent chains (lo, mid, hi), scaled into the accumulators
+    auto compute = [&](const Round& R, int base) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            bf16x8 wb[NMAT];
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) wb[m] = q8_bf16(R.q[u][m][0], R.q[u][m][1]);
+#pragma unroll
+            for (int t = 0; t < BT; t++) {
+                float v[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = R.x[t][u][i];
+                if constexpr (NORM) {
+                    const float inv = norm_s[t * 16 + r];
+                    const int k0 = min(base + u, nb - 1) * Q8_BLOCK + 8 * g;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[i] = norm_w[k0 + i] * (inv * v[i]);
+                }
+                bf16x8 xh, xm, xl;
+                split3(v, xh, xm, xl);
+                f32x4 sm[NMAT];
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) sm[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wb[m], zero, 0, 0, 0);
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) sm[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, wb[m], sm[m], 0, 0, 0);
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) sm[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wb[m], sm[m], 0, 0, 0);
+#pragma unroll
+                for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) acc[m][t][j] = fmaf(R.scale[u][m], sm[m][j], acc[m][t][j]);
+            }
+        }
+    };
+    // The two round buffers alternate: the next round's loads are all issued
+    // before the current round is computed.
+    Round ra, rb;
+    int base = wave * U;
+    if (base < nb) load_round(ra, base);
+    while (base < nb) {  // uniform
+        if (base + STRIDE < nb) load_round(rb, base + STRIDE);
+        compute(ra, base);
+        base += STRIDE;
+        if (base >= nb) break;
+        if (base + STRIDE < nb) load_round(ra, base + STRIDE);
+        compute(rb, base);
+        base += STRIDE;
+    }
+
+    // Per batch tile: every wave stages its tile (lane l: batch rows
+    // 4*(l/16)+j, row l%16), then thread (m, b = (tid/16)%16, i = tid%16)
+    // adds the waves in order; the epilogue runs on the first 256 threads.
+    __shared__ float sums[NMAT][256];
+#pragma unroll
+    for (int t = 0; t < BT; t++) {
+        if (b0 + t * 16 >= batch) break;  // uniform
+        if (t > 0) __syncthreads();  // the previous tile's reads are done
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) red[wave][m][(4 * g + j) * MMA_TILE_STRIDE + r] = acc[m][t][j];
+        __syncthreads();
+        for (int e = threadIdx.x; e < NMAT * 256; e += 64 * MMA_WAVES) {
+            const int m = e >> 8, bl = (e >> 4) & 15, i = e & 15;
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < MMA_WAVES; w++) v += red[w][m][bl * MMA_TILE_STRIDE + i];
+            sums[m][e & 255] = v;
+        }
+        __syncthreads();
+        if (threadIdx.x < 256) {
+            const int bl = threadIdx.x >> 4, i = threadIdx.x & 15;
+            const int b = b0 + t * 16 + bl;
+            if (b < batch) {  // uniform over the 16 threads of batch row b
+                float sum[NMAT], pair[2] = {0.0f, 0.0f};
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) sum[m] = sums[m][threadIdx.x];
+                if constexpr (ROPE) {
+                    pair[0] = sums[0][threadIdx.x ^ 1];
+                    pair[1] = sums[1][threadIdx.x ^ 1];
+                }
+                store_row_sums<NMAT, SWIGLU, RESID, ROPE>(grp, resid, rope, b, row0 + i, sum, pair);
+            }
+        }
+    }
+}
+
+bool use_mma() {
+    static const bool on = [] {
+        const char* e = getenv("NITRO_Q8_MMA");
+        return !(e && e[0] == 'f');  // "f32": the fp32 matrix-core kernel (comparison runs)
+    }();
+    return on;
 }
 
 // Row streaming pays off once a row has at least two 1024-k chunks (both k
@@ -799,6 +1081,45 @@ void launch_gemv(const Q8Group& grp, const float* x, int n, int dmax, bool last,
                            grp, x, n, nm, rs, rp);
 }
 
+template <int NMAT, bool TILED, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
+void launch_mma(const Q8Group& grp, const float* x, int batch, int n, int dmax, const Q8Norm& nm, const Q8Resid& rs,
+                const Q8Rope& rp, hipStream_t stream) {
+    const dim3 block(64 * MMA_WAVES);
+    const unsigned tiles = (unsigned)((dmax + 15) / 16);
+    // (three members with two batch tiles would exceed the registers)
+    constexpr int BT = NMAT == 3 ? 1 : MMA_MAX_BT;
+    if (batch <= 16) {
+        hipLaunchKernelGGL((q8_mma_kernel<NMAT, 1, TILED, SWIGLU, NORM, RESID, ROPE>), dim3(tiles), block, 0, stream,
+                           grp, x, batch, n, nm, rs, rp);
+    } else {
+        const dim3 g2(tiles, (unsigned)((batch + 16 * BT - 1) / (16 * BT)));
+        hipLaunchKernelGGL((q8_mma_kernel<NMAT, BT, TILED, SWIGLU, NORM, RESID, ROPE>), g2, block, 0, stream, grp, x,
+                           batch, n, nm, rs, rp);
+    }
+}
+
+// The tile layout (Q8Tiled): workgroup (block, tile), lane c copies run c
+// (8 weights of row 16*tile + c%16) and lanes 0..15 the scales.
+__global__ __launch_bounds__(64) void q8_tile_kernel(const uint8_t* __restrict__ w, uint8_t* __restrict__ tiled,
+                                                     int d, int nb, int tiles) {
+    const int blk = blockIdx.x, c = threadIdx.x;
+    for (int tile = blockIdx.y; tile < tiles; tile += gridDim.y) {
+        const int row = tile * 16 + (c & 15);
+        uint32_t q0 = 0, q1 = 0;
+        float sc = 0.0f;
+        if (row < d) {
+            const uint8_t* bp = w + ((size_t)row * nb + blk) * Q8_BLOCK_BYTES;
+            const uint32_t* qp = reinterpret_cast<const uint32_t*>(bp + 4 + 8 * (c >> 4));
+            q0 = qp[0];
+            q1 = qp[1];
+            sc = *reinterpret_cast<const float*>(bp);
+        }
+        uint8_t* rec = tiled + ((size_t)tile * nb + blk) * 576;
+        *reinterpret_cast<uint2*>(rec + 64 + 8 * c) = make_uint2(q0, q1);
+        if (c < 16) *reinterpret_cast<float*>(rec + 4 * c) = sc;
+    }
+}
+
 template <int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE = false>
 void launch_group(const Q8Group& grp, const float* x, int batch, int n, int dmax, bool last, const Q8Norm& nm,
                   const Q8Resid& rs, hipStream_t stream, const Q8Rope& rp = Q8Rope{}) {
@@ -813,6 +1134,18 @@ void launch_group(const Q8Group& grp, const float* x, int batch, int n, int dmax
     }
     const dim3 grid((unsigned)((dmax + 15) / 16),
                     (unsigned)((batch + 16 * Q8_MAX_BTILES - 1) / (16 * Q8_MAX_BTILES)));
+    // the bf16 kernel addresses weights and x with 32-bit offsets
+    const bool mma_fits = q8_tiled_bytes(dmax, n) < (1ull << 32) && (size_t)batch * n < (1ull << 32) &&
+                          (!NORM || n <= MMA_NORM_MAX_N);
+    if (!last && use_mma() && mma_fits) {
+        bool tiled = true;
+        for (int m = 0; m < NMAT; m++) tiled = tiled && grp.wt[m] != nullptr;
+        if (tiled)
+            launch_mma<NMAT, true, SWIGLU, NORM, RESID, ROPE>(grp, x, batch, n, dmax, nm, rs, rp, stream);
+        else
+            launch_mma<NMAT, false, SWIGLU, NORM, RESID, ROPE>(grp, x, batch, n, dmax, nm, rs, rp, stream);
+        return;
+    }
     const dim3 block(64 * Q8_WAVES);
     if (last)
         hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, true, NORM, RESID, ROPE>), grid, block, 0, stream, grp,
@@ -824,28 +1157,41 @@ void launch_group(const Q8Group& grp, const float* x, int batch, int n, int dmax
 
 }  // namespace
 
+hipError_t launch_q8_tile(const void* w, void* tiled, int d, int n, hipStream_t stream) {
+    if (d <= 0 || n <= 0 || n % Q8_BLOCK) return hipErrorInvalidValue;
+    const int tiles = (d + 15) / 16;
+    hipLaunchKernelGGL(q8_tile_kernel, dim3((unsigned)(n / Q8_BLOCK), (unsigned)std::min(tiles, 65535)), dim3(64), 0,
+                       stream, static_cast<const uint8_t*>(w), static_cast<uint8_t*>(tiled), d, n / Q8_BLOCK, tiles);
+    return hipGetLastError();
+}
+
 hipError_t launch_q8_matmul(const void* w, const float* x, float* out, int batch, int n, int d,
                             bool last_block_only, hipStream_t stream) {
-    Q8Group grp{{static_cast<const uint8_t*>(w), nullptr, nullptr}, {out, nullptr, nullptr}, {d, 0, 0}};
+    Q8Group grp{{static_cast<const uint8_t*>(w), nullptr, nullptr}, {out, nullptr, nullptr}, {d, 0, 0}, {}};
     launch_group<1, false, false, false>(grp, x, batch, n, d, last_block_only, Q8Norm{}, Q8Resid{}, stream);
     return hipGetLastError();
 }
 
 hipError_t launch_q8_residual(const void* w, const float* in, float* x, float* ss, int batch, int n, int d,
-                              bool last_block_only, hipStream_t stream) {
-    Q8Group grp{{static_cast<const uint8_t*>(w), nullptr, nullptr}, {x, nullptr, nullptr}, {d, 0, 0}};
+                              bool last_block_only, hipStream_t stream, const void* w_tiled) {
+    Q8Group grp{{static_cast<const uint8_t*>(w), nullptr, nullptr},
+                {x, nullptr, nullptr},
+                {d, 0, 0},
+                {static_cast<const uint8_t*>(w_tiled), nullptr, nullptr}};
     launch_group<1, false, false, true>(grp, in, batch, n, d, last_block_only, Q8Norm{}, Q8Resid{ss, batch},
                                         stream);
     return hipGetLastError();
 }
 
 hipError_t launch_q8_qkv(const void* const* w, const float* x, float* out_q, const int* d, int batch, int n,
-                         bool last_block_only, const Q8Norm& nm, const Q8Rope& rope, hipStream_t stream) {
+                         bool last_block_only, const Q8Norm& nm, const Q8Rope& rope, hipStream_t stream,
+                         const Q8Tiled& tiled) {
     if (!nm.weight || !rope.freq_real || d[1] != d[2] || d[0] % 32 || d[1] % 32) return hipErrorInvalidValue;
     Q8Group grp{};
     for (int m = 0; m < 3; m++) {
         grp.w[m] = static_cast<const uint8_t*>(w[m]);
         grp.d[m] = d[m];
+        grp.wt[m] = static_cast<const uint8_t*>(tiled.w[m]);
     }
     grp.out[0] = out_q;  // k and v go to the pools
     const int dmax = std::max(d[0], d[1]);
@@ -854,10 +1200,12 @@ hipError_t launch_q8_qkv(const void* const* w, const float* x, float* out_q, con
 }
 
 hipError_t launch_q8_swiglu(const void* w1, const void* w3, const float* x, float* hb, int batch, int n,
-                            int hidden, bool last_block_only, const Q8Norm& nm, hipStream_t stream) {
+                            int hidden, bool last_block_only, const Q8Norm& nm, hipStream_t stream,
+                            const Q8Tiled& tiled) {
     Q8Group grp{{static_cast<const uint8_t*>(w1), static_cast<const uint8_t*>(w3), nullptr},
                 {hb, nullptr, nullptr},
-                {hidden, hidden, 0}};
+                {hidden, hidden, 0},
+                {static_cast<const uint8_t*>(tiled.w[0]), static_cast<const uint8_t*>(tiled.w[1]), nullptr}};
     if (!nm.weight) return hipErrorInvalidValue;
     launch_group<2, true, true, false>(grp, x, batch, n, hidden, last_block_only, nm, Q8Resid{}, stream);
     return hipGetLastError();

@@ -59,6 +59,9 @@ SHAPES = [
     # 1024-k chunks split over two k halves (odd and even chunk counts), tiles
     # of 16 rows not filling the matrix, more tiles than workgroups
     (2048, 40, 1), (2304, 96, 2), (11008, 64, 3), (4096, 4100, 4), (4128, 16400, 1),
+    # long rows with 5..64 activation rows (bf16 matrix-core kernel): a partial
+    # 16-row batch tile, row tiles not filling the matrix, 344 blocks per row
+    (4096, 4100, 8), (11008, 80, 33), (4096, 48, 5),
 ]
 
 
