@@ -343,7 +343,9 @@ class Q8Workload:
         return self.B
 
     def kernel(self):
-        return ("q8_gemv_kernel (VALU)" if self.B <= 4 else "q8_matmul_kernel (MFMA fp32)")
+        if self.B <= 4:
+            return "q8_rowdot_kernel (VALU)" if self.n >= 2048 else "q8_gemv_kernel (VALU)"
+        return "q8_mma_kernel (bf16 matrix cores, x split in three exact parts)"
 
     def config(self):
         return {"workload": self.describe, "batch": self.B, "n": self.n, "d": self.d,

@@ -881,20 +881,6 @@ __global__ __launch_bounds__(64 * MMA_WAVES) void q8_mma_kernel(Q8Group grp, con
     const int row0 = blockIdx.x * 16;
     const int b0 = blockIdx.y * 16 * BT;
     const int nb = n / Q8_BLOCK;
-    if constexpr (NORM) {
-        // thread (row j = tid % 64, class c = tid / 64) adds partials c, c + 16, ...;
-        // row j's class sums are then added in class order: norm_s[j] = inv_rms
-        const int j = threadIdx.x & 63, c = threadIdx.x >> 6;
-        norm_s[c * 64 + j] = j < 16 * BT && b0 + j < batch ? partial_sum(nm, b0 + j, c, MMA_WAVES) : 0.0f;
-        for (int k = threadIdx.x; k < n; k += 64 * MMA_WAVES) norm_w[k] = nm.weight[k];
-        __syncthreads();
-        float ss = 0.0f;
-#pragma unroll
-        for (int cc = 0; cc < MMA_WAVES; cc++) ss += norm_s[cc * 64 + lane];
-        __syncthreads();
-        if (wave == 0) norm_s[lane] = inv_rms(ss, n);
-        __syncthreads();
-    }
     // Lanes past the batch read the last batch row and rows past a member's
     // end read its last row (finite values, never stored); blocks past the
     // row read the last block with scale 0.
@@ -990,7 +976,21 @@ __global__ __launch_bounds__(64 * MMA_WAVES) void q8_mma_kernel(Q8Group grp, con
     // before the current round is computed.
     Round ra, rb;
     int base = wave * U;
-    if (base < nb) load_round(ra, base);
+    if (base < nb) load_round(ra, base);  // in flight while the norm prologue runs
+    if constexpr (NORM) {
+        // thread (row j = tid % 64, class c = tid / 64) adds partials c, c + 16, ...;
+        // row j's class sums are then added in class order: norm_s[j] = inv_rms
+        const int j = threadIdx.x & 63, c = threadIdx.x >> 6;
+        norm_s[c * 64 + j] = j < 16 * BT && b0 + j < batch ? partial_sum(nm, b0 + j, c, MMA_WAVES) : 0.0f;
+        for (int k = threadIdx.x; k < n; k += 64 * MMA_WAVES) norm_w[k] = nm.weight[k];
+        __syncthreads();
+        float ss = 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < MMA_WAVES; cc++) ss += norm_s[cc * 64 + lane];
+        __syncthreads();
+        if (wave == 0) norm_s[lane] = inv_rms(ss, n);
+        __syncthreads();
+    }
     while (base < nb) {  // uniform
         if (base + STRIDE < nb) load_round(rb, base + STRIDE);
         compute(ra, base);
