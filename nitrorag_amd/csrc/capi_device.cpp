@@ -474,9 +474,13 @@ int nitro_paged_attn_prefill(nitro_kvpool* pool, int32_t layer, const float* q, 
         a.num_pages = pool->num_pages;
         a.work_items = p.work_items;
         a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
-        // NITRO_PREFILL_KERNEL=valu selects the VALU kernel (A/B counter comparisons).
+        // NITRO_PREFILL_KERNEL=valu / mfma32 selects the VALU / fp32 matrix-core
+        // kernel (A/B counter comparisons).
         const char* kern = std::getenv("NITRO_PREFILL_KERNEL");
-        a.use_valu = (kern && std::strcmp(kern, "valu") == 0) ? 1 : 0;
+        a.kernel = !kern                                ? PREFILL_KERNEL_DEFAULT
+                   : std::strcmp(kern, "valu") == 0     ? PREFILL_KERNEL_VALU
+                   : std::strcmp(kern, "mfma32") == 0   ? PREFILL_KERNEL_MFMA_F32
+                                                        : PREFILL_KERNEL_DEFAULT;
         hipStream_t s = as_stream(stream);
         hip_check(launch_paged_attn_prefill(a, s), "paged_attn_prefill launch");
         pool->last_stream = s;

@@ -276,8 +276,11 @@ struct PrefillLaunch {
     int64_t page_stride, layer_off;
     int32_t kv_dim, n_heads, kv_mul, head_dim, max_pages, num_pages, work_items;
     float qscale;
-    int32_t use_valu;  // 1: the VALU kernel even where an MFMA one exists
+    int32_t kernel;  // PREFILL_KERNEL_*: which form runs where several exist
 };
+constexpr int32_t PREFILL_KERNEL_DEFAULT = 0;   // bf16 matrix cores at fp32 accuracy (hd <= 128)
+constexpr int32_t PREFILL_KERNEL_VALU = 1;      // fp32 VALU FMAs
+constexpr int32_t PREFILL_KERNEL_MFMA_F32 = 2;  // fp32 matrix cores (v_mfma_f32_16x16x4_f32)
 // Query rows per prefill work item.
 int prefill_block_m(int head_dim);
 hipError_t launch_paged_attn_prefill(const PrefillLaunch& a, hipStream_t stream);

@@ -49,6 +49,7 @@
 
 #include <cmath>
 
+#include "bf16_split.hpp"
 #include "device_pool.hpp"
 
 namespace nitro {
@@ -501,13 +502,327 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_mfma_kern
     }
 }
 
+// paged_attn_prefill_x3_kernel<hd, KSPLIT, BNM>: the MFMA kernel's work
+// split and softmax with both products on the bf16 matrix cores at fp32
+// accuracy.  Q, K, V and the probabilities P are each split into three bf16
+// parts (hi, mid, lo; exact, 24 significant bits in all), and each product
+// takes the six part products whose order is at most 2 (hi.hi, hi.mid,
+// mid.hi, hi.lo, mid.mid, lo.hi; the dropped ones are below 2^-24 of the
+// total), smallest first, accumulated in fp32 by v_mfma_f32_16x16x32_bf16:
+//  - S^T = K Q^T per 16-key block and 32 d: lane l supplies K[key l%16] and
+//    Q[query l%16] at d = 32c + 8*(l/16) .. +8, so the accumulator leaves lane
+//    l holding S[query l%16][keys 4g..4g+3] (g = l/16) as before;
+//  - O^T += V^T P^T per pair of 16-key blocks (32 keys): lane l's B operand
+//    is its own probabilities of the two blocks (keys 4g..4g+3 of each), and
+//    its A operand V^T[d = 16n + l%16] at the same 8 keys, read from a
+//    transposed V tile.
+// K and V are split once, when a tile is staged: three bf16 planes each in
+// LDS, K as [key][d] and V as [d][key].  K is loaded a float4 of one key row
+// per thread; V one d of four consecutive keys per thread (a wave's lanes
+// cover consecutive d of a row, so the loads coalesce), which becomes one
+// 8-byte store per plane into the transposed tile.
+template <int HD, int KSPLIT, int BNM>
+__global__ __launch_bounds__(256 * KSPLIT) void paged_attn_prefill_x3_kernel(PrefillLaunch a) {
+    constexpr int QT = 4;                      // query sub-tiles (one work item per workgroup)
+    constexpr int NT = 64 * QT * KSPLIT;
+    constexpr int KB = BNM / 16;               // 16-key blocks per tile
+    constexpr int NBW = KB / KSPLIT;           // 16-key blocks per wave per tile
+    static_assert(KB % KSPLIT == 0 && NBW % 2 == 0, "a wave's blocks pair up into 32-key products");
+    constexpr int F4 = HD / 4;                 // float4 per K/V row
+    constexpr int NC = HD / 32;                // 32-d chunks of S
+    constexpr int NB = HD / 16;                // 16-column blocks of the output
+    constexpr int KST = HD + 8;                // K plane row (bf16; 16-byte aligned rows)
+    constexpr int VST = BNM + 4;               // V^T plane row (bf16; 8-byte aligned rows, stores spread over banks)
+    constexpr int LOADS = BNM * F4 / NT;       // K float4 per thread per tile
+    constexpr int VSLOTS = BNM * HD / (4 * NT);  // V (d, 4-key group) slots per thread per tile
+    static_assert(LOADS >= 1 && BNM * F4 % NT == 0 && VSLOTS >= 1 && BNM * HD % (4 * NT) == 0, "tile shape");
+    static_assert((KSPLIT - 1) * QT * 16 * HD * 4 <= 3 * BNM * KST * 2, "partials fit the K planes");
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[3 * BNM * KST];
+    __shared__ __attribute__((aligned(16))) uint16_t v_lds[3 * HD * VST];
+    __shared__ int32_t s_table[TABLE_LDS];
+    __shared__ float s_ml[KSPLIT > 1 ? QT * (KSPLIT - 1) * 16 * 2 : 1];
+
+    const int h = blockIdx.x % a.n_heads;
+    const int item = blockIdx.x / a.n_heads;
+    const int seq = a.work[2 * item];
+    const int q0 = a.work[2 * item + 1];
+    const int kv_h = h / a.kv_mul;
+    const int start = a.start_pos[seq];
+    const int qcount = min(BM, a.num_tokens[seq] - q0);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int qs = wave % QT;
+    const int kg = wave / QT;
+    const int ql = lane & 15;
+    const int g = lane >> 4;
+    const int row = qs * 16 + ql;
+    const int last_pos = start + q0 + qcount - 1;
+    const int my_pos = start + q0 + min(row, qcount - 1);
+    const int wave_last = start + q0 + min(qs * 16 + 15, qcount - 1);
+    const int wave_first = start + q0 + min(qs * 16, qcount - 1);
+    const int32_t* trow = a.tables + (size_t)seq * a.max_pages;
+    const int n_tiles = last_pos / BNM + 1;
+    const size_t dim = (size_t)a.n_heads * HD;
+    const size_t qrow = (size_t)(a.row_off[seq] + q0 + min(row, qcount - 1));
+
+    const int n_pages = min((last_pos >> 4) + 1, TABLE_LDS);
+    for (int i = threadIdx.x; i < n_pages; i += NT) s_table[i] = trow[i];
+    __syncthreads();
+
+    // Q (pre-scaled) of this lane's query at d = 32c + 8g .. +8, in parts
+    bf16x8 qp[3][NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const float4* src = reinterpret_cast<const float4*>(a.q + qrow * dim + (size_t)h * HD + 32 * c + 8 * g);
+        const float4 u = src[0], w = src[1];
+        const float v[8] = {u.x * a.qscale, u.y * a.qscale, u.z * a.qscale, u.w * a.qscale,
+                            w.x * a.qscale, w.y * a.qscale, w.z * a.qscale, w.w * a.qscale};
+        split3(v, qp[0][c], qp[1][c], qp[2][c]);
+    }
+    f32x4 acc[NB];
+#pragma unroll
+    for (int n = 0; n < NB; n++) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, lsum = 0.0f;
+
+    const float* kbase = a.k_pool + a.layer_off + (size_t)kv_h * HD;
+    const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * HD;
+    float4 kreg[LOADS];
+    float vreg[VSLOTS][4];
+    auto page_of = [&](int key) {
+        const int pi = key >> 4;
+        return pi < TABLE_LDS ? s_table[pi] : trow[pi];
+    };
+    auto fetch = [&](int tile) {
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int f = threadIdx.x + i * NT;
+            const int r = f / F4, col = f % F4;
+            const int key = tile * BNM + r;
+            kreg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (key <= last_pos) {
+                const int page = page_of(key);
+                if ((unsigned)page < (unsigned)a.num_pages) {
+                    const size_t off = (size_t)page * a.page_stride + (size_t)(key & 15) * a.kv_dim;
+                    kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
+                } else if (col == 0) {
+                    atomicAdd(a.bad_pages, 1);  // once per key (V reads the same page)
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VSLOTS; i++) {
+            const int sl = threadIdx.x + i * NT;
+            const int d = sl % HD, key0 = tile * BNM + 4 * (sl / HD);  // 4 keys, one page
+            const int page = key0 <= last_pos ? page_of(key0) : -1;
+            const bool ok = (unsigned)page < (unsigned)a.num_pages;
+            const float* vp = vbase + (ok ? (size_t)page * a.page_stride : 0) + (size_t)(key0 & 15) * a.kv_dim + d;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                vreg[i][e] = ok && key0 + e <= last_pos ? vp[(size_t)e * a.kv_dim] : 0.0f;
+        }
+    };
+    constexpr int KPLANE = BNM * KST, VPLANE = HD * VST;
+    auto mfma = [](const bf16x8& x, const bf16x8& y, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, c, 0, 0, 0);
+    };
+
+    fetch(0);
+    for (int tile = 0; tile < n_tiles; tile++) {
+        __syncthreads();  // previous tile fully consumed
+        // four values as three bf16 planes, one 8-byte store each
+        auto stage4 = [](uint16_t* dst, int plane, const float (&v)[4]) {
+            const float r0 = v[0] - upper16(v[0]), r1 = v[1] - upper16(v[1]);
+            const float r2 = v[2] - upper16(v[2]), r3 = v[3] - upper16(v[3]);
+            const float l0 = r0 - upper16(r0), l1 = r1 - upper16(r1);
+            const float l2 = r2 - upper16(r2), l3 = r3 - upper16(r3);
+            *reinterpret_cast<uint2*>(dst) = make_uint2(bf16_pair(v[0], v[1]), bf16_pair(v[2], v[3]));
+            *reinterpret_cast<uint2*>(dst + plane) = make_uint2(bf16_pair(r0, r1), bf16_pair(r2, r3));
+            *reinterpret_cast<uint2*>(dst + 2 * plane) = make_uint2(bf16_pair(l0, l1), bf16_pair(l2, l3));
+        };
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int f = threadIdx.x + i * NT;
+            const int r = f / F4, col = f % F4;
+            const float kv4[4] = {kreg[i].x, kreg[i].y, kreg[i].z, kreg[i].w};
+            stage4(&k_lds[r * KST + col * 4], KPLANE, kv4);
+        }
+#pragma unroll
+        for (int i = 0; i < VSLOTS; i++) {
+            const int sl = threadIdx.x + i * NT;
+            stage4(&v_lds[(sl % HD) * VST + 4 * (sl / HD)], VPLANE, vreg[i]);
+        }
+        __syncthreads();
+        if (tile + 1 < n_tiles) fetch(tile + 1);
+
+        int nvb = 0;
+#pragma unroll
+        for (int j = 0; j < NBW; j++)
+            if (tile * BNM + (kg + j * KSPLIT) * 16 <= wave_last) nvb = j + 1;
+        if (nvb > 0) {  // wave-uniform
+            f32x4 st[NBW];
+#pragma unroll
+            for (int j = 0; j < NBW; j++) {
+                st[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (j < nvb) {  // wave-uniform
+                    const uint16_t* kr = &k_lds[((kg + j * KSPLIT) * 16 + ql) * KST + 8 * g];
+#pragma unroll
+                    for (int c = 0; c < NC; c++) {
+                        const bf16x8 kh = *reinterpret_cast<const bf16x8*>(kr + 32 * c);
+                        const bf16x8 km = *reinterpret_cast<const bf16x8*>(kr + KPLANE + 32 * c);
+                        const bf16x8 kl = *reinterpret_cast<const bf16x8*>(kr + 2 * KPLANE + 32 * c);
+                        st[j] = mfma(kl, qp[0][c], st[j]);
+                        st[j] = mfma(km, qp[1][c], st[j]);
+                        st[j] = mfma(kh, qp[2][c], st[j]);
+                        st[j] = mfma(km, qp[0][c], st[j]);
+                        st[j] = mfma(kh, qp[1][c], st[j]);
+                        st[j] = mfma(kh, qp[0][c], st[j]);
+                    }
+                }
+            }
+            const int last_key0 = tile * BNM + (kg + (nvb - 1) * KSPLIT) * 16;
+            float p[NBW][4];
+            if (nvb == NBW && last_key0 + 15 <= wave_first) {
+                float bmax = fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3]));
+#pragma unroll
+                for (int j = 1; j < NBW; j++)
+                    bmax = fmaxf(bmax, fmaxf(fmaxf(st[j][0], st[j][1]), fmaxf(st[j][2], st[j][3])));
+                bmax = max_over_rows(bmax);
+                if (__builtin_amdgcn_ballot_w64(bmax > m + kLazyRescaleLog2) != 0) {  // wave-uniform
+                    const float m_new = fmaxf(m, bmax);
+                    const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // m = -inf: 0
+                    lsum *= alpha;
+#pragma unroll
+                    for (int n = 0; n < NB; n++) acc[n] *= alpha;
+                    m = m_new;
+                }
+#pragma unroll
+                for (int j = 0; j < NBW; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) p[j][r] = __builtin_amdgcn_exp2f(st[j][r] - m);
+            } else {
+                float sm[NBW][4];
+                float bmax = -INFINITY;
+#pragma unroll
+                for (int j = 0; j < NBW; j++) {
+                    const int kj = tile * BNM + (kg + j * KSPLIT) * 16 + 4 * g;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        sm[j][r] = (j < nvb && kj + r <= my_pos) ? st[j][r] : -INFINITY;
+                        bmax = fmaxf(bmax, sm[j][r]);
+                    }
+                }
+                bmax = max_over_rows(bmax);
+                const float m_new = fmaxf(m, bmax);
+                const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - m_new);
+#pragma unroll
+                for (int j = 0; j < NBW; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        p[j][r] = sm[j][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sm[j][r] - m_new);
+                lsum *= alpha;
+#pragma unroll
+                for (int n = 0; n < NB; n++) acc[n] *= alpha;
+                m = m_new;
+            }
+#pragma unroll
+            for (int j = 0; j < NBW; j++) lsum += (p[j][0] + p[j][1]) + (p[j][2] + p[j][3]);
+            // O^T += V^T P^T over block pairs (2jj, 2jj+1); a pair whose first
+            // block no query of the wave sees is skipped (its p are 0)
+#pragma unroll
+            for (int jj = 0; jj < NBW / 2; jj++) {
+                if (2 * jj < nvb) {  // wave-uniform
+                    const float pv[8] = {p[2 * jj][0],     p[2 * jj][1],     p[2 * jj][2],     p[2 * jj][3],
+                                         p[2 * jj + 1][0], p[2 * jj + 1][1], p[2 * jj + 1][2], p[2 * jj + 1][3]};
+                    bf16x8 ph, pm, pl;
+                    split3(pv, ph, pm, pl);
+                    const int key_a = (kg + 2 * jj * KSPLIT) * 16 + 4 * g;        // within the tile
+                    const int key_b = (kg + (2 * jj + 1) * KSPLIT) * 16 + 4 * g;
+#pragma unroll
+                    for (int n = 0; n < NB; n++) {
+                        const uint16_t* vr = &v_lds[(16 * n + ql) * VST];
+                        bf16x8 vp[3];
+#pragma unroll
+                        for (int q = 0; q < 3; q++) {
+                            const uint2 x0 = *reinterpret_cast<const uint2*>(vr + q * VPLANE + key_a);
+                            const uint2 x1 = *reinterpret_cast<const uint2*>(vr + q * VPLANE + key_b);
+                            u32x4 t;
+                            t[0] = x0.x, t[1] = x0.y, t[2] = x1.x, t[3] = x1.y;
+                            vp[q] = __builtin_bit_cast(bf16x8, t);
+                        }
+                        f32x4 o = acc[n];
+                        o = mfma(vp[2], ph, o);
+                        o = mfma(vp[1], pm, o);
+                        o = mfma(vp[0], pl, o);
+                        o = mfma(vp[1], ph, o);
+                        o = mfma(vp[0], pm, o);
+                        o = mfma(vp[0], ph, o);
+                        acc[n] = o;
+                    }
+                }
+            }
+        }
+    }
+
+    lsum = sum_over_rows(lsum);
+    if constexpr (KSPLIT > 1) {
+        __syncthreads();  // every wave is done with the K/V tiles
+        float* part = reinterpret_cast<float*>(k_lds);  // [(KSPLIT-1) x QT sub-tiles][16 queries][HD]
+        if (kg > 0) {
+            const int slot = (kg - 1) * QT + qs;
+            float* o = part + (size_t)slot * 16 * HD + ql * HD;
+#pragma unroll
+            for (int n = 0; n < NB; n++)
+                *reinterpret_cast<float4*>(o + 16 * n + 4 * g) =
+                    make_float4(acc[n][0], acc[n][1], acc[n][2], acc[n][3]);
+            if (g == 0) {
+                s_ml[(slot * 16 + ql) * 2 + 0] = m;
+                s_ml[(slot * 16 + ql) * 2 + 1] = lsum;
+            }
+        }
+        __syncthreads();
+        if (kg > 0) return;
+#pragma unroll
+        for (int k = 1; k < KSPLIT; k++) {
+            const int slot = (k - 1) * QT + qs;
+            const float mo = s_ml[(slot * 16 + ql) * 2 + 0];
+            const float lo = s_ml[(slot * 16 + ql) * 2 + 1];
+            const float mm = fmaxf(m, mo);
+            const float f = scale_of(m, mm), fo = scale_of(mo, mm);
+            lsum = lsum * f + lo * fo;
+            const float* o = part + (size_t)slot * 16 * HD + ql * HD;
+#pragma unroll
+            for (int n = 0; n < NB; n++) {
+                const float4 t = *reinterpret_cast<const float4*>(o + 16 * n + 4 * g);
+                acc[n] = acc[n] * f + f32x4{t.x, t.y, t.z, t.w} * fo;
+            }
+            m = mm;
+        }
+    }
+    if (row < qcount) {
+        const float inv = 1.0f / lsum;
+        float* op = a.out + qrow * dim + (size_t)h * HD;
+#pragma unroll
+        for (int n = 0; n < NB; n++)
+            *reinterpret_cast<float4*>(op + 16 * n + 4 * g) =
+                make_float4(acc[n][0] * inv, acc[n][1] * inv, acc[n][2] * inv, acc[n][3] * inv);
+    }
+}
+
 }  // namespace
 
 int prefill_block_m(int) { return BM; }
 
 hipError_t launch_paged_attn_prefill(const PrefillLaunch& a, hipStream_t stream) {
     const dim3 grid((unsigned)((size_t)a.work_items * a.n_heads));
-    if (!a.use_valu) {
+    if (a.kernel == PREFILL_KERNEL_DEFAULT) {
+        switch (a.head_dim) {
+            case 32: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<32, 2, 64>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 64: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<64, 2, 64>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 128: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<128, 1, 32>), grid, dim3(256), 0, stream, a); return hipGetLastError();
+            default: break;  // hd 256: VALU kernel
+        }
+    }
+    if (a.kernel == PREFILL_KERNEL_MFMA_F32) {
         // 4 query sub-tiles x 2 key groups per workgroup, one workgroup per
         // work item.  (Splitting an item over two workgroups of 2 x 4 balances
         // the schedule better but doubles the K/V each item stages: measured

@@ -49,6 +49,7 @@
 #include <algorithm>
 #include <cstdlib>
 
+#include "bf16_split.hpp"
 #include "device_pool.hpp"
 
 namespace nitro {
@@ -806,17 +807,6 @@ __global__ __launch_bounds__(512) void q8_rowdot_kernel(Q8Group grp, const float
 constexpr int MMA_WAVES = 16;
 constexpr int MMA_TILE_STRIDE = 20;  // floats per batch row of a staged tile (stores hit 64 distinct banks)
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Elements (a, b) as a bf16 pair: the upper 16 bits of each (a truncation,
-// exact where a and b have at most 8 significant bits).
-__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
-    // bytes 2, 3 of a then bytes 2, 3 of b (v_perm_b32: bytes 0-3 are the
-    // second operand, 4-7 the first)
-    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
-}
-
 __device__ __forceinline__ float q8_value(uint32_t w, int j) { return (float)(int)(int8_t)(w >> (8 * j)); }
 
 // Eight int8 weights (two words, k order) as bf16.
@@ -827,26 +817,6 @@ __device__ __forceinline__ bf16x8 q8_bf16(uint32_t w0, uint32_t w1) {
     r[2] = bf16_pair(q8_value(w1, 0), q8_value(w1, 1));
     r[3] = bf16_pair(q8_value(w1, 2), q8_value(w1, 3));
     return __builtin_bit_cast(bf16x8, r);
-}
-
-__device__ __forceinline__ float upper16(float v) { return __uint_as_float(__float_as_uint(v) & 0xffff0000u); }
-
-// v = hi + mid + lo exactly (v finite and not below 2^-102 in magnitude
-// unless zero: each part keeps 8 significant bits of what is left).
-__device__ __forceinline__ void split3(const float (&v)[8], bf16x8& hi, bf16x8& mid, bf16x8& lo) {
-    u32x4 h, m, l;
-#pragma unroll
-    for (int p = 0; p < 4; p++) {
-        const float a = v[2 * p], b = v[2 * p + 1];
-        const float ar = a - upper16(a), br = b - upper16(b);
-        const float al = ar - upper16(ar), bl = br - upper16(br);
-        h[p] = bf16_pair(a, b);
-        m[p] = bf16_pair(ar, br);
-        l[p] = bf16_pair(al, bl);
-    }
-    hi = __builtin_bit_cast(bf16x8, h);
-    mid = __builtin_bit_cast(bf16x8, m);
-    lo = __builtin_bit_cast(bf16x8, l);
 }
 
 // Blocks per wave per round: two rounds of weights and x stay within the 128

@@ -22,10 +22,11 @@ def gpu():
     torch.cuda.synchronize()
 
 
-@pytest.fixture(params=["mfma", "valu"], autouse=True)
+@pytest.fixture(params=["x3", "mfma32", "valu"], autouse=True)
 def prefill_kernel(request, monkeypatch):
-    """Every prefill test runs on both kernels: MFMA fp32 (default for hd <= 128)
-    and the VALU one (hd 256, or NITRO_PREFILL_KERNEL=valu)."""
+    """Every prefill test runs on the three kernels: bf16 matrix cores with
+    three-part splits (default for hd <= 128), fp32 matrix cores
+    (NITRO_PREFILL_KERNEL=mfma32) and the VALU one (hd 256, or =valu)."""
     monkeypatch.setenv("NITRO_PREFILL_KERNEL", request.param)
     return request.param
 
