@@ -236,9 +236,11 @@ class OracleModel:
         x = rms_norm(x, self.rms_final)
         return f32_matmul(self.emb, x, bulk=bulk)
 
-    def forward_prefill_chunk(self, k_pool, v_pool, table, start_pos, tokens):
+    def forward_prefill_chunk(self, k_pool, v_pool, table, start_pos, tokens, bulk=True):
         """forward_prefill_chunk (src/model_q8.cpp:424-557) after the caller's
-        allocate_next_token for the chunk: logits [vocab] of its last token."""
+        allocate_next_token for the chunk: logits [vocab] of its last token.
+        The reference's products there are matmul_bulk; bulk=False composes the
+        same step from full-row products (matmul, :92-125)."""
         A = self._attn
         tokens = np.asarray(tokens, np.int64)
         positions = (start_pos + np.arange(tokens.size)).astype(np.int32)
@@ -250,6 +252,6 @@ class OracleModel:
             return A.prefill_chunk(k_pool, v_pool, l, q, table, start_pos, self.n_heads,
                                    self.n_kv_heads, self.head_size)
 
-        x = self._layers(x, k_pool, v_pool, True, attend)
+        x = self._layers(x, k_pool, v_pool, bulk, attend)
         last = rms_norm(x[-1:], self.rms_final)
-        return f32_matmul(self.emb, last, bulk=True)[0]
+        return f32_matmul(self.emb, last, bulk=bulk)[0]

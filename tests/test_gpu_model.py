@@ -131,6 +131,58 @@ MODELS = {
 }
 
 
+@pytest.mark.parametrize("name", ["mha_hd64_l3", "gqa_hd128_l2", "gqa_hd32_l2"])
+def test_full_row_products_over_many_rows(name):
+    """Full-row products over more than 4 activation rows take the bf16
+    matrix-core kernel over the tile-layout weights, with rms_norm, RoPE + K/V
+    append, the residual adds and SwiGLU fused into its launches: a 40-token
+    prefill chunk (several launch rows), then decode batches of 6, 20 and 36
+    sequences (one and two batch tiles, several launch rows), against the
+    oracle composed from full-row matmul."""
+    import torch
+
+    import nitrorag_amd as na
+    from nitrorag_amd.model import FULL_ROWS, synthetic_model_file
+    from oracle import model as om
+
+    dim, hid, L, H, Hkv, V, S = MODELS[name]
+    say(f"full rows, many rows: {name}")
+    # wo / w2 scaled up so the products, not the embedding carried along the
+    # residual stream, decide the logits
+    blob = om.scale_residual_outputs(synthetic_model_file(dim, hid, L, H, Hkv, V, S, seed=len(name) + 7), 64.0)
+    model, ora = na.Model(blob), om.OracleModel(blob)
+    pages = 160
+    pool = na.KVPool(pages, L, model.kv_dim)
+    k = np.zeros((pages, L, 16, model.kv_dim), np.float32)
+    v = np.zeros_like(k)
+    bm = na.BlockManager(pages)
+    rng = np.random.default_rng(11)
+    seqs = [na.Sequence(i) for i in range(36)]
+    for i, s in enumerate(seqs):
+        n = 40 if i == 0 else int(rng.integers(1, 20))
+        toks = rng.integers(0, V, n).astype(np.int32)
+        start = s.logical_token_count
+        for t in toks:
+            s.allocate_next_token(int(t), bm)
+        pool.upload_prefill_batch(na.pack_block_tables([s]), [start], [n])
+        got = model.forward_prefill(pool, toks, semantics=FULL_ROWS).cpu().numpy()
+        want = ora.forward_prefill_chunk(k, v, na.pack_block_tables([s])[0], start, toks, bulk=False)[None, :]
+        check_logits(got, want, f"{name} full-row prefill {n}")
+    for nb in (6, 20, 36):
+        batch = seqs[:nb]
+        toks = rng.integers(0, V, nb).astype(np.int32)
+        pos = [s.logical_token_count for s in batch]
+        for s, t in zip(batch, toks):
+            s.allocate_next_token(int(t), bm)
+        tables = na.pack_block_tables(batch)
+        pool.upload_decode_batch(tables, pos)
+        got = model.forward_decode_batch(pool, toks, semantics=FULL_ROWS).cpu().numpy()
+        want = ora.forward_decode_batch(k, v, tables, pos, toks, bulk=False)
+        check_logits(got, want, f"{name} full-row decode batch {nb}")
+    torch.cuda.synchronize()
+    assert pool.take_device_errors() == 0
+
+
 @pytest.mark.parametrize("name", sorted(MODELS))
 def test_forward_vs_oracle_on_synthetic_models(name):
     """A synthetic model file through both: the GPU forward passes against the
