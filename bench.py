@@ -755,6 +755,23 @@ def kernel_name(w) -> str:
     return f"paged_attn_prefill_x3_kernel<{w.hd}> (bf16 matrix cores, three-part splits)"
 
 
+def host_cpu():
+    """The host's CPU model, socket count and logical CPUs (from /proc/cpuinfo)."""
+    model, sockets = None, set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                key, _, val = ln.partition(":")
+                key = key.strip()
+                if key == "model name" and model is None:
+                    model = val.strip()
+                elif key == "physical id":
+                    sockets.add(val.strip())
+    except OSError:
+        pass
+    return {"cpu_model": model, "sockets": len(sockets) or None, "logical_cpus": os.cpu_count()}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -864,6 +881,8 @@ def main():
     line.update(w.extra(kernel_s))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = w.cpu_baseline(args.cpu_seconds, args.cpu_sample)
+        if line["cpu_baseline"]:
+            line["cpu_baseline"]["host"] = host_cpu()
     print(json.dumps(line), flush=True)
 
 
