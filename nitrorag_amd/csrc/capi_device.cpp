@@ -359,19 +359,26 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
         }
         require(total > 0 && total < (1LL << 30), ERR_INVALID_ARGUMENT, "bad total token count");
         const int bm = prefill_block_m(0);
-        // Work items (seq, first query row), longest key range first.
-        std::vector<std::pair<long long, std::pair<int, int>>> items;
-        for (int b = 0; b < batch; b++)
-            for (int q0 = 0; q0 < num_tokens[b]; q0 += bm) {
-                const int last = start_pos[b] + std::min(num_tokens[b], q0 + bm) - 1;
-                items.push_back({-(long long)last, {b, q0}});
-            }
-        std::stable_sort(items.begin(), items.end(),
-                         [](const auto& x, const auto& y) { return x.first < y.first; });
+        // Work items (seq, first query row), longest key range first: one list
+        // of bm-row items and one of PREFILL_WIDE_ROWS-row items (the launch
+        // takes the list its kernel serves).
+        auto work_list = [&](int rows) {
+            std::vector<std::pair<long long, std::pair<int, int>>> items;
+            for (int b = 0; b < batch; b++)
+                for (int q0 = 0; q0 < num_tokens[b]; q0 += rows) {
+                    const int last = start_pos[b] + std::min(num_tokens[b], q0 + rows) - 1;
+                    items.push_back({-(long long)last, {b, q0}});
+                }
+            std::stable_sort(items.begin(), items.end(),
+                             [](const auto& x, const auto& y) { return x.first < y.first; });
+            return items;
+        };
+        const auto items = work_list(bm);
+        const auto wide = work_list(PREFILL_WIDE_ROWS);
 
         const size_t nt = (size_t)batch * max_pages;
-        const size_t n_work = items.size() * 2;
-        const size_t need = nt + 3 * (size_t)batch + 2 * (size_t)total + n_work;
+        const size_t n_work = items.size() * 2, n_wide = wide.size() * 2;
+        const size_t need = nt + 3 * (size_t)batch + 2 * (size_t)total + n_work + n_wide;
         hipStream_t s = as_stream(stream);
         Staging& st = pool->prefill_staging;
         int32_t* h = st.acquire(need);
@@ -382,6 +389,7 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
         int32_t* h_slots = h_off + batch;
         int32_t* h_row_pos = h_slots + total;
         int32_t* h_work = h_row_pos + total;
+        int32_t* h_wide = h_work + n_work;
         std::memcpy(h_tables, tables, nt * sizeof(int32_t));
         std::memcpy(h_start, start_pos, batch * sizeof(int32_t));
         std::memcpy(h_len, num_tokens, batch * sizeof(int32_t));
@@ -396,6 +404,10 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
             h_work[2 * i] = items[i].second.first;
             h_work[2 * i + 1] = items[i].second.second;
         }
+        for (size_t i = 0; i < wide.size(); i++) {
+            h_wide[2 * i] = wide[i].second.first;
+            h_wide[2 * i + 1] = wide[i].second.second;
+        }
         p.tables.reserve(nt);
         p.d_start.reserve(batch);
         p.d_len.reserve(batch);
@@ -403,6 +415,7 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
         p.slots.reserve(total);
         p.row_pos.reserve(total);
         p.work.reserve(n_work);
+        p.work_wide.reserve(n_wide);
         st.copy(p.tables.ptr, h_tables, nt, s);
         st.copy(p.d_start.ptr, h_start, batch, s);
         st.copy(p.d_len.ptr, h_len, batch, s);
@@ -410,6 +423,7 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
         st.copy(p.slots.ptr, h_slots, total, s);
         st.copy(p.row_pos.ptr, h_row_pos, total, s);
         st.copy(p.work.ptr, h_work, n_work, s);
+        st.copy(p.work_wide.ptr, h_wide, n_wide, s);
         st.finish(s);
         p.start_pos.assign(start_pos, start_pos + batch);
         p.num_tokens.assign(num_tokens, num_tokens + batch);
@@ -422,6 +436,7 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
         p.max_pos = max_pos;
         p.work_items = (int32_t)items.size();
         p.work_block_m = bm;
+        p.work_items_wide = (int32_t)wide.size();
         p.max_pages = max_pages;
         p.batch = batch;
         pool->last_stream = s;
@@ -481,6 +496,12 @@ int nitro_paged_attn_prefill(nitro_kvpool* pool, int32_t layer, const float* q, 
                    : std::strcmp(kern, "valu") == 0     ? PREFILL_KERNEL_VALU
                    : std::strcmp(kern, "mfma32") == 0   ? PREFILL_KERNEL_MFMA_F32
                                                         : PREFILL_KERNEL_DEFAULT;
+        a.item_rows = p.work_block_m;
+        if (prefill_uses_wide_items(a.kernel, head_dim)) {
+            a.work = p.work_wide.ptr;
+            a.work_items = p.work_items_wide;
+            a.item_rows = PREFILL_WIDE_ROWS;
+        }
         hipStream_t s = as_stream(stream);
         hip_check(launch_paged_attn_prefill(a, s), "paged_attn_prefill launch");
         pool->last_stream = s;

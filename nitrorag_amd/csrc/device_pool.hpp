@@ -106,6 +106,8 @@ struct PrefillBatch {
     DeviceBuffer<int32_t> work;       // per work item: (seq, first query) pairs
     int32_t work_items = 0;
     int32_t work_block_m = 0;         // query rows per work item the list was built for
+    DeviceBuffer<int32_t> work_wide;  // the same for items of PREFILL_WIDE_ROWS rows
+    int32_t work_items_wide = 0;
     int32_t max_pos = 0;              // largest position of any row
 };
 
@@ -276,8 +278,13 @@ struct PrefillLaunch {
     int64_t page_stride, layer_off;
     int32_t kv_dim, n_heads, kv_mul, head_dim, max_pages, num_pages, work_items;
     float qscale;
-    int32_t kernel;  // PREFILL_KERNEL_*: which form runs where several exist
+    int32_t kernel;     // PREFILL_KERNEL_*: which form runs where several exist
+    int32_t item_rows;  // query rows per work item of `work` (64, or PREFILL_WIDE_ROWS)
 };
+// Query rows per work item of the wide list (the default kernel at hd 128).
+constexpr int32_t PREFILL_WIDE_ROWS = 128;
+// Whether a launch of this kernel / head_dim takes the wide work list.
+bool prefill_uses_wide_items(int32_t kernel, int32_t head_dim);
 constexpr int32_t PREFILL_KERNEL_DEFAULT = 0;   // bf16 matrix cores at fp32 accuracy (hd <= 128)
 constexpr int32_t PREFILL_KERNEL_VALU = 1;      // fp32 VALU FMAs
 constexpr int32_t PREFILL_KERNEL_MFMA_F32 = 2;  // fp32 matrix cores (v_mfma_f32_16x16x4_f32)

@@ -516,14 +516,16 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_mfma_kern
 //    is its own probabilities of the two blocks (keys 4g..4g+3 of each), and
 //    its A operand V^T[d = 16n + l%16] at the same 8 keys, read from a
 //    transposed V tile.
+// A workgroup serves one work item of 16*QT query rows (QT = 8: 128 rows,
+// the wide work list, so each staged tile serves twice the queries) with QT
+// query sub-tiles x KSPLIT key groups of waves.
 // K and V are split once, when a tile is staged: three bf16 planes each in
 // LDS, K as [key][d] and V as [d][key].  K is loaded a float4 of one key row
 // per thread; V one d of four consecutive keys per thread (a wave's lanes
 // cover consecutive d of a row, so the loads coalesce), which becomes one
 // 8-byte store per plane into the transposed tile.
-template <int HD, int KSPLIT, int BNM>
-__global__ __launch_bounds__(256 * KSPLIT) void paged_attn_prefill_x3_kernel(PrefillLaunch a) {
-    constexpr int QT = 4;                      // query sub-tiles (one work item per workgroup)
+template <int HD, int QT, int KSPLIT, int BNM>
+__global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_x3_kernel(PrefillLaunch a) {
     constexpr int NT = 64 * QT * KSPLIT;
     constexpr int KB = BNM / 16;               // 16-key blocks per tile
     constexpr int NBW = KB / KSPLIT;           // 16-key blocks per wave per tile
@@ -536,9 +538,11 @@ __global__ __launch_bounds__(256 * KSPLIT) void paged_attn_prefill_x3_kernel(Pre
     constexpr int LOADS = BNM * F4 / NT;       // K float4 per thread per tile
     constexpr int VSLOTS = BNM * HD / (4 * NT);  // V (d, 4-key group) slots per thread per tile
     static_assert(LOADS >= 1 && BNM * F4 % NT == 0 && VSLOTS >= 1 && BNM * HD % (4 * NT) == 0, "tile shape");
-    static_assert((KSPLIT - 1) * QT * 16 * HD * 4 <= 3 * BNM * KST * 2, "partials fit the K planes");
-    __shared__ __attribute__((aligned(16))) uint16_t k_lds[3 * BNM * KST];
-    __shared__ __attribute__((aligned(16))) uint16_t v_lds[3 * HD * VST];
+    constexpr int KPLANE = BNM * KST, VPLANE = HD * VST;
+    static_assert((KSPLIT - 1) * QT * 16 * HD * 4 <= 3 * (KPLANE + VPLANE) * 2, "partials fit the tile planes");
+    __shared__ __attribute__((aligned(16))) uint16_t kv_lds[3 * (KPLANE + VPLANE)];
+    uint16_t* const k_lds = kv_lds;
+    uint16_t* const v_lds = kv_lds + 3 * KPLANE;
     __shared__ int32_t s_table[TABLE_LDS];
     __shared__ float s_ml[KSPLIT > 1 ? QT * (KSPLIT - 1) * 16 * 2 : 1];
 
@@ -548,7 +552,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void paged_attn_prefill_x3_kernel(Pre
     const int q0 = a.work[2 * item + 1];
     const int kv_h = h / a.kv_mul;
     const int start = a.start_pos[seq];
-    const int qcount = min(BM, a.num_tokens[seq] - q0);
+    const int qcount = min(16 * QT, a.num_tokens[seq] - q0);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int qs = wave % QT;
@@ -621,7 +625,6 @@ __global__ __launch_bounds__(256 * KSPLIT) void paged_attn_prefill_x3_kernel(Pre
                 vreg[i][e] = ok && key0 + e <= last_pos ? vp[(size_t)e * a.kv_dim] : 0.0f;
         }
     };
-    constexpr int KPLANE = BNM * KST, VPLANE = HD * VST;
     auto mfma = [](const bf16x8& x, const bf16x8& y, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, c, 0, 0, 0);
     };
@@ -766,7 +769,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void paged_attn_prefill_x3_kernel(Pre
     lsum = sum_over_rows(lsum);
     if constexpr (KSPLIT > 1) {
         __syncthreads();  // every wave is done with the K/V tiles
-        float* part = reinterpret_cast<float*>(k_lds);  // [(KSPLIT-1) x QT sub-tiles][16 queries][HD]
+        float* part = reinterpret_cast<float*>(kv_lds);  // [(KSPLIT-1) x QT sub-tiles][16 queries][HD]
         if (kg > 0) {
             const int slot = (kg - 1) * QT + qs;
             float* o = part + (size_t)slot * 16 * HD + ql * HD;
@@ -812,13 +815,25 @@ __global__ __launch_bounds__(256 * KSPLIT) void paged_attn_prefill_x3_kernel(Pre
 
 int prefill_block_m(int) { return BM; }
 
+// hd 128 runs one key group per workgroup (its registers), so 128-row items
+// (8 waves, each staged tile serving 128 queries) measured 15-20% faster
+// than 64-row ones.  At hd 64 the 64-row items of two key groups are kept:
+// 128-row items there need 16-wave workgroups, one per CU, and measured 9%
+// slower on the 8-prompt mix (faster on large balanced batches).
+bool prefill_uses_wide_items(int32_t kernel, int32_t head_dim) {
+    return kernel == PREFILL_KERNEL_DEFAULT && head_dim == 128;
+}
+
 hipError_t launch_paged_attn_prefill(const PrefillLaunch& a, hipStream_t stream) {
     const dim3 grid((unsigned)((size_t)a.work_items * a.n_heads));
+    const bool wide = a.item_rows == PREFILL_WIDE_ROWS;
+    if (wide != prefill_uses_wide_items(a.kernel, a.head_dim) || (!wide && a.item_rows != BM))
+        return hipErrorInvalidValue;  // the work list must match the kernel's rows per item
     if (a.kernel == PREFILL_KERNEL_DEFAULT) {
         switch (a.head_dim) {
-            case 32: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<32, 2, 64>), grid, dim3(512), 0, stream, a); return hipGetLastError();
-            case 64: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<64, 2, 64>), grid, dim3(512), 0, stream, a); return hipGetLastError();
-            case 128: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<128, 1, 32>), grid, dim3(256), 0, stream, a); return hipGetLastError();
+            case 32: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<32, 4, 2, 64>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 64: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<64, 4, 2, 64>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 128: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<128, 8, 1, 32>), grid, dim3(512), 0, stream, a); return hipGetLastError();
             default: break;  // hd 256: VALU kernel
         }
     }
