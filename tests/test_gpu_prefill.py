@@ -130,6 +130,10 @@ CASES = {
     "short_chunks_hd32": (3, 6, 1, 70, 4, 4, 32, 1, 0, 0, 40),
     "mha_hd256": (4, 2, 30, 150, 2, 2, 256, 1, 0, 0, 20),
     "single_token_chunks": (5, 5, 1, 1, 4, 4, 64, 1, 0, 0, 100),
+    # keys past the 2048 block-table entries a workgroup keeps in LDS (32k
+    # tokens): the rest of the table is read from global memory
+    "beyond_lds_table_hd64": (6, 2, 5, 40, 2, 2, 64, 1, 0, 33000, 33100),
+    "beyond_lds_table_gqa_hd128": (7, 2, 5, 150, 2, 1, 128, 1, 0, 33000, 33100),
 }
 
 
