@@ -12,16 +12,16 @@
 //    loop stores each block's sum over the previous one, so only the final
 //    32 columns of every row reach the output.
 //
-// Layout on the matrix cores (v_mfma_f32_16x16x4_f32, fp32 in, fp32
-// accumulate): a workgroup owns 16 output rows; out^T[16 rows][16 batch] +=
-// W[16 rows][4 k] . x^T[4 k][16 batch] per instruction.  Per 64-k chunk (two
-// blocks), lane l = (r = l%16, g = l/16) loads the 16 int8 of row r in half
-// g%2 of block 2*chunk + g/2 (one 16-byte run) and that block's scale; MFMA
-// m (0..15) takes the lane's m-th weight, so the k-slot g of instruction m is
-// k = (2*chunk + g/2)*32 + (g%2)*16 + m, and the B operand lane (c, g) holds
-// x[c][that k] (16 contiguous floats per lane).  The four waves take chunks
-// round-robin and add their partial tiles through LDS.  Batches of more than
-// 16 rows reuse the dequantised weights for every 16-row batch tile.
+// Kernels, by activation rows and semantics (the launcher picks):
+//  - 1..4 rows: VALU dot products.  q8_rowdot_kernel streams rows of >= 2048
+//    k (full rows); q8_gemv_kernel covers short rows and the last-block form.
+//  - more rows, full rows: q8_mma_kernel, the bf16 matrix cores at fp32
+//    accuracy (x split into three exact bf16 parts), over the model's
+//    tile-layout copy of the matrix when there is one (Q8Tiled) or the BlockQ8
+//    rows otherwise.
+//  - more rows, last block only (and NITRO_Q8_MMA=f32): q8_matmul_kernel on
+//    v_mfma_f32_16x16x4_f32 (fp32 in, fp32 accumulate).
+// Each kernel's comment gives its lane layout.
 //
 // A launch may cover a group of up to 3 matrices with the same input x and
 // n (wq/wk/wv; w1/w3): a workgroup computes the same 16 rows of each member
@@ -37,13 +37,8 @@
 //    the launch that last changed x), added in a fixed order;
 //  - RESID (wo, w2): the product is added into x in place and, per 16-row
 //    output tile, the squares of each batch row's 16 new entries are summed
-//    into one partial (tile p of row b at ss[p * ss_stride + b]).
-//
-// Batches of 1..4 rows use a VALU form of the same lane layout (q8_gemv):
-// each lane forms the dot products of its 16 weights with x directly, the
-// four lane groups of a row are summed with gfx950's row-swap permutes and
-// the waves through LDS.  Both kernels issue the weight loads of Q8_UNROLL
-// chunks before using any, so enough HBM reads are in flight per wave.
+//    into one partial (tile p of row b at ss[p * ss_stride + b]);
+//  - ROPE (wq/wk/wv): q and k rotated, q to its buffer, k and v to the pools.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -166,6 +161,16 @@ struct Q8Group {
 
 namespace {
 
+// fp32 matrix cores (v_mfma_f32_16x16x4_f32): a workgroup owns 16 output
+// rows; out^T[16 rows][16 batch] += W[16 rows][4 k] . x^T[4 k][16 batch] per
+// instruction.  Per 64-k chunk (two blocks), lane l = (r = l%16, g = l/16)
+// loads the 16 int8 of row r in half g%2 of block 2*chunk + g/2 (one 16-byte
+// run) and that block's scale; MFMA m (0..15) takes the lane's m-th weight, so
+// the k-slot g of instruction m is k = (2*chunk + g/2)*32 + (g%2)*16 + m, and
+// the B operand lane (c, g) holds x[c][that k] (16 contiguous floats per
+// lane).  The four waves take chunks round-robin (U at a time, loads issued
+// before use) and add their partial tiles through LDS.  Batches of more than
+// 16 rows reuse the dequantised weights for every 16-row batch tile.
 template <int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY, bool NORM, bool RESID, bool ROPE>
 __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, const float* __restrict__ x,
                                                                    int batch, int n, Q8Norm nm, Q8Resid resid,
