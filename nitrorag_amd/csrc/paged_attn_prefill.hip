@@ -5,11 +5,17 @@
 // pos = start_pos + t attends keys 0..pos of its sequence (prefix-hit pages,
 // earlier chunks and the chunk's own rows, already scattered into the pool).
 //
-// Two kernels, both fp32 throughout (no reduced-precision inputs):
+// Three kernels, all at fp32 accuracy:
+//  - paged_attn_prefill_x3_kernel (hd 32/64/128, the default): the bf16
+//    matrix cores on exact three-part bf16 splits of Q, K, V and P (its
+//    comment below);
+//  - paged_attn_prefill_mfma_kernel (NITRO_PREFILL_KERNEL=mfma32): the fp32
+//    matrix cores;
+//  - paged_attn_prefill_kernel (hd 256, or NITRO_PREFILL_KERNEL=valu): fp32
+//    VALU FMAs.
 //
-// paged_attn_prefill_mfma_kernel<hd, QT, KSPLIT, BNM> (hd 32/64/128, the
-// default) runs both matrix products on v_mfma_f32_16x16x4_f32 (fp32 inputs,
-// fp32 accumulate):
+// paged_attn_prefill_mfma_kernel<hd, QT, KSPLIT, BNM> runs both matrix
+// products on v_mfma_f32_16x16x4_f32 (fp32 inputs, fp32 accumulate):
 //  - Work item = 64 query rows of one chunk x one head; a workgroup has QT = 4
 //    query sub-tiles of 16 rows x KSPLIT = 2 key groups (8 waves; two
 //    workgroups per CU interleave their phases).  Keys stream in tiles of BNM
