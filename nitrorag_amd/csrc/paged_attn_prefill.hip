@@ -126,23 +126,51 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaun
     const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * HD;
     float4 kreg[LOADS], vreg[LOADS];
 
+    // Fetch: the tile's page ids first, then every K/V load unconditionally
+    // (a key past the context or on a bad page reads page 0 instead), so no
+    // load waits behind another; kmask records which rows are real and the
+    // LDS store zeroes the rest.  At hd 256 (256 VGPRs) each row is looked up
+    // and loaded in turn, under the page check, and fetch zeroes the rest
+    // itself: the other form measured 5-10% slower there.
+    static_assert(LOADS <= 32, "validity mask");
+    uint32_t kmask = 0;
     auto fetch = [&](int tile) {
+        kmask = 0;
+        if constexpr (HD == 256) {
 #pragma unroll
-        for (int i = 0; i < LOADS; i++) {
-            const int f = threadIdx.x + i * THREADS;
-            const int r = f / F4, col = f % F4;
-            const int key = tile * BN + r;
-            kreg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            vreg[i] = kreg[i];
-            if (key <= last_pos) {
-                const int page = trow[key >> 4];
-                if ((unsigned)page < (unsigned)a.num_pages) {
-                    const size_t off = (size_t)page * a.page_stride + (size_t)(key & 15) * a.kv_dim;
-                    kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
-                    vreg[i] = reinterpret_cast<const float4*>(vbase + off)[col];
-                } else if (col == 0) {
-                    atomicAdd(a.bad_pages, 1);
+            for (int i = 0; i < LOADS; i++) {
+                const int f = threadIdx.x + i * THREADS;
+                const int r = f / F4, col = f % F4;
+                const int key = tile * BN + r;
+                kreg[i] = vreg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (key <= last_pos) {
+                    const int page = trow[key >> 4];
+                    if ((unsigned)page < (unsigned)a.num_pages) {
+                        const size_t off = (size_t)page * a.page_stride + (size_t)(key & 15) * a.kv_dim;
+                        kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
+                        vreg[i] = reinterpret_cast<const float4*>(vbase + off)[col];
+                    } else if (col == 0) {
+                        atomicAdd(a.bad_pages, 1);
+                    }
                 }
+            }
+        } else {
+            int page[LOADS];
+#pragma unroll
+            for (int i = 0; i < LOADS; i++)
+                page[i] = trow[min(tile * BN + (int)(threadIdx.x + i * THREADS) / F4, last_pos) >> 4];
+#pragma unroll
+            for (int i = 0; i < LOADS; i++) {
+                const int f = threadIdx.x + i * THREADS;
+                const int r = f / F4, col = f % F4;
+                const int key = tile * BN + r;
+                const bool in = key <= last_pos;
+                const bool ok = in && (unsigned)page[i] < (unsigned)a.num_pages;
+                if (in && !ok && col == 0) atomicAdd(a.bad_pages, 1);
+                kmask |= (uint32_t)ok << i;
+                const size_t off = ok ? (size_t)page[i] * a.page_stride + (size_t)(key & 15) * a.kv_dim : 0;
+                kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
+                vreg[i] = reinterpret_cast<const float4*>(vbase + off)[col];
             }
         }
     };
@@ -153,8 +181,9 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaun
 #pragma unroll
         for (int i = 0; i < LOADS; i++) {
             const int f = threadIdx.x + i * THREADS;
-            ks[f / F4][f % F4] = kreg[i];
-            vs[f / F4][f % F4] = vreg[i];
+            const bool ok = HD == 256 || ((kmask >> i) & 1);  // hd 256: fetch zeroed the rest
+            ks[f / F4][f % F4] = ok ? kreg[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            vs[f / F4][f % F4] = ok ? vreg[i] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
         __syncthreads();
         if (tile + 1 < n_tiles) fetch(tile + 1);
@@ -325,26 +354,43 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_mfma_kern
     const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * HD;
     float4 kreg[LOADS], vreg[LOADS];
 
-    auto fetch = [&](int tile) {
+    // Fetch: a tile's page ids are all looked up first, then every K/V load
+    // is issued unconditionally (a key past the context or on a bad page reads
+    // page 0 instead), so no load waits behind another; kmask records which
+    // rows are real and the LDS store zeroes the rest.  The ids come from the
+    // LDS copy of the table when all of the work item's pages are in it
+    // (block-uniform); otherwise pages past the copy are read from memory.
+    static_assert(LOADS <= 32, "validity mask");
+    const bool table_in_lds = (last_pos >> 4) < TABLE_LDS;
+    uint32_t kmask = 0;
+    auto fetch_with = [&](int tile, auto page_of) {
+        int page[LOADS];
+#pragma unroll
+        for (int i = 0; i < LOADS; i++)
+            page[i] = page_of(min(tile * BNM + (int)(threadIdx.x + i * NT) / F4, last_pos));
+        kmask = 0;
 #pragma unroll
         for (int i = 0; i < LOADS; i++) {
             const int f = threadIdx.x + i * NT;
             const int r = f / F4, col = f % F4;
             const int key = tile * BNM + r;
-            kreg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            vreg[i] = kreg[i];
-            if (key <= last_pos) {
-                const int pi = key >> 4;
-                const int page = pi < TABLE_LDS ? s_table[pi] : trow[pi];
-                if ((unsigned)page < (unsigned)a.num_pages) {
-                    const size_t off = (size_t)page * a.page_stride + (size_t)(key & 15) * a.kv_dim;
-                    kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
-                    vreg[i] = reinterpret_cast<const float4*>(vbase + off)[col];
-                } else if (col == 0) {
-                    atomicAdd(a.bad_pages, 1);
-                }
-            }
+            const bool in = key <= last_pos;
+            const bool ok = in && (unsigned)page[i] < (unsigned)a.num_pages;
+            if (in && !ok && col == 0) atomicAdd(a.bad_pages, 1);
+            kmask |= (uint32_t)ok << i;
+            const size_t off = ok ? (size_t)page[i] * a.page_stride + (size_t)(key & 15) * a.kv_dim : 0;
+            kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
+            vreg[i] = reinterpret_cast<const float4*>(vbase + off)[col];
         }
+    };
+    auto fetch = [&](int tile) {
+        if (table_in_lds)
+            fetch_with(tile, [&](int key) { return s_table[key >> 4]; });
+        else
+            fetch_with(tile, [&](int key) {
+                const int pi = key >> 4;
+                return pi < TABLE_LDS ? s_table[pi] : trow[pi];
+            });
     };
 
     fetch(0);
@@ -354,8 +400,9 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_mfma_kern
         for (int i = 0; i < LOADS; i++) {
             const int f = threadIdx.x + i * NT;
             const int r = f / F4, col = f % F4;
-            *reinterpret_cast<float4*>(&ks[r * STRIDE + col * 4]) = kreg[i];
-            *reinterpret_cast<float4*>(&vs[r * STRIDE + col * 4]) = vreg[i];
+            const bool ok = (kmask >> i) & 1;
+            *reinterpret_cast<float4*>(&ks[r * STRIDE + col * 4]) = ok ? kreg[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<float4*>(&vs[r * STRIDE + col * 4]) = ok ? vreg[i] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
         __syncthreads();
         if (tile + 1 < n_tiles) fetch(tile + 1);
@@ -598,38 +645,57 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_x3_kernel
     const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * HD;
     float4 kreg[LOADS];
     float vreg[VSLOTS][4];
-    auto page_of = [&](int key) {
-        const int pi = key >> 4;
-        return pi < TABLE_LDS ? s_table[pi] : trow[pi];
-    };
-    auto fetch = [&](int tile) {
+    // Fetch: a tile's page ids are all looked up first, then every K/V load
+    // is issued unconditionally (a key past the context or on a bad page reads
+    // page 0 instead), so no load waits behind another; kmask/vmask record
+    // which values are real and staging zeroes the rest.  The ids come from
+    // the LDS copy of the table when all of the work item's pages are in it
+    // (block-uniform); otherwise pages past the copy are read from memory.
+    static_assert(LOADS <= 32 && 4 * VSLOTS <= 32, "validity masks");
+    const bool table_in_lds = (last_pos >> 4) < TABLE_LDS;
+    uint32_t kmask = 0, vmask = 0;
+    auto fetch_with = [&](int tile, auto page_of) {
+        int kpage[LOADS], vpage[VSLOTS];
+#pragma unroll
+        for (int i = 0; i < LOADS; i++)
+            kpage[i] = page_of(min(tile * BNM + (int)(threadIdx.x + i * NT) / F4, last_pos));
+#pragma unroll
+        for (int i = 0; i < VSLOTS; i++)
+            vpage[i] = page_of(min(tile * BNM + 4 * ((int)(threadIdx.x + i * NT) / HD), last_pos));
+        kmask = vmask = 0;
 #pragma unroll
         for (int i = 0; i < LOADS; i++) {
             const int f = threadIdx.x + i * NT;
             const int r = f / F4, col = f % F4;
             const int key = tile * BNM + r;
-            kreg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (key <= last_pos) {
-                const int page = page_of(key);
-                if ((unsigned)page < (unsigned)a.num_pages) {
-                    const size_t off = (size_t)page * a.page_stride + (size_t)(key & 15) * a.kv_dim;
-                    kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
-                } else if (col == 0) {
-                    atomicAdd(a.bad_pages, 1);  // once per key (V reads the same page)
-                }
-            }
+            const bool in = key <= last_pos;
+            const bool ok = in && (unsigned)kpage[i] < (unsigned)a.num_pages;
+            if (in && !ok && col == 0) atomicAdd(a.bad_pages, 1);  // once per key (V reads the same page)
+            kmask |= (uint32_t)ok << i;
+            const size_t off = ok ? (size_t)kpage[i] * a.page_stride + (size_t)(key & 15) * a.kv_dim : 0;
+            kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
         }
 #pragma unroll
         for (int i = 0; i < VSLOTS; i++) {
             const int sl = threadIdx.x + i * NT;
             const int d = sl % HD, key0 = tile * BNM + 4 * (sl / HD);  // 4 keys, one page
-            const int page = key0 <= last_pos ? page_of(key0) : -1;
-            const bool ok = (unsigned)page < (unsigned)a.num_pages;
-            const float* vp = vbase + (ok ? (size_t)page * a.page_stride : 0) + (size_t)(key0 & 15) * a.kv_dim + d;
+            const bool ok = key0 <= last_pos && (unsigned)vpage[i] < (unsigned)a.num_pages;
+            const float* vp = vbase + (ok ? (size_t)vpage[i] * a.page_stride : 0) + (size_t)(key0 & 15) * a.kv_dim + d;
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                vreg[i][e] = ok && key0 + e <= last_pos ? vp[(size_t)e * a.kv_dim] : 0.0f;
+            for (int e = 0; e < 4; e++) {
+                vreg[i][e] = vp[(size_t)e * a.kv_dim];
+                vmask |= (uint32_t)(ok && key0 + e <= last_pos) << (4 * i + e);
+            }
         }
+    };
+    auto fetch = [&](int tile) {
+        if (table_in_lds)
+            fetch_with(tile, [&](int key) { return s_table[key >> 4]; });
+        else
+            fetch_with(tile, [&](int key) {
+                const int pi = key >> 4;
+                return pi < TABLE_LDS ? s_table[pi] : trow[pi];
+            });
     };
     auto mfma = [](const bf16x8& x, const bf16x8& y, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, c, 0, 0, 0);
@@ -652,13 +718,18 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_x3_kernel
         for (int i = 0; i < LOADS; i++) {
             const int f = threadIdx.x + i * NT;
             const int r = f / F4, col = f % F4;
-            const float kv4[4] = {kreg[i].x, kreg[i].y, kreg[i].z, kreg[i].w};
+            const bool ok = (kmask >> i) & 1;
+            const float kv4[4] = {ok ? kreg[i].x : 0.f, ok ? kreg[i].y : 0.f, ok ? kreg[i].z : 0.f,
+                                  ok ? kreg[i].w : 0.f};
             stage4(&k_lds[r * KST + col * 4], KPLANE, kv4);
         }
 #pragma unroll
         for (int i = 0; i < VSLOTS; i++) {
             const int sl = threadIdx.x + i * NT;
-            stage4(&v_lds[(sl % HD) * VST + 4 * (sl / HD)], VPLANE, vreg[i]);
+            float v4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) v4[e] = (vmask >> (4 * i + e)) & 1 ? vreg[i][e] : 0.f;
+            stage4(&v_lds[(sl % HD) * VST + 4 * (sl / HD)], VPLANE, v4);
         }
         __syncthreads();
         if (tile + 1 < n_tiles) fetch(tile + 1);
