@@ -119,6 +119,22 @@ __device__ __forceinline__ float partial_sum(const Q8Norm& nm, int b, int first,
     return s;
 }
 
+// partial_sum with no branch around its loads: an index past the end rereads
+// the last partial and adds 0 (same order of adds), so all L loads of a round
+// go out together, behind any loads issued before.
+template <int L>
+__device__ __forceinline__ float partial_sum_unbranched(const Q8Norm& nm, int b, int first, int step) {
+    float s = 0.0f;
+    for (int p0 = first; p0 < nm.nparts; p0 += L * step) {
+        float v[L];
+#pragma unroll
+        for (int i = 0; i < L; i++) v[i] = nm.ss[(size_t)min(p0 + i * step, nm.nparts - 1) * nm.ss_stride + b];
+#pragma unroll
+        for (int i = 0; i < L; i++) s += p0 + i * step < nm.nparts ? v[i] : 0.0f;
+    }
+    return s;
+}
+
 __device__ __forceinline__ float inv_rms(float ss, int n) { return 1.0f / sqrtf(ss / (float)n + 1e-5f); }
 
 // Where batch row b's K/V goes and the position it rotates with.
@@ -858,7 +874,7 @@ __global__ __launch_bounds__(64 * MMA_WAVES) void q8_mma_kernel(Q8Group grp, con
     const int nb = n / Q8_BLOCK;
     // Lanes past the batch read the last batch row and rows past a member's
     // end read its last row (finite values, never stored); blocks past the
-    // row read the last block with scale 0.
+    // row read the last block, and compute gives them scale 0.
     // (32-bit offsets from the uniform bases: the launcher keeps each matrix
     // and x under 2^32 bytes).  Block blk of this lane: its 8 weights at
     // qoff + blk * BSTEP, its row's scale at soff + blk * BSTEP.
@@ -900,8 +916,7 @@ __global__ __launch_bounds__(64 * MMA_WAVES) void q8_mma_kernel(Q8Group grp, con
                 const uint2 q = *reinterpret_cast<const uint2*>(wbase[m] + (qoff[m] + (uint32_t)blk * BSTEP));
                 R.q[u][m][0] = q.x;
                 R.q[u][m][1] = q.y;
-                const float sc = *reinterpret_cast<const float*>(wbase[m] + (soff[m] + (uint32_t)blk * BSTEP));
-                R.scale[u][m] = valid ? sc : 0.0f;
+                R.scale[u][m] = *reinterpret_cast<const float*>(wbase[m] + (soff[m] + (uint32_t)blk * BSTEP));
             }
 #pragma unroll
             for (int t = 0; t < BT; t++) {
@@ -940,10 +955,15 @@ __global__ __launch_bounds__(64 * MMA_WAVES) void q8_mma_kernel(Q8Group grp, con
                 for (int m = 0; m < NMAT; m++) sm[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, wb[m], sm[m], 0, 0, 0);
 #pragma unroll
                 for (int m = 0; m < NMAT; m++) sm[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wb[m], sm[m], 0, 0, 0);
+                // a block past the row (a repeat of the last one) counts 0;
+                // tested here, not at the load, so nothing waits on the loads
+                // of the round in flight
 #pragma unroll
-                for (int m = 0; m < NMAT; m++)
+                for (int m = 0; m < NMAT; m++) {
+                    const float sc = base + u < nb ? R.scale[u][m] : 0.0f;
 #pragma unroll
-                    for (int j = 0; j < 4; j++) acc[m][t][j] = fmaf(R.scale[u][m], sm[m][j], acc[m][t][j]);
+                    for (int j = 0; j < 4; j++) acc[m][t][j] = fmaf(sc, sm[m][j], acc[m][t][j]);
+                }
             }
         }
     };
@@ -955,9 +975,25 @@ __global__ __launch_bounds__(64 * MMA_WAVES) void q8_mma_kernel(Q8Group grp, con
     if constexpr (NORM) {
         // thread (row j = tid % 64, class c = tid / 64) adds partials c, c + 16, ...;
         // row j's class sums are then added in class order: norm_s[j] = inv_rms
+        // The rms weights' loads and the partials' loads go out together
+        // (only wave-uniform branches around them), then the stores.  Lanes
+        // past the workgroup's batch rows reread a real row's partials (same
+        // addresses as a lane that needs them) and store 0.
         const int j = threadIdx.x & 63, c = threadIdx.x >> 6;
-        norm_s[c * 64 + j] = j < 16 * BT && b0 + j < batch ? partial_sum(nm, b0 + j, c, MMA_WAVES) : 0.0f;
-        for (int k = threadIdx.x; k < n; k += 64 * MMA_WAVES) norm_w[k] = nm.weight[k];
+        constexpr int NW = MMA_NORM_MAX_N / (64 * MMA_WAVES);
+        const int nw = (n + 64 * MMA_WAVES - 1) / (64 * MMA_WAVES);  // uniform
+        float wv[NW];
+#pragma unroll
+        for (int i = 0; i < NW; i++)
+            if (i < nw) wv[i] = nm.weight[min((int)threadIdx.x + i * 64 * MMA_WAVES, n - 1)];
+        const int prow = min(b0 + min(j, 16 * BT - 1), batch - 1);
+        // 4 loads per class cover up to 64 partials (rows of 1024): fewer wasted loads
+        const float ps = nm.nparts <= 4 * MMA_WAVES ? partial_sum_unbranched<4>(nm, prow, c, MMA_WAVES)
+                                                    : partial_sum_unbranched<16>(nm, prow, c, MMA_WAVES);
+        norm_s[c * 64 + j] = j < 16 * BT && b0 + j < batch ? ps : 0.0f;
+#pragma unroll
+        for (int i = 0; i < NW; i++)
+            if (i < nw) norm_w[threadIdx.x + i * 64 * MMA_WAVES] = wv[i];
         __syncthreads();
         float ss = 0.0f;
 #pragma unroll
