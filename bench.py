@@ -346,7 +346,9 @@ class Q8Workload:
 
     def kernel(self):
         if self.B <= 4:
-            return "q8_rowdot_kernel (VALU)" if self.n >= 2048 else "q8_gemv_kernel (VALU)"
+            if self.n < 2048:
+                return "q8_gemv_kernel (VALU)"
+            return "q8_flat_kernel (VALU, x in LDS)" if self.B * self.n <= 16384 else "q8_rowdot_kernel (VALU)"
         return "q8_mma_kernel (bf16 matrix cores, x split in three exact parts)"
 
     def config(self):

@@ -97,6 +97,9 @@ __device__ __forceinline__ float sum_over_rows(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Weight j (0..3) of a word of int8 weights, as a float.
+__device__ __forceinline__ float q8_value(uint32_t w, int j) { return (float)(int)(int8_t)(w >> (8 * j)); }
+
 __device__ __forceinline__ float dequant(uint32_t q4, int j, float scale) {
     return (float)(int)(int8_t)(q4 >> (8 * j)) * scale;
 }
@@ -802,6 +805,210 @@ __global__ __launch_bounds__(512) void q8_rowdot_kernel(Q8Group grp, const float
     }
 }
 
+// The slice of block blk (in range) with no test on the loaded values: a
+// select on them would make the wave wait for these loads where they are
+// issued.  Lanes past the row are masked through their activations.
+__device__ __forceinline__ Q8Slice load_slice_raw(const uint8_t* wrow, int blk, int half) {
+    const uint8_t* bp = wrow + (size_t)blk * Q8_BLOCK_BYTES;
+    const uint32_t* qp = reinterpret_cast<const uint32_t*>(bp + 4 + 16 * half);
+    return Q8Slice{{qp[0], qp[1], qp[2], qp[3]}, *reinterpret_cast<const float*>(bp)};
+}
+
+// Batches of 1..NB rows over long rows (n >= 2048) whose activations fit LDS
+// (NB * n <= FLAT_X_MAX floats).  x, rms-normalised when NORM, is staged in
+// LDS once per workgroup, so a wave's only loads from memory in its loop are
+// weights: x reads wait on the LDS counter, and the next item's weights stay
+// in flight while the current item is used.  Persistent workgroups own
+// balanced ranges of row units (16 rows with the residual epilogue, whose
+// sums of squares are per 16-row tile; 2 rows otherwise, so RoPE pairs stay
+// together).  Items are (group of FLAT_R rows, 1024-k chunk); the
+// workgroup's items are split between its waves in contiguous runs.  Lane l
+// reads half l%2 of block 32*chunk + l/2 of each row (1152 contiguous bytes
+// per row and load instruction).  A block's products are summed, then scaled
+// (sum_k q*x times the block's scale).  At a group's last chunk, or the end
+// of the wave's run, the 64 lanes of each row are summed with a fixed
+// butterfly into the wave's slot in LDS; the epilogue adds the slots in wave
+// order, so results do not depend on timing.
+constexpr int FLAT_WAVES = 8;
+constexpr int FLAT_R = 2;              // rows per item
+constexpr int FLAT_X_MAX = 16384;      // NB * n floats of staged activations (64 KiB)
+constexpr int FLAT_LDS_MAX = 80 * 1024;
+
+template <bool RESID>
+constexpr int flat_unit_rows() {
+    return RESID ? 16 : 2;
+}
+
+template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
+__global__ __launch_bounds__(64 * FLAT_WAVES) void q8_flat_kernel(Q8Group grp, const float* __restrict__ x, int n,
+                                                                 int dmax, Q8Norm nm, Q8Resid resid, Q8Rope rope) {
+    constexpr int W = FLAT_WAVES, NT = 64 * W, R = FLAT_R;
+    constexpr int UG = flat_unit_rows<RESID>();
+    constexpr int XV = FLAT_X_MAX / 4 / NT;  // float4 of x per thread at most
+    extern __shared__ float flat_lds[];
+    __shared__ float inv_s[NB];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nb = n / Q8_BLOCK;
+    const int nch = (nb + 31) / 32;
+    const int units = (dmax + UG - 1) / UG;
+    const int u0 = (int)((long long)units * blockIdx.x / gridDim.x);
+    const int u1 = (int)((long long)units * (blockIdx.x + 1) / gridDim.x);
+    const int row0 = u0 * UG, rows = (u1 - u0) * UG;  // rows past dmax are computed, never stored
+    const int items = rows / R * nch;
+    const int i0 = items * wave / W, i1 = items * (wave + 1) / W;
+    float* xs = flat_lds;          // [NB][n]
+    float* red = flat_lds + NB * n;  // [rows][NMAT][NB][W]
+    const size_t rowbytes = (size_t)nb * Q8_BLOCK_BYTES;
+
+    // item i of the run -> local group g and chunk c (i clamped into the run,
+    // so a wave with no items still loads in-range weights, never used)
+    auto load_item = [&](Q8Slice (&sl)[NMAT][R], int i) {
+        i = max(min(i, i1 - 1), 0);
+        const int g = i / nch, c = i - g * nch;
+        const int blk = 32 * c + (lane >> 1);
+        const int bk = blk < nb ? blk : 0;  // a lane past the row reads block 0; its x are 0
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int row = min(row0 + g * R + r, grp.d[m] - 1);
+                sl[m][r] = load_slice_raw(grp.w[m] + (size_t)row * rowbytes, bk, lane & 1);
+            }
+    };
+    Q8Slice sa[NMAT][R], sb[NMAT][R];
+    load_item(sa, i0);  // in flight while x is staged
+    if constexpr (NORM) {
+        // wave b < NB adds row b's partials (lane i takes i, i + 64, ...)
+        if (wave < NB) {
+            float v = partial_sum(nm, wave, lane, 64);
+#pragma unroll
+            for (int msk = 32; msk > 0; msk >>= 1) v += __shfl_xor(v, msk);
+            if (lane == 0) inv_s[wave] = inv_rms(v, n);
+        }
+        __syncthreads();
+    }
+    {
+        // x -> LDS: every load of this thread first (only uniform branches
+        // between them), then the stores; a float4 index past the end is
+        // clamped to the last one, whose value its threads store again
+        const int total = NB * n / 4, nv = (total + NT - 1) / NT;  // uniform
+        float4 xr[XV], wr[XV];
+#pragma unroll
+        for (int v = 0; v < XV; v++)
+            if (v < nv) {
+                const int t = min((int)threadIdx.x + v * NT, total - 1);
+                xr[v] = reinterpret_cast<const float4*>(x)[t];
+                if constexpr (NORM) wr[v] = reinterpret_cast<const float4*>(nm.weight)[t % (n / 4)];
+            }
+#pragma unroll
+        for (int v = 0; v < XV; v++)
+            if (v < nv) {
+                const int t = min((int)threadIdx.x + v * NT, total - 1);
+                float4 o = xr[v];
+                if constexpr (NORM) {
+                    const float inv = inv_s[t / (n / 4)];
+                    o = make_float4(wr[v].x * (inv * o.x), wr[v].y * (inv * o.y), wr[v].z * (inv * o.z),
+                                    wr[v].w * (inv * o.w));
+                }
+                reinterpret_cast<float4*>(xs)[t] = o;
+            }
+    }
+    for (int t = threadIdx.x; t < rows * NMAT * NB * W; t += NT) red[t] = 0.0f;
+    __syncthreads();
+
+    float acc[NMAT][R][NB];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int b = 0; b < NB; b++) acc[m][r][b] = 0.0f;
+    // the next item's weights, then this item's products from LDS x
+    auto step = [&](const Q8Slice (&now)[NMAT][R], Q8Slice (&next)[NMAT][R], int i) {
+        load_item(next, i + 1);
+        const int g = i / nch, c = i - g * nch;
+        const int blk = 32 * c + (lane >> 1);
+        const bool valid = blk < nb;
+        const int k0 = (valid ? blk : 0) * Q8_BLOCK + 16 * (lane & 1);
+        float xv[NB][16];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const float4* xp = reinterpret_cast<const float4*>(xs + b * n + k0);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 v = xp[q];
+                xv[b][4 * q] = valid ? v.x : 0.0f;
+                xv[b][4 * q + 1] = valid ? v.y : 0.0f;
+                xv[b][4 * q + 2] = valid ? v.z : 0.0f;
+                xv[b][4 * q + 3] = valid ? v.w : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float wv[16];
+#pragma unroll
+                for (int q = 0; q < 16; q++) wv[q] = q8_value(now[m][r].q[q >> 2], q & 3);
+#pragma unroll
+                for (int b = 0; b < NB; b++) {
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 16; q++) sum = fmaf(wv[q], xv[b][q], sum);
+                    acc[m][r][b] = fmaf(sum, now[m][r].scale, acc[m][r][b]);
+                }
+            }
+        if (c == nch - 1 || i == i1 - 1) {  // the group's last chunk in this run (wave-uniform)
+#pragma unroll
+            for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                for (int r = 0; r < R; r++)
+#pragma unroll
+                    for (int b = 0; b < NB; b++) {
+                        float v = acc[m][r][b];
+#pragma unroll
+                        for (int msk = 32; msk > 0; msk >>= 1) v += __shfl_xor(v, msk);
+                        if (lane == 0) red[(((g * R + r) * NMAT + m) * NB + b) * W + wave] = v;
+                        acc[m][r][b] = 0.0f;
+                    }
+        }
+    };
+    int i = i0;
+    for (; i + 1 < i1; i += 2) {
+        step(sa, sb, i);
+        step(sb, sa, i + 1);
+    }
+    if (i < i1) step(sa, sb, i);
+    __syncthreads();
+
+    // epilogue: thread (b, local row il), rows in order within each batch row
+    // (16 consecutive lanes per 16-row tile for the residual partials)
+    static_assert(!RESID || UG % 16 == 0, "residual partials are per 16 rows");
+    for (int t = threadIdx.x; t < NB * rows; t += NT) {
+        const int b = t / rows, il = t - b * rows;
+        float sum[NMAT], pair[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < W; w++) v += red[((il * NMAT + m) * NB + b) * W + w];
+            sum[m] = v;
+        }
+        if constexpr (ROPE) {
+            // RoPE pairs are local rows (il, il ^ 1)
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < W; w++) v += red[(((il ^ 1) * NMAT + m) * NB + b) * W + w];
+                pair[m] = v;
+            }
+        }
+        store_row_sums<NMAT, SWIGLU, RESID, ROPE>(grp, resid, rope, b, row0 + il, sum, pair);
+    }
+}
+
 // Batches of more than 4 rows (full-row products) on the bf16 matrix cores
 // at fp32 accuracy.  An int8 weight is exact in bf16, and an fp32 activation
 // is the exact sum of three bf16 numbers: hi = its upper 16 bits, mid = the
@@ -828,7 +1035,6 @@ __global__ __launch_bounds__(512) void q8_rowdot_kernel(Q8Group grp, const float
 constexpr int MMA_WAVES = 16;
 constexpr int MMA_TILE_STRIDE = 20;  // floats per batch row of a staged tile (stores hit 64 distinct banks)
 
-__device__ __forceinline__ float q8_value(uint32_t w, int j) { return (float)(int)(int8_t)(w >> (8 * j)); }
 
 // Eight int8 weights (two words, k order) as bf16.
 __device__ __forceinline__ bf16x8 q8_bf16(uint32_t w0, uint32_t w1) {
@@ -1064,18 +1270,62 @@ bool use_mma() {
 constexpr int ROWDOT_MIN_N = 2048;
 constexpr int ROWDOT_MAX_GROUPS = 1024;
 
-bool use_rowdot() {
-    static const bool on = [] {
+// NITRO_Q8_GEMV (read once): "slab" sends rows of >= 2048 k to the slab
+// kernel, "rowdot" to the row-streaming one; by default they take the flat
+// kernel when their activations fit its LDS, else the row-streaming one.
+int gemv_choice() {
+    static const int c = [] {
         const char* e = getenv("NITRO_Q8_GEMV");
-        return !(e && e[0] == 's');  // "s": the slab kernel (comparison runs)
+        return e && e[0] == 's' ? 0 : e && e[0] == 'r' ? 1 : 2;
     }();
-    return on;
+    return c;
+}
+
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return cus[dev];
+}
+
+// The flat kernel, if its activations and partial sums fit its LDS budget.
+template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
+bool launch_flat(const Q8Group& grp, const float* x, int n, int dmax, const Q8Norm& nm, const Q8Resid& rs,
+                 const Q8Rope& rp, hipStream_t stream) {
+    if ((long long)NB * n > FLAT_X_MAX) return false;
+    const auto kern = q8_flat_kernel<NB, NMAT, SWIGLU, NORM, RESID, ROPE>;
+    // workgroups resident per CU at the largest LDS the launch may take
+    // (once per instantiation; the dynamic LDS limit is raised to that size)
+    static const int per_cu = [kern] {
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            FLAT_LDS_MAX);
+        int blocks = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 64 * FLAT_WAVES, FLAT_LDS_MAX) != hipSuccess)
+            blocks = 1;
+        return std::max(blocks, 1);
+    }();
+    constexpr int UG = flat_unit_rows<RESID>();
+    const int units = (dmax + UG - 1) / UG;
+    const int groups = std::min(units, per_cu * device_cus());
+    const long long rows_max = (long long)(units + groups - 1) / groups * UG;
+    const size_t lds = ((size_t)NB * n + (size_t)rows_max * NMAT * NB * FLAT_WAVES) * sizeof(float);
+    if (lds > (size_t)FLAT_LDS_MAX) return false;
+    hipLaunchKernelGGL(kern, dim3((unsigned)groups), dim3(64 * FLAT_WAVES), lds, stream, grp, x, n, dmax, nm, rs, rp);
+    return true;
 }
 
 template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
 void launch_gemv(const Q8Group& grp, const float* x, int n, int dmax, bool last, const Q8Norm& nm,
                  const Q8Resid& rs, const Q8Rope& rp, hipStream_t stream) {
-    if (!last && n >= ROWDOT_MIN_N && use_rowdot()) {
+    if (!last && n >= ROWDOT_MIN_N && gemv_choice() == 2 &&
+        launch_flat<NB, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, nm, rs, rp, stream))
+        return;
+    if (!last && n >= ROWDOT_MIN_N && gemv_choice() >= 1) {
         constexpr int ROWS = ROWDOT_SETS * 4 * rowdot_rows<NB, NMAT>();
         const int ntiles = (dmax + ROWS - 1) / ROWS;
         const dim3 grid((unsigned)std::min(ntiles, ROWDOT_MAX_GROUPS)), block(512);

@@ -125,8 +125,8 @@ MODELS = {
     "mha_hd64_l3": (256, 512, 3, 4, 4, 1000, 256),
     "gqa_hd128_l2": (512, 1024, 2, 4, 2, 700, 200),
     "gqa_hd32_l2": (128, 256, 2, 4, 1, 300, 300),
-    # rows of >= 2048 k: the row-streaming products with rms_norm, RoPE + K/V
-    # append, SwiGLU and residual epilogues (3 decode rows)
+    # rows of >= 2048 k: the flat products with rms_norm, RoPE + K/V append,
+    # SwiGLU and residual epilogues (3 decode rows)
     "gqa_hd128_wide_l1": (2048, 2304, 1, 16, 4, 500, 128),
 }
 
@@ -179,6 +179,61 @@ def test_full_row_products_over_many_rows(name):
         got = model.forward_decode_batch(pool, toks, semantics=FULL_ROWS).cpu().numpy()
         want = ora.forward_decode_batch(k, v, tables, pos, toks, bulk=False)
         check_logits(got, want, f"{name} full-row decode batch {nb}")
+    torch.cuda.synchronize()
+    assert pool.take_device_errors() == 0
+
+
+@pytest.mark.parametrize("name,dims", [
+    # rows of 2048-2304 k: every product of 1-4 rows takes the flat kernel (x in LDS)
+    ("wide", (2048, 2304, 1, 16, 4, 500, 128)),
+    # rows of 4608 k: 1-3 rows take the flat kernel, 4 rows (4 * 4608 floats of x
+    # exceed its LDS) the row-streaming one
+    ("wider", (4608, 2304, 1, 36, 4, 300, 64)),
+])
+def test_small_batches_over_long_rows(name, dims):
+    """Full-row products of 1-4 activation rows over rows of >= 2048 k, with
+    rms_norm, RoPE + K/V append, the residual adds and SwiGLU fused into their
+    launches: decode batches of 1, 2, 3 and 4 sequences against the oracle
+    composed from full-row matmul."""
+    import torch
+
+    import nitrorag_amd as na
+    from nitrorag_amd.model import FULL_ROWS, synthetic_model_file
+    from oracle import model as om
+
+    dim, hid, L, H, Hkv, V, S = dims
+    say(f"small batches over long rows: {name}")
+    blob = om.scale_residual_outputs(synthetic_model_file(dim, hid, L, H, Hkv, V, S, seed=len(name) + 3), 64.0)
+    model, ora = na.Model(blob), om.OracleModel(blob)
+    pages = 32
+    pool = na.KVPool(pages, L, model.kv_dim)
+    k = np.zeros((pages, L, 16, model.kv_dim), np.float32)
+    v = np.zeros_like(k)
+    bm = na.BlockManager(pages)
+    rng = np.random.default_rng(17)
+    seqs = [na.Sequence(i) for i in range(4)]
+    for s in seqs:
+        n = int(rng.integers(3, 12))
+        toks = rng.integers(0, V, n).astype(np.int32)
+        start = s.logical_token_count
+        for t in toks:
+            s.allocate_next_token(int(t), bm)
+        pool.upload_prefill_batch(na.pack_block_tables([s]), [start], [n])
+        got = model.forward_prefill(pool, toks, semantics=FULL_ROWS).cpu().numpy()
+        want = ora.forward_prefill_chunk(k, v, na.pack_block_tables([s])[0], start, toks, bulk=False)[None, :]
+        check_logits(got, want, f"{name} prefill {n}")
+    for nb in (1, 2, 3, 4):
+        say(f"  decode batch {nb}")
+        batch = seqs[:nb]
+        toks = rng.integers(0, V, nb).astype(np.int32)
+        pos = [s.logical_token_count for s in batch]
+        for s, t in zip(batch, toks):
+            s.allocate_next_token(int(t), bm)
+        tables = na.pack_block_tables(batch)
+        pool.upload_decode_batch(tables, pos)
+        got = model.forward_decode_batch(pool, toks, semantics=FULL_ROWS).cpu().numpy()
+        want = ora.forward_decode_batch(k, v, tables, pos, toks, bulk=False)
+        check_logits(got, want, f"{name} decode batch {nb}")
     torch.cuda.synchronize()
     assert pool.take_device_errors() == 0
 

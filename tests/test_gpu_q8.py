@@ -55,10 +55,13 @@ SHAPES = [
     # tiles of 16 (1, 15, 16, 17, 64, 65), rows not a multiple of 16, odd blocks per row
     (768, 768, 1), (768, 2048, 3), (2048, 768, 16), (768, 768, 17), (2048, 768, 64),
     (768, 200, 65), (96, 40, 100), (32, 7, 5), (4096, 48, 2),
-    # rows of >= 2048 k with 1-4 activation rows take the row-streaming kernel:
-    # 1024-k chunks split over two k halves (odd and even chunk counts), tiles
-    # of 16 rows not filling the matrix, more tiles than workgroups
-    (2048, 40, 1), (2304, 96, 2), (11008, 64, 3), (4096, 4100, 4), (4128, 16400, 1),
+    # rows of >= 2048 k with 1-4 activation rows whose x fits 16384 floats take
+    # the flat kernel (x in LDS): a last chunk of one block, 7 rows, more row
+    # units than workgroups, batch x n at the limit
+    (2048, 40, 1), (2304, 96, 2), (2080, 7, 3), (4096, 4100, 4), (4128, 16400, 1), (16384, 20, 1),
+    # larger batch x n: the row-streaming kernel, 1024-k chunks split over two
+    # k halves (odd and even chunk counts), tiles of 16 rows not filling the matrix
+    (11008, 64, 3), (6144, 40, 4), (8224, 4100, 2),
     # long rows with 5..64 activation rows (bf16 matrix-core kernel): a partial
     # 16-row batch tile, row tiles not filling the matrix, 344 blocks per row
     (4096, 4100, 8), (11008, 80, 33), (4096, 48, 5),
