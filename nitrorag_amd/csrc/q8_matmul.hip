@@ -13,8 +13,10 @@
 //    32 columns of every row reach the output.
 //
 // Kernels, by activation rows and semantics (the launcher picks):
-//  - 1..4 rows: VALU dot products.  q8_rowdot_kernel streams rows of >= 2048
-//    k (full rows); q8_gemv_kernel covers short rows and the last-block form.
+//  - 1..4 rows: VALU dot products.  Full rows of >= 2048 k take
+//    q8_flat_kernel when the activations fit its LDS (batch x n <= 16384
+//    floats), else q8_rowdot_kernel; q8_gemv_kernel covers short rows and the
+//    last-block form.
 //  - more rows, full rows: q8_mma_kernel, the bf16 matrix cores at fp32
 //    accuracy (x split into three exact bf16 parts), over the model's
 //    tile-layout copy of the matrix when there is one (Q8Tiled) or the BlockQ8
