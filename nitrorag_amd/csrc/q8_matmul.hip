@@ -831,7 +831,6 @@ __device__ __forceinline__ Q8Slice load_slice_raw(const uint8_t* wrow, int blk, 
 // of the wave's run, the 64 lanes of each row are summed with a fixed
 // butterfly into the wave's slot in LDS; the epilogue adds the slots in wave
 // order, so results do not depend on timing.
-constexpr int FLAT_WAVES = 8;
 constexpr int FLAT_R = 2;              // rows per item
 constexpr int FLAT_X_MAX = 16384;      // NB * n floats of staged activations (64 KiB)
 constexpr int FLAT_LDS_MAX = 80 * 1024;
@@ -840,11 +839,17 @@ template <bool RESID>
 constexpr int flat_unit_rows() {
     return RESID ? 16 : 2;
 }
+// Waves per workgroup: 16 with the residual epilogue, whose 16-row units
+// leave fewer workgroups (256 for a 4096-row matrix), 8 otherwise.
+template <bool RESID>
+constexpr int flat_waves() {
+    return RESID ? 16 : 8;
+}
 
 template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
-__global__ __launch_bounds__(64 * FLAT_WAVES) void q8_flat_kernel(Q8Group grp, const float* __restrict__ x, int n,
+__global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Group grp, const float* __restrict__ x, int n,
                                                                  int dmax, Q8Norm nm, Q8Resid resid, Q8Rope rope) {
-    constexpr int W = FLAT_WAVES, NT = 64 * W, R = FLAT_R;
+    constexpr int W = flat_waves<RESID>(), NT = 64 * W, R = FLAT_R;
     constexpr int UG = flat_unit_rows<RESID>();
     constexpr int XV = FLAT_X_MAX / 4 / NT;  // float4 of x per thread at most
     extern __shared__ float flat_lds[];
@@ -1307,7 +1312,8 @@ bool launch_flat(const Q8Group& grp, const float* x, int n, int dmax, const Q8No
         hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                             FLAT_LDS_MAX);
         int blocks = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 64 * FLAT_WAVES, FLAT_LDS_MAX) != hipSuccess)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 64 * flat_waves<RESID>(), FLAT_LDS_MAX) !=
+            hipSuccess)
             blocks = 1;
         return std::max(blocks, 1);
     }();
@@ -1315,9 +1321,10 @@ bool launch_flat(const Q8Group& grp, const float* x, int n, int dmax, const Q8No
     const int units = (dmax + UG - 1) / UG;
     const int groups = std::min(units, per_cu * device_cus());
     const long long rows_max = (long long)(units + groups - 1) / groups * UG;
-    const size_t lds = ((size_t)NB * n + (size_t)rows_max * NMAT * NB * FLAT_WAVES) * sizeof(float);
+    const size_t lds = ((size_t)NB * n + (size_t)rows_max * NMAT * NB * flat_waves<RESID>()) * sizeof(float);
     if (lds > (size_t)FLAT_LDS_MAX) return false;
-    hipLaunchKernelGGL(kern, dim3((unsigned)groups), dim3(64 * FLAT_WAVES), lds, stream, grp, x, n, dmax, nm, rs, rp);
+    hipLaunchKernelGGL(kern, dim3((unsigned)groups), dim3(64 * flat_waves<RESID>()), lds, stream, grp, x, n, dmax, nm, rs,
+                       rp);
     return true;
 }
 
