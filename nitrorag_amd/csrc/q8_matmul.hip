@@ -852,7 +852,7 @@ __global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Gro
     constexpr int W = flat_waves<RESID>(), NT = 64 * W, R = FLAT_R;
     constexpr int UG = flat_unit_rows<RESID>();
     constexpr int XV = FLAT_X_MAX / 4 / NT;  // float4 of x per thread at most
-    extern __shared__ float flat_lds[];
+    extern __shared__ __attribute__((aligned(16))) float flat_lds[];  // float4 access: 16-byte base
     __shared__ float inv_s[NB];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
