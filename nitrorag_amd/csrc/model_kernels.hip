@@ -11,6 +11,7 @@
 //      classifier wcls), VALU for up to 4 rows, fp32 MFMA above.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "device_pool.hpp"
@@ -182,6 +183,112 @@ __global__ __launch_bounds__(64 * F32_WAVES) void f32_gemv_kernel(const float* _
     out[(size_t)b * d + row0 + rr] = s;
 }
 
+// Up to NB activation rows whose x fits LDS (NB * n <= F32F_X_MAX floats):
+// x is staged in LDS once per workgroup, so a wave's only loads from memory
+// in its loop are weights and the next item's stay in flight while the
+// current one is used.  Persistent workgroups own balanced ranges of 2-row
+// groups; items are (group, 1024-k chunk), split between the 8 waves in
+// contiguous runs.  Lane l takes k = 1024*chunk + 16*l .. +15 of both rows
+// (64 contiguous bytes; a wave reads 4 KB of a row per chunk).  At a group's
+// last chunk (or the end of the wave's run) each row's 64 lanes are summed
+// with a fixed butterfly into the wave's LDS slot; the slots are added in
+// wave order.
+constexpr int F32F_WAVES = 8;
+constexpr int F32F_X_MAX = 16384;
+
+template <int NB>
+__global__ __launch_bounds__(64 * F32F_WAVES) void f32_flat_kernel(const float* __restrict__ w,
+                                                                   const float* __restrict__ x,
+                                                                   float* __restrict__ out, int n, int d) {
+    constexpr int W = F32F_WAVES, NT = 64 * W, R = 2;
+    extern __shared__ __attribute__((aligned(16))) float f32f_lds[];  // [NB][n] x, then [rows][NB][W] sums
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nch = (n + 1023) / 1024;
+    const int groups = (d + R - 1) / R;
+    const int g0 = (int)((long long)groups * blockIdx.x / gridDim.x);
+    const int g1 = (int)((long long)groups * (blockIdx.x + 1) / gridDim.x);
+    const int items = (g1 - g0) * nch;
+    const int i0 = items * wave / W, i1 = items * (wave + 1) / W;
+    float* xs = f32f_lds;
+    float* red = f32f_lds + NB * n;
+    auto load_item = [&](float4 (&v)[R][4], int i) {
+        i = max(min(i, i1 - 1), 0);  // clamped into the run: a wave with no items loads in range, never used
+        const int g = g0 + i / nch, c = i % nch;
+        const int k = min(1024 * c + 16 * lane, n - 16);  // a lane past the row rereads the last 16 (x zeroed)
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float4* p = reinterpret_cast<const float4*>(w + (size_t)min(g * R + r, d - 1) * n + k);
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[r][q] = p[q];
+        }
+    };
+    float4 va[R][4], vb[R][4];
+    load_item(va, i0);
+    // x -> LDS (NB * n / 4 float4, at most 2 per thread for a 4096-wide row)
+    for (int t = threadIdx.x; t < NB * n / 4; t += NT)
+        reinterpret_cast<float4*>(xs)[t] = reinterpret_cast<const float4*>(x)[t];
+    const int rows = (g1 - g0) * R;
+    for (int t = threadIdx.x; t < rows * NB * W; t += NT) red[t] = 0.0f;
+    __syncthreads();
+    float acc[R][NB];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < NB; b++) acc[r][b] = 0.0f;
+    auto step = [&](const float4 (&now)[R][4], float4 (&next)[R][4], int i) {
+        load_item(next, i + 1);
+        const int gl = i / nch, c = i % nch;
+        const int k = 1024 * c + 16 * lane;
+        const bool valid = k < n;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const float4* xp = reinterpret_cast<const float4*>(xs + b * n + (valid ? k : 0));
+            float4 xv[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 t = xp[q];
+                xv[q] = valid ? t : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    acc[r][b] = fmaf(now[r][q].x, xv[q].x, acc[r][b]);
+                    acc[r][b] = fmaf(now[r][q].y, xv[q].y, acc[r][b]);
+                    acc[r][b] = fmaf(now[r][q].z, xv[q].z, acc[r][b]);
+                    acc[r][b] = fmaf(now[r][q].w, xv[q].w, acc[r][b]);
+                }
+        }
+        if (c == nch - 1 || i == i1 - 1) {  // wave-uniform
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int b = 0; b < NB; b++) {
+                    float v = acc[r][b];
+#pragma unroll
+                    for (int msk = 32; msk > 0; msk >>= 1) v += __shfl_xor(v, msk);
+                    if (lane == 0) red[((gl * R + r) * NB + b) * W + wave] = v;
+                    acc[r][b] = 0.0f;
+                }
+        }
+    };
+    int i = i0;
+    for (; i + 1 < i1; i += 2) {
+        step(va, vb, i);
+        step(vb, va, i + 1);
+    }
+    if (i < i1) step(va, vb, i);
+    __syncthreads();
+    for (int t = threadIdx.x; t < NB * rows; t += NT) {
+        const int b = t / rows, il = t - b * rows;
+        const int row = g0 * R + il;
+        float v = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < W; ww++) v += red[(il * NB + b) * W + ww];
+        if (row < d) out[(size_t)b * d + row] = v;
+    }
+}
+
 // More rows on fp32 MFMA: out^T[16 rows][16 batch] per wave, 4 waves split k
 // by 64-k chunks; lane (r, g) feeds w[row0+r][64c + 16g + m] and
 // x[b][64c + 16g + m] to instruction m.
@@ -290,9 +397,42 @@ hipError_t launch_swiglu(float* hb, const float* hb2, size_t n, hipStream_t stre
     return hipGetLastError();
 }
 
+namespace {
+int f32_device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return cus[dev];
+}
+
+// f32_flat_kernel, one round of workgroups (2 per CU at up to 2 activation
+// rows, whose registers allow it, else 1), if x and the sums fit 64 KiB of LDS.
+bool launch_f32_flat(const float* w, const float* x, float* out, int batch, int n, int d, hipStream_t stream) {
+    const int groups_total = (d + 1) / 2;
+    const int wgs = std::min(groups_total, (batch <= 2 ? 2 : 1) * f32_device_cus());
+    const size_t rows_max = (size_t)((groups_total + wgs - 1) / wgs) * 2;
+    const size_t lds = ((size_t)batch * n + rows_max * batch * F32F_WAVES) * sizeof(float);
+    if (lds > 64 * 1024) return false;  // the default dynamic LDS limit
+    const dim3 grid((unsigned)wgs), block(64 * F32F_WAVES);
+    switch (batch) {
+        case 1: hipLaunchKernelGGL(f32_flat_kernel<1>, grid, block, lds, stream, w, x, out, n, d); break;
+        case 2: hipLaunchKernelGGL(f32_flat_kernel<2>, grid, block, lds, stream, w, x, out, n, d); break;
+        case 3: hipLaunchKernelGGL(f32_flat_kernel<3>, grid, block, lds, stream, w, x, out, n, d); break;
+        default: hipLaunchKernelGGL(f32_flat_kernel<4>, grid, block, lds, stream, w, x, out, n, d); break;
+    }
+    return true;
+}
+}  // namespace
+
 hipError_t launch_f32_matmul(const float* w, const float* x, float* out, int batch, int n, int d,
                              hipStream_t stream) {
     if (n % 64 != 0) return hipErrorInvalidValue;
+    if (batch <= 4 && batch * n <= F32F_X_MAX && launch_f32_flat(w, x, out, batch, n, d, stream)) return hipGetLastError();
     if (batch <= 4) {
         const dim3 grid((unsigned)((d + 15) / 16)), block(64 * F32_WAVES);
         switch (batch) {
