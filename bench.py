@@ -22,7 +22,8 @@ Reported:
 Algorithmic bytes per decode launch: sum_b ctx_b*Hkv*hd*4*2 (K and V) +
 B*H*hd*4*2 (q in, out) + sum_b ceil(ctx_b/16)*4 (block-table entries).
 
-Other workloads (survey configs and the next rows, measured for the design notes):
+Other workloads (the other paged-attention shapes, the model step around the path,
+Q8 products and the serving loop):
   decode-single-110m     1 sequence, 12 layers x 12 heads x 64, ctx 256, 64-page pool;
                          a step is one token through all 12 layers' append + attention
   decode-b32-mixed       B=32, 12x64, ctx ~ U[16,1024], 4096-page pool (12 layers, one timed)
@@ -793,8 +794,8 @@ def main():
                     help="rocprofv3 summary holding the measured HBM traffic per decode launch")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: the paged-attention path shards by sequence or "
-              "by head with no exchange, and multi-GPU runs are not part of this build",
+        print("bench.py measures one GPU only (the paged-attention path shards by sequence or "
+              "by head with no exchange between GPUs)",
               file=sys.stderr)
         sys.exit(2)
 
