@@ -281,8 +281,17 @@ int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, f
         int waves = env_int("NITRO_DECODE_WAVES", 0);
         if (waves <= 0) {
             waves = kDecodeMinWaves;
-            while (waves < max_waves && bh_count * waves * 2 <= target && waves < max_tiles)
-                waves *= 2;
+            if (bh_count * kDecodeMinWaves > target) {
+                // several dispatch rounds even at the fewest waves: the launch is
+                // throughput-bound, and the most waves per workgroup (each
+                // workgroup's waves streaming one sequence's K/V together)
+                // measured 0.3-1% faster at B=64 ctx 4096 than 4 waves
+                waves = max_waves;
+                while (waves > kDecodeMinWaves && waves > max_tiles) waves /= 2;
+            } else {
+                while (waves < max_waves && bh_count * waves * 2 <= target && waves < max_tiles)
+                    waves *= 2;
+            }
         }
         waves = std::max(kDecodeMinWaves, std::min(waves, max_waves));
         int tps = env_int("NITRO_DECODE_SPLIT_TILES", 0);
