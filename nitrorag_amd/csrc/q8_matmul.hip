@@ -827,7 +827,9 @@ __device__ __forceinline__ Q8Slice load_slice_raw(const uint8_t* wrow, int blk, 
 // workgroup's items are split between its waves in contiguous runs.  Lane l
 // reads half l%2 of block 32*chunk + l/2 of each row (1152 contiguous bytes
 // per row and load instruction).  A block's products are summed, then scaled
-// (sum_k q*x times the block's scale).  At a group's last chunk, or the end
+// (sum_k q*x times the block's scale; the reference scales each weight
+// first, src/model_q8.cpp:106-112, and the two agree to fp32 rounding).  At
+// a group's last chunk, or the end
 // of the wave's run, the 64 lanes of each row are summed with a fixed
 // butterfly into the wave's slot in LDS; the epilogue adds the slots in wave
 // order, so results do not depend on timing.
@@ -847,8 +849,9 @@ constexpr int flat_waves() {
 }
 
 template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
-__global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Group grp, const float* __restrict__ x, int n,
-                                                                 int dmax, Q8Norm nm, Q8Resid resid, Q8Rope rope) {
+__global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Group grp, const float* __restrict__ x,
+                                                                           int n, int dmax, Q8Norm nm, Q8Resid resid,
+                                                                           Q8Rope rope) {
     constexpr int W = flat_waves<RESID>(), NT = 64 * W, R = FLAT_R;
     constexpr int UG = flat_unit_rows<RESID>();
     constexpr int XV = FLAT_X_MAX / 4 / NT;  // float4 of x per thread at most
