@@ -733,7 +733,7 @@ def make_workload(name, seed):
 
 WORKLOADS = ["decode-b64-ctx4096", "decode-single-110m", "decode-b32-mixed",
              "decode-prefix-shared", "prefill-b8-12x64", "q8-gemv-7b-ffn", "q8-matmul-110m-b32",
-             "model-110m-decode-b32", "model-7b-decode-b1", "model-7b-decode-b8", "serve-110m-u1", "serve-110m-u4", "serve-110m-u8",
+             "model-110m-decode-b32", "model-7b-decode-b1", "model-7b-decode-b2", "model-7b-decode-b8", "serve-110m-u1", "serve-110m-u4", "serve-110m-u8",
              "serve-110m-u16", "serve-110m-u32"]
 
 

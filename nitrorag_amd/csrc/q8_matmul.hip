@@ -817,7 +817,7 @@ __device__ __forceinline__ Q8Slice load_slice_raw(const uint8_t* wrow, int blk, 
 }
 
 // Batches of 1..NB rows over long rows (n >= 2048) whose activations fit LDS
-// (NB * n <= FLAT_X_MAX floats).  x, rms-normalised when NORM, is staged in
+// (NB * n <= flat_x_max floats).  x, rms-normalised when NORM, is staged in
 // LDS once per workgroup, so a wave's only loads from memory in its loop are
 // weights: x reads wait on the LDS counter, and the next item's weights stay
 // in flight while the current item is used.  Persistent workgroups own
@@ -834,8 +834,19 @@ __device__ __forceinline__ Q8Slice load_slice_raw(const uint8_t* wrow, int blk, 
 // butterfly into the wave's slot in LDS; the epilogue adds the slots in wave
 // order, so results do not depend on timing.
 constexpr int FLAT_R = 2;              // rows per item
-constexpr int FLAT_X_MAX = 16384;      // NB * n floats of staged activations (64 KiB)
-constexpr int FLAT_LDS_MAX = 80 * 1024;
+
+// Staged activations (NB * n floats) and LDS per workgroup at most: 64 KiB of
+// x and 80 KiB in all, two workgroups per CU; with the residual epilogue, one
+// 16-wave workgroup per CU (its registers allow no second), so 156 KiB of x
+// and 160 KiB in all (rows of 11008 k at 2-3 activation rows).
+template <bool RESID>
+constexpr int flat_x_max() {
+    return RESID ? 39936 : 16384;
+}
+template <bool RESID>
+constexpr int flat_lds_max() {
+    return RESID ? 160 * 1024 : 80 * 1024;
+}
 
 template <bool RESID>
 constexpr int flat_unit_rows() {
@@ -854,7 +865,7 @@ __global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Gro
                                                                            Q8Rope rope) {
     constexpr int W = flat_waves<RESID>(), NT = 64 * W, R = FLAT_R;
     constexpr int UG = flat_unit_rows<RESID>();
-    constexpr int XV = FLAT_X_MAX / 4 / NT;  // float4 of x per thread at most
+    constexpr int XV = flat_x_max<RESID>() / 4 / NT;  // float4 of x per thread at most
     extern __shared__ __attribute__((aligned(16))) float flat_lds[];  // float4 access: 16-byte base
     __shared__ float inv_s[NB];
     const int lane = threadIdx.x & 63;
@@ -1307,15 +1318,15 @@ int device_cus() {
 template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
 bool launch_flat(const Q8Group& grp, const float* x, int n, int dmax, const Q8Norm& nm, const Q8Resid& rs,
                  const Q8Rope& rp, hipStream_t stream) {
-    if ((long long)NB * n > FLAT_X_MAX) return false;
+    if ((long long)NB * n > flat_x_max<RESID>()) return false;
     const auto kern = q8_flat_kernel<NB, NMAT, SWIGLU, NORM, RESID, ROPE>;
     // workgroups resident per CU at the largest LDS the launch may take
     // (once per instantiation; the dynamic LDS limit is raised to that size)
     static const int per_cu = [kern] {
         hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            FLAT_LDS_MAX);
+                            flat_lds_max<RESID>());
         int blocks = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 64 * flat_waves<RESID>(), FLAT_LDS_MAX) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 64 * flat_waves<RESID>(), flat_lds_max<RESID>()) !=
             hipSuccess)
             blocks = 1;
         return std::max(blocks, 1);
@@ -1325,7 +1336,7 @@ bool launch_flat(const Q8Group& grp, const float* x, int n, int dmax, const Q8No
     const int groups = std::min(units, per_cu * device_cus());
     const long long rows_max = (long long)(units + groups - 1) / groups * UG;
     const size_t lds = ((size_t)NB * n + (size_t)rows_max * NMAT * NB * flat_waves<RESID>()) * sizeof(float);
-    if (lds > (size_t)FLAT_LDS_MAX) return false;
+    if (lds > (size_t)flat_lds_max<RESID>()) return false;
     hipLaunchKernelGGL(kern, dim3((unsigned)groups), dim3(64 * flat_waves<RESID>()), lds, stream, grp, x, n, dmax, nm, rs,
                        rp);
     return true;
