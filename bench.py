@@ -34,6 +34,9 @@ Q8 products and the serving loop):
   q8-gemv-7b-ffn         Q8_0 product, W 11008 x 4096 BlockQ8, 1 activation row
   q8-matmul-110m-b32     Q8_0 product, W 2048 x 768 BlockQ8, 32 activation rows
   model-110m-decode-b32  one decode step of a 110M-shaped Q8 model, B=32 at context 512
+  model-7b-decode-bN     one decode step of a Llama-2-7B-shaped Q8 model, N = 1, 2 or 8
+                         sequences at context 1024
+  serve-110m-uN          the reference's continuous-batching experiment, N users
 The three small decode workloads fit in the 256 MB Infinity Cache, so a 1 GiB
 buffer is read before every timed launch and only the launch itself is timed
 (events).
