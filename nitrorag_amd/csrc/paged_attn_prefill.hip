@@ -714,23 +714,33 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_x3_kernel
             *reinterpret_cast<uint2*>(dst + plane) = make_uint2(bf16_pair(r0, r1), bf16_pair(r2, r3));
             *reinterpret_cast<uint2*>(dst + 2 * plane) = make_uint2(bf16_pair(l0, l1), bf16_pair(l2, l3));
         };
+        // the masks are applied only where a wave holds a row to zero
+        // (the last tile of a sequence, bad pages): other tiles skip the selects
+        auto stage_tile = [&](bool masked) {
 #pragma unroll
-        for (int i = 0; i < LOADS; i++) {
-            const int f = threadIdx.x + i * NT;
-            const int r = f / F4, col = f % F4;
-            const bool ok = (kmask >> i) & 1;
-            const float kv4[4] = {ok ? kreg[i].x : 0.f, ok ? kreg[i].y : 0.f, ok ? kreg[i].z : 0.f,
-                                  ok ? kreg[i].w : 0.f};
-            stage4(&k_lds[r * KST + col * 4], KPLANE, kv4);
-        }
+            for (int i = 0; i < LOADS; i++) {
+                const int f = threadIdx.x + i * NT;
+                const int r = f / F4, col = f % F4;
+                const bool ok = !masked || ((kmask >> i) & 1);
+                const float kv4[4] = {ok ? kreg[i].x : 0.f, ok ? kreg[i].y : 0.f, ok ? kreg[i].z : 0.f,
+                                      ok ? kreg[i].w : 0.f};
+                stage4(&k_lds[r * KST + col * 4], KPLANE, kv4);
+            }
 #pragma unroll
-        for (int i = 0; i < VSLOTS; i++) {
-            const int sl = threadIdx.x + i * NT;
-            float v4[4];
+            for (int i = 0; i < VSLOTS; i++) {
+                const int sl = threadIdx.x + i * NT;
+                float v4[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) v4[e] = (vmask >> (4 * i + e)) & 1 ? vreg[i][e] : 0.f;
-            stage4(&v_lds[(sl % HD) * VST + 4 * (sl / HD)], VPLANE, v4);
-        }
+                for (int e = 0; e < 4; e++) v4[e] = !masked || ((vmask >> (4 * i + e)) & 1) ? vreg[i][e] : 0.f;
+                stage4(&v_lds[(sl % HD) * VST + 4 * (sl / HD)], VPLANE, v4);
+            }
+        };
+        constexpr uint32_t KFULL = LOADS == 32 ? ~0u : (1u << LOADS) - 1;
+        constexpr uint32_t VFULL = 4 * VSLOTS == 32 ? ~0u : (1u << (4 * VSLOTS)) - 1;
+        if (__builtin_amdgcn_ballot_w64(kmask != KFULL || vmask != VFULL) != 0)  // wave-uniform
+            stage_tile(true);
+        else
+            stage_tile(false);
         __syncthreads();
         if (tile + 1 < n_tiles) fetch(tile + 1);
 
