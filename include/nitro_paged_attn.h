@@ -276,8 +276,18 @@ typedef struct nitro_scheduler nitro_scheduler;
 int nitro_sched_create(nitro_block_manager* bm, int32_t max_tokens_per_batch, int32_t max_generated,
                        nitro_scheduler** out);
 int nitro_sched_destroy(nitro_scheduler* sched);
-/* new Request(req_id, prompt) + add_request (:309-312); n > 0, ids unique. */
+/* new Request(req_id, prompt) + add_request (:309-312); n > 0, ids unique.
+ * Once limits are set (nitro_sched_set_limits, or bound from the model by
+ * the first nitro_sched_step), a prompt holding a token outside [0, vocab)
+ * or with n + max_generated - 1 > seq_len (its last decode would sit at
+ * position seq_len or later) is refused with NITRO_ERR_INVALID_ARGUMENT;
+ * the reference has no such limit and would index its pools out of bounds. */
 int nitro_sched_add_request(nitro_scheduler* sched, int32_t req_id, const int32_t* prompt, int32_t n);
+/* The model's seq_len and vocabulary size for admission (0 = no limit).
+ * nitro_sched_step sets them from its model on every call, and first finishes
+ * (with the tokens they have) requests queued earlier that the model cannot
+ * run, instead of failing the step. */
+int nitro_sched_set_limits(nitro_scheduler* sched, int32_t seq_len, int32_t vocab);
 int nitro_sched_has_active_requests(const nitro_scheduler* sched, int32_t* active); /* :313-315 */
 /* step (:316-378) up to its two forward calls, including the
  * allocate_next_token loops those forwards begin with (src/model_q8.cpp:
@@ -348,7 +358,10 @@ int nitro_rpc_recv_structured_query(int32_t fd, int32_t dim, uint64_t* subset_ma
  * vector of at most max_prompt_tokens) and adds it as request 0, 1, 2, ...
  * (req_counter, :27-34); each nitro_server_step runs one nitro_sched_step,
  * sends every request's new tokens as bare int32 values and closes the
- * connections of finished requests.  *active = has_active_requests. */
+ * connections of finished requests, whose requests it forgets once the
+ * scheduler has released them.  *active = has_active_requests.  A prompt the
+ * scheduler refuses (nitro_sched_add_request) fails nitro_server_accept_fd;
+ * the fd then stays the caller's, as it does after any failure there. */
 typedef struct nitro_server nitro_server;
 int nitro_server_create(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* pool, int32_t semantics,
                         int32_t max_prompt_tokens, nitro_server** out);

@@ -98,6 +98,7 @@ SIGNATURES = {
     "nitro_sched_create": [_vp, _i32, _i32, ctypes.POINTER(_vp)],
     "nitro_sched_destroy": [_vp],
     "nitro_sched_add_request": [_vp, _i32, _i32p, _i32],
+    "nitro_sched_set_limits": [_vp, _i32, _i32],
     "nitro_sched_has_active_requests": [_vp, _i32p],
     "nitro_sched_plan": [_vp, _i32p, _i32p, _i32p, _i32p, _i32, _i32p],
     "nitro_sched_commit": [_vp, _i32, _i32p, _i32],

@@ -14,9 +14,13 @@
 namespace nitro {
 
 inline void hip_check(hipError_t e, const char* what) {
-    if (e != hipSuccess)
+    if (e != hipSuccess) {
+        // HIP also records the failure as the thread's last error, which the
+        // next launch check (hipGetLastError) would report as its own: clear it.
+        (void)hipGetLastError();
         throw Error(e == hipErrorOutOfMemory ? ERR_DEVICE_ALLOC : ERR_HIP,
                     std::string(what) + ": " + hipGetErrorString(e));
+    }
 }
 
 // A device allocation that only grows (hipMalloc outside any capture).

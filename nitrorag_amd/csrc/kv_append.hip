@@ -21,43 +21,52 @@ namespace {
 
 constexpr int APPEND_THREADS = 256;
 
+// Both append kernels walk the flat (row, float4) index space with a
+// grid-stride loop, so any row count runs (rows are not on gridDim.y, whose
+// 65,535 limit a large prefill batch would exceed).
 __global__ __launch_bounds__(APPEND_THREADS) void kv_append_decode_kernel(
     float* __restrict__ k_pool, float* __restrict__ v_pool, const float* __restrict__ k,
     const float* __restrict__ v, const int32_t* __restrict__ tables,
-    const int32_t* __restrict__ positions, int max_pages, int kv_dim, int64_t page_stride,
+    const int32_t* __restrict__ positions, int batch, int max_pages, int kv_dim, int64_t page_stride,
     int64_t layer_off, int num_pages, int32_t* bad_pages) {
-    const int b = blockIdx.y;
-    const int i = blockIdx.x * APPEND_THREADS + threadIdx.x;  // float4 index within the row
-    if (i * 4 >= kv_dim) return;
-    const int pos = positions[b];
-    const int page = tables[(size_t)b * max_pages + (pos >> 4)];
-    if ((unsigned)page >= (unsigned)num_pages) {
-        if (i == 0) atomicAdd(bad_pages, 1);
-        return;
+    const int f4 = kv_dim >> 2;
+    const size_t total = (size_t)batch * f4;
+    for (size_t t = (size_t)blockIdx.x * APPEND_THREADS + threadIdx.x; t < total;
+         t += (size_t)gridDim.x * APPEND_THREADS) {
+        const int b = (int)(t / f4), i = (int)(t - (size_t)b * f4);
+        const int pos = positions[b];
+        const int page = tables[(size_t)b * max_pages + (pos >> 4)];
+        if ((unsigned)page >= (unsigned)num_pages) {
+            if (i == 0) atomicAdd(bad_pages, 1);
+            continue;
+        }
+        const size_t dst = (size_t)page * page_stride + layer_off + (size_t)(pos & 15) * kv_dim;
+        const size_t src = (size_t)b * kv_dim;
+        reinterpret_cast<float4*>(k_pool + dst)[i] = reinterpret_cast<const float4*>(k + src)[i];
+        reinterpret_cast<float4*>(v_pool + dst)[i] = reinterpret_cast<const float4*>(v + src)[i];
     }
-    const size_t dst = (size_t)page * page_stride + layer_off + (size_t)(pos & 15) * kv_dim;
-    const size_t src = (size_t)b * kv_dim;
-    reinterpret_cast<float4*>(k_pool + dst)[i] = reinterpret_cast<const float4*>(k + src)[i];
-    reinterpret_cast<float4*>(v_pool + dst)[i] = reinterpret_cast<const float4*>(v + src)[i];
 }
 
 __global__ __launch_bounds__(APPEND_THREADS) void kv_scatter_rows_kernel(
     float* __restrict__ k_pool, float* __restrict__ v_pool, const float* __restrict__ k,
-    const float* __restrict__ v, const int32_t* __restrict__ slots, int kv_dim,
+    const float* __restrict__ v, const int32_t* __restrict__ slots, int rows, int kv_dim,
     int64_t page_stride, int64_t layer_off, int num_pages, int32_t* bad_pages) {
-    const int r = blockIdx.y;
-    const int i = blockIdx.x * APPEND_THREADS + threadIdx.x;
-    if (i * 4 >= kv_dim) return;
-    const int slot = slots[r];
-    const int page = slot >> 4;
-    if (slot < 0 || page >= num_pages) {
-        if (i == 0) atomicAdd(bad_pages, 1);
-        return;
+    const int f4 = kv_dim >> 2;
+    const size_t total = (size_t)rows * f4;
+    for (size_t t = (size_t)blockIdx.x * APPEND_THREADS + threadIdx.x; t < total;
+         t += (size_t)gridDim.x * APPEND_THREADS) {
+        const int r = (int)(t / f4), i = (int)(t - (size_t)r * f4);
+        const int slot = slots[r];
+        const int page = slot >> 4;
+        if (slot < 0 || page >= num_pages) {
+            if (i == 0) atomicAdd(bad_pages, 1);
+            continue;
+        }
+        const size_t dst = (size_t)page * page_stride + layer_off + (size_t)(slot & 15) * kv_dim;
+        const size_t src = (size_t)r * kv_dim;
+        reinterpret_cast<float4*>(k_pool + dst)[i] = reinterpret_cast<const float4*>(k + src)[i];
+        reinterpret_cast<float4*>(v_pool + dst)[i] = reinterpret_cast<const float4*>(v + src)[i];
     }
-    const size_t dst = (size_t)page * page_stride + layer_off + (size_t)(slot & 15) * kv_dim;
-    const size_t src = (size_t)r * kv_dim;
-    reinterpret_cast<float4*>(k_pool + dst)[i] = reinterpret_cast<const float4*>(k + src)[i];
-    reinterpret_cast<float4*>(v_pool + dst)[i] = reinterpret_cast<const float4*>(v + src)[i];
 }
 
 // Decode rows: position positions[row], page tables[row][pos/16].  Prefill
@@ -125,16 +134,22 @@ hipError_t launch_rope_kv_append(float* k_pool, float* v_pool, float* q, float* 
     return hipGetLastError();
 }
 
+// Workgroups of the append launches: enough to cover the rows (one float4
+// per thread), at most 65,536 (each thread then takes several).
+static unsigned append_groups(size_t float4s) {
+    const size_t g = (float4s + APPEND_THREADS - 1) / APPEND_THREADS;
+    return (unsigned)(g < 1 ? 1 : g > 65536 ? 65536 : g);
+}
+
 hipError_t launch_kv_append_decode(float* k_pool, float* v_pool, const float* k, const float* v,
                                    const int32_t* tables, const int32_t* positions, int batch,
                                    int max_pages, int kv_dim, int64_t page_stride,
                                    int64_t layer_off, int num_pages, int32_t* bad_pages,
                                    hipStream_t stream) {
-    const int f4 = kv_dim / 4;
-    const dim3 grid((f4 + APPEND_THREADS - 1) / APPEND_THREADS, batch);
+    const dim3 grid(append_groups((size_t)batch * (kv_dim / 4)));
     hipLaunchKernelGGL(kv_append_decode_kernel, grid, dim3(APPEND_THREADS), 0, stream, k_pool,
-                       v_pool, k, v, tables, positions, max_pages, kv_dim, page_stride, layer_off,
-                       num_pages, bad_pages);
+                       v_pool, k, v, tables, positions, batch, max_pages, kv_dim, page_stride,
+                       layer_off, num_pages, bad_pages);
     return hipGetLastError();
 }
 
@@ -142,10 +157,10 @@ hipError_t launch_kv_scatter_rows(float* k_pool, float* v_pool, const float* k, 
                                   const int32_t* slots, int rows, int kv_dim, int64_t page_stride,
                                   int64_t layer_off, int num_pages, int32_t* bad_pages,
                                   hipStream_t stream) {
-    const int f4 = kv_dim / 4;
-    const dim3 grid((f4 + APPEND_THREADS - 1) / APPEND_THREADS, rows);
+    const dim3 grid(append_groups((size_t)rows * (kv_dim / 4)));
     hipLaunchKernelGGL(kv_scatter_rows_kernel, grid, dim3(APPEND_THREADS), 0, stream, k_pool,
-                       v_pool, k, v, slots, kv_dim, page_stride, layer_off, num_pages, bad_pages);
+                       v_pool, k, v, slots, rows, kv_dim, page_stride, layer_off, num_pages,
+                       bad_pages);
     return hipGetLastError();
 }
 

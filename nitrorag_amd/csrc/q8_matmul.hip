@@ -865,7 +865,10 @@ __global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Gro
                                                                            Q8Rope rope) {
     constexpr int W = flat_waves<RESID>(), NT = 64 * W, R = FLAT_R;
     constexpr int UG = flat_unit_rows<RESID>();
-    constexpr int XV = flat_x_max<RESID>() / 4 / NT;  // float4 of x per thread at most
+    // float4 of x per thread at most (rounded up: the last round may be partial)
+    constexpr int XV = (flat_x_max<RESID>() / 4 + NT - 1) / NT;
+    static_assert(flat_x_max<RESID>() % 4 == 0 && XV * 4 * NT >= flat_x_max<RESID>(),
+                  "the staging loop must cover every float of x the launcher admits");
     extern __shared__ __attribute__((aligned(16))) float flat_lds[];  // float4 access: 16-byte base
     __shared__ float inv_s[NB];
     const int lane = threadIdx.x & 63;

@@ -191,6 +191,7 @@ int nitro_server_accept_fd(nitro_server* server, int32_t fd, int32_t* req_id) {
         std::vector<int32_t> prompt(server->max_prompt);
         const int32_t n = recv_count(fd, server->max_prompt);
         if (n) recv_all(fd, prompt.data(), 4 * (size_t)n);
+        // add_request refuses a prompt the model cannot finish (the fd stays the caller's)
         const int32_t id = server->next_id;
         server->sched->host.add_request(id, prompt.data(), n);
         server->next_id++;
@@ -204,6 +205,19 @@ int nitro_server_step(nitro_server* server, void* stream, int32_t* active) {
         require(server != nullptr && active != nullptr, ERR_INVALID_ARGUMENT, "null pointer");
         ContinuousScheduler& h = server->sched->host;
         *active = 0;
+        // Forget what is over: a closed connection whose request has finished
+        // and been released by the scheduler (so neither list grows with the
+        // number of requests served).
+        std::vector<nitro_server::Conn> kept;
+        kept.reserve(server->conns.size());
+        for (const auto& c : server->conns) {
+            if (c.closed && h.droppable(c.req_id)) {
+                h.drop(c.req_id);
+                continue;
+            }
+            kept.push_back(c);
+        }
+        server->conns.swap(kept);
         if (!h.has_active_requests()) return;
         require(nitro_sched_step(server->sched, server->model, server->pool, server->semantics, stream) == NITRO_OK,
                 ERR_INVALID_ARGUMENT, nitro_last_error());

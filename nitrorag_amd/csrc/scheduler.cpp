@@ -21,11 +21,25 @@ Request& ContinuousScheduler::add_request(int req_id, const int32_t* prompt, int
     require(prompt != nullptr && n > 0, ERR_INVALID_ARGUMENT, "a request needs a non-empty prompt");
     require(find(req_id) == nullptr, ERR_INVALID_ARGUMENT, "request id already in use");
     require(!planned_, ERR_INVALID_ARGUMENT, "a planned step has not been committed");
+    if (seq_len_ > 0 && (long long)n + max_generated_ - 1 > seq_len_)
+        throw Error(ERR_INVALID_ARGUMENT, "a prompt of " + std::to_string(n) + " tokens plus " +
+                                              std::to_string(max_generated_) + " generated ones does not fit " +
+                                              "the model's seq_len of " + std::to_string(seq_len_));
+    if (vocab_ > 0)
+        for (int i = 0; i < n; i++)
+            require(prompt[i] >= 0 && prompt[i] < vocab_, ERR_INVALID_ARGUMENT,
+                    "prompt token outside the vocabulary");
     requests_.push_back(std::make_unique<Request>(req_id, prompt, n));
     Request* r = requests_.back().get();
     r->next_token_to_process = r->prompt_tokens[0];  // :310
     waiting_.push_back(r);                             // :311
     return *r;
+}
+
+void ContinuousScheduler::set_limits(int seq_len, int vocab) {
+    require(seq_len >= 0 && vocab >= 0, ERR_INVALID_ARGUMENT, "limits must not be negative");
+    seq_len_ = seq_len;
+    vocab_ = vocab;
 }
 
 const StepPlan& ContinuousScheduler::plan() {
@@ -133,15 +147,28 @@ const Request* ContinuousScheduler::find(int req_id) const {
     return nullptr;
 }
 
+void ContinuousScheduler::reject_head() {
+    require(!planned_, ERR_INVALID_ARGUMENT, "a planned step has not been committed");
+    require(!waiting_.empty(), ERR_INVALID_ARGUMENT, "no queued request");
+    Request* r = waiting_.front();
+    waiting_.pop_front();
+    if (!r->seq.block_table.empty()) r->seq.release(bm_.mem, bm_.cache);
+    r->is_finished = true;
+}
+
+bool ContinuousScheduler::droppable(int req_id) const {
+    const Request* r = find(req_id);
+    if (!r || !r->is_finished || planned_) return false;
+    return std::find(waiting_.begin(), waiting_.end(), r) == waiting_.end() &&
+           std::find(running_.begin(), running_.end(), r) == running_.end();
+}
+
 void ContinuousScheduler::drop(int req_id) {
     require(!planned_, ERR_INVALID_ARGUMENT, "a planned step has not been committed");
     auto it = std::find_if(requests_.begin(), requests_.end(),
                            [&](const std::unique_ptr<Request>& r) { return r->req_id == req_id; });
     require(it != requests_.end(), ERR_INVALID_ARGUMENT, "unknown request id");
-    Request* r = it->get();
-    const bool queued = std::find(waiting_.begin(), waiting_.end(), r) != waiting_.end() ||
-                        std::find(running_.begin(), running_.end(), r) != running_.end();
-    require(r->is_finished && !queued, ERR_INVALID_ARGUMENT,
+    require(droppable(req_id), ERR_INVALID_ARGUMENT,
             "only a finished request that a later step has released can be dropped");
     requests_.erase(it);
 }
@@ -213,6 +240,13 @@ int nitro_sched_add_request(nitro_scheduler* s, int32_t req_id, const int32_t* p
     return guarded([&] {
         require_sched(s);
         s->host.add_request(req_id, prompt, n);
+    });
+}
+
+int nitro_sched_set_limits(nitro_scheduler* s, int32_t seq_len, int32_t vocab) {
+    return guarded([&] {
+        require_sched(s);
+        s->host.set_limits(seq_len, vocab);
     });
 }
 

@@ -61,7 +61,12 @@ class ContinuousScheduler {
     ContinuousScheduler& operator=(const ContinuousScheduler&) = delete;
 
     // add_request (:309-312): the first token to process is prompt[0].
+    // With limits set, a prompt holding a token outside [0, vocab) or whose
+    // generation would decode at or past seq_len (its last decode sits at
+    // position n + max_generated - 2) is refused; the reference has no limit.
     Request& add_request(int req_id, const int32_t* prompt, int n);
+    // The model's seq_len and vocabulary size (0 = no limit).
+    void set_limits(int seq_len, int vocab);
     bool has_active_requests() const { return !waiting_.empty() || !running_.empty(); }  // :313-315
     // The queue head (the only request plan() may prefill), or null.
     const Request* waiting_head() const { return waiting_.empty() ? nullptr : waiting_.front(); }
@@ -73,8 +78,14 @@ class ContinuousScheduler {
     void commit(int32_t prefill_token, const int32_t* decode_tokens, int n);
     bool planned() const { return planned_; }
 
+    // Takes the queue head out of the queue unserved: it is marked finished
+    // with the tokens it has (none) and any pages it holds are released.  For
+    // a request the model cannot run (the reference has no such check).
+    void reject_head();
     // Forgets a request that has finished and been released.
     void drop(int req_id);
+    // True when drop(req_id) would succeed: finished and in no queue.
+    bool droppable(int req_id) const;
     Request* find(int req_id);
     const Request* find(int req_id) const;
 
@@ -90,6 +101,7 @@ class ContinuousScheduler {
   private:
     BlockManager& bm_;
     int budget_, max_generated_;
+    int seq_len_ = 0, vocab_ = 0;
     std::deque<Request*> waiting_;
     std::vector<Request*> running_;
     std::vector<std::unique_ptr<Request>> requests_;

@@ -93,25 +93,29 @@ bool rows_share_pages(SchedDevice& d, const StepPlan& p, int num_pages) {
     return false;
 }
 
-// Refuses, before any state changes, a step the model could not run: a
-// position at or past seq_len, a token outside the vocabulary.
-void check_step_fits(const ContinuousScheduler& h, int seq_len, int vocab) {
-    for (const Request* r : h.running()) {
+// Requests the model cannot run are finished with the tokens they have,
+// before any state changes, instead of failing this and every later step:
+// a running request that would decode at or past seq_len or whose next token
+// lies outside the vocabulary; a queue head whose prompt holds a token outside
+// the vocabulary or would decode past seq_len before it finishes (its prompt
+// of n tokens ends at position n + max_generated - 2).  The reference has no
+// such check (its pools would be indexed out of bounds).
+void retire_unrunnable(ContinuousScheduler& h, SchedDevice& d, int seq_len, int vocab) {
+    for (Request* r : h.running()) {
         if (r->is_finished) continue;
-        if (r->seq.logical_token_count >= seq_len)
-            throw Error(ERR_INVALID_ARGUMENT, "request " + std::to_string(r->req_id) +
-                                                  " would decode at position " +
-                                                  std::to_string(r->seq.logical_token_count) +
-                                                  ", past the model's seq_len");
-        if (r->next_token_to_process < 0 || r->next_token_to_process >= vocab)
-            throw Error(ERR_INVALID_ARGUMENT, "token outside the vocabulary");
+        if (r->seq.logical_token_count >= seq_len || r->next_token_to_process < 0 ||
+            r->next_token_to_process >= vocab)
+            r->is_finished = true;  // released at the start of this step's plan
     }
-    if (const Request* r = h.waiting_head()) {
-        if ((int)r->prompt_tokens.size() > seq_len)
-            throw Error(ERR_INVALID_ARGUMENT, "request " + std::to_string(r->req_id) +
-                                                  " has a prompt longer than the model's seq_len");
-        for (int32_t t : r->prompt_tokens)
-            if (t < 0 || t >= vocab) throw Error(ERR_INVALID_ARGUMENT, "prompt token outside the vocabulary");
+    while (const Request* head = h.waiting_head()) {
+        bool ok = (long long)head->prompt_tokens.size() + h.max_generated() - 1 <= seq_len;
+        for (int32_t t : head->prompt_tokens) ok &= t >= 0 && t < vocab;
+        if (ok) break;
+        Request* r = h.find(head->req_id);
+        if (r->slot >= 0) d.free_rows.push_back(r->slot);  // a resident table row, if it had one
+        r->slot = -1;
+        r->pages_on_device = 0;
+        h.reject_head();
     }
 }
 
@@ -150,7 +154,9 @@ int nitro_sched_step(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* p
         SchedDevice& d = *sched->dev;
         require(d.pool == pool && d.model == model, ERR_INVALID_ARGUMENT,
                 "a scheduler steps one model over one pool (those of its first step)");
-        check_step_fits(h, seq_len, vocab);
+        h.set_limits(seq_len, vocab);
+        retire_unrunnable(h, d, seq_len, vocab);
+        if (!h.has_active_requests()) return;
 
         const StepPlan& p = h.plan();
         // From here on a failure leaves the step planned: the scheduler can

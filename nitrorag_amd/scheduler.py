@@ -82,6 +82,12 @@ class ContinuousScheduler:
         N.call("nitro_sched_add_request", self._h, int(req_id), t.ctypes.data_as(N._i32p), t.size)
         self.prompts[int(req_id)] = t.tolist()
 
+    def set_limits(self, seq_len: int, vocab: int) -> None:
+        """Admission limits (0 = none): add_request then refuses a prompt with a
+        token outside [0, vocab) or with len + max_generated - 1 > seq_len.  A
+        device step sets them from its model."""
+        N.call("nitro_sched_set_limits", self._h, int(seq_len), int(vocab))
+
     def has_active_requests(self) -> bool:
         v = ctypes.c_int32()
         N.call("nitro_sched_has_active_requests", self._h, ctypes.byref(v))

@@ -351,3 +351,68 @@ def test_full_size_b64_ctx4096_32x128_subset_vs_oracle():
     assert pool.take_device_errors() == 0
     del k, v
     torch.cuda.empty_cache()
+
+
+def test_long_context_decode_splits_past_the_lds_table_slice():
+    """Contexts past 1,022 pages per split (16,352 tokens) force split-K whatever
+    the launch heuristic picks (each split's block-table slice is staged in
+    LDS): two sequences at 20,000 and 33,000 tokens beside a short one."""
+    say("long-context decode (ctx 20000 / 33000)")
+    rng = np.random.default_rng(21)
+    c = DecodeCase(rng, np.array([20000, 7, 33000]), 4, 4, 64, 3400, 1, 0)
+    assert_parity(c.run_gpu(), c.run_oracle(), "long context")
+    assert c.pool.take_device_errors() == 0
+
+
+def test_oversized_pool_reports_device_alloc():
+    """A pool larger than the GPU's memory fails with NITRO_ERR_DEVICE_ALLOC (the
+    reference exits at src/pagedMemory.hpp:96) and leaves later launches working."""
+    say("oversized pool")
+    import nitrorag_amd as na
+    from nitrorag_amd import _native as N
+
+    h = ctypes.c_void_p()
+    # 1.2M pages x 16 x 4096 floats = 314 GB per pool, above the 288 GB of HBM
+    st = N.lib().nitro_kvpool_create(1_200_000, 1, 4096, ctypes.byref(h))
+    assert st == N.DEVICE_ALLOC and not h.value, N.last_error()
+    c = make_case("mha_hd32")
+    assert_parity(c.run_gpu(), c.run_oracle(), "after a failed allocation")
+
+
+def test_prefill_scatter_of_more_rows_than_a_grid_dimension():
+    """KV scatter of a prefill batch of 72,000 rows (72 chunks of 1,000 tokens at
+    non-page-aligned starts), more than the 65,535 workgroups one grid dimension
+    holds: the pools match the oracle's scatter (src/model_q8.cpp:473-484) bit
+    for bit."""
+    say("prefill scatter of 72,000 rows")
+    import torch
+
+    import nitrorag_amd as na
+
+    rng = np.random.default_rng(33)
+    B, T, kv_dim = 72, 1000, 32
+    starts = rng.integers(0, 40, size=B).astype(np.int32)
+    lens = np.full(B, T, np.int32)
+    need = (starts + lens + 15) // 16
+    pages = int(need.sum())
+    perm = rng.permutation(pages).astype(np.int32)
+    tables = np.zeros((B, int(need.max())), np.int32)
+    off = 0
+    for b in range(B):
+        tables[b, :need[b]] = perm[off:off + need[b]]
+        off += need[b]
+    k = rng.standard_normal((pages, 1, 16, kv_dim)).astype(np.float32)
+    v = rng.standard_normal((pages, 1, 16, kv_dim)).astype(np.float32)
+    kc = rng.standard_normal((B * T, kv_dim)).astype(np.float32)
+    vc = rng.standard_normal((B * T, kv_dim)).astype(np.float32)
+    dk, dv = to_gpu(k), to_gpu(v)
+    pool = na.KVPool.wrap(dk, dv)
+    pool.upload_prefill_batch(tables, starts, lens)
+    pool.kv_append_prefill(0, to_gpu(kc), to_gpu(vc))
+    torch.cuda.synchronize()
+    for b in range(B):
+        attn.kv_scatter_prefill(k, v, 0, kc[b * T:(b + 1) * T], vc[b * T:(b + 1) * T], tables[b],
+                                int(starts[b]))
+    assert np.array_equal(dk.cpu().numpy(), k)
+    assert np.array_equal(dv.cpu().numpy(), v)
+    assert pool.take_device_errors() == 0

@@ -186,9 +186,15 @@ def test_full_row_products_over_many_rows(name):
 @pytest.mark.parametrize("name,dims", [
     # rows of 2048-2304 k: every product of 1-4 rows takes the flat kernel (x in LDS)
     ("wide", (2048, 2304, 1, 16, 4, 500, 128)),
-    # rows of 4608 k: 1-3 rows take the flat kernel, 4 rows (4 * 4608 floats of x
-    # exceed its LDS) the row-streaming one
+    # rows of 4608 k: wq/wk/wv and w1/w3 take the flat kernel at 1-3 rows and the
+    # row-streaming one at 4 (4 * 4608 floats of x exceed its 16384-float budget);
+    # wo (residual epilogue, 39936 floats) stays on the flat kernel at 1-4 rows
     ("wider", (4608, 2304, 1, 36, 4, 300, 64)),
+    # w2 over rows of 18944 k (a Qwen2-7B FFN width): 2 rows = 37888 floats of x, the
+    # top of the residual flat kernel's budget, where every thread stages 10 float4
+    ("ffn18944", (512, 18944, 1, 8, 8, 300, 64)),
+    # w2 over rows of 11008 k (Llama-2-7B): 3 rows = 33024 floats on the flat kernel
+    ("ffn11008", (512, 11008, 1, 8, 8, 300, 64)),
 ])
 def test_small_batches_over_long_rows(name, dims):
     """Full-row products of 1-4 activation rows over rows of >= 2048 k, with

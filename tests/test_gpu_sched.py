@@ -83,8 +83,12 @@ def test_scheduler_steps_match_reference(golden_sched, golden_model):
         pool.close()
 
 
-def test_scheduler_refuses_positions_past_seq_len(golden_model):
-    """A step that would decode at seq_len is refused before any state changes."""
+def test_scheduler_finishes_requests_the_model_cannot_run(golden_model):
+    """A request the model cannot run no longer fails the step (and with it every
+    later step): the device step binds the model's limits, finishes a queued
+    prompt that cannot fit seq_len unserved, and finishes a running request
+    that would decode at seq_len with the tokens it has; add_request then
+    refuses such prompts up front."""
     import nitrorag_amd as na
     from nitrorag_amd.q8 import LAST_BLOCK
 
@@ -94,19 +98,26 @@ def test_scheduler_refuses_positions_past_seq_len(golden_model):
     pool = na.KVPool(16, model.n_layers, model.kv_dim)
     bm = na.BlockManager(16)
     S = na.ContinuousScheduler(bm, 256, 1000)
-    S.add_request(0, [1] * (seq_len + 1))
-    words = S.state_words()
+    S.add_request(0, [1] * (seq_len + 1))  # no limits bound yet: queued
+    S.step(model, pool, LAST_BLOCK)
+    st = S.request_status(0)
+    assert st["is_finished"] == 1 and st["generated"] == 0 and st["logical_token_count"] == 0
+    assert not S.has_active_requests()
     with pytest.raises(na.NitroError):
-        S.step(model, pool, LAST_BLOCK)
-    assert S.state_words() == words
+        S.add_request(1, [1] * (seq_len + 1))
+    S.drop_request(0)
+    assert bm.get_free_count() == 16
     S2 = na.ContinuousScheduler(bm, 256, 1000)
     S2.add_request(1, [2] * (seq_len - 1))
-    S2.step(model, pool, LAST_BLOCK)      # prefill to seq_len - 1 tokens
-    S2.step(model, pool, LAST_BLOCK)      # decodes at position seq_len - 1
-    words = S2.state_words()
-    with pytest.raises(na.NitroError):
-        S2.step(model, pool, LAST_BLOCK)  # position seq_len: refused
-    assert S2.state_words() == words
+    S2.plan()
+    S2.commit(5, [])                      # host path: the prompt's one chunk
+    S2.plan()
+    S2.commit(0, [6])                     # decode at position seq_len - 1
+    S2.step(model, pool, LAST_BLOCK)      # would decode at seq_len: finished instead
+    st = S2.request_status(1)
+    assert st["is_finished"] == 1 and S2.generated(1) == [5, 6]
+    assert not S2.has_active_requests()
+    assert pool.take_device_errors() == 0
 
 
 def test_device_argmax_quirks():

@@ -147,3 +147,45 @@ def test_server_intake_numbers_requests_like_the_reference():
     N.call("nitro_server_destroy", srv)  # closes the three duplicated descriptors
     for x, y in pairs + [(a, b)]:
         x.close(), y.close()
+
+
+def test_server_refuses_prompts_the_model_cannot_finish():
+    """With the model's limits set on the scheduler, a prompt of n tokens is
+    admitted only if its last decode (position n + max_generated - 2) lies
+    below seq_len and every token is in the vocabulary; a refused prompt adds
+    no request, takes no request id and leaves the fd with the caller."""
+    from oracle import scheduler as sc
+
+    bm = na.BlockManager(16)
+    sched = na.ContinuousScheduler(bm, 256, 20)
+    sched.set_limits(64, 100)
+    srv = ctypes.c_void_p()
+    N.call("nitro_server_create", sched.handle, ctypes.c_void_p(1), ctypes.c_void_p(1), 1, 128, ctypes.byref(srv))
+    cases = [(list(range(1, 46)), True),        # 45 + 19 = 64 <= 64: the last decode sits at 63
+             (list(range(1, 47)), False),       # 46 + 19 = 65 > 64
+             ([3, 100, 4], False),              # token outside the vocabulary
+             ([-1], False),
+             ([99], True)]
+    pairs, want_ids = [], []
+    for prompt, ok in cases:
+        a, b = socket.socketpair()
+        b.sendall(np.asarray([len(prompt)] + prompt, np.int32).tobytes())
+        rid = ctypes.c_int32(-7)
+        fd = os.dup(a.fileno())
+        st = N.lib().nitro_server_accept_fd(srv, fd, ctypes.byref(rid))
+        if ok:
+            assert st == N.OK and rid.value == len(want_ids)
+            want_ids.append(rid.value)
+        else:
+            assert st == N.INVALID_ARGUMENT and rid.value == -7
+            os.close(fd)  # still the caller's
+        pairs.append((a, b))
+    st = sc.decode_state(sched.state_words())
+    assert st["waiting"] == want_ids
+    # the scheduler's own entry point applies the same limits
+    with pytest.raises(N.NitroError):
+        sched.add_request(50, list(range(1, 47)))
+    sched.add_request(50, list(range(1, 46)))
+    N.call("nitro_server_destroy", srv)
+    for x, y in pairs:
+        x.close(), y.close()
