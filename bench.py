@@ -19,8 +19,10 @@ Reported:
                     per launch measured with rocprofv3 (profiles/)
   cpu_baseline      the CPU oracle (C restatement of the reference's OpenMP
                     loops, all host cores) on a sample of the same workload
-Algorithmic bytes per decode launch: sum_b ctx_b*Hkv*hd*4*2 (K and V) +
-B*H*hd*4*2 (q in, out) + sum_b ceil(ctx_b/16)*4 (block-table entries).
+Algorithmic bytes per decode launch (append fused): sum_b ctx_b*Hkv*hd*4*2 (K
+and V, the new row read from the appended k/v) + B*H*hd*4*2 (q in, out) +
+sum_b ceil(ctx_b/16)*4 (block-table entries) + B*Hkv*hd*4*2 (the new rows
+written into their pages).
 
 Other workloads (the other paged-attention shapes, the model step around the path,
 Q8 products and the serving loop):
@@ -63,6 +65,11 @@ DEFAULT_WORKLOAD = "decode-b64-ctx4096"
 def decode_bytes(ctx, B: int, H: int, Hkv: int, hd: int) -> int:
     ctx = np.asarray(ctx, dtype=np.int64)
     return int((ctx * Hkv * hd * 4 * 2).sum() + B * H * hd * 4 * 2 + ((ctx + 15) // 16 * 4).sum())
+
+
+def append_bytes(B: int, Hkv: int, hd: int) -> int:
+    """The new K and V row of every sequence written into its page."""
+    return B * Hkv * hd * 4 * 2
 
 
 def seeded_tables(ctx, pages: int, seed: int) -> np.ndarray:
@@ -144,10 +151,11 @@ class DecodeWorkload:
         for i, layer in enumerate(self.steps_layers):
             if self.scratch is not None:
                 torch.sum(self.scratch, dim=0, out=self.flush_out)
-            self.pool.kv_append(layer, self.knew[i], self.vnew[i], stream)
             if events is not None:
                 events[i][0].record(stream)
-            self.pool.decode(layer, self.q[i], self.out[i], self.H, self.Hkv, self.hd, stream)
+            # append + attend (one launch: no other sequence reads a page being appended to)
+            self.pool.decode_append(layer, self.q[i], self.knew[i], self.vnew[i], self.out[i], self.H,
+                                    self.Hkv, self.hd, stream)
             if events is not None:
                 events[i][1].record(stream)
 
@@ -155,7 +163,8 @@ class DecodeWorkload:
         return len(self.steps_layers)
 
     def work_per_launch(self):
-        return decode_bytes(self.ctx, self.B, self.H, self.Hkv, self.hd)
+        # the launch also writes each sequence's new K/V row into its page
+        return decode_bytes(self.ctx, self.B, self.H, self.Hkv, self.hd) + append_bytes(self.B, self.Hkv, self.hd)
 
     def tokens_per_step(self):
         return self.B
@@ -752,7 +761,7 @@ def kernel_name(w) -> str:
         while qh * 2 <= (8 if w.hd <= 64 else 4 if w.hd == 128 else 2) and kv_mul % (qh * 2) == 0:
             qh *= 2
         stream = qh == kv_mul and w.unique_pages is None
-        return f"paged_attn_decode_kernel<{w.hd}, {qh}, {str(stream).lower()}>"
+        return f"paged_attn_decode_kernel<{w.hd}, {qh}, {str(stream).lower()}, true> (append fused)"
     kern = os.environ.get("NITRO_PREFILL_KERNEL")
     if w.hd == 256 or kern == "valu":
         return f"paged_attn_prefill_kernel<{w.hd}> (VALU)"

@@ -38,7 +38,7 @@ extern "C" {
 enum {
     NITRO_OK = 0,
     NITRO_ERR_INVALID_ARGUMENT = 1, /* bad pointer, id, shape or layer */
-    NITRO_ERR_UNSUPPORTED = 2,      /* head_dim outside {32, 64, 128, 256}, n_heads % n_kv_heads != 0 */
+    NITRO_ERR_UNSUPPORTED = 2,      /* head_dim not a multiple of 4 in [4, 256], n_heads % n_kv_heads != 0 */
     NITRO_ERR_DEVICE_ALLOC = 3,     /* hipMalloc failed (reference: src/pagedMemory.hpp:96) */
     NITRO_ERR_OUT_OF_PAGES = 4,     /* no free page and nothing evictable (src/pagedMemory.hpp:117,212) */
     NITRO_ERR_BAD_BLOCK_TABLE = 5,  /* page id outside the pool, or pos beyond the table */
@@ -155,12 +155,27 @@ int nitro_kv_append(nitro_kvpool* pool, int32_t layer, const float* k, const flo
 /* Batched paged-attention decode — src/model_q8.cpp:625-662 (batched) and
  * :290-347 (single sequence, batch = 1).  q, out: device [batch][n_heads*head_dim].
  * For each (b, h): softmax over keys 0..pos_b of q.k/sqrt(head_dim), times V,
- * with kv head h / (n_heads/n_kv_heads).  One kernel launch: split-K over
- * pages with an online softmax; the last workgroup of each (b, h) merges the
- * partials.  Not re-entrant per pool: launches that overlap on one pool race
- * on its split-K workspace. */
+ * with kv head h / (n_heads/n_kv_heads).  head_dim: any multiple of 4 from 4
+ * to 256.  One kernel launch: long contexts are split over workgroups (sized
+ * from the batch's context lengths, so the GPU fills with even work), each
+ * keeps an online softmax, and the last workgroup of a (b, head) to finish
+ * merges the splits' partials in split order.  The first launch for an
+ * uploaded batch may also copy a small work list (host to device, on
+ * `stream`), and a launch that needs more split-K workspace than the pool
+ * holds allocates it (hipMalloc, hipMemset).  Not re-entrant per pool:
+ * launches that overlap on one pool race on its workspace and counters. */
 int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
                             int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void* stream);
+
+/* nitro_kv_append followed by nitro_paged_attn_decode, as forward_decode_batch
+ * does them (src/model_q8.cpp:616-662): k, v device [batch][kv_dim] are written
+ * at each sequence's pos and attended.  One launch when no other sequence of
+ * the batch reads the page holding a sequence's pos (the row is then read from
+ * k / v directly); otherwise the append and the decode launch in turn.  The
+ * pool and output equal those of the two calls. */
+int nitro_paged_attn_decode_append(nitro_kvpool* pool, int32_t layer, const float* q, const float* k,
+                                   const float* v, float* out, int32_t n_heads, int32_t n_kv_heads,
+                                   int32_t head_dim, void* stream);
 
 /* ----------------------------- prefill -----------------------------------
  * A prefill batch of chunks, one per sequence — forward_prefill_chunk
@@ -181,7 +196,8 @@ int nitro_kv_append_prefill(nitro_kvpool* pool, int32_t layer, const float* k, c
 
 /* Causal paged prefill attention — src/model_q8.cpp:485-523.  q, out: device
  * [total_tokens][n_heads*head_dim]; the token at pos attends keys 0..pos
- * (prefix-hit pages, earlier chunks and this chunk's own rows). */
+ * (prefix-hit pages, earlier chunks and this chunk's own rows).  head_dim: any
+ * multiple of 4 from 4 to 256 (32, 64 and 128 run on the matrix cores). */
 int nitro_paged_attn_prefill(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
                              int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void* stream);
 

@@ -117,6 +117,17 @@ class KVPool:
         N.call("nitro_paged_attn_decode", self._h, layer, _dev(q, "q"), _dev(out, "out"), n_heads,
                n_kv_heads, head_dim, _stream_ptr(stream))
 
+    def decode_append(self, layer: int, q, k, v, out, n_heads: int, n_kv_heads: int, head_dim: int,
+                      stream=None) -> None:
+        """kv_append + decode in one call (one launch where no other sequence
+        reads the page a sequence appends to)."""
+        self._need(q, self.decode_batch * n_heads * head_dim, "q")
+        self._need(out, self.decode_batch * n_heads * head_dim, "out")
+        self._need(k, self.decode_batch * self.kv_dim, "k")
+        self._need(v, self.decode_batch * self.kv_dim, "v")
+        N.call("nitro_paged_attn_decode_append", self._h, layer, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"),
+               _dev(out, "out"), n_heads, n_kv_heads, head_dim, _stream_ptr(stream))
+
     # --------------------------------------------------------------- prefill
     def upload_prefill_batch(self, tables, start_pos, num_tokens, stream=None) -> None:
         t = _host_i32(tables)

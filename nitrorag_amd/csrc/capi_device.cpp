@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -47,13 +48,17 @@ void check_table_rows(const nitro_kvpool* pool, const int32_t* tables, int b, in
                                                  std::to_string(pool->num_pages) + ")");
 }
 
-// True when a page id occurs in the used part of more than one table row (a
-// prefix shared through the prefix cache), or twice in one row.  Decode then
-// keeps plain loads so that the page's lines stay cached for the other readers.
+// Scans the pages the batch reads.  Returns true when a page id occurs in the
+// used part of more than one table row (a prefix shared through the prefix
+// cache), or twice in one row: decode then keeps plain loads so that the
+// page's lines stay cached for the other readers.  Also records whether every
+// row's page at pos_b is read by that row alone (then the fused append may
+// write it while the other rows read the pool).
 bool any_page_shared(const nitro_kvpool* pool, DecodeBatch& d, const int32_t* tables,
                      const int32_t* positions, int batch, int max_pages) {
     if (d.page_mark.size() != (size_t)pool->num_pages || d.stamp == UINT32_MAX) {
         d.page_mark.assign(pool->num_pages, 0);
+        d.page_multi.assign(pool->num_pages, 0);
         d.stamp = 0;
     }
     const uint32_t stamp = ++d.stamp;
@@ -62,10 +67,16 @@ bool any_page_shared(const nitro_kvpool* pool, DecodeBatch& d, const int32_t* ta
         const int32_t* row = tables + (size_t)b * max_pages;
         for (int i = 0; i <= (positions[b] >> 4); i++) {
             uint32_t& m = d.page_mark[row[i]];  // ids were checked against the pool
-            shared |= m == stamp;
+            if (m == stamp) {
+                shared = true;
+                d.page_multi[row[i]] = stamp;
+            }
             m = stamp;
         }
     }
+    d.new_rows_private = true;
+    for (int b = 0; b < batch && shared; b++)
+        d.new_rows_private &= d.page_multi[tables[(size_t)b * max_pages + (positions[b] >> 4)]] != stamp;
     return shared;
 }
 
@@ -73,7 +84,7 @@ void check_shape(const nitro_kvpool* pool, int layer, int n_heads, int n_kv_head
     require(layer >= 0 && layer < pool->num_layers, ERR_INVALID_ARGUMENT, "layer out of range");
     require(n_heads > 0 && n_kv_heads > 0, ERR_INVALID_ARGUMENT, "head counts must be positive");
     require(n_heads % n_kv_heads == 0, ERR_UNSUPPORTED, "n_heads must be a multiple of n_kv_heads");
-    require(supported_head_dim(head_dim), ERR_UNSUPPORTED, "head_dim must be 32, 64, 128 or 256");
+    require(attention_head_dim(head_dim), ERR_UNSUPPORTED, "head_dim must be a multiple of 4 from 4 to 256");
     require(n_kv_heads * head_dim == pool->kv_dim, ERR_INVALID_ARGUMENT,
             "n_kv_heads * head_dim must equal the pool's kv_dim");
 }
@@ -81,6 +92,201 @@ void check_shape(const nitro_kvpool* pool, int layer, int n_heads, int n_kv_head
 int env_int(const char* name, int fallback) {
     const char* v = std::getenv(name);
     return v && *v ? std::atoi(v) : fallback;
+}
+
+// Launch shape of one decode launch, chosen from the batch's context lengths.
+struct DecodeShape {
+    int qh = 1, waves = 4, tps = 1;  // query heads / waves per workgroup, tiles per split
+    std::vector<int> splits;         // per sequence
+    bool uniform = true;             // every sequence has the same number of splits
+};
+
+// Waves resident per CU at the kernel's occupancy (16; 8 with several query
+// heads per workgroup, which take twice the registers) and the waves per
+// workgroup, 4..16.  Splits are sized so that every workgroup of the launch is
+// resident in one dispatch round with as few tile rounds per wave as possible:
+//  - a batch that fills the GPU at 4 waves per workgroup is not split (the
+//    most waves per workgroup when the launch takes several dispatch rounds
+//    anyway: each workgroup's waves stream one sequence's K/V together, which
+//    measured 0.3-1% faster at B=64 ctx 4096 than 4 waves);
+//  - otherwise, for W = 4, 8, 16 waves, the smallest split of W*R tiles whose
+//    workgroups all fit; the W with the fewest rounds R wins, then the one
+//    with the fewest splits.  Long sequences split into equal runs, short ones
+//    not at all, and every split is at most R tile rounds per wave.
+DecodeShape plan_decode_shape(const nitro_kvpool* pool, const std::vector<int32_t>& positions, int n_heads,
+                              int n_kv_heads, int head_dim) {
+    DecodeShape sh;
+    const int tile = decode_tile_rows(head_dim);
+    const int B = (int)positions.size();
+    std::vector<int> n(B);
+    int max_n = 1;
+    for (int b = 0; b < B; b++) max_n = std::max(max_n, n[b] = (positions[b] + 1 + tile - 1) / tile);
+    const int kv_mul = n_heads / n_kv_heads;
+    int qh = env_int("NITRO_DECODE_HEADS_PER_WG", 0);
+    if (qh <= 0) {
+        qh = 1;
+        while (qh * 2 <= decode_max_heads_per_wg(head_dim) && kv_mul % (qh * 2) == 0) qh *= 2;
+    }
+    require(qh <= decode_max_heads_per_wg(head_dim) && kv_mul % qh == 0, ERR_INVALID_ARGUMENT,
+            "NITRO_DECODE_HEADS_PER_WG must divide n_heads/n_kv_heads and fit the head_dim");
+    sh.qh = qh;
+    const long long cols = n_heads / qh;  // workgroups per item
+    const int max_waves = qh == 1 ? kDecodeMaxWaves : kDecodeMaxWaves / 2;
+    const long long target = (long long)(qh == 1 ? kDecodeWavesPerCU : kDecodeWavesPerCU / 2) *
+                             std::max(pool->num_cus, 1);
+    const int max_tps = (DECODE_MAX_SPLIT_PAGES - 2) * BLOCK_SIZE / tile;  // the LDS table slice
+    auto items_for = [&](int tps) {
+        long long k = 0;
+        for (int b = 0; b < B; b++) k += (n[b] + tps - 1) / tps;
+        return k;
+    };
+    const int env_waves = env_int("NITRO_DECODE_WAVES", 0);
+    const int env_tps = env_int("NITRO_DECODE_SPLIT_TILES", 0);
+    int waves = 0, tps = 0;
+    if (env_waves <= 0 && env_tps <= 0) {
+        if ((long long)B * cols * kDecodeMinWaves >= target) {
+            waves = kDecodeMinWaves;
+            if ((long long)B * cols * kDecodeMinWaves > target) {
+                waves = max_waves;
+                while (waves > kDecodeMinWaves && waves > max_n) waves /= 2;
+            }
+            tps = max_n;
+        } else {
+            long long best_rounds = LLONG_MAX, best_items = LLONG_MAX;
+            for (int w = kDecodeMinWaves; w <= max_waves; w *= 2) {
+                for (int rounds = 1;; rounds++) {
+                    const int c = std::min(w * rounds, max_tps);
+                    const long long k = items_for(c);
+                    if (k * cols * w <= target || c >= max_n || c == max_tps) {
+                        if (k * cols * w > target) break;  // this wave count never fits
+                        const long long r = (std::min(c, max_n) + w - 1) / w;
+                        if (r < best_rounds || (r == best_rounds && k < best_items)) {
+                            best_rounds = r;
+                            best_items = k;
+                            waves = w;
+                            tps = c;
+                        }
+                        break;
+                    }
+                }
+            }
+            if (waves == 0) {  // unreachable: 4 waves fit in this branch
+                waves = kDecodeMinWaves;
+                tps = max_n;
+            }
+        }
+    } else {
+        waves = env_waves > 0 ? env_waves : kDecodeMinWaves;
+        tps = env_tps > 0 ? env_tps : max_n;
+    }
+    sh.waves = std::max(kDecodeMinWaves, std::min(waves, max_waves));
+    sh.tps = std::max(1, std::min(tps, max_tps));
+    sh.splits.resize(B);
+    for (int b = 0; b < B; b++) {
+        sh.splits[b] = (n[b] + sh.tps - 1) / sh.tps;
+        sh.uniform &= sh.splits[b] == sh.splits[0];
+    }
+    return sh;
+}
+
+// One decode launch over the pool's uploaded batch (k_new / v_new: the fused
+// append, used by the caller only where it is safe).
+void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, const float* k_new,
+                   const float* v_new, int n_heads, int n_kv_heads, int head_dim, hipStream_t s) {
+    DecodeBatch& d = pool->decode;
+    const DecodeShape sh = plan_decode_shape(pool, d.positions, n_heads, n_kv_heads, head_dim);
+    const int tile = decode_tile_rows(head_dim);
+    const int B = d.batch;
+    int max_splits = 1;
+    long long slots = 0;
+    for (int x : sh.splits) {
+        max_splits = std::max(max_splits, x);
+        slots += x;
+    }
+    // A work list when sequences split unevenly (NITRO_DECODE_WORK_LIST=0/1
+    // forces it off/on); otherwise items are implied by the block id.
+    const int list_env = env_int("NITRO_DECODE_WORK_LIST", -1);
+    const bool use_list = list_env >= 0 ? list_env != 0 : (max_splits > 1 && !sh.uniform);
+    const int32_t* work = nullptr;
+    int work_items = 0;
+    if (use_list) {
+        if (d.work_generation != d.generation || d.work_tile != tile || d.work_tps != sh.tps) {
+            // items {b, split, first partial slot of b, ctx}: full splits first, then the
+            // last splits by size (longest first), each group in batch order
+            std::vector<std::pair<int, int>> order;  // (tiles, item)
+            std::vector<int32_t> host;
+            host.reserve(4 * (size_t)slots);
+            int slot0 = 0;
+            for (int b = 0; b < B; b++) {
+                const int ctx = d.positions[b] + 1, nt = (ctx + tile - 1) / tile;
+                for (int x = 0; x < sh.splits[b]; x++) {
+                    order.push_back({std::min(sh.tps, nt - x * sh.tps), (int)host.size() / 4});
+                    host.insert(host.end(), {b, x, slot0, ctx});
+                }
+                slot0 += sh.splits[b];
+            }
+            std::stable_sort(order.begin(), order.end(),
+                             [](const auto& x, const auto& y) { return x.first > y.first; });
+            const size_t n = host.size();
+            d.work.reserve(n);
+            int32_t* h = d.work_staging.acquire(n);
+            for (size_t i = 0; i < order.size(); i++)
+                std::memcpy(h + 4 * i, host.data() + 4 * (size_t)order[i].second, 4 * sizeof(int32_t));
+            d.work_staging.copy(d.work.ptr, h, n, s);
+            d.work_staging.finish(s);
+            d.work_generation = d.generation;
+            d.work_tile = tile;
+            d.work_tps = sh.tps;
+            d.work_items = (int32_t)order.size();
+        }
+        work = d.work.ptr;
+        work_items = d.work_items;
+    } else {
+        slots = (long long)B * max_splits;
+    }
+    const int pstride = (head_dim + 2 + 31) / 32 * 32;
+    if (max_splits > 1) {
+        pool->partials.reserve((size_t)slots * n_heads * pstride);
+        if (pool->counters.reserve((size_t)B * (n_heads / sh.qh)))
+            hip_check(hipMemset(pool->counters.ptr, 0, pool->counters.count * sizeof(int32_t)), "hipMemset");
+    }
+    DecodeLaunch a{};
+    a.q = q;
+    a.out = out;
+    a.k_pool = pool->k;
+    a.v_pool = pool->v;
+    a.tables = d.tables.ptr;
+    a.positions = d.pos.ptr;
+    a.work = work;
+    a.work_items = work_items;
+    a.partials = pool->partials.ptr;
+    a.counters = pool->counters.ptr;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.bad_pages = pool->bad_pages.ptr;
+    a.page_stride = pool->page_stride();
+    a.layer_off = pool->layer_offset(layer);
+    a.kv_dim = pool->kv_dim;
+    a.batch = B;
+    a.n_heads = n_heads;
+    a.kv_mul = n_heads / n_kv_heads;
+    a.head_dim = head_dim;
+    a.max_pages = d.max_pages;
+    a.num_pages = pool->num_pages;
+    a.tiles_per_split = sh.tps;
+    a.num_splits = use_list ? 0 : max_splits;
+    a.pstride = pstride;
+    a.waves = sh.waves;
+    a.heads_per_wg = sh.qh;
+    // Non-temporal K/V loads when every K/V line is read once per launch:
+    // one workgroup per KV head and no page shared between sequences.
+    const int stream_env = env_int("NITRO_DECODE_STREAM", -1);
+    a.stream_kv = stream_env >= 0 ? stream_env != 0 : (sh.qh == a.kv_mul && !d.shared_pages);
+    const int remap_env = env_int("NITRO_DECODE_XCD_REMAP", -1);
+    a.xcd_remap = remap_env >= 0 ? remap_env != 0 : sh.qh < a.kv_mul;
+    a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+    hip_check(launch_paged_attn_decode(a, s), "paged_attn_decode launch");
+    pool->last_stream = s;
 }
 
 }  // namespace
@@ -100,6 +306,8 @@ void set_device_decode_batch(nitro_kvpool* pool, int batch, int max_pages, const
     *device_slots = d.slots.ptr;
     d.positions.assign(positions, positions + batch);
     d.shared_pages = shared_pages;
+    d.new_rows_private = false;
+    d.generation++;
     d.batch = batch;
     d.max_pages = max_pages;
     *tables = d.tables.ptr;
@@ -222,6 +430,7 @@ int nitro_decode_batch_upload(nitro_kvpool* pool, const int32_t* tables, const i
         st.finish(s);
         d.positions.assign(positions, positions + batch);
         d.shared_pages = any_page_shared(pool, d, tables, positions, batch, max_pages);
+        d.generation++;
         d.batch = batch;
         d.max_pages = max_pages;
         pool->last_stream = s;
@@ -251,97 +460,32 @@ int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, f
         require_pool(pool);
         require(q != nullptr && out != nullptr, ERR_INVALID_ARGUMENT, "null q/out");
         check_shape(pool, layer, n_heads, n_kv_heads, head_dim);
+        require(pool->decode.batch > 0, ERR_NO_BATCH, "no decode batch uploaded");
+        launch_decode(pool, layer, q, out, nullptr, nullptr, n_heads, n_kv_heads, head_dim, as_stream(stream));
+    });
+}
+
+int nitro_paged_attn_decode_append(nitro_kvpool* pool, int32_t layer, const float* q, const float* k,
+                                   const float* v, float* out, int32_t n_heads, int32_t n_kv_heads,
+                                   int32_t head_dim, void* stream) {
+    return guarded([&] {
+        require_pool(pool);
+        require(q != nullptr && out != nullptr && k != nullptr && v != nullptr, ERR_INVALID_ARGUMENT,
+                "null q/k/v/out");
+        check_shape(pool, layer, n_heads, n_kv_heads, head_dim);
         const DecodeBatch& d = pool->decode;
         require(d.batch > 0, ERR_NO_BATCH, "no decode batch uploaded");
-
-        const int tile = decode_tile_rows(head_dim);
-        int max_tiles = 0;
-        for (int p : d.positions) max_tiles = std::max(max_tiles, (p + 1 + tile - 1) / tile);
-        // Query heads per workgroup: the most (1, 2, 4, 8) that divides the
-        // group size kv_mul within the register budget, so K/V rows are
-        // loaded once for all of them.
-        const int kv_mul = n_heads / n_kv_heads;
-        int qh = env_int("NITRO_DECODE_HEADS_PER_WG", 0);
-        if (qh <= 0) {
-            qh = 1;
-            while (qh * 2 <= decode_max_heads_per_wg(head_dim) && kv_mul % (qh * 2) == 0) qh *= 2;
-        }
-        require(qh <= decode_max_heads_per_wg(head_dim) && kv_mul % qh == 0, ERR_INVALID_ARGUMENT,
-                "NITRO_DECODE_HEADS_PER_WG must divide n_heads/n_kv_heads and fit the head_dim");
-        // Launch shape: ~16 resident waves per CU (8 with several heads per
-        // workgroup, which take twice the registers).  Give each workgroup as
-        // many waves (4, 8 or 16, never more than it has tiles) as keep every
-        // workgroup resident in one dispatch round, then split the context
-        // (split-K, one extra merge launch) only if the GPU is still less than
-        // half full.  Each split's block-table slice must fit in LDS.
-        const long long bh_count = (long long)d.batch * (n_heads / qh);
-        const int max_waves = qh == 1 ? kDecodeMaxWaves : kDecodeMaxWaves / 2;
-        const long long target =
-            (long long)(qh == 1 ? kDecodeWavesPerCU : kDecodeWavesPerCU / 2) * std::max(pool->num_cus, 1);
-        int waves = env_int("NITRO_DECODE_WAVES", 0);
-        if (waves <= 0) {
-            waves = kDecodeMinWaves;
-            if (bh_count * kDecodeMinWaves > target) {
-                // several dispatch rounds even at the fewest waves: the launch is
-                // throughput-bound, and the most waves per workgroup (each
-                // workgroup's waves streaming one sequence's K/V together)
-                // measured 0.3-1% faster at B=64 ctx 4096 than 4 waves
-                waves = max_waves;
-                while (waves > kDecodeMinWaves && waves > max_tiles) waves /= 2;
-            } else {
-                while (waves < max_waves && bh_count * waves * 2 <= target && waves < max_tiles)
-                    waves *= 2;
-            }
-        }
-        waves = std::max(kDecodeMinWaves, std::min(waves, max_waves));
-        int tps = env_int("NITRO_DECODE_SPLIT_TILES", 0);
-        if (tps <= 0) {
-            if (bh_count * waves >= target / 2 || max_tiles <= 2 * waves) {
-                tps = max_tiles;
-            } else {
-                const long long want_splits = (target + bh_count * waves - 1) / (bh_count * waves);
-                tps = (int)((max_tiles + want_splits - 1) / want_splits);
-                tps = (tps + waves - 1) / waves * waves;
-            }
-        }
-        const int max_tps = (DECODE_MAX_SPLIT_PAGES - 2) * BLOCK_SIZE / tile;
-        tps = std::max(1, std::min(tps, max_tps));
-        const int splits = (max_tiles + tps - 1) / tps;
-
         hipStream_t s = as_stream(stream);
-        const size_t bh = (size_t)d.batch * n_heads;
-        if (splits > 1) pool->partials.reserve(bh * splits * (head_dim + 2));
-        DecodeLaunch a{};
-        a.q = q;
-        a.out = out;
-        a.k_pool = pool->k;
-        a.v_pool = pool->v;
-        a.tables = d.tables.ptr;
-        a.positions = d.pos.ptr;
-        a.partials = pool->partials.ptr;
-        a.bad_pages = pool->bad_pages.ptr;
-        a.page_stride = pool->page_stride();
-        a.layer_off = pool->layer_offset(layer);
-        a.kv_dim = pool->kv_dim;
-        a.batch = d.batch;
-        a.n_heads = n_heads;
-        a.kv_mul = kv_mul;
-        a.head_dim = head_dim;
-        a.max_pages = d.max_pages;
-        a.num_pages = pool->num_pages;
-        a.tiles_per_split = tps;
-        a.num_splits = splits;
-        a.waves = waves;
-        // Non-temporal K/V loads when every K/V line is read once per launch:
-        // one workgroup per KV head and no page shared between sequences.
-        const int stream_env = env_int("NITRO_DECODE_STREAM", -1);
-        a.heads_per_wg = qh;
-        a.stream_kv = stream_env >= 0 ? stream_env != 0 : (qh == kv_mul && !d.shared_pages);
-        const int remap_env = env_int("NITRO_DECODE_XCD_REMAP", -1);
-        a.xcd_remap = remap_env >= 0 ? remap_env != 0 : qh < kv_mul;
-        a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
-        hip_check(launch_paged_attn_decode(a, s), "paged_attn_decode launch");
-        pool->last_stream = s;
+        if (d.new_rows_private || !d.shared_pages) {
+            launch_decode(pool, layer, q, out, k, v, n_heads, n_kv_heads, head_dim, s);
+        } else {  // another row reads a page being appended to: append first
+            hip_check(launch_kv_append_decode(pool->k, pool->v, k, v, d.tables.ptr, d.pos.ptr, d.batch,
+                                              d.max_pages, pool->kv_dim, pool->page_stride(),
+                                              pool->layer_offset(layer), pool->num_pages,
+                                              pool->bad_pages.ptr, s),
+                      "kv_append launch");
+            launch_decode(pool, layer, q, out, nullptr, nullptr, n_heads, n_kv_heads, head_dim, s);
+        }
     });
 }
 

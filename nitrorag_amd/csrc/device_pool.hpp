@@ -88,17 +88,24 @@ struct Staging {
     }
 };
 
-// Which head_dim values have kernels (template instantiations).
+// Head sizes the model step's fused kernels take.
 inline bool supported_head_dim(int hd) { return hd == 32 || hd == 64 || hd == 128 || hd == 256; }
 
 struct DecodeBatch {
     int32_t batch = 0, max_pages = 0;
     bool shared_pages = false;       // some page id is read by more than one sequence
+    bool new_rows_private = false;   // no row's page at pos_b is read by another row
     std::vector<int32_t> positions;  // host copy (launch geometry)
-    std::vector<uint32_t> page_mark; // per pool page: upload stamp (shared-page scan)
+    std::vector<uint32_t> page_mark, page_multi;  // per pool page: upload stamps (shared-page scan)
     uint32_t stamp = 0;
+    uint64_t generation = 0;         // bumped by every new batch (work-list cache key)
     DeviceBuffer<int32_t> tables, pos;
     DeviceBuffer<int32_t> slots;     // per row: page * 16 + position % 16 (where its K/V row goes)
+    // The decode work list last built for this batch, and what it was built for.
+    DeviceBuffer<int32_t> work;
+    uint64_t work_generation = ~0ull;
+    int32_t work_tile = 0, work_tps = 0, work_items = 0;
+    Staging work_staging;
 };
 
 struct PrefillBatch {
@@ -129,7 +136,8 @@ struct nitro_kvpool {
     hipStream_t last_stream = nullptr;
     nitro::DecodeBatch decode;
     nitro::PrefillBatch prefill;
-    nitro::DeviceBuffer<float> partials;      // split-K (m, l, acc[hd]) per (b, h, split)
+    nitro::DeviceBuffer<float> partials;      // split-K (acc[hd], m, l) per (partial slot, head)
+    nitro::DeviceBuffer<int32_t> counters;    // split-K arrivals per (b, head group), zero between launches
     nitro::DeviceBuffer<int32_t> bad_pages;   // [1] device error counter
     nitro::Staging decode_staging, prefill_staging;
 
@@ -143,21 +151,35 @@ namespace nitro {
 struct DecodeLaunch {
     const float* q;
     float* out;
-    const float* k_pool;
-    const float* v_pool;
+    float* k_pool;  // written only by the fused append (k_new != nullptr)
+    float* v_pool;
     const int32_t* tables;
     const int32_t* positions;
-    float* partials;
+    // Work list: 4 int32 per item {b, split, first partial slot of b, ctx_b},
+    // full items first; nullptr: item i is split i % num_splits of sequence
+    // i / num_splits (context from positions).
+    const int32_t* work;
+    int32_t work_items;
+    float* partials;    // split-K (acc[hd], m, l) per (partial slot, head), pstride floats each
+    int32_t* counters;  // per (b, head group): arrivals of the splits (zero between launches)
+    const float* k_new;  // fused append: [batch][kv_dim] rows written at pos_b (nullptr: none)
+    const float* v_new;
     int32_t* bad_pages;
     int64_t page_stride, layer_off;
     int32_t kv_dim, batch, n_heads, kv_mul, head_dim, max_pages, num_pages;
     int32_t tiles_per_split, num_splits;
-    int32_t waves;  // wavefronts per workgroup, 1..16, 64*waves >= head_dim
+    int32_t pstride;    // floats per partial, >= head_dim + 2
+    int32_t waves;  // wavefronts per workgroup, 4..16
     int32_t stream_kv;  // non-temporal K/V loads (lines read once per launch)
     int32_t xcd_remap;  // keep the workgroups that read one K/V range on one XCD
     int32_t heads_per_wg;  // query heads of one KV head per workgroup (divides kv_mul)
     float qscale;
 };
+// Head sizes attention takes: multiples of 4 up to 256 (kernels are built for
+// 32, 64, 128 and 256 and mask the columns past a smaller head size).
+inline bool attention_head_dim(int hd) { return hd >= 4 && hd <= 256 && hd % 4 == 0; }
+// The kernel width a head size runs at (32, 64, 128 or 256).
+int decode_padded_head_dim(int head_dim);
 // Rows per decode tile for a head_dim (the unit split-K partitions).
 int decode_tile_rows(int head_dim);
 // Most query heads one decode workgroup serves for a head_dim (1, 2, 4 or 8).

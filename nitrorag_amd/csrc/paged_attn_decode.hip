@@ -6,30 +6,44 @@
 //   table, kv head h / (H/Hkv)), p = softmax(s), o_h = sum_t p_t v_t.
 //
 // Design (bandwidth-bound: K and V are read exactly once per query head):
-//  - Grid: one workgroup of W wavefronts per (b, h, split), W = 4..16 chosen
-//    per launch (more waves per sequence when the batch is small, so enough
-//    loads are in flight and long contexts finish in few rounds).  A split is
-//    a run of `tiles_per_split` tiles of TILE consecutive context rows; waves
-//    take the split's tiles round-robin.
-//  - Lane layout: LG = 8 lanes share one K/V row (16 for hd=256) so that every
-//    global_load_dwordx4 reads whole 128-byte lines; a lane holds hd/LG floats
-//    of each of its RL rows (columns c*4 + j*4*LG).  The 64/LG row groups of a
-//    wave take interleaved rows of a TILE-row tile (64, 32, 16, 8 rows for
-//    hd = 32, 64, 128, 256); all 16 K/V float4 loads of a tile are issued
-//    before use.
-//  - q.k: hd/LG FMAs per lane and row, then a DPP butterfly across the LG lanes.
+//  - Work items: a (sequence, split) pair covers a run of at most
+//    `tiles_per_split` tiles of TILE consecutive context rows.  The grid is
+//    items x KV heads x head sub-groups, one workgroup of W wavefronts each
+//    (W = 4..16 per launch); waves take the item's tiles round-robin.  With
+//    a work list the host hands out only real items, full ones first
+//    (longest first), so every workgroup streams about the same number of
+//    tiles whatever the mix of context lengths; without one, item i is split
+//    i % num_splits of sequence i / num_splits and workgroups past a
+//    sequence's last split exit at once.
+//  - Lane layout: LG = 8 lanes share one K/V row (16 for a 256-wide head) so
+//    that every global_load_dwordx4 reads whole 128-byte lines; a lane holds
+//    HDP/LG floats of each of its RL rows (columns c*4 + j*4*LG).  HDP is the
+//    head size rounded up to 32, 64, 128 or 256: columns past the head size
+//    are masked (loaded as zero, never stored).  The 64/LG row groups of a
+//    wave take interleaved rows of a tile (64, 32, 16, 8 rows for HDP = 32,
+//    64, 128, 256); all 16 K/V float4 loads of a tile are issued before use.
+//  - q.k: HDP/LG FMAs per lane and row, then a DPP butterfly across LG lanes.
 //  - Softmax: every lane group keeps its own running (max, sum, acc) in base 2
 //    (q is pre-scaled by log2(e)/sqrt(hd)); groups, then waves (through LDS),
 //    then splits are merged with the usual rescaling.  No score scratch.
-//  - Split-K: when one split per (b, h) would leave the GPU underfilled, each
-//    workgroup writes (m, l, acc[hd]) for its split and a second, small
-//    kernel merges the splits.  With one split the workgroup writes the output
-//    directly and decode is a single launch.  (Merging inside the kernel by
-//    the last-arriving workgroup needs agent-scope release/acquire fences,
-//    which write back and invalidate the whole XCD L2 per workgroup on
-//    gfx950; measured, that halved throughput at two splits.)
-//  - The split's block-table slice is staged in LDS once; page ids outside
-//    the pool are counted in *bad_pages and their rows skipped (no fault).
+//  - Split-K merge in the same launch: a split writes (acc[hd], m, l) per
+//    query head with device-coherent stores (global_store ... sc1, written
+//    through the XCD's L2), waits for them (vmcnt(0)) and bumps its (b, head
+//    group)'s arrival counter; the workgroup that arrives last reads every
+//    split's partials with device-coherent loads, merges them in split order
+//    (results do not depend on arrival order), writes the output and resets
+//    the counter to zero for the next launch.  Nothing waits on another
+//    workgroup, and no fence writes back or invalidates a whole L2 (agent-
+//    scope release/acquire fences do both on gfx950; measured, those halved
+//    throughput at two splits).
+//  - Fused append (k_new / v_new given): row pos_b = ctx_b - 1 is read from
+//    the new K/V rows instead of the pool, and the workgroup holding that
+//    row (head sub-group 0 of the last split) writes them into the pool slot,
+//    i.e. forward_decode_batch's memcpy (src/model_q8.cpp:616-623) and its
+//    attention in one launch.  The host uses it only when no other row of the
+//    batch reads that page.
+//  - The item's block-table slice is staged in LDS once; page ids outside the
+//    pool are counted in *bad_pages and their rows skipped (no fault).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -42,18 +56,18 @@ namespace {
 constexpr int MAX_WAVES = 16;
 constexpr int MAX_THREADS = 64 * MAX_WAVES;
 
-template <int HD>
+template <int HDP>
 struct DecodeGeom {
     // LG lanes share a K/V row so that one load instruction reads whole
-    // 128-byte lines (8 lanes x 16 B; 16 lanes for hd=256, two lines).  Each
+    // 128-byte lines (8 lanes x 16 B; 16 lanes for HDP=256, two lines).  Each
     // lane holds NF4 float4 of a row (columns c*4 + j*4*LG) for RL rows per
     // tile: RL*NF4 = 8 float4 of K and 8 of V in flight per lane.
-    static constexpr int LG = HD <= 128 ? 8 : 16;
-    static constexpr int NF4 = HD / (4 * LG);
+    static constexpr int LG = HDP <= 128 ? 8 : 16;
+    static constexpr int NF4 = HDP / (4 * LG);
     static constexpr int RL = 8 / NF4;
     static constexpr int GROUPS = 64 / LG;  // row groups per wave
     static constexpr int TILE = RL * GROUPS;
-    static_assert(NF4 >= 1 && RL * NF4 == 8, "head_dim 32, 64, 128 or 256");
+    static_assert(NF4 >= 1 && RL * NF4 == 8, "padded head size 32, 64, 128 or 256");
 };
 
 template <int CTRL>
@@ -99,18 +113,35 @@ __device__ __forceinline__ float scale_of(float m, float m_new) {
     return m == -INFINITY ? 0.0f : exp2f(m - m_new);
 }
 
+// Device-coherent accesses of the split-K partials and arrival counters:
+// relaxed atomics at agent scope are global_store / global_load ... sc1 on
+// gfx950 (written through to, and read from, the point where the XCDs'
+// caches agree) with no whole-cache writeback or invalidate.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): this wave's
+// stores have completed.
+__device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // QH query heads of one KV head per workgroup (QH = 1 for MHA): each K/V
 // row is loaded once and scored against all QH queries.  QH > 1 needs about
-// twice the registers, so those workgroups hold at most 8 waves.
-template <int HD, int QH, bool STREAM>
+// twice the registers, so those workgroups hold at most 8 waves.  FULL: the
+// head size is HDP (no column masks).
+template <int HDP, int QH, bool STREAM, bool FULL>
 __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged_attn_decode_kernel(
     DecodeLaunch a) {
-    using G = DecodeGeom<HD>;
+    using G = DecodeGeom<HDP>;
     constexpr int LG = G::LG, NF4 = G::NF4, RL = G::RL, GROUPS = G::GROUPS, TILE = G::TILE;
     constexpr int MAXW = QH == 1 ? MAX_WAVES : MAX_WAVES / 2;
     __shared__ int32_t s_pages[DECODE_MAX_SPLIT_PAGES];
-    __shared__ float s_acc[MAXW][QH][HD];
+    __shared__ float s_acc[MAXW][QH][HDP];
     __shared__ float s_m[MAXW][QH], s_l[MAXW][QH];
+    __shared__ int s_last;
+    const int hd = FULL ? HDP : a.head_dim;
     const int waves = blockDim.x >> 6;
     const int threads = blockDim.x;
 
@@ -119,12 +150,12 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     const int g = lane / LG;
     const int c = lane % LG;
 
-    // Work order: ((b*Hkv + kv_h)*splits + split)*(kv_mul/QH) + r; the
-    // workgroup serves query heads h0 .. h0+QH-1, h0 = kv_h*kv_mul + r*QH, so
-    // the workgroups that read one K/V range are consecutive.  With
-    // xcd_remap, block ids are dealt to the 8 XCDs round-robin, so XCD x takes
-    // the x-th contiguous eighth of that order: workgroups sharing a K/V range
-    // run together on one XCD and re-read it from its L2.
+    // Work order: (item * Hkv + kv_h) * (kv_mul/QH) + r; the workgroup serves
+    // query heads h0 .. h0+QH-1, h0 = kv_h*kv_mul + r*QH, so the workgroups
+    // that read one K/V range are consecutive.  With xcd_remap, block ids are
+    // dealt to the 8 XCDs round-robin, so XCD x takes the x-th contiguous
+    // eighth of that order: workgroups sharing a K/V range run together on
+    // one XCD and re-read it from its L2.
     int w = blockIdx.x;
     if (a.xcd_remap) {
         const int n = gridDim.x, per = n >> 3, rem = n & 7;
@@ -132,18 +163,34 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
         w = x * per + min(x, rem) + (w >> 3);
     }
     const int hsubs = a.kv_mul / QH;
+    const int n_kv = a.n_heads / a.kv_mul;
     const int r = w % hsubs;
     const int rest = w / hsubs;
-    const int split = rest % a.num_splits;
-    const int grp = rest / a.num_splits;  // b*Hkv + kv_h
-    const int n_kv = a.n_heads / a.kv_mul;
-    const int b = grp / n_kv;
-    const int kv_h = grp - b * n_kv;
-    const int bh0 = b * a.n_heads + kv_h * a.kv_mul + r * QH;
-    // The position, q and this split's block-table slice are independent
-    // loads: issue them together.  The slice is read speculatively over the
-    // split's whole page range (clipped to the table row) and only the
-    // entries below the context length are validated and used.
+    const int kv_h = rest % n_kv;
+    const int item = rest / n_kv;
+    const int hg = kv_h * hsubs + r;  // head group of the sequence (arrival counter)
+    const int bh_in_seq = kv_h * a.kv_mul + r * QH;
+
+    // The item: from the work list {b, split, first partial slot of b, ctx},
+    // or implied by the block id (then the position load goes out together
+    // with the block-table slice and q below).
+    int b, split, pslot0, ctx;
+    if (a.work) {
+        const int4 it = reinterpret_cast<const int4*>(a.work)[item];
+        b = it.x;
+        split = it.y;
+        pslot0 = it.z;
+        ctx = it.w;
+    } else {
+        b = item / a.num_splits;
+        split = item - b * a.num_splits;
+        pslot0 = b * a.num_splits;
+        ctx = a.positions[b] + 1;
+    }
+    const int bh0 = b * a.n_heads + bh_in_seq;
+    // The split's block-table slice is read speculatively over the split's
+    // whole page range (clipped to the table row); only the entries below the
+    // context length are validated and used.
     constexpr int TBL_PER_THREAD = DECODE_MAX_SPLIT_PAGES / 256;  // >= 4 waves per workgroup
     const int tile_begin = split * a.tiles_per_split;
     const int page_begin = (tile_begin * TILE) >> 4;
@@ -155,22 +202,25 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
         const int i = threadIdx.x + k * threads;
         tv[k] = i < spec_end - page_begin ? trow[page_begin + i] : -1;
     }
-    const int ctx = a.positions[b] + 1;
 
-    // q slices of this lane, pre-scaled to base-2 logits.
+    // q slices of this lane, pre-scaled to base-2 logits (columns past the
+    // head size are zero).
     float4 qv[QH][NF4];
 #pragma unroll
     for (int qi = 0; qi < QH; qi++) {
-        const float* qp = a.q + (size_t)(bh0 + qi) * HD;
+        const float* qp = a.q + (size_t)(bh0 + qi) * hd;
 #pragma unroll
         for (int j = 0; j < NF4; j++) {
-            float4 t = *reinterpret_cast<const float4*>(qp + (c + j * LG) * 4);
+            const int col = (c + j * LG) * 4;
+            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (FULL || col < hd) t = *reinterpret_cast<const float4*>(qp + col);
             qv[qi][j] = make_float4(t.x * a.qscale, t.y * a.qscale, t.z * a.qscale, t.w * a.qscale);
         }
     }
 
+    ctx = min(ctx, a.max_pages * 16);  // a position past the table reads no further
     const int n_tiles = (ctx + TILE - 1) / TILE;
-    if (tile_begin >= n_tiles) return;  // uniform for the workgroup
+    if (tile_begin >= n_tiles) return;  // uniform for the workgroup (implied items only)
     const int tile_end = min(n_tiles, tile_begin + a.tiles_per_split);
     const int splits_b = (n_tiles + a.tiles_per_split - 1) / a.tiles_per_split;
 
@@ -190,8 +240,24 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     }
     __syncthreads();
 
-    const float* kbase = a.k_pool + a.layer_off + (size_t)kv_h * HD;
-    const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * HD;
+    const float* kbase = a.k_pool + a.layer_off + (size_t)kv_h * hd;
+    const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * hd;
+    // Fused append: the new row is read from k_new / v_new, and head
+    // sub-group 0 of the last split writes it into its page slot.
+    const int new_row = a.k_new ? ctx - 1 : -1;
+    const float* knew = a.k_new ? a.k_new + (size_t)b * a.kv_dim + (size_t)kv_h * hd : nullptr;
+    const float* vnew = a.v_new ? a.v_new + (size_t)b * a.kv_dim + (size_t)kv_h * hd : nullptr;
+    if (knew && r == 0 && tile_end == n_tiles) {
+        const int page = s_pages[((ctx - 1) >> 4) - page_begin];
+        if (page >= 0) {
+            const size_t off = a.layer_off + (size_t)page * a.page_stride + (size_t)((ctx - 1) & 15) * a.kv_dim +
+                               (size_t)kv_h * hd;
+            for (int f = threadIdx.x; f < hd / 4; f += threads) {
+                reinterpret_cast<float4*>(a.k_pool + off)[f] = reinterpret_cast<const float4*>(knew)[f];
+                reinterpret_cast<float4*>(a.v_pool + off)[f] = reinterpret_cast<const float4*>(vnew)[f];
+            }
+        }
+    }
 
     float m[QH], l[QH];
     float4 acc[QH][NF4];
@@ -215,10 +281,18 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
             any |= valid[i];
             if (valid[i]) {
                 const size_t off = (size_t)page * a.page_stride + (size_t)(row & 15) * a.kv_dim;
+                const bool fresh = row == new_row;
+                const float* kp = fresh ? knew : kbase + off;
+                const float* vp = fresh ? vnew : vbase + off;
 #pragma unroll
                 for (int j = 0; j < NF4; j++) {
-                    kr[i][j] = load_kv<STREAM>(kbase + off + (c + j * LG) * 4);
-                    vr[i][j] = load_kv<STREAM>(vbase + off + (c + j * LG) * 4);
+                    const int col = (c + j * LG) * 4;
+                    if (FULL || col < hd) {
+                        kr[i][j] = load_kv<STREAM>(kp + col);
+                        vr[i][j] = load_kv<STREAM>(vp + col);
+                    } else {
+                        kr[i][j] = vr[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
                 }
             } else {
 #pragma unroll
@@ -305,9 +379,9 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     }
     __syncthreads();
 
-    // Merge the waves: thread o owns output column o % HD of head o / HD.
-    for (int o = threadIdx.x; o < QH * HD; o += threads) {
-        const int qi = o / HD, d = o - qi * HD;
+    // Merge the waves: thread o owns output column o % hd of head o / hd.
+    for (int o = threadIdx.x; o < QH * hd; o += threads) {
+        const int qi = o / hd, d = o - qi * hd;
         float M = -INFINITY, L = 0.0f, A = 0.0f;
         for (int wv = 0; wv < waves; wv++) M = fmaxf(M, s_m[wv][qi]);
         for (int wv = 0; wv < waves; wv++) {
@@ -317,91 +391,96 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
         }
         const int bh = bh0 + qi;
         if (splits_b == 1) {
-            a.out[(size_t)bh * HD + d] = A / L;
+            a.out[(size_t)bh * hd + d] = A / L;
         } else {
-            float* part = a.partials + ((size_t)bh * a.num_splits + split) * (HD + 2);
-            part[d] = A;
+            float* part = a.partials + ((size_t)(pslot0 + split) * a.n_heads + bh - b * a.n_heads) * a.pstride;
+            store_coherent(part + d, A);
             if (d == 0) {
-                part[HD] = M;
-                part[HD + 1] = L;
+                store_coherent(part + hd, M);
+                store_coherent(part + hd + 1, L);
             }
         }
     }
-}
+    if (splits_b == 1) return;  // uniform for the workgroup
 
-// Merges the per-split partials of every (b, h) that has more than one split.
-template <int HD>
-__global__ __launch_bounds__(HD < 64 ? 64 : HD) void paged_attn_decode_merge_kernel(DecodeLaunch a) {
-    constexpr int TILE = DecodeGeom<HD>::TILE;
-    const int bh = blockIdx.x;
-    const int b = bh / a.n_heads;
-    const int ctx = a.positions[b] + 1;
-    const int n_tiles = (ctx + TILE - 1) / TILE;
-    const int splits_b = (n_tiles + a.tiles_per_split - 1) / a.tiles_per_split;
-    const int d = threadIdx.x;
-    if (splits_b <= 1 || d >= HD) return;  // single split: written by the main kernel
-    const float* pb = a.partials + (size_t)bh * a.num_splits * (HD + 2);
-    float M = -INFINITY;
-    for (int sp = 0; sp < splits_b; sp++) M = fmaxf(M, pb[sp * (HD + 2) + HD]);
-    float L = 0.0f, A = 0.0f;
-    for (int sp = 0; sp < splits_b; sp++) {
-        const float* ps = pb + sp * (HD + 2);
-        const float f = scale_of(ps[HD], M);
-        L += ps[HD + 1] * f;
-        A += ps[d] * f;
+    // Split-K: the last workgroup of this (b, head group) to arrive merges.
+    wait_vector_memory();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int* counter = a.counters + (size_t)b * (a.n_heads / QH) + hg;
+        const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = before == splits_b - 1;
+        if (before == splits_b - 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    a.out[(size_t)bh * HD + d] = A / L;
+    __syncthreads();
+    if (!s_last) return;
+    for (int o = threadIdx.x; o < QH * hd; o += threads) {
+        const int qi = o / hd, d = o - qi * hd;
+        const int h = bh_in_seq + qi;
+        float M = -INFINITY, L = 0.0f, A = 0.0f;
+        for (int sp = 0; sp < splits_b; sp++) {
+            const float* part = a.partials + ((size_t)(pslot0 + sp) * a.n_heads + h) * a.pstride;
+            const float ms = load_coherent(part + hd), ls = load_coherent(part + hd + 1);
+            const float as = load_coherent(part + d);
+            const float mm = fmaxf(M, ms);
+            const float f = scale_of(M, mm), fs = scale_of(ms, mm);
+            L = L * f + ls * fs;
+            A = A * f + as * fs;
+            M = mm;
+        }
+        a.out[(size_t)(bh0 + qi) * hd + d] = A / L;
+    }
 }
 
 }  // namespace
 
 int decode_max_heads_per_wg(int head_dim) {
-    return head_dim <= 64 ? 8 : head_dim == 128 ? 4 : 2;  // QH * head_dim <= 512
+    const int hdp = decode_padded_head_dim(head_dim);
+    return hdp <= 64 ? 8 : hdp == 128 ? 4 : 2;  // QH * HDP <= 512
+}
+
+int decode_padded_head_dim(int head_dim) {
+    return head_dim <= 32 ? 32 : head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
 }
 
 int decode_tile_rows(int head_dim) {
-    switch (head_dim) {
+    switch (decode_padded_head_dim(head_dim)) {
         case 32: return DecodeGeom<32>::TILE;
         case 64: return DecodeGeom<64>::TILE;
         case 128: return DecodeGeom<128>::TILE;
-        case 256: return DecodeGeom<256>::TILE;
-        default: return 0;
+        default: return DecodeGeom<256>::TILE;
     }
 }
 
-template <int HD, int QH>
+template <int HDP, int QH>
 static void launch_main(const DecodeLaunch& a, dim3 grid, hipStream_t stream) {
-    if (a.stream_kv)
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HD, QH, true>), grid, dim3(64 * a.waves), 0,
-                           stream, a);
+    const dim3 block(64 * a.waves);
+    if (a.head_dim != HDP)  // padded head: plain loads
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, false>), grid, block, 0, stream, a);
+    else if (a.stream_kv)
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, true, true>), grid, block, 0, stream, a);
     else
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HD, QH, false>), grid, dim3(64 * a.waves), 0,
-                           stream, a);
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, true>), grid, block, 0, stream, a);
 }
 
-template <int HD>
+template <int HDP>
 static hipError_t launch_hd(const DecodeLaunch& a, hipStream_t stream) {
     if (a.heads_per_wg < 1 || a.kv_mul % a.heads_per_wg != 0 ||
-        a.heads_per_wg > decode_max_heads_per_wg(HD) ||
+        a.heads_per_wg > decode_max_heads_per_wg(HDP) ||
         (a.heads_per_wg > 1 && a.waves > MAX_WAVES / 2))
         return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((size_t)a.batch * (a.n_heads / a.heads_per_wg) * a.num_splits));
+    const size_t items = a.work ? (size_t)a.work_items : (size_t)a.batch * a.num_splits;
+    const dim3 grid((unsigned)(items * (a.n_heads / a.heads_per_wg)));
     switch (a.heads_per_wg) {
-        case 1: launch_main<HD, 1>(a, grid, stream); break;
-        case 2: launch_main<HD, 2>(a, grid, stream); break;
+        case 1: launch_main<HDP, 1>(a, grid, stream); break;
+        case 2: launch_main<HDP, 2>(a, grid, stream); break;
         case 4:
-            if constexpr (4 * HD <= 512) launch_main<HD, 4>(a, grid, stream);
+            if constexpr (4 * HDP <= 512) launch_main<HDP, 4>(a, grid, stream);
             break;
         case 8:
-            if constexpr (8 * HD <= 512) launch_main<HD, 8>(a, grid, stream);
+            if constexpr (8 * HDP <= 512) launch_main<HDP, 8>(a, grid, stream);
             break;
         default: return hipErrorInvalidValue;
-    }
-    if (a.num_splits > 1) {
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(paged_attn_decode_merge_kernel<HD>, dim3((unsigned)(a.batch * a.n_heads)),
-                           dim3(HD < 64 ? 64 : HD), 0, stream, a);
     }
     return hipGetLastError();
 }
@@ -409,13 +488,14 @@ static hipError_t launch_hd(const DecodeLaunch& a, hipStream_t stream) {
 hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream) {
     // >= 4 waves: the block-table slice (<= DECODE_MAX_SPLIT_PAGES entries) is
     // loaded at most 4 entries per thread.
-    if (a.waves < 4 || a.waves > MAX_WAVES || 64 * a.waves < a.head_dim) return hipErrorInvalidValue;
-    switch (a.head_dim) {
+    if (a.waves < 4 || a.waves > MAX_WAVES || a.head_dim < 4 || a.head_dim > 256 || a.head_dim % 4 ||
+        a.pstride < a.head_dim + 2)
+        return hipErrorInvalidValue;
+    switch (decode_padded_head_dim(a.head_dim)) {
         case 32: return launch_hd<32>(a, stream);
         case 64: return launch_hd<64>(a, stream);
         case 128: return launch_hd<128>(a, stream);
-        case 256: return launch_hd<256>(a, stream);
-        default: return hipErrorInvalidValue;
+        default: return launch_hd<256>(a, stream);
     }
 }
 

@@ -40,7 +40,8 @@
 //    wave-uniformly: no per-lane skip may surround an MFMA.
 //  - Key groups hand (m, l, O) to key group 0 through LDS at the end.
 //
-// paged_attn_prefill_kernel<hd> (all hd; used for hd 256) is the VALU form:
+// paged_attn_prefill_kernel<HDP, FULL> (any head size that is a multiple of
+// 4 up to 256; used for hd 256 and sizes other than 32/64/128) is the VALU form:
 //  - A work item is up to BM=64 query rows of one chunk; grid = (work items,
 //    heads).  The host sorts work items by key count, longest first.
 //  - 256 threads: 4 lanes per query row, each lane holding hd/4 of q and of
@@ -81,14 +82,20 @@ __device__ __forceinline__ float scale_of(float m, float m_new) {
     return m == -INFINITY ? 0.0f : exp2f(m - m_new);
 }
 
-template <int HD>
+// HDP: the head size rounded up to 32, 64, 128 or 256 (the LDS and register
+// layout); FULL: the head size is HDP, otherwise columns past it are loaded
+// as zero and never stored.
+template <int HDP, bool FULL>
 __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaunch a) {
+    constexpr int HD = HDP;
     constexpr int F4 = HD / 4;               // float4 per row
     constexpr int SLOTS = F4 / 4;            // float4 per lane
     constexpr int LOADS = BN * F4 / THREADS; // float4 per thread per tile per matrix
     static_assert(LOADS >= 1 && BN * F4 % THREADS == 0, "tile shape");
     __shared__ float4 ks[BN][F4];
     __shared__ float4 vs[BN][F4];
+    const int hd = FULL ? HD : a.head_dim;
+    const int hd4 = hd / 4;
 
     // 1-D grid, heads fastest: the work list is sorted longest first, so every
     // head of the longest items is dispatched before any shorter item.
@@ -105,15 +112,15 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaun
     const int my_pos = start + q0 + min(row, qcount - 1);
     const int32_t* trow = a.tables + (size_t)seq * a.max_pages;
     const int n_tiles = last_pos / BN + 1;
-    const size_t dim = (size_t)a.n_heads * HD;
+    const size_t dim = (size_t)a.n_heads * hd;
     const size_t qrow = (size_t)(a.row_off[seq] + q0 + min(row, qcount - 1));
 
     float4 qv[SLOTS];
     {
-        const float4* qp = reinterpret_cast<const float4*>(a.q + qrow * dim + (size_t)h * HD);
+        const float4* qp = reinterpret_cast<const float4*>(a.q + qrow * dim + (size_t)h * hd);
 #pragma unroll
         for (int e = 0; e < SLOTS; e++) {
-            float4 t = qp[c + 4 * e];
+            float4 t = FULL || c + 4 * e < hd4 ? qp[c + 4 * e] : make_float4(0.f, 0.f, 0.f, 0.f);
             qv[e] = make_float4(t.x * a.qscale, t.y * a.qscale, t.z * a.qscale, t.w * a.qscale);
         }
     }
@@ -122,8 +129,8 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaun
     for (int e = 0; e < SLOTS; e++) acc[e] = make_float4(0.f, 0.f, 0.f, 0.f);
     float m = -INFINITY, l = 0.0f;
 
-    const float* kbase = a.k_pool + a.layer_off + (size_t)kv_h * HD;
-    const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * HD;
+    const float* kbase = a.k_pool + a.layer_off + (size_t)kv_h * hd;
+    const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * hd;
     float4 kreg[LOADS], vreg[LOADS];
 
     // Fetch: the tile's page ids first, then every K/V load unconditionally
@@ -147,8 +154,10 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaun
                     const int page = trow[key >> 4];
                     if ((unsigned)page < (unsigned)a.num_pages) {
                         const size_t off = (size_t)page * a.page_stride + (size_t)(key & 15) * a.kv_dim;
-                        kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
-                        vreg[i] = reinterpret_cast<const float4*>(vbase + off)[col];
+                        if (FULL || col < hd4) {
+                            kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
+                            vreg[i] = reinterpret_cast<const float4*>(vbase + off)[col];
+                        }
                     } else if (col == 0) {
                         atomicAdd(a.bad_pages, 1);
                     }
@@ -167,10 +176,11 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaun
                 const bool in = key <= last_pos;
                 const bool ok = in && (unsigned)page[i] < (unsigned)a.num_pages;
                 if (in && !ok && col == 0) atomicAdd(a.bad_pages, 1);
-                kmask |= (uint32_t)ok << i;
+                const bool colok = FULL || col < hd4;  // a column past the head reads column 0
+                kmask |= (uint32_t)(ok && colok) << i;
                 const size_t off = ok ? (size_t)page[i] * a.page_stride + (size_t)(key & 15) * a.kv_dim : 0;
-                kreg[i] = reinterpret_cast<const float4*>(kbase + off)[col];
-                vreg[i] = reinterpret_cast<const float4*>(vbase + off)[col];
+                kreg[i] = reinterpret_cast<const float4*>(kbase + off)[colok ? col : 0];
+                vreg[i] = reinterpret_cast<const float4*>(vbase + off)[colok ? col : 0];
             }
         }
     };
@@ -236,10 +246,11 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaun
 
     if (row < qcount) {
         const float inv = 1.0f / l;
-        float4* op = reinterpret_cast<float4*>(a.out + qrow * dim + (size_t)h * HD);
+        float4* op = reinterpret_cast<float4*>(a.out + qrow * dim + (size_t)h * hd);
 #pragma unroll
         for (int e = 0; e < SLOTS; e++)
-            op[c + 4 * e] = make_float4(acc[e].x * inv, acc[e].y * inv, acc[e].z * inv, acc[e].w * inv);
+            if (FULL || c + 4 * e < hd4)
+                op[c + 4 * e] = make_float4(acc[e].x * inv, acc[e].y * inv, acc[e].z * inv, acc[e].w * inv);
     }
 }
 
@@ -921,7 +932,7 @@ hipError_t launch_paged_attn_prefill(const PrefillLaunch& a, hipStream_t stream)
             case 32: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<32, 4, 2, 64>), grid, dim3(512), 0, stream, a); return hipGetLastError();
             case 64: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<64, 4, 2, 64>), grid, dim3(512), 0, stream, a); return hipGetLastError();
             case 128: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<128, 8, 1, 32>), grid, dim3(512), 0, stream, a); return hipGetLastError();
-            default: break;  // hd 256: VALU kernel
+            default: break;  // other head sizes: VALU kernel
         }
     }
     if (a.kernel == PREFILL_KERNEL_MFMA_F32) {
@@ -933,15 +944,31 @@ hipError_t launch_paged_attn_prefill(const PrefillLaunch& a, hipStream_t stream)
             case 32: hipLaunchKernelGGL((paged_attn_prefill_mfma_kernel<32, 4, 2, 64>), grid, dim3(512), 0, stream, a); return hipGetLastError();
             case 64: hipLaunchKernelGGL((paged_attn_prefill_mfma_kernel<64, 4, 2, 64>), grid, dim3(512), 0, stream, a); return hipGetLastError();
             case 128: hipLaunchKernelGGL((paged_attn_prefill_mfma_kernel<128, 4, 2, 32>), grid, dim3(512), 0, stream, a); return hipGetLastError();
-            default: break;  // hd 256: VALU kernel
+            default: break;  // other head sizes: VALU kernel
         }
     }
-    switch (a.head_dim) {
-        case 32: hipLaunchKernelGGL(paged_attn_prefill_kernel<32>, grid, dim3(THREADS), 0, stream, a); break;
-        case 64: hipLaunchKernelGGL(paged_attn_prefill_kernel<64>, grid, dim3(THREADS), 0, stream, a); break;
-        case 128: hipLaunchKernelGGL(paged_attn_prefill_kernel<128>, grid, dim3(THREADS), 0, stream, a); break;
-        case 256: hipLaunchKernelGGL(paged_attn_prefill_kernel<256>, grid, dim3(THREADS), 0, stream, a); break;
-        default: return hipErrorInvalidValue;
+    // VALU kernel: hd 256, head sizes other than 32/64/128/256 (padded), or
+    // NITRO_PREFILL_KERNEL=valu
+    if (a.head_dim < 4 || a.head_dim > 256 || a.head_dim % 4) return hipErrorInvalidValue;
+    const int hdp = a.head_dim <= 32 ? 32 : a.head_dim <= 64 ? 64 : a.head_dim <= 128 ? 128 : 256;
+    const bool full = a.head_dim == hdp;
+    switch (hdp) {
+        case 32:
+            if (full) hipLaunchKernelGGL((paged_attn_prefill_kernel<32, true>), grid, dim3(THREADS), 0, stream, a);
+            else hipLaunchKernelGGL((paged_attn_prefill_kernel<32, false>), grid, dim3(THREADS), 0, stream, a);
+            break;
+        case 64:
+            if (full) hipLaunchKernelGGL((paged_attn_prefill_kernel<64, true>), grid, dim3(THREADS), 0, stream, a);
+            else hipLaunchKernelGGL((paged_attn_prefill_kernel<64, false>), grid, dim3(THREADS), 0, stream, a);
+            break;
+        case 128:
+            if (full) hipLaunchKernelGGL((paged_attn_prefill_kernel<128, true>), grid, dim3(THREADS), 0, stream, a);
+            else hipLaunchKernelGGL((paged_attn_prefill_kernel<128, false>), grid, dim3(THREADS), 0, stream, a);
+            break;
+        default:
+            if (full) hipLaunchKernelGGL((paged_attn_prefill_kernel<256, true>), grid, dim3(THREADS), 0, stream, a);
+            else hipLaunchKernelGGL((paged_attn_prefill_kernel<256, false>), grid, dim3(THREADS), 0, stream, a);
+            break;
     }
     return hipGetLastError();
 }

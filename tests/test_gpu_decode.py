@@ -29,8 +29,9 @@ def say(msg):
     sys.stdout.flush()
 
 
+# every decode case of the reference's golden vectors (head sizes 16, 32, 64, 128)
 GOLDEN_DECODE = ["decode_hd64", "decode_hd128", "decode_gqa_h4kv2_hd32", "single_hd32_l2",
-                 "single_gqa_hd64", "single_pos0"]
+                 "single_gqa_hd64", "single_pos0", "decode_mha_hd16_l2", "decode_gqa_h8kv2_hd16"]
 
 
 @pytest.mark.parametrize("name", GOLDEN_DECODE)
@@ -75,6 +76,15 @@ SHAPES = {
     "gqa_8x1_hd32": ((4, 1, 900), 8, 1, 32, 240, 2, 1),
     "gqa_4x2_hd256": ((3, 1, 300), 4, 2, 256, 64, 1, 0),
     "gqa_24x4_hd128": ([5, 16, 17, 600], 24, 4, 128, 60, 1, 0),
+    # head sizes other than 32/64/128/256: kernels padded to the next width
+    "hd16_gqa_8x2": ((5, 1, 700), 8, 2, 16, 260, 1, 0),
+    "hd48": ((4, 1, 400), 3, 3, 48, 120, 2, 1),
+    "hd80_gqa_10x2": ((3, 1, 500), 10, 2, 80, 110, 1, 0),
+    "hd96_gqa_12x4": ([1, 33, 300, 1100], 12, 4, 96, 100, 1, 0),
+    "hd112": ((3, 1, 300), 2, 2, 112, 64, 1, 0),
+    "hd4": ((3, 1, 200), 4, 1, 4, 40, 1, 0),
+    "hd200": ((3, 1, 300), 2, 2, 200, 64, 1, 0),
+    "hd252_gqa_4x2": ((2, 1, 200), 4, 2, 252, 32, 1, 0),
 }
 
 
@@ -298,7 +308,8 @@ def test_decode_argument_errors():
         return N.lib().nitro_paged_attn_decode(pool.handle, layer, ctypes.c_void_p(q.data_ptr()),
                                                ctypes.c_void_p(out.data_ptr()), H, Hkv, hd, None)
 
-    assert raw(0, 1, 1, 96) == N.UNSUPPORTED
+    assert raw(0, 1, 1, 126) == N.UNSUPPORTED  # not a multiple of 4
+    assert raw(0, 1, 1, 260) == N.UNSUPPORTED  # wider than 256
     assert raw(0, 3, 2, 64) == N.UNSUPPORTED
     assert raw(1, 1, 1, 128) == N.INVALID_ARGUMENT  # layer outside a 1-layer pool
     assert raw(0, 2, 1, 64) == N.INVALID_ARGUMENT   # kv_dim mismatch (1*64 != 128)
@@ -416,3 +427,100 @@ def test_prefill_scatter_of_more_rows_than_a_grid_dimension():
     assert np.array_equal(dk.cpu().numpy(), k)
     assert np.array_equal(dv.cpu().numpy(), v)
     assert pool.take_device_errors() == 0
+
+
+@pytest.mark.parametrize("name", ["batched_12x64_b32", "gqa_32x8_hd128", "hd96_gqa_12x4", "edges_hd64"])
+@pytest.mark.parametrize("tiles,waves,worklist", [("2", "4", "1"), ("2", "4", "0"), ("3", "8", "1"),
+                                                  ("1", "16", "1"), ("", "", "1"), ("", "", "0")])
+def test_decode_work_list_and_implied_items_agree(name, tiles, waves, worklist, monkeypatch):
+    """Sequences split into runs of `tiles` tiles, handed out by a work list
+    (only real items, full ones first) or implied by the block id (workgroups
+    past a sequence's last split exit): both match the oracle, and repeated
+    launches are bit-identical (the split merge runs in split order whichever
+    workgroup arrives last)."""
+    say(f"decode {name} tiles={tiles} waves={waves} work_list={worklist}")
+    monkeypatch.setenv("NITRO_DECODE_SPLIT_TILES", tiles)
+    monkeypatch.setenv("NITRO_DECODE_WAVES", waves)
+    monkeypatch.setenv("NITRO_DECODE_WORK_LIST", worklist)
+    c = make_case(name, seed=9)
+    want = c.run_oracle()
+    first = c.run_gpu()
+    assert_parity(first, want, f"{name} tiles={tiles} list={worklist}")
+    for _ in range(3):
+        assert np.array_equal(c.run_gpu(), first)
+    assert c.pool.take_device_errors() == 0
+
+
+@pytest.mark.parametrize("name", ["llama110m_single_ctx256", "batched_12x64_b32", "gqa_32x8_hd128",
+                                  "gqa_8x2_hd64", "edges_hd128", "hd48", "mha_hd256"])
+@pytest.mark.parametrize("tiles", ["", "2"])
+def test_decode_append_equals_append_then_decode(name, tiles, monkeypatch):
+    """nitro_paged_attn_decode_append (the new row read from k/v and written by
+    the decode launch itself) leaves the same pools, byte for byte, and the
+    same outputs, bit for bit, as nitro_kv_append then nitro_paged_attn_decode;
+    both match the oracle's append + decode (src/model_q8.cpp:616-662)."""
+    import torch
+
+    import nitrorag_amd as na
+
+    say(f"decode_append {name} tiles={tiles}")
+    monkeypatch.setenv("NITRO_DECODE_SPLIT_TILES", tiles)
+    c = make_case(name, seed=13)
+    B, kv_dim = len(c.ctx), c.Hkv * c.hd
+    rng = np.random.default_rng(17)
+    knew = rng.standard_normal((B, kv_dim)).astype(np.float32)
+    vnew = rng.standard_normal((B, kv_dim)).astype(np.float32)
+    q = to_gpu(c.q)
+    # fused
+    out1 = torch.full_like(q, float("nan"))
+    c.pool.decode_append(c.layer, q, to_gpu(knew), to_gpu(vnew), out1, c.H, c.Hkv, c.hd)
+    torch.cuda.synchronize()
+    k1, v1 = c.dk.cpu().numpy(), c.dv.cpu().numpy()
+    # separate, on a fresh copy of the original pools
+    dk2, dv2 = to_gpu(c.k), to_gpu(c.v)
+    pool2 = na.KVPool.wrap(dk2, dv2)
+    pool2.upload_decode_batch(c.tables, c.positions)
+    pool2.kv_append(c.layer, to_gpu(knew), to_gpu(vnew))
+    out2 = torch.full_like(q, float("nan"))
+    pool2.decode(c.layer, q, out2, c.H, c.Hkv, c.hd)
+    torch.cuda.synchronize()
+    assert np.array_equal(k1, dk2.cpu().numpy()) and np.array_equal(v1, dv2.cpu().numpy())
+    assert np.array_equal(out1.cpu().numpy(), out2.cpu().numpy())
+    attn.kv_append_decode(c.k, c.v, c.layer, knew, vnew, c.tables, c.positions)
+    assert np.array_equal(k1, c.k) and np.array_equal(v1, c.v)
+    assert_parity(out1.cpu().numpy(), c.run_oracle(), f"decode_append {name}")
+    assert c.pool.take_device_errors() == 0
+
+
+def test_decode_append_when_rows_share_the_appended_page():
+    """Rows of one sequence at consecutive positions (a short prefill chunk run
+    as decode rows) read the page the others append to: decode_append then
+    appends every row before attending, as the reference does, and row i sees
+    the rows appended before it."""
+    import torch
+
+    import nitrorag_amd as na
+
+    say("decode_append with a shared appended page")
+    rng = np.random.default_rng(23)
+    H, hd, pages = 4, 64, 40
+    kv_dim = H * hd
+    start, n = 37, 6  # positions 37..42 share page 2 of the table
+    table = rng.permutation(pages)[:4].astype(np.int32)
+    tables = np.repeat(table[None, :], n, axis=0)
+    positions = np.arange(start, start + n, dtype=np.int32)
+    k = rng.standard_normal((pages, 1, 16, kv_dim)).astype(np.float32)
+    v = rng.standard_normal((pages, 1, 16, kv_dim)).astype(np.float32)
+    q = rng.standard_normal((n, kv_dim)).astype(np.float32)
+    knew = rng.standard_normal((n, kv_dim)).astype(np.float32)
+    vnew = rng.standard_normal((n, kv_dim)).astype(np.float32)
+    dk, dv = to_gpu(k), to_gpu(v)
+    pool = na.KVPool.wrap(dk, dv)
+    pool.upload_decode_batch(tables, positions)
+    out = torch.full_like(to_gpu(q), float("nan"))
+    pool.decode_append(0, to_gpu(q), to_gpu(knew), to_gpu(vnew), out, H, H, hd)
+    torch.cuda.synchronize()
+    attn.kv_append_decode(k, v, 0, knew, vnew, tables, positions)
+    assert np.array_equal(dk.cpu().numpy(), k) and np.array_equal(dv.cpu().numpy(), v)
+    assert_parity(out.cpu().numpy(), attn.decode_batch(k, v, 0, q, tables, positions, H, H, hd),
+                  "shared appended page")

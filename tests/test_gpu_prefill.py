@@ -54,7 +54,10 @@ def run_prefill(k, v, layer, tables, start_pos, lens, q, kc, vc, H, Hkv, hd):
     return out.cpu().numpy(), dk.cpu().numpy(), dv.cpu().numpy()
 
 
-@pytest.mark.parametrize("name", ["prefill_hd64", "prefill_gqa_hd32_l2", "prefix_hit_hd32"])
+# every paged prefill case of the reference's golden vectors (head sizes 16, 32, 64;
+# 16 runs the VALU kernel padded to 32 whichever kernel is asked for)
+@pytest.mark.parametrize("name", ["prefill_hd64", "prefill_gqa_hd32_l2", "prefix_hit_hd32",
+                                  "prefill_fresh_hd16_l2", "prefill_continued_gqa", "prefix_hit_gqa_l2"])
 def test_prefill_matches_reference_golden(golden_attention, name):
     meta, arr = golden_attention[name]
     say(f"golden prefill {name}")
@@ -134,6 +137,14 @@ CASES = {
     # tokens): the rest of the table is read from global memory
     "beyond_lds_table_hd64": (6, 2, 5, 40, 2, 2, 64, 1, 0, 33000, 33100),
     "beyond_lds_table_gqa_hd128": (7, 2, 5, 150, 2, 1, 128, 1, 0, 33000, 33100),
+    # head sizes other than 32/64/128/256 (multiples of 4): the VALU kernel with
+    # the head padded to the next kernel width and the extra columns masked
+    "hd16_gqa_4x2": (8, 3, 1, 90, 4, 2, 16, 1, 0, 0, 30),
+    "hd48": (9, 3, 20, 140, 3, 3, 48, 2, 1, 0, 17),
+    "hd80_gqa_6x2": (10, 2, 1, 120, 6, 2, 80, 1, 0, 5, 40),
+    "hd96": (11, 2, 30, 100, 2, 2, 96, 1, 0, 0, 0),
+    "hd4": (12, 2, 1, 60, 2, 1, 4, 1, 0, 0, 20),
+    "hd200": (13, 2, 10, 80, 2, 2, 200, 1, 0, 0, 9),
 }
 
 
