@@ -167,6 +167,26 @@ int nitro_kv_append(nitro_kvpool* pool, int32_t layer, const float* k, const flo
 int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
                             int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void* stream);
 
+/* Allocation-free batched decode.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory at call time (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * result as nitro_paged_attn_decode, but the caller passes the batch as device
+ * arrays — tables [batch][max_pages] int32 and positions [batch] int32 (the
+ * slot written this step, attended inclusive) — and max_context, a host bound
+ * with positions[b] + 1 <= max_context for every b (keys past it are not
+ * attended; page ids are range-checked on the device, nothing else of the
+ * device arrays is validated).  Nothing is uploaded or allocated: split-K
+ * partials and arrival counters live in a fixed 8 MiB workspace, one copy per
+ * GPU for the life of the process (65,536 counters of batch * n_heads / query
+ * heads per workgroup, the rest partials); a launch that needs more is refused
+ * with NITRO_ERR_INVALID_ARGUMENT.  Every launch leaves the counters at zero.
+ * All calls on one GPU share that workspace: calls that overlap on one GPU (two
+ * streams, two threads) race. */
+int nitro_paged_attn_decode_static(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
+                                   const int32_t* tables, const int32_t* positions, int32_t batch,
+                                   int32_t max_pages, int32_t max_context, int32_t n_heads, int32_t n_kv_heads,
+                                   int32_t head_dim, void* stream);
+
 /* nitro_kv_append followed by nitro_paged_attn_decode, as forward_decode_batch
  * does them (src/model_q8.cpp:616-662): k, v device [batch][kv_dim] are written
  * at each sequence's pos and attended.  One launch when no other sequence of

@@ -97,8 +97,6 @@ int env_int(const char* name, int fallback) {
 // Launch shape of one decode launch, chosen from the batch's context lengths.
 struct DecodeShape {
     int qh = 1, waves = 4, tps = 1;  // query heads / waves per workgroup, tiles per split
-    std::vector<int> splits;         // per sequence
-    bool uniform = true;             // every sequence has the same number of splits
 };
 
 // Waves resident per CU at the kernel's occupancy (16; 8 with several query
@@ -113,14 +111,15 @@ struct DecodeShape {
 //    workgroups all fit; the W with the fewest rounds R wins, then the one
 //    with the fewest splits.  Long sequences split into equal runs, short ones
 //    not at all, and every split is at most R tile rounds per wave.
-DecodeShape plan_decode_shape(const nitro_kvpool* pool, const std::vector<int32_t>& positions, int n_heads,
-                              int n_kv_heads, int head_dim) {
+// ctx(b) gives sequence b's context length; nothing is allocated.
+template <class Ctx>
+DecodeShape plan_decode_shape(const nitro_kvpool* pool, int B, Ctx ctx, int n_heads, int n_kv_heads,
+                              int head_dim) {
     DecodeShape sh;
     const int tile = decode_tile_rows(head_dim);
-    const int B = (int)positions.size();
-    std::vector<int> n(B);
+    auto tiles = [&](int b) { return (ctx(b) + tile - 1) / tile; };
     int max_n = 1;
-    for (int b = 0; b < B; b++) max_n = std::max(max_n, n[b] = (positions[b] + 1 + tile - 1) / tile);
+    for (int b = 0; b < B; b++) max_n = std::max(max_n, tiles(b));
     const int kv_mul = n_heads / n_kv_heads;
     int qh = env_int("NITRO_DECODE_HEADS_PER_WG", 0);
     if (qh <= 0) {
@@ -137,7 +136,7 @@ DecodeShape plan_decode_shape(const nitro_kvpool* pool, const std::vector<int32_
     const int max_tps = (DECODE_MAX_SPLIT_PAGES - 2) * BLOCK_SIZE / tile;  // the LDS table slice
     auto items_for = [&](int tps) {
         long long k = 0;
-        for (int b = 0; b < B; b++) k += (n[b] + tps - 1) / tps;
+        for (int b = 0; b < B; b++) k += (tiles(b) + tps - 1) / tps;
         return k;
     };
     const int env_waves = env_int("NITRO_DECODE_WAVES", 0);
@@ -181,12 +180,37 @@ DecodeShape plan_decode_shape(const nitro_kvpool* pool, const std::vector<int32_
     }
     sh.waves = std::max(kDecodeMinWaves, std::min(waves, max_waves));
     sh.tps = std::max(1, std::min(tps, max_tps));
-    sh.splits.resize(B);
-    for (int b = 0; b < B; b++) {
-        sh.splits[b] = (n[b] + sh.tps - 1) / sh.tps;
-        sh.uniform &= sh.splits[b] == sh.splits[0];
-    }
     return sh;
+}
+
+// Launch fields shared by every decode entry point.
+DecodeLaunch decode_launch_base(const nitro_kvpool* pool, int layer, const float* q, float* out, int n_heads,
+                                int n_kv_heads, int head_dim, const DecodeShape& sh, bool shared_pages) {
+    DecodeLaunch a{};
+    a.q = q;
+    a.out = out;
+    a.k_pool = pool->k;
+    a.v_pool = pool->v;
+    a.bad_pages = pool->bad_pages.ptr;
+    a.page_stride = pool->page_stride();
+    a.layer_off = pool->layer_offset(layer);
+    a.kv_dim = pool->kv_dim;
+    a.n_heads = n_heads;
+    a.kv_mul = n_heads / n_kv_heads;
+    a.head_dim = head_dim;
+    a.num_pages = pool->num_pages;
+    a.tiles_per_split = sh.tps;
+    a.pstride = (head_dim + 2 + 31) / 32 * 32;
+    a.waves = sh.waves;
+    a.heads_per_wg = sh.qh;
+    // Non-temporal K/V loads when every K/V line is read once per launch:
+    // one workgroup per KV head and no page shared between sequences.
+    const int stream_env = env_int("NITRO_DECODE_STREAM", -1);
+    a.stream_kv = stream_env >= 0 ? stream_env != 0 : (sh.qh == a.kv_mul && !shared_pages);
+    const int remap_env = env_int("NITRO_DECODE_XCD_REMAP", -1);
+    a.xcd_remap = remap_env >= 0 ? remap_env != 0 : sh.qh < a.kv_mul;
+    a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+    return a;
 }
 
 // One decode launch over the pool's uploaded batch (k_new / v_new: the fused
@@ -194,19 +218,23 @@ DecodeShape plan_decode_shape(const nitro_kvpool* pool, const std::vector<int32_
 void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, const float* k_new,
                    const float* v_new, int n_heads, int n_kv_heads, int head_dim, hipStream_t s) {
     DecodeBatch& d = pool->decode;
-    const DecodeShape sh = plan_decode_shape(pool, d.positions, n_heads, n_kv_heads, head_dim);
-    const int tile = decode_tile_rows(head_dim);
     const int B = d.batch;
+    auto ctx = [&](int b) { return d.positions[b] + 1; };
+    const DecodeShape sh = plan_decode_shape(pool, B, ctx, n_heads, n_kv_heads, head_dim);
+    const int tile = decode_tile_rows(head_dim);
+    auto splits = [&](int b) { return ((ctx(b) + tile - 1) / tile + sh.tps - 1) / sh.tps; };
     int max_splits = 1;
     long long slots = 0;
-    for (int x : sh.splits) {
-        max_splits = std::max(max_splits, x);
-        slots += x;
+    bool uniform = true;
+    for (int b = 0; b < B; b++) {
+        max_splits = std::max(max_splits, splits(b));
+        slots += splits(b);
+        uniform &= splits(b) == splits(0);
     }
     // A work list when sequences split unevenly (NITRO_DECODE_WORK_LIST=0/1
     // forces it off/on); otherwise items are implied by the block id.
     const int list_env = env_int("NITRO_DECODE_WORK_LIST", -1);
-    const bool use_list = list_env >= 0 ? list_env != 0 : (max_splits > 1 && !sh.uniform);
+    const bool use_list = list_env >= 0 ? list_env != 0 : (max_splits > 1 && !uniform);
     const int32_t* work = nullptr;
     int work_items = 0;
     if (use_list) {
@@ -218,12 +246,12 @@ void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, co
             host.reserve(4 * (size_t)slots);
             int slot0 = 0;
             for (int b = 0; b < B; b++) {
-                const int ctx = d.positions[b] + 1, nt = (ctx + tile - 1) / tile;
-                for (int x = 0; x < sh.splits[b]; x++) {
+                const int nt = (ctx(b) + tile - 1) / tile;
+                for (int x = 0; x < splits(b); x++) {
                     order.push_back({std::min(sh.tps, nt - x * sh.tps), (int)host.size() / 4});
-                    host.insert(host.end(), {b, x, slot0, ctx});
+                    host.insert(host.end(), {b, x, slot0, ctx(b)});
                 }
-                slot0 += sh.splits[b];
+                slot0 += splits(b);
             }
             std::stable_sort(order.begin(), order.end(),
                              [](const auto& x, const auto& y) { return x.first > y.first; });
@@ -244,17 +272,12 @@ void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, co
     } else {
         slots = (long long)B * max_splits;
     }
-    const int pstride = (head_dim + 2 + 31) / 32 * 32;
+    DecodeLaunch a = decode_launch_base(pool, layer, q, out, n_heads, n_kv_heads, head_dim, sh, d.shared_pages);
     if (max_splits > 1) {
-        pool->partials.reserve((size_t)slots * n_heads * pstride);
+        pool->partials.reserve((size_t)slots * n_heads * a.pstride);
         if (pool->counters.reserve((size_t)B * (n_heads / sh.qh)))
             hip_check(hipMemset(pool->counters.ptr, 0, pool->counters.count * sizeof(int32_t)), "hipMemset");
     }
-    DecodeLaunch a{};
-    a.q = q;
-    a.out = out;
-    a.k_pool = pool->k;
-    a.v_pool = pool->v;
     a.tables = d.tables.ptr;
     a.positions = d.pos.ptr;
     a.work = work;
@@ -263,28 +286,11 @@ void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, co
     a.counters = pool->counters.ptr;
     a.k_new = k_new;
     a.v_new = v_new;
-    a.bad_pages = pool->bad_pages.ptr;
-    a.page_stride = pool->page_stride();
-    a.layer_off = pool->layer_offset(layer);
-    a.kv_dim = pool->kv_dim;
     a.batch = B;
-    a.n_heads = n_heads;
-    a.kv_mul = n_heads / n_kv_heads;
-    a.head_dim = head_dim;
     a.max_pages = d.max_pages;
-    a.num_pages = pool->num_pages;
-    a.tiles_per_split = sh.tps;
     a.num_splits = use_list ? 0 : max_splits;
-    a.pstride = pstride;
-    a.waves = sh.waves;
-    a.heads_per_wg = sh.qh;
-    // Non-temporal K/V loads when every K/V line is read once per launch:
-    // one workgroup per KV head and no page shared between sequences.
-    const int stream_env = env_int("NITRO_DECODE_STREAM", -1);
-    a.stream_kv = stream_env >= 0 ? stream_env != 0 : (sh.qh == a.kv_mul && !d.shared_pages);
-    const int remap_env = env_int("NITRO_DECODE_XCD_REMAP", -1);
-    a.xcd_remap = remap_env >= 0 ? remap_env != 0 : sh.qh < a.kv_mul;
-    a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+    a.ctx_limit = use_list ? d.max_pages * BLOCK_SIZE
+                           : std::min(d.max_pages * BLOCK_SIZE, max_splits * sh.tps * tile);
     hip_check(launch_paged_attn_decode(a, s), "paged_attn_decode launch");
     pool->last_stream = s;
 }
@@ -462,6 +468,54 @@ int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, f
         check_shape(pool, layer, n_heads, n_kv_heads, head_dim);
         require(pool->decode.batch > 0, ERR_NO_BATCH, "no decode batch uploaded");
         launch_decode(pool, layer, q, out, nullptr, nullptr, n_heads, n_kv_heads, head_dim, as_stream(stream));
+    });
+}
+
+int nitro_paged_attn_decode_static(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
+                                   const int32_t* tables, const int32_t* positions, int32_t batch,
+                                   int32_t max_pages, int32_t max_context, int32_t n_heads, int32_t n_kv_heads,
+                                   int32_t head_dim, void* stream) {
+    return guarded([&] {
+        require_pool(pool);
+        require(q != nullptr && out != nullptr && tables != nullptr && positions != nullptr,
+                ERR_INVALID_ARGUMENT, "null q/out/tables/positions");
+        check_shape(pool, layer, n_heads, n_kv_heads, head_dim);
+        require(batch > 0 && max_pages > 0, ERR_INVALID_ARGUMENT, "batch and max_pages must be positive");
+        require(max_context > 0 && max_context <= max_pages * BLOCK_SIZE, ERR_INVALID_ARGUMENT,
+                "max_context must be in [1, max_pages * 16]");
+        // Every sequence is planned at max_context, so the splits are uniform
+        // and implied by the block id: no work list, nothing to upload.
+        auto ctx = [&](int) { return (int)max_context; };
+        const DecodeShape sh = plan_decode_shape(pool, batch, ctx, n_heads, n_kv_heads, head_dim);
+        const int tile = decode_tile_rows(head_dim);
+        const int splits = ((max_context + tile - 1) / tile + sh.tps - 1) / sh.tps;
+        // page sharing is unknown here: plain (cacheable) K/V loads
+        DecodeLaunch a = decode_launch_base(pool, layer, q, out, n_heads, n_kv_heads, head_dim, sh, true);
+        float* ws = nullptr;
+        if (splits > 1) {
+            const size_t counters = (size_t)batch * (n_heads / sh.qh);
+            const size_t partial_floats = (size_t)batch * splits * n_heads * a.pstride;
+            const size_t room = DECODE_STATIC_SCRATCH_BYTES / sizeof(float) - DECODE_STATIC_COUNTERS;
+            if (counters > DECODE_STATIC_COUNTERS || partial_floats > room)
+                throw Error(ERR_INVALID_ARGUMENT,
+                            "this launch needs " + std::to_string(counters) + " counters and " +
+                                std::to_string(partial_floats * sizeof(float)) +
+                                " bytes of split-K partials; the static workspace holds " +
+                                std::to_string(DECODE_STATIC_COUNTERS) + " and " +
+                                std::to_string(room * sizeof(float)) + " (use nitro_paged_attn_decode)");
+            hip_check(decode_static_scratch(&ws), "hipGetSymbolAddress(scratch)");
+        }
+        a.tables = tables;
+        a.positions = positions;
+        a.partials = ws ? ws + DECODE_STATIC_COUNTERS : nullptr;
+        a.counters = reinterpret_cast<int32_t*>(ws);
+        a.batch = batch;
+        a.max_pages = max_pages;
+        a.num_splits = splits;
+        a.ctx_limit = std::min(max_context, splits * sh.tps * tile);
+        hipStream_t s = as_stream(stream);
+        hip_check(launch_paged_attn_decode(a, s), "paged_attn_decode launch");
+        pool->last_stream = s;
     });
 }
 

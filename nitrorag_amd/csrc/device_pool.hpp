@@ -168,6 +168,7 @@ struct DecodeLaunch {
     int64_t page_stride, layer_off;
     int32_t kv_dim, batch, n_heads, kv_mul, head_dim, max_pages, num_pages;
     int32_t tiles_per_split, num_splits;
+    int32_t ctx_limit;  // contexts are clamped to this (the table's and the splits' reach)
     int32_t pstride;    // floats per partial, >= head_dim + 2
     int32_t waves;  // wavefronts per workgroup, 4..16
     int32_t stream_kv;  // non-temporal K/V loads (lines read once per launch)
@@ -186,6 +187,14 @@ int decode_tile_rows(int head_dim);
 int decode_max_heads_per_wg(int head_dim);
 // Largest number of pages one split may cover (its block-table slice lives in LDS).
 constexpr int DECODE_MAX_SPLIT_PAGES = 1024;
+// The allocation-free decode entry's workspace: a file-scope device array of
+// this many bytes, the first DECODE_STATIC_COUNTERS int32 arrival counters,
+// the rest split-K partials.
+constexpr size_t DECODE_STATIC_SCRATCH_BYTES = 8u << 20;
+constexpr size_t DECODE_STATIC_COUNTERS = 65536;
+// Address of that array on the current device (hipGetSymbolAddress on the
+// first call per device, kept per device).
+hipError_t decode_static_scratch(float** ptr);
 hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream);
 
 hipError_t launch_kv_append_decode(float* k_pool, float* v_pool, const float* k, const float* v,

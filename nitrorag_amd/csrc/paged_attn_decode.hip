@@ -47,10 +47,43 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <mutex>
 
 #include "device_pool.hpp"
 
+// Workspace of the allocation-free decode entry (nitro_paged_attn_decode_static):
+// arrival counters, then split-K partials.  Each GPU the library runs on holds
+// its own copy until the process ends; zero at load, and every launch leaves
+// its counters at zero again.  Host code never passes this name to a kernel
+// (in host code it is a stand-in, not a device address): it takes the address
+// from decode_static_scratch below.
+static __device__ __align__(256) float scratch[nitro::DECODE_STATIC_SCRATCH_BYTES / sizeof(float)];
+
 namespace nitro {
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+hipError_t decode_static_scratch(float** ptr) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *ptr = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
 namespace {
 
 constexpr int MAX_WAVES = 16;
@@ -218,7 +251,7 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
         }
     }
 
-    ctx = min(ctx, a.max_pages * 16);  // a position past the table reads no further
+    ctx = max(0, min(ctx, a.ctx_limit));  // a position past the table (or the splits) reads no further
     const int n_tiles = (ctx + TILE - 1) / TILE;
     if (tile_begin >= n_tiles) return;  // uniform for the workgroup (implied items only)
     const int tile_end = min(n_tiles, tile_begin + a.tiles_per_split);
