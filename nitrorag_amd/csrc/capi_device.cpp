@@ -231,47 +231,34 @@ void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, co
         slots += splits(b);
         uniform &= splits(b) == splits(0);
     }
-    // A work list when sequences split unevenly (NITRO_DECODE_WORK_LIST=0/1
-    // forces it off/on); otherwise items are implied by the block id.
+    // A work list when sequences split unevenly and the list fits the kernel
+    // arguments (NITRO_DECODE_WORK_LIST=0/1 forces it off/on where it fits);
+    // otherwise items are implied by the block id.
     const int list_env = env_int("NITRO_DECODE_WORK_LIST", -1);
-    const bool use_list = list_env >= 0 ? list_env != 0 : (max_splits > 1 && !uniform);
-    const int32_t* work = nullptr;
-    int work_items = 0;
-    if (use_list) {
-        if (d.work_generation != d.generation || d.work_tile != tile || d.work_tps != sh.tps) {
-            // items {b, split, first partial slot of b, ctx}: full splits first, then the
-            // last splits by size (longest first), each group in batch order
-            std::vector<std::pair<int, int>> order;  // (tiles, item)
-            std::vector<int32_t> host;
-            host.reserve(4 * (size_t)slots);
-            int slot0 = 0;
-            for (int b = 0; b < B; b++) {
-                const int nt = (ctx(b) + tile - 1) / tile;
-                for (int x = 0; x < splits(b); x++) {
-                    order.push_back({std::min(sh.tps, nt - x * sh.tps), (int)host.size() / 4});
-                    host.insert(host.end(), {b, x, slot0, ctx(b)});
-                }
-                slot0 += splits(b);
-            }
-            std::stable_sort(order.begin(), order.end(),
-                             [](const auto& x, const auto& y) { return x.first > y.first; });
-            const size_t n = host.size();
-            d.work.reserve(n);
-            int32_t* h = d.work_staging.acquire(n);
-            for (size_t i = 0; i < order.size(); i++)
-                std::memcpy(h + 4 * i, host.data() + 4 * (size_t)order[i].second, 4 * sizeof(int32_t));
-            d.work_staging.copy(d.work.ptr, h, n, s);
-            d.work_staging.finish(s);
-            d.work_generation = d.generation;
-            d.work_tile = tile;
-            d.work_tps = sh.tps;
-            d.work_items = (int32_t)order.size();
+    bool use_list = (list_env >= 0 ? list_env != 0 : (max_splits > 1 && !uniform)) &&
+                    slots <= DECODE_ARG_ITEMS;
+    if (use_list &&
+        (d.work_generation != d.generation || d.work_tile != tile || d.work_tps != sh.tps)) {
+        // items {b, split, first partial slot of b, ctx}: full splits first, then the
+        // last splits by size (longest first), each group in batch order
+        std::vector<std::pair<int, int4>> order;  // (tiles, item)
+        order.reserve((size_t)slots);
+        int slot0 = 0;
+        for (int b = 0; b < B; b++) {
+            const int nt = (ctx(b) + tile - 1) / tile;
+            for (int x = 0; x < splits(b); x++)
+                order.push_back({std::min(sh.tps, nt - x * sh.tps), make_int4(b, x, slot0, ctx(b))});
+            slot0 += splits(b);
         }
-        work = d.work.ptr;
-        work_items = d.work_items;
-    } else {
-        slots = (long long)B * max_splits;
+        std::stable_sort(order.begin(), order.end(),
+                         [](const auto& x, const auto& y) { return x.first > y.first; });
+        for (size_t i = 0; i < order.size(); i++) d.arg_list.item[i] = order[i].second;
+        d.work_generation = d.generation;
+        d.work_tile = tile;
+        d.work_tps = sh.tps;
+        d.work_items = (int32_t)order.size();
     }
+    if (!use_list) slots = (long long)B * max_splits;
     DecodeLaunch a = decode_launch_base(pool, layer, q, out, n_heads, n_kv_heads, head_dim, sh, d.shared_pages);
     if (max_splits > 1) {
         pool->partials.reserve((size_t)slots * n_heads * a.pstride);
@@ -280,8 +267,8 @@ void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, co
     }
     a.tables = d.tables.ptr;
     a.positions = d.pos.ptr;
-    a.work = work;
-    a.work_items = work_items;
+    a.work_items = use_list ? d.work_items : 0;
+    a.arg_items = use_list ? 1 : 0;
     a.partials = pool->partials.ptr;
     a.counters = pool->counters.ptr;
     a.k_new = k_new;
@@ -291,7 +278,7 @@ void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, co
     a.num_splits = use_list ? 0 : max_splits;
     a.ctx_limit = use_list ? d.max_pages * BLOCK_SIZE
                            : std::min(d.max_pages * BLOCK_SIZE, max_splits * sh.tps * tile);
-    hip_check(launch_paged_attn_decode(a, s), "paged_attn_decode launch");
+    hip_check(launch_paged_attn_decode(a, s, use_list ? &d.arg_list : nullptr), "paged_attn_decode launch");
     pool->last_stream = s;
 }
 

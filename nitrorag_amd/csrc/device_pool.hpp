@@ -88,6 +88,13 @@ struct Staging {
     }
 };
 
+// A decode work list short enough to travel in the kernel arguments (fetched
+// with the launch's other arguments, so no load precedes the table and q loads).
+constexpr int DECODE_ARG_ITEMS = 200;
+struct DecodeArgItems {
+    int4 item[DECODE_ARG_ITEMS];
+};
+
 // Head sizes the model step's fused kernels take.
 inline bool supported_head_dim(int hd) { return hd == 32 || hd == 64 || hd == 128 || hd == 256; }
 
@@ -101,11 +108,11 @@ struct DecodeBatch {
     uint64_t generation = 0;         // bumped by every new batch (work-list cache key)
     DeviceBuffer<int32_t> tables, pos;
     DeviceBuffer<int32_t> slots;     // per row: page * 16 + position % 16 (where its K/V row goes)
-    // The decode work list last built for this batch, and what it was built for.
-    DeviceBuffer<int32_t> work;
+    // The decode work list last built for this batch, and what it was built for
+    // (work_items = 0: longer than the kernel arguments hold).
+    DecodeArgItems arg_list;
     uint64_t work_generation = ~0ull;
     int32_t work_tile = 0, work_tps = 0, work_items = 0;
-    Staging work_staging;
 };
 
 struct PrefillBatch {
@@ -155,10 +162,11 @@ struct DecodeLaunch {
     float* v_pool;
     const int32_t* tables;
     const int32_t* positions;
-    // Work list: 4 int32 per item {b, split, first partial slot of b, ctx_b},
-    // full items first; nullptr: item i is split i % num_splits of sequence
-    // i / num_splits (context from positions).
-    const int32_t* work;
+    // arg_items: the work list is the DecodeArgItems kernel argument, work_items
+    // entries {b, split, first partial slot of b, ctx_b}, full items first;
+    // otherwise item i is split i % num_splits of sequence i / num_splits
+    // (context from positions).
+    int32_t arg_items;
     int32_t work_items;
     float* partials;    // split-K (acc[hd], m, l) per (partial slot, head), pstride floats each
     int32_t* counters;  // per (b, head group): arrivals of the splits (zero between launches)
@@ -195,7 +203,8 @@ constexpr size_t DECODE_STATIC_COUNTERS = 65536;
 // Address of that array on the current device (hipGetSymbolAddress on the
 // first call per device, kept per device).
 hipError_t decode_static_scratch(float** ptr);
-hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream);
+hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream,
+                                    const DecodeArgItems* items = nullptr);
 
 hipError_t launch_kv_append_decode(float* k_pool, float* v_pool, const float* k, const float* v,
                                    const int32_t* tables, const int32_t* positions, int batch,

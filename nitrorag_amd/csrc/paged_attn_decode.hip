@@ -12,9 +12,10 @@
 //    (W = 4..16 per launch); waves take the item's tiles round-robin.  With
 //    a work list the host hands out only real items, full ones first
 //    (longest first), so every workgroup streams about the same number of
-//    tiles whatever the mix of context lengths; without one, item i is split
-//    i % num_splits of sequence i / num_splits and workgroups past a
-//    sequence's last split exit at once.
+//    tiles whatever the mix of context lengths.  The list (up to
+//    DECODE_ARG_ITEMS items) rides in the kernel arguments.  Without one, item
+//    i is split i % num_splits of sequence i / num_splits and workgroups past
+//    a sequence's last split exit at once.
 //  - Lane layout: LG = 8 lanes share one K/V row (16 for a 256-wide head) so
 //    that every global_load_dwordx4 reads whole 128-byte lines; a lane holds
 //    HDP/LG floats of each of its RL rows (columns c*4 + j*4*LG).  HDP is the
@@ -24,8 +25,9 @@
 //    64, 128, 256); all 16 K/V float4 loads of a tile are issued before use.
 //  - q.k: HDP/LG FMAs per lane and row, then a DPP butterfly across LG lanes.
 //  - Softmax: every lane group keeps its own running (max, sum, acc) in base 2
-//    (q is pre-scaled by log2(e)/sqrt(hd)); groups, then waves (through LDS),
-//    then splits are merged with the usual rescaling.  No score scratch.
+//    (q is pre-scaled by log2(e)/sqrt(hd)); groups (DPP and permlane swaps),
+//    then waves (through LDS), then splits are merged with the usual
+//    rescaling.  No score scratch.
 //  - Split-K merge in the same launch: a split writes (acc[hd], m, l) per
 //    query head with device-coherent stores (global_store ... sc1, written
 //    through the XCD's L2), waits for them (vmcnt(0)) and bumps its (b, head
@@ -146,6 +148,43 @@ __device__ __forceinline__ float scale_of(float m, float m_new) {
     return m == -INFINITY ? 0.0f : exp2f(m - m_new);
 }
 
+// The two values of a lane pair (l, l ^ 16 with HALVES = false; l, l ^ 32
+// with HALVES = true) via v_permlane16_swap / v_permlane32_swap of x with
+// itself, which leave both in every lane.
+template <bool HALVES>
+__device__ __forceinline__ void pair_values(float x, float& a, float& b) {
+    if constexpr (HALVES) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        a = __uint_as_float(r[0]);
+        b = __uint_as_float(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        a = __uint_as_float(r[0]);
+        b = __uint_as_float(r[1]);
+    }
+}
+
+// Online-softmax state (m, l, acc) of a lane merged with its pair's.
+template <int NF4, bool HALVES>
+__device__ __forceinline__ void merge_pair(float& m, float& l, float4 (&acc)[NF4]) {
+    float m0, m1, l0, l1;
+    pair_values<HALVES>(m, m0, m1);
+    pair_values<HALVES>(l, l0, l1);
+    const float mm = fmaxf(m0, m1);
+    const float f0 = scale_of(m0, mm), f1 = scale_of(m1, mm);
+    l = l0 * f0 + l1 * f1;
+#pragma unroll
+    for (int j = 0; j < NF4; j++) {
+        float x0, x1, y0, y1, z0, z1, w0, w1;
+        pair_values<HALVES>(acc[j].x, x0, x1);
+        pair_values<HALVES>(acc[j].y, y0, y1);
+        pair_values<HALVES>(acc[j].z, z0, z1);
+        pair_values<HALVES>(acc[j].w, w0, w1);
+        acc[j] = make_float4(x0 * f0 + x1 * f1, y0 * f0 + y1 * f1, z0 * f0 + z1 * f1, w0 * f0 + w1 * f1);
+    }
+    m = mm;
+}
+
 // Device-coherent accesses of the split-K partials and arrival counters:
 // relaxed atomics at agent scope are global_store / global_load ... sc1 on
 // gfx950 (written through to, and read from, the point where the XCDs'
@@ -166,7 +205,7 @@ __device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcn
 // head size is HDP (no column masks).
 template <int HDP, int QH, bool STREAM, bool FULL>
 __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged_attn_decode_kernel(
-    DecodeLaunch a) {
+    DecodeLaunch a, DecodeArgItems arg_items) {
     using G = DecodeGeom<HDP>;
     constexpr int LG = G::LG, NF4 = G::NF4, RL = G::RL, GROUPS = G::GROUPS, TILE = G::TILE;
     constexpr int MAXW = QH == 1 ? MAX_WAVES : MAX_WAVES / 2;
@@ -208,8 +247,10 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     // or implied by the block id (then the position load goes out together
     // with the block-table slice and q below).
     int b, split, pslot0, ctx;
-    if (a.work) {
-        const int4 it = reinterpret_cast<const int4*>(a.work)[item];
+    if (a.arg_items) {
+        // the list rides in the kernel arguments, fetched with the rest of
+        // them: no load precedes the table and q loads
+        const int4 it = arg_items.item[item];
         b = it.x;
         split = it.y;
         pslot0 = it.z;
@@ -378,28 +419,29 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
         }
     }
 
-    // Merge the lane groups of the wave (lanes with equal c, across g).
+    // Merge the lane groups of the wave (lanes with equal c, across g) on VALU
+    // permutes, no LDS round trips: lane l ^ 8 by DPP row_ror:8 (LG = 8), then
+    // l ^ 16 and l ^ 32 by gfx950's permlane16 / permlane32 swaps, each of
+    // which hands a lane both values of its pair.  Lanes of group 0 end up
+    // with the wave's (m, l, acc).
 #pragma unroll
     for (int qi = 0; qi < QH; qi++) {
-#pragma unroll
-        for (int mask = LG; mask < 64; mask <<= 1) {
-            const float mo = __shfl_xor(m[qi], mask);
-            const float lo = __shfl_xor(l[qi], mask);
+        if constexpr (LG == 8) {
+            const float mo = dpp_mov<0x128>(m[qi]), lo = dpp_mov<0x128>(l[qi]);
             const float mm = fmaxf(m[qi], mo);
             const float f = scale_of(m[qi], mm), fo = scale_of(mo, mm);
             l[qi] = l[qi] * f + lo * fo;
 #pragma unroll
             for (int j = 0; j < NF4; j++) {
-                float4 o;
-                o.x = __shfl_xor(acc[qi][j].x, mask);
-                o.y = __shfl_xor(acc[qi][j].y, mask);
-                o.z = __shfl_xor(acc[qi][j].z, mask);
-                o.w = __shfl_xor(acc[qi][j].w, mask);
+                const float4 o = make_float4(dpp_mov<0x128>(acc[qi][j].x), dpp_mov<0x128>(acc[qi][j].y),
+                                             dpp_mov<0x128>(acc[qi][j].z), dpp_mov<0x128>(acc[qi][j].w));
                 acc[qi][j] = make_float4(acc[qi][j].x * f + o.x * fo, acc[qi][j].y * f + o.y * fo,
                                          acc[qi][j].z * f + o.z * fo, acc[qi][j].w * f + o.w * fo);
             }
             m[qi] = mm;
         }
+        merge_pair<NF4, false>(m[qi], l[qi], acc[qi]);  // rows of 16 lanes: l ^ 16
+        merge_pair<NF4, true>(m[qi], l[qi], acc[qi]);   // halves of 32 lanes: l ^ 32
         if (g == 0) {
 #pragma unroll
             for (int j = 0; j < NF4; j++)
@@ -412,15 +454,24 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     }
     __syncthreads();
 
-    // Merge the waves: thread o owns output column o % hd of head o / hd.
+    // Merge the waves: thread o owns output column o % hd of head o / hd
+    // (every wave's values read from LDS at once, then added in wave order).
     for (int o = threadIdx.x; o < QH * hd; o += threads) {
         const int qi = o / hd, d = o - qi * hd;
+        float mw[MAXW];
         float M = -INFINITY, L = 0.0f, A = 0.0f;
-        for (int wv = 0; wv < waves; wv++) M = fmaxf(M, s_m[wv][qi]);
-        for (int wv = 0; wv < waves; wv++) {
-            const float f = scale_of(s_m[wv][qi], M);
-            L += s_l[wv][qi] * f;
-            A += s_acc[wv][qi][d] * f;
+#pragma unroll
+        for (int wv = 0; wv < MAXW; wv++) {
+            mw[wv] = wv < waves ? s_m[wv][qi] : -INFINITY;
+            M = fmaxf(M, mw[wv]);
+        }
+#pragma unroll
+        for (int wv = 0; wv < MAXW; wv++) {
+            if (wv < waves) {
+                const float f = scale_of(mw[wv], M);
+                L += s_l[wv][qi] * f;
+                A += s_acc[wv][qi][d] * f;
+            }
         }
         const int bh = bh0 + qi;
         if (splits_b == 1) {
@@ -447,19 +498,32 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     }
     __syncthreads();
     if (!s_last) return;
+    // Every split's (m, l, acc[d]) loads go out together, MERGE_BATCH splits
+    // at a time, then they are combined in split order.
+    constexpr int MERGE_BATCH = 8;
     for (int o = threadIdx.x; o < QH * hd; o += threads) {
         const int qi = o / hd, d = o - qi * hd;
         const int h = bh_in_seq + qi;
         float M = -INFINITY, L = 0.0f, A = 0.0f;
-        for (int sp = 0; sp < splits_b; sp++) {
-            const float* part = a.partials + ((size_t)(pslot0 + sp) * a.n_heads + h) * a.pstride;
-            const float ms = load_coherent(part + hd), ls = load_coherent(part + hd + 1);
-            const float as = load_coherent(part + d);
-            const float mm = fmaxf(M, ms);
-            const float f = scale_of(M, mm), fs = scale_of(ms, mm);
-            L = L * f + ls * fs;
-            A = A * f + as * fs;
-            M = mm;
+        for (int sp0 = 0; sp0 < splits_b; sp0 += MERGE_BATCH) {
+            float ms[MERGE_BATCH], ls[MERGE_BATCH], as[MERGE_BATCH];
+#pragma unroll
+            for (int j = 0; j < MERGE_BATCH; j++) {
+                const int sp = min(sp0 + j, splits_b - 1);  // past the last split: a repeat, unused
+                const float* part = a.partials + ((size_t)(pslot0 + sp) * a.n_heads + h) * a.pstride;
+                ms[j] = load_coherent(part + hd);
+                ls[j] = load_coherent(part + hd + 1);
+                as[j] = load_coherent(part + d);
+            }
+#pragma unroll
+            for (int j = 0; j < MERGE_BATCH; j++) {
+                if (sp0 + j >= splits_b) break;
+                const float mm = fmaxf(M, ms[j]);
+                const float f = scale_of(M, mm), fs = scale_of(ms[j], mm);
+                L = L * f + ls[j] * fs;
+                A = A * f + as[j] * fs;
+                M = mm;
+            }
         }
         a.out[(size_t)(bh0 + qi) * hd + d] = A / L;
     }
@@ -486,49 +550,52 @@ int decode_tile_rows(int head_dim) {
 }
 
 template <int HDP, int QH>
-static void launch_main(const DecodeLaunch& a, dim3 grid, hipStream_t stream) {
+static void launch_main(const DecodeLaunch& a, const DecodeArgItems& it, dim3 grid, hipStream_t stream) {
     const dim3 block(64 * a.waves);
     if (a.head_dim != HDP)  // padded head: plain loads
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, false>), grid, block, 0, stream, a, it);
     else if (a.stream_kv)
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, true, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, true, true>), grid, block, 0, stream, a, it);
     else
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, true>), grid, block, 0, stream, a, it);
 }
 
 template <int HDP>
-static hipError_t launch_hd(const DecodeLaunch& a, hipStream_t stream) {
+static hipError_t launch_hd(const DecodeLaunch& a, const DecodeArgItems& it, hipStream_t stream) {
     if (a.heads_per_wg < 1 || a.kv_mul % a.heads_per_wg != 0 ||
         a.heads_per_wg > decode_max_heads_per_wg(HDP) ||
         (a.heads_per_wg > 1 && a.waves > MAX_WAVES / 2))
         return hipErrorInvalidValue;
-    const size_t items = a.work ? (size_t)a.work_items : (size_t)a.batch * a.num_splits;
+    const size_t items = a.arg_items ? (size_t)a.work_items : (size_t)a.batch * a.num_splits;
     const dim3 grid((unsigned)(items * (a.n_heads / a.heads_per_wg)));
     switch (a.heads_per_wg) {
-        case 1: launch_main<HDP, 1>(a, grid, stream); break;
-        case 2: launch_main<HDP, 2>(a, grid, stream); break;
+        case 1: launch_main<HDP, 1>(a, it, grid, stream); break;
+        case 2: launch_main<HDP, 2>(a, it, grid, stream); break;
         case 4:
-            if constexpr (4 * HDP <= 512) launch_main<HDP, 4>(a, grid, stream);
+            if constexpr (4 * HDP <= 512) launch_main<HDP, 4>(a, it, grid, stream);
             break;
         case 8:
-            if constexpr (8 * HDP <= 512) launch_main<HDP, 8>(a, grid, stream);
+            if constexpr (8 * HDP <= 512) launch_main<HDP, 8>(a, it, grid, stream);
             break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream) {
+hipError_t launch_paged_attn_decode(const DecodeLaunch& a, hipStream_t stream, const DecodeArgItems* items) {
+    static const DecodeArgItems none{};
+    const DecodeArgItems& it = items ? *items : none;
+    if (a.arg_items && (!items || a.work_items > DECODE_ARG_ITEMS)) return hipErrorInvalidValue;
     // >= 4 waves: the block-table slice (<= DECODE_MAX_SPLIT_PAGES entries) is
     // loaded at most 4 entries per thread.
     if (a.waves < 4 || a.waves > MAX_WAVES || a.head_dim < 4 || a.head_dim > 256 || a.head_dim % 4 ||
         a.pstride < a.head_dim + 2)
         return hipErrorInvalidValue;
     switch (decode_padded_head_dim(a.head_dim)) {
-        case 32: return launch_hd<32>(a, stream);
-        case 64: return launch_hd<64>(a, stream);
-        case 128: return launch_hd<128>(a, stream);
-        default: return launch_hd<256>(a, stream);
+        case 32: return launch_hd<32>(a, it, stream);
+        case 64: return launch_hd<64>(a, it, stream);
+        case 128: return launch_hd<128>(a, it, stream);
+        default: return launch_hd<256>(a, it, stream);
     }
 }
 
