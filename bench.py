@@ -48,8 +48,13 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
+
+# The CPU baseline's OpenMP threads stay on neighbouring cores (set before
+# anything in this process initialises the OpenMP runtime).
+os.environ.setdefault("OMP_PROC_BIND", "close")
 
 import numpy as np
 
@@ -99,15 +104,18 @@ def measured_traffic(path: str):
     return None
 
 
-def time_cpu(fn, seconds: float):
-    fn()  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while True:
+def time_cpu(fn, seconds: float, warmup: int = 2, min_reps: int = 5):
+    """Median seconds per call over at least min_reps timed calls (and about
+    `seconds` of them), after `warmup` untimed ones; returns (median, reps,
+    elapsed)."""
+    for _ in range(warmup):
         fn()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            return el / reps, reps, el
+    times, t0 = [], time.perf_counter()
+    while len(times) < min_reps or time.perf_counter() - t0 < seconds:
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return float(np.median(times)), len(times), time.perf_counter() - t0
 
 
 class DecodeWorkload:
@@ -205,7 +213,7 @@ class DecodeWorkload:
             "value": round(nbytes / per_rep / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": (f"{sample} of the {self.B} sequences of this workload, append + batched "
-                       f"decode over {len(self.steps_layers)} layer(s), {reps} reps in {el:.1f} s; "
+                       f"decode over {len(self.steps_layers)} layer(s), median of {reps} runs in {el:.1f} s; "
                        f"{sample / per_rep:.1f} tokens/s"),
             "tokens_per_s": round(sample / per_rep, 3),
         }
@@ -305,7 +313,7 @@ class PrefillWorkload:
         return {"value": round(flops / per_rep / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
                 "kind": "port",
                 "sample": (f"prompts 0..{sample - 1} of the {self.B} ({toks} tokens), scatter + "
-                           f"causal prefill, {reps} reps in {el:.1f} s; {toks / per_rep:.1f} tokens/s"),
+                           f"causal prefill, median of {reps} runs in {el:.1f} s; {toks / per_rep:.1f} tokens/s"),
                 "tokens_per_s": round(toks / per_rep, 3)}
 
     def extra(self, kernel_s):
@@ -391,8 +399,8 @@ class Q8Workload:
         return {"value": round(nbytes / per_rep / 1e9, 3), "unit": "GB/s", "cores": threads,
                 "kind": "port",
                 "sample": (f"{rows} of the {self.B} activation rows of this workload, one matmul "
-                           f"(src/model_q8.cpp:92-125) per row over the full matrix, {reps} reps "
-                           f"in {el:.1f} s")}
+                           f"(src/model_q8.cpp:92-125) per row over the full matrix, median of "
+                           f"{reps} runs in {el:.1f} s")}
 
     def extra(self, kernel_s):
         return {}
@@ -495,7 +503,7 @@ class ModelDecodeWorkload:
                 "kind": "port",
                 "sample": (f"{rows} of the {self.B} sequences of this workload, one decode step of "
                            f"the oracle's composed forward (src/model_q8.cpp:571-694 with full-row "
-                           f"matmul), {reps} reps in {el:.1f} s")}
+                           f"matmul), median of {reps} runs in {el:.1f} s")}
 
     def device_errors(self):
         return self.pool.take_device_errors()
@@ -771,20 +779,35 @@ def kernel_name(w) -> str:
 
 
 def host_cpu():
-    """The host's CPU model, socket count and logical CPUs (from /proc/cpuinfo)."""
-    model, sockets = None, set()
+    """The host's CPU model, sockets and logical CPUs as lscpu reports them
+    (/proc/cpuinfo where lscpu is missing), and whether it runs AVX-512."""
+    from oracle import attn
+
+    info = {}
     try:
-        with open("/proc/cpuinfo") as f:
-            for ln in f:
-                key, _, val = ln.partition(":")
-                key = key.strip()
-                if key == "model name" and model is None:
-                    model = val.strip()
-                elif key == "physical id":
-                    sockets.add(val.strip())
-    except OSError:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for ln in out.splitlines():
+            key, _, val = ln.partition(":")
+            info[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return {"cpu_model": model, "sockets": len(sockets) or None, "logical_cpus": os.cpu_count()}
+    model, sockets = info.get("Model name"), info.get("Socket(s)")
+    if model is None:
+        ids = set()
+        try:
+            with open("/proc/cpuinfo") as f:
+                for ln in f:
+                    key, _, val = ln.partition(":")
+                    if key.strip() == "model name" and model is None:
+                        model = val.strip()
+                    elif key.strip() == "physical id":
+                        ids.add(val.strip())
+        except OSError:
+            pass
+        sockets = len(ids) or None
+    return {"cpu_model": model, "sockets": int(sockets) if sockets and str(sockets).isdigit() else sockets,
+            "logical_cpus": os.cpu_count(), "avx512": attn.host_has_avx512(),
+            "omp_proc_bind": os.environ.get("OMP_PROC_BIND")}
 
 
 def main():
@@ -895,9 +918,15 @@ def main():
         line.update(w.headline(ms_per_step))
     line.update(w.extra(kernel_s))
     if not args.no_cpu_baseline:
+        from oracle import attn
+
+        build = attn.use_timing_build()
         line["cpu_baseline"] = w.cpu_baseline(args.cpu_seconds, args.cpu_sample)
         if line["cpu_baseline"]:
             line["cpu_baseline"]["host"] = host_cpu()
+            if line["cpu_baseline"].get("kind") == "port":
+                line["cpu_baseline"]["build"] = build
+            line["cpu_baseline"]["timing"] = "2 warm-up runs, then the median of >= 5 timed runs"
     print(json.dumps(line), flush=True)
 
 

@@ -144,8 +144,13 @@ __device__ __forceinline__ float4 load_kv(const float* p) {
     }
 }
 
+// 2^x for x <= 0 on v_exp_f32 directly: results below 2^-126 flush to zero
+// (exp2f adds range handling for them), far below what an fp32 sum of
+// weights up to 1 can hold.
+__device__ __forceinline__ float exp2_nonpos(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ float scale_of(float m, float m_new) {
-    return m == -INFINITY ? 0.0f : exp2f(m - m_new);
+    return m == -INFINITY ? 0.0f : exp2_nonpos(m - m_new);
 }
 
 // The two values of a lane pair (l, l ^ 16 with HALVES = false; l, l ^ 32
@@ -398,7 +403,7 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
             float psum = 0.0f;
 #pragma unroll
             for (int i = 0; i < RL; i++) {
-                p[i] = valid[i] ? exp2f(s[i] - m_new) : 0.0f;
+                p[i] = valid[i] ? exp2_nonpos(s[i] - m_new) : 0.0f;
                 psum += p[i];
             }
             l[qi] = l[qi] * alpha + psum;

@@ -13,7 +13,34 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle_attn.so")
+_V4_PATH = os.path.join(_HERE, "liboracle_attn_v4.so")
 _lib = None
+
+# Flags /proc/cpuinfo lists on a host that runs x86-64-v4 code.
+_V4_FLAGS = {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"}
+_BUILD_FLAGS = "-O3 -ffast-math -fopenmp -march={}"
+
+
+def host_has_avx512() -> bool:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("flags"):
+                    return _V4_FLAGS <= set(ln.split(":", 1)[1].split())
+    except OSError:
+        pass
+    return False
+
+
+def use_timing_build() -> str:
+    """For the benchmark's CPU baseline only: load the x86-64-v4 build (what
+    -march=native selects on an AVX-512 host, the reference's build line) when
+    this host runs it, else the x86-64-v3 one.  Must precede the first call.
+    Returns the flags of the build in use."""
+    global _LIB_PATH
+    if _lib is None and host_has_avx512() and os.path.exists(_V4_PATH):
+        _LIB_PATH = _V4_PATH
+    return _BUILD_FLAGS.format("x86-64-v4" if _LIB_PATH == _V4_PATH else "x86-64-v3")
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i32p = ctypes.POINTER(ctypes.c_int32)

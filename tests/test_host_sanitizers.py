@@ -50,3 +50,119 @@ def test_traces_replay_clean_under_asan_ubsan(driver, golden_traces):
         words = [int(x) for x in out[-1].split()[1:]]
         state = pm.decode_snapshot(words, trace["total_blocks"], trace["max_seqs"])
         assert state == trace["final"], trace["name"]
+
+
+# ---- the scheduler, the NitroRPC wire format and the serving loop --------------
+# (tests/host_driver_sched_rpc.cpp; the device step is a test double there)
+
+SAN_ENV = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=1",
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
+
+
+@pytest.fixture(scope="module")
+def sched_rpc_driver(tmp_path_factory):
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    exe = str(tmp_path_factory.mktemp("asan2") / "host_driver_sched_rpc")
+    inc = os.path.join(ROOT, "include")
+    cmd = ["g++", "-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer",
+           "-fsanitize=address,undefined", "-fno-sanitize-recover=all", f"-I{CSRC}", f"-I{inc}",
+           os.path.join(ROOT, "tests", "host_driver_sched_rpc.cpp"),
+           *[os.path.join(CSRC, f) for f in ("paged_memory.cpp", "capi_host.cpp", "scheduler.cpp", "rpc.cpp")],
+           "-o", exe]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    return exe
+
+
+def run_driver(exe, mode, script=""):
+    r = subprocess.run([exe, mode], input=script, capture_output=True, text=True, env=SAN_ENV, timeout=120)
+    assert r.returncode == 0 and "runtime error" not in r.stderr and "ERROR:" not in r.stderr, r.stderr[-3000:]
+    return r.stdout.strip().splitlines()
+
+
+def test_scheduler_replays_reference_traces_under_asan_ubsan(sched_rpc_driver, golden_sched):
+    """Teacher-forced replay of the reference scheduler's five scenarios
+    (src/pagedMemory.hpp:287-399): every step's scheduler state words and block
+    manager state equal the reference's, with no sanitizer report."""
+    from oracle import scheduler as sc
+
+    meta, traces = golden_sched
+    for tr in traces:
+        lines = [f"S {tr.total_blocks} {tr.budget} {meta['max_generated']}"]
+        for t in range(tr.steps):
+            arr = tr.arrivals.get(t, [])
+            nxt = [(r["req_id"], r["next"]) for r in sc.decode_state(tr.state(t))["requests"]]
+            lines.append(f"T {len(arr)} {len(nxt)}")
+            lines += [" ".join(str(x) for x in [rid, len(p), *p]) for rid, p in arr]
+            lines.append(" ".join(f"{rid} {tok}" for rid, tok in nxt))
+        out = run_driver(sched_rpc_driver, "sched", "\n".join(lines) + "\n")
+        states = [ln for ln in out if ln.startswith("STATE")]
+        bms = [ln for ln in out if ln.startswith("BM")]
+        assert len(states) == tr.steps == len(bms), tr.name
+        for t in range(tr.steps):
+            assert [int(x) for x in states[t].split()[1:]] == tr.state(t), (tr.name, t)
+            got = pm.decode_snapshot([int(x) for x in bms[t].split()[1:]], tr.total_blocks, 0)
+            want = pm.decode_snapshot(tr.bm(t), tr.total_blocks, 0)
+            got.pop("seqs"), want.pop("seqs")
+            assert got == want, (tr.name, t)
+        assert out[-1] == "FINAL 3", tr.name  # every request dropped: [0 running][0 waiting][0 requests]
+
+
+def test_rpc_wire_format_under_asan_ubsan(sched_rpc_driver):
+    """The reference's own bytes (tests/golden/rpc.json: send_ints, recv_ints,
+    recv_structured_query, src/NitroRPC.hpp:39-67) plus malformed messages — a
+    count over the receiver's limit, a negative count, a message shorter than
+    its count, an empty stream — with no sanitizer report."""
+    import json
+    import struct
+
+    with open(os.path.join(ROOT, "tests", "golden", "rpc.json")) as f:
+        cases = json.load(f)
+    lines, want = [], []
+    for c in cases:
+        if c["kind"] == "send_ints":
+            lines.append(" ".join(str(x) for x in ["ENC", len(c["values"]), *c["values"]]))
+            want.append(f"ENC 0 {c['wire']} 0 0 1")
+            lines.append(f"DEC {c['wire']}")
+            want.append(" ".join(str(x) for x in ["DEC", 0, 0, len(c["values"]), len(c["wire"]) // 2, *c["values"]]))
+        elif c["kind"] == "recv_ints":
+            lines.append(f"RECV {max(1, c['count'])} {c['wire']}")
+            want.append(" ".join(str(x) for x in ["RECV", 0, c["count"], *c["values"]]))
+        elif c["kind"] == "recv_ints_truncated":
+            lines.append(f"TRUNC 64 {c['wire']}")
+            want.append("TRUNC 1")
+        elif c["kind"] == "recv_structured_query":
+            bits = lambda x: struct.unpack("<I", struct.pack("<f", x))[0]
+            m = c["subset_mask"]
+            lines.append(" ".join(str(x) for x in ["SQ", c["dim"], m & 0xffffffff, m >> 32, bits(c["range_min"]),
+                                                   bits(c["range_max"]), *[bits(v) for v in c["vec"]]]))
+            want.append(f"SQ 0 {c['wire']} 0 1")
+    le = lambda *v: struct.pack(f"<{len(v)}i", *v).hex()
+    malformed = [(f"RECV 4 {le(5, 1, 2, 3, 4, 5)}", "RECV 1"),       # count over the limit
+                 (f"RECV 4 {le(-3)}", "RECV 1"),                     # negative count
+                 (f"TRUNC 8 {le(6, 1, 2)}", "TRUNC 1"),              # shorter than its count
+                 ("TRUNC 8 -", "TRUNC 1"),                           # nothing at all
+                 (f"TRUNC 8 {le(2)[:4]}", "TRUNC 1"),                # half a count
+                 (f"DEC {le(9, 1)}", "DEC 1"),                       # buffer shorter than its count
+                 (f"DEC {le(-1)}", "DEC 1"),
+                 ("DEC 0102", "DEC 1"),
+                 (f"RECV 1 {le(0)}", "RECV 0 0")]                    # an empty vector is fine
+    lines += [m for m, _ in malformed]
+    want += [w for _, w in malformed]
+    out = run_driver(sched_rpc_driver, "rpc", "\n".join(lines) + "\n")
+    assert out == want
+
+
+def test_serving_loop_under_asan_ubsan(sched_rpc_driver):
+    """The serving loop over socket pairs with a stand-in device step: clients
+    whose prompts fit get max_generated tokens each and their connections
+    closed; a prompt that cannot finish inside seq_len, or holds a token outside
+    the vocabulary, is refused at accept; finished requests are forgotten."""
+    out = run_driver(sched_rpc_driver, "server")
+    clients = [ln.split() for ln in out if ln.startswith("CLIENT")]
+    assert [c[1] for c in clients] == ["0", "1", "0", "1", "0"]       # statuses
+    assert [c[2] for c in clients if c[1] == "0"] == ["0", "1", "2"]   # request ids in accept order
+    assert [c[3] for c in clients] == ["5", "0", "5", "0", "5"]        # tokens received
+    assert all(c[4] == "1" for c in clients)                           # the stand-in step's tokens
+    assert out[-1].startswith("REQUESTS 0 ")
