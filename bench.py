@@ -27,7 +27,10 @@ written into their pages).
 Other workloads (the other paged-attention shapes, the model step around the path,
 Q8 products and the serving loop):
   decode-single-110m     1 sequence, 12 layers x 12 heads x 64, ctx 256, 64-page pool;
-                         a step is one token through all 12 layers' append + attention
+                         a step is one token through all 12 layers' append + attention,
+                         the 12 launches replayed as one HIP graph (decode-single-110m-
+                         flushed: eager, 1 GiB read before each layer's launch, only the
+                         launches timed)
   decode-b32-mixed       B=32, 12x64, ctx ~ U[16,1024], 4096-page pool (12 layers, one timed)
   decode-prefix-shared   B=48, 12x64, 512 shared prefix tokens (32 pages, FNV-1a cache
                          hits) + private suffixes ~ U[64,512]
@@ -39,9 +42,10 @@ Q8 products and the serving loop):
   model-7b-decode-bN     one decode step of a Llama-2-7B-shaped Q8 model, N = 1, 2 or 8
                          sequences at context 1024
   serve-110m-uN          the reference's continuous-batching experiment, N users
-The three small decode workloads fit in the 256 MB Infinity Cache, so a 1 GiB
-buffer is read before every timed launch and only the launch itself is timed
-(events).
+The mixed-length and prefix-shared decode workloads fit in the 256 MB Infinity
+Cache, so a 1 GiB buffer is read before every timed launch and only the launch
+itself is timed (events).  Elsewhere the K steps run back to back under the wall
+clock, and a second pass of K steps times every launch between its own events.
 """
 from __future__ import annotations
 
@@ -124,14 +128,19 @@ class DecodeWorkload:
     bound = "hbm"
 
     def __init__(self, name, B, H, Hkv, hd, pages, layers, steps_layers, ctx, flush, seed,
-                 tables=None, unique_pages=None, describe=""):
+                 tables=None, shared_pages=False, describe=""):
         self.name, self.B, self.H, self.Hkv, self.hd = name, B, H, Hkv, hd
         self.pages, self.layers, self.steps_layers = pages, layers, steps_layers
         self.ctx = np.asarray(ctx, dtype=np.int64)
         self.positions = (self.ctx - 1).astype(np.int32)
         self.flush, self.seed, self.describe = flush, seed, describe
         self.tables = seeded_tables(self.ctx, pages, seed) if tables is None else tables
-        self.unique_pages = unique_pages
+        self.shared_pages = shared_pages
+        # K/V rows the launch reads, each (page, row) slot counted once however
+        # many sequences' tables hold its page
+        rows = np.concatenate([self.tables[b, np.arange(c) >> 4].astype(np.int64) * 16 + (np.arange(c) & 15)
+                               for b, c in enumerate(self.ctx)])
+        self.unique_rows = int(np.unique(rows).size)
 
     def setup(self, dev, g):
         import torch
@@ -174,6 +183,12 @@ class DecodeWorkload:
         # the launch also writes each sequence's new K/V row into its page
         return decode_bytes(self.ctx, self.B, self.H, self.Hkv, self.hd) + append_bytes(self.B, self.Hkv, self.hd)
 
+    def hbm_bytes_per_launch(self):
+        """Bytes the launch must move through HBM: a page that several sequences'
+        tables share is counted once (the logical bytes count it per sequence)."""
+        kv_row = self.Hkv * self.hd * 4 * 2
+        return self.work_per_launch() - (int(self.ctx.sum()) - self.unique_rows) * kv_row
+
     def tokens_per_step(self):
         return self.B
 
@@ -181,6 +196,13 @@ class DecodeWorkload:
         import torch
 
         assert torch.isfinite(self.out).all().item(), "non-finite decode output"
+
+    def check_graph_replay(self):
+        """The graph's replays recompute the eager step's outputs bit for bit."""
+        import torch
+
+        torch.cuda.synchronize()
+        assert torch.equal(self.out, self.eager_out), "graph replay differs from the eager step"
 
     def cpu_baseline(self, seconds, sample):
         """Oracle append + decode on `sample` sequences (their pages copied to a compact pool)."""
@@ -219,11 +241,12 @@ class DecodeWorkload:
         }
 
     def extra(self, kernel_s):
-        if self.unique_pages is None:
+        if not self.shared_pages:
             return {}
-        ub = self.unique_pages * 16 * self.Hkv * self.hd * 4 * 2
+        ub = self.unique_rows * self.Hkv * self.hd * 4 * 2
         return {"unique_kv_bytes_per_launch": int(ub),
-                "unique_kv_gbps": round(ub / kernel_s / 1e9, 2)}
+                "logical_bytes_per_launch": self.work_per_launch(),
+                "logical_gbps": round(self.work_per_launch() / kernel_s / 1e9, 2)}
 
 
 class PrefillWorkload:
@@ -527,6 +550,7 @@ class ServeWorkload:
 
     bound = "hbm"
     flush = False
+    event_pass = False
     PROMPT, TOKEN, GEN, BUDGET, PAGES = 256, 263, 20, 256, 8000
 
     def __init__(self, name, users, seed, describe):
@@ -685,9 +709,8 @@ def prefix_shared_workload(seed):
     for s in seqs:
         s.allocate_next_token(7, bm)
     tables = na.pack_block_tables(seqs)
-    unique = len({p for s in seqs for p in s.block_table})
     return DecodeWorkload("decode-prefix-shared", B, 12, 12, 64, pages, 1, [0], positions + 1,
-                          True, seed, tables=tables, unique_pages=unique,
+                          True, seed, tables=tables, shared_pages=True,
                           describe=(f"prefix-shared decode, B=48, 12 heads x 64, 512 shared tokens "
                                     f"(32 pages, ref_count 48) + private suffixes U[64,512], "
                                     f"{pages}-page pool, one layer, Infinity Cache flushed per launch"))
@@ -699,11 +722,17 @@ def make_workload(name, seed):
                               describe=("paged-attention decode, B=64, ctx=4096, 32 heads x 128 "
                                         "(kv heads 32), 20000-page pool, 16-token pages, one layer, "
                                         "append + attend per step"))
-    if name == "decode-single-110m":
-        return DecodeWorkload(name, 1, 12, 12, 64, 64, 12, list(range(12)), [256], True, seed,
-                              describe=("single-sequence decode, 12 layers x 12 heads x 64, ctx 256 "
-                                        "in a 64-page pool; one token through all 12 layers, "
-                                        "Infinity Cache flushed per launch"))
+    if name in ("decode-single-110m", "decode-single-110m-flushed"):
+        # the 37.7 MB pool stays in the 256 MB Infinity Cache across a decode step,
+        # as it does while serving; the -flushed form reads it cold every layer
+        flushed = name.endswith("-flushed")
+        w = DecodeWorkload(name, 1, 12, 12, 64, 64, 12, list(range(12)), [256], flushed, seed,
+                           describe=("single-sequence decode, 12 layers x 12 heads x 64, ctx 256 "
+                                     "in a 64-page pool; one token through all 12 layers" +
+                                     (", Infinity Cache flushed per launch" if flushed else
+                                      ", the 12 launches replayed as one HIP graph")))
+        w.graph = not flushed
+        return w
     if name == "decode-b32-mixed":
         rng = np.random.default_rng(seed)
         return DecodeWorkload(name, 32, 12, 12, 64, 4096, 12, [0], rng.integers(16, 1025, size=32),
@@ -751,7 +780,19 @@ def make_workload(name, seed):
     raise ValueError(name)
 
 
-WORKLOADS = ["decode-b64-ctx4096", "decode-single-110m", "decode-b32-mixed",
+# rocprofv3 summaries (under profiles/) whose traffic_bytes_per_launch line holds the
+# HBM bytes per launch of the workload's dominant kernel
+TRAFFIC_PROFILES = {
+    "decode-b64-ctx4096": "paged_attn_decode_b64_ctx4096_32x128.md",
+    "decode-single-110m": "paged_attn_decode_single_ctx256_12x64.md",
+    "decode-single-110m-flushed": "paged_attn_decode_single_ctx256_12x64.md",
+    "decode-b32-mixed": "paged_attn_decode_b32_mixed_12x64.md",
+    "decode-prefix-shared": "paged_attn_decode_prefix_shared_b48_12x64.md",
+    "prefill-b8-12x64": "paged_attn_prefill_b8_12x64.md",
+    "model-7b-decode-b1": "model_7b_decode_b1.md",
+}
+
+WORKLOADS = ["decode-b64-ctx4096", "decode-single-110m", "decode-single-110m-flushed", "decode-b32-mixed",
              "decode-prefix-shared", "prefill-b8-12x64", "q8-gemv-7b-ffn", "q8-matmul-110m-b32",
              "model-110m-decode-b32", "model-7b-decode-b1", "model-7b-decode-b2", "model-7b-decode-b8", "serve-110m-u1", "serve-110m-u4", "serve-110m-u8",
              "serve-110m-u16", "serve-110m-u32"]
@@ -768,7 +809,7 @@ def kernel_name(w) -> str:
         qh = 1
         while qh * 2 <= (8 if w.hd <= 64 else 4 if w.hd == 128 else 2) and kv_mul % (qh * 2) == 0:
             qh *= 2
-        stream = qh == kv_mul and w.unique_pages is None
+        stream = qh == kv_mul and not w.shared_pages
         return f"paged_attn_decode_kernel<{w.hd}, {qh}, {str(stream).lower()}, true> (append fused)"
     kern = os.environ.get("NITRO_PREFILL_KERNEL")
     if w.hd == 256 or kern == "valu":
@@ -805,9 +846,39 @@ def host_cpu():
         except OSError:
             pass
         sockets = len(ids) or None
+    # a guest may see only a generic model name: family, model and cache
+    # sizes identify the part
+    ident = {k.lower().replace(" ", "_").replace("(s)", "s"): info[k]
+             for k in ("CPU family", "Model", "Stepping", "Thread(s) per core", "L2 cache", "L3 cache")
+             if k in info}
     return {"cpu_model": model, "sockets": int(sockets) if sockets and str(sockets).isdigit() else sockets,
             "logical_cpus": os.cpu_count(), "avx512": attn.host_has_avx512(),
-            "omp_proc_bind": os.environ.get("OMP_PROC_BIND")}
+            "omp_proc_bind": os.environ.get("OMP_PROC_BIND"), **ident}
+
+
+def spin_cycles(torch, ms: float) -> int:
+    """Cycles of torch.cuda._sleep's spin kernel that take about `ms` milliseconds."""
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cycles = 1 << 20
+    a.record()
+    torch.cuda._sleep(cycles)
+    b.record()
+    b.synchronize()
+    return int(cycles * ms / max(a.elapsed_time(b), 1e-3))
+
+
+def capture_step(torch, w):
+    """One HIP graph holding a step's launches (captured after the warm-up, so
+    every buffer the launches use is already allocated)."""
+    torch.cuda.synchronize()
+    w.step(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    w.eager_out = w.out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        w.step(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    return graph
 
 
 def main():
@@ -824,9 +895,9 @@ def main():
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="also run a plain device-to-device copy of this many MiB three times "
                          "(the known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
-    ap.add_argument("--traffic-profile",
-                    default=os.path.join(ROOT, "profiles", "paged_attn_decode_b64_ctx4096_32x128.md"),
-                    help="rocprofv3 summary holding the measured HBM traffic per decode launch")
+    ap.add_argument("--traffic-profile", default=None,
+                    help="rocprofv3 summary holding the measured HBM traffic per launch "
+                         "(default: the workload's summary under profiles/)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only (the paged-attention path shards by sequence or "
@@ -860,19 +931,63 @@ def main():
     events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(nl)] for _ in range(args.steps)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        w.step(stream, events[i])
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    if w.flush:
+        # the flushes between launches are not part of the step: only the
+        # launches, each between its own pair of events, are timed
+        for i in range(args.steps):
+            w.step(stream, events[i])
+        torch.cuda.synchronize()
+        elapsed = None
+    elif not getattr(w, "event_pass", True):
+        # a step that is a whole serving run: its events bracket the run
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            w.step(stream, events[i])
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    else:
+        # the steps back to back with nothing recorded between their launches
+        # (replays of one HIP graph for a workload whose step is many short
+        # launches), then the same number again, eagerly, with an event pair around
+        # every launch.  A spin kernel queued ahead of each step of that pass lets
+        # the host enqueue the whole step before the GPU reaches it, so the events
+        # time the launches back to back rather than the host's launch rate.
+        graph = None
+        if getattr(w, "graph", False):
+            graph = capture_step(torch, w)
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            if graph is not None:
+                graph.replay()
+            else:
+                w.step(stream)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        if graph is not None:
+            w.check_graph_replay()
+        spin = spin_cycles(torch, 1.0)
+        for i in range(args.steps):
+            torch.cuda._sleep(spin)
+            if graph is not None:
+                # one event pair around each replay: a launch's share of it
+                events[i][0][0].record(stream)
+                graph.replay()
+                events[i][0][1].record(stream)
+            else:
+                w.step(stream, events[i])
+        torch.cuda.synchronize()
+        if graph is not None:
+            events = [ev[:1] for ev in events]
     launch_ms = [a.elapsed_time(b) for ev in events for a, b in ev]
     kernel_ms = float(np.mean(launch_ms))
+    if getattr(w, "graph", False) and not w.flush:
+        kernel_ms /= nl
     w.check()
     assert (w.device_errors() if hasattr(w, "device_errors") else w.pool.take_device_errors()) == 0
 
     work = w.work_per_launch()
+    hbm_work = w.hbm_bytes_per_launch() if hasattr(w, "hbm_bytes_per_launch") else work
     if w.flush:
-        # interleaved cache flushes are not part of the step: the step is its launches
         ms_per_step = kernel_ms * nl
     else:
         ms_per_step = elapsed / args.steps * 1e3
@@ -882,8 +997,11 @@ def main():
     else:
         unit, scale, peak = "TFLOP/s", 1e12, FP32_PEAK_TFLOPS
     step_rate = work * nl / (ms_per_step * 1e-3) / scale
-    kernel_rate = work / kernel_s / scale
+    kernel_rate = hbm_work / kernel_s / scale
     default = args.workload == DEFAULT_WORKLOAD
+    traffic_profile = args.traffic_profile or (
+        os.path.join(ROOT, "profiles", TRAFFIC_PROFILES[args.workload])
+        if args.workload in TRAFFIC_PROFILES else None)
     line = {
         "metric": METRIC if default else f"{args.workload} {unit}",
         "value": round(step_rate, 2 if unit == "GB/s" else 4),
@@ -908,8 +1026,8 @@ def main():
             "peak": peak,
             "unit": unit,
             "frac": round(kernel_rate / peak, 4),
-            "traffic": measured_traffic(args.traffic_profile) if default else None,
-            ("bytes_per_launch" if w.bound == "hbm" else "flops_per_launch"): work,
+            "traffic": measured_traffic(traffic_profile) if traffic_profile else None,
+            ("bytes_per_launch" if w.bound == "hbm" else "flops_per_launch"): hbm_work,
             "kernel_ms": round(kernel_ms, 4),
         },
         "cpu_baseline": None,

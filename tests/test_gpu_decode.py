@@ -524,3 +524,48 @@ def test_decode_append_when_rows_share_the_appended_page():
     assert np.array_equal(dk.cpu().numpy(), k) and np.array_equal(dv.cpu().numpy(), v)
     assert_parity(out.cpu().numpy(), attn.decode_batch(k, v, 0, q, tables, positions, H, H, hd),
                   "shared appended page")
+
+
+@pytest.mark.parametrize("name,tiles", [("llama110m_single_ctx256", ""), ("batched_12x64_b32", "2"),
+                                        ("gqa_32x8_hd128", "2"), ("edges_hd64", "1")])
+def test_decode_graph_replays_match_eager(name, tiles, monkeypatch):
+    """decode_append captured into a HIP graph (after an eager call has sized
+    the workspace) replays to the eager outputs and pools bit for bit, replay
+    after replay, with eager launches on the same pool in between: the launch
+    records no memset (the split-merge counters are reset by the kernel)."""
+    import torch
+
+    say(f"decode_append graph replays {name} tiles={tiles}")
+    monkeypatch.setenv("NITRO_DECODE_SPLIT_TILES", tiles)
+    c = make_case(name, seed=29)
+    B, kv_dim = len(c.ctx), c.Hkv * c.hd
+    rng = np.random.default_rng(31)
+    knew = rng.standard_normal((B, kv_dim)).astype(np.float32)
+    vnew = rng.standard_normal((B, kv_dim)).astype(np.float32)
+    q, kn, vn = to_gpu(c.q), to_gpu(knew), to_gpu(vnew)
+    want = torch.full_like(q, float("nan"))
+    c.pool.decode_append(c.layer, q, kn, vn, want, c.H, c.Hkv, c.hd)
+    torch.cuda.synchronize()
+    k_after, v_after = c.dk.clone(), c.dv.clone()
+    attn.kv_append_decode(c.k, c.v, c.layer, knew, vnew, c.tables, c.positions)
+    assert np.array_equal(k_after.cpu().numpy(), c.k) and np.array_equal(v_after.cpu().numpy(), c.v)
+    assert_parity(want.cpu().numpy(), c.run_oracle(), f"graph case {name} (eager)")
+
+    out = torch.full_like(q, float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        c.pool.decode_append(c.layer, q, kn, vn, out, c.H, c.Hkv, c.hd,
+                             torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    for i in range(4):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"
+        assert torch.equal(c.dk, k_after) and torch.equal(c.dv, v_after), f"pools after replay {i}"
+        eager = torch.full_like(q, float("nan"))
+        c.pool.decode_append(c.layer, q, kn, vn, eager, c.H, c.Hkv, c.hd)
+        torch.cuda.synchronize()
+        assert torch.equal(eager, want), f"eager call after replay {i}"
+    del graph
+    assert c.pool.take_device_errors() == 0
