@@ -239,8 +239,12 @@ void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, co
                     slots <= DECODE_ARG_ITEMS;
     if (use_list &&
         (d.work_generation != d.generation || d.work_tile != tile || d.work_tps != sh.tps)) {
-        // items {b, split, first partial slot of b, ctx}: full splits first, then the
-        // last splits by size (longest first), each group in batch order
+        // items {b, split, first partial slot of b, ctx}, shortest first (equal
+        // sizes in batch order).  The planner sizes splits so that the whole
+        // launch is resident at once; the order then only sets which loads
+        // reach the memory queue first, and the short items' loads going
+        // first measured 0.6% (mixed lengths) to 2% (shared prefixes) faster
+        // than longest first.
         std::vector<std::pair<int, int4>> order;  // (tiles, item)
         order.reserve((size_t)slots);
         int slot0 = 0;
@@ -251,7 +255,7 @@ void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, co
             slot0 += splits(b);
         }
         std::stable_sort(order.begin(), order.end(),
-                         [](const auto& x, const auto& y) { return x.first > y.first; });
+                         [](const auto& x, const auto& y) { return x.first < y.first; });
         for (size_t i = 0; i < order.size(); i++) d.arg_list.item[i] = order[i].second;
         d.work_generation = d.generation;
         d.work_tile = tile;

@@ -10,12 +10,12 @@
 //    `tiles_per_split` tiles of TILE consecutive context rows.  The grid is
 //    items x KV heads x head sub-groups, one workgroup of W wavefronts each
 //    (W = 4..16 per launch); waves take the item's tiles round-robin.  With
-//    a work list the host hands out only real items, full ones first
-//    (longest first), so every workgroup streams about the same number of
-//    tiles whatever the mix of context lengths.  The list (up to
-//    DECODE_ARG_ITEMS items) rides in the kernel arguments.  Without one, item
-//    i is split i % num_splits of sequence i / num_splits and workgroups past
-//    a sequence's last split exit at once.
+//    a work list the host hands out only real items (shortest first), and
+//    long sequences are split into equal runs, so no workgroup streams more
+//    than one split's tiles whatever the mix of context lengths.  The list
+//    (up to DECODE_ARG_ITEMS items) rides in the kernel arguments.  Without
+//    one, item i is split i % num_splits of sequence i / num_splits and
+//    workgroups past a sequence's last split exit at once.
 //  - Lane layout: LG = 8 lanes share one K/V row (16 for a 256-wide head) so
 //    that every global_load_dwordx4 reads whole 128-byte lines; a lane holds
 //    HDP/LG floats of each of its RL rows (columns c*4 + j*4*LG).  HDP is the
