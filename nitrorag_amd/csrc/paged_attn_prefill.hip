@@ -54,6 +54,8 @@
 //    online softmax rescaled once per 8 keys.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include <cmath>
 
 #include "bf16_split.hpp"
@@ -589,7 +591,9 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_mfma_kern
 // cover consecutive d of a row, so the loads coalesce), which becomes one
 // 8-byte store per plane into the transposed tile.
 template <int HD, int QT, int KSPLIT, int BNM>
-__global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_x3_kernel(PrefillLaunch a) {
+// Up to hd 64 two workgroups share a CU (LDS), which takes at most 128
+// VGPRs (4 waves per SIMD); hd 128 runs one workgroup per CU.
+__global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn_prefill_x3_kernel(PrefillLaunch a) {
     constexpr int NT = 64 * QT * KSPLIT;
     constexpr int KB = BNM / 16;               // 16-key blocks per tile
     constexpr int NBW = KB / KSPLIT;           // 16-key blocks per wave per tile
@@ -633,8 +637,17 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_x3_kernel
     const size_t dim = (size_t)a.n_heads * HD;
     const size_t qrow = (size_t)(a.row_off[seq] + q0 + min(row, qcount - 1));
 
+    // The LDS copy of the table holds -1 for an id outside the pool (counted
+    // here, once per workgroup), so the tile fetch checks only the sign.
     const int n_pages = min((last_pos >> 4) + 1, TABLE_LDS);
-    for (int i = threadIdx.x; i < n_pages; i += NT) s_table[i] = trow[i];
+    for (int i = threadIdx.x; i < n_pages; i += NT) {
+        int p = trow[i];
+        if ((unsigned)p >= (unsigned)a.num_pages) {
+            atomicAdd(a.bad_pages, 1);
+            p = -1;
+        }
+        s_table[i] = p;
+    }
     __syncthreads();
 
     // Q (pre-scaled) of this lane's query at d = 32c + 8g .. +8, in parts
@@ -699,9 +712,61 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_x3_kernel
             }
         }
     };
+    // With the whole table in LDS, a thread's loads differ from tile to tile
+    // only in their page ids: its K loads read row (tid / F4) % 16 of a page at
+    // column tid % F4, its V slots rows 4 * (tid / HD) % 16 .. +3 at column
+    // tid % HD (the strides NT / F4 and 4 * NT / HD are whole pages of keys).
+    // Each address is then one 32 x 32 -> 64-bit multiply-add on a base fixed
+    // for the launch, where the page stride in bytes fits 32 bits (a page of
+    // 16 rows over every layer is far below 4 GiB in practice; otherwise
+    // fetch_with runs).
+    static_assert((NT / F4) % 16 == 0 && (4 * NT / HD) % 16 == 0 && BNM % 16 == 0,
+                  "a thread's rows within a page are the same in every tile");
+    const uint32_t stride_b = (uint32_t)((uint64_t)a.page_stride * sizeof(float));
+    const char* const kb = reinterpret_cast<const char*>(
+        kbase + (size_t)((threadIdx.x / F4) % 16) * a.kv_dim + (threadIdx.x % F4) * 4);
+    const char* const vb = reinterpret_cast<const char*>(
+        vbase + (size_t)((4 * (threadIdx.x / HD)) % 16) * a.kv_dim + threadIdx.x % HD);
+    const size_t vrow_b = (size_t)a.kv_dim * sizeof(float);
+    // FULL: every key of the tile is at most last_pos (wave-uniform), so
+    // only the page ids decide validity and no index needs clamping.
+    auto fetch_lds_as = [&](int tile, auto full) {
+        constexpr bool FULL = decltype(full)::value;
+        kmask = vmask = 0;
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int key = tile * BNM + (int)(threadIdx.x + i * NT) / F4;
+            const int page = s_table[(FULL ? key : min(key, last_pos)) >> 4];  // -1: outside the pool
+            const bool ok = (FULL || key <= last_pos) && page >= 0;
+            kmask |= (uint32_t)ok << i;
+            kreg[i] = *reinterpret_cast<const float4*>(kb + (size_t)(uint32_t)(ok ? page : 0) * stride_b);
+        }
+#pragma unroll
+        for (int i = 0; i < VSLOTS; i++) {
+            const int key0 = tile * BNM + 4 * ((int)(threadIdx.x + i * NT) / HD);  // 4 keys, one page
+            const int page = s_table[(FULL ? key0 : min(key0, last_pos)) >> 4];
+            const bool ok = (FULL || key0 <= last_pos) && page >= 0;
+            const char* vp = vb + (size_t)(uint32_t)(ok ? page : 0) * stride_b;
+#pragma unroll
+            for (int e = 0; e < 4; e++) vreg[i][e] = *reinterpret_cast<const float*>(vp + e * vrow_b);
+            if (FULL) {
+                vmask |= (ok ? 0xFu : 0u) << (4 * i);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) vmask |= (uint32_t)(ok && key0 + e <= last_pos) << (4 * i + e);
+            }
+        }
+    };
+    auto fetch_lds = [&](int tile) {
+        if (tile * BNM + BNM - 1 <= last_pos)
+            fetch_lds_as(tile, std::true_type{});
+        else
+            fetch_lds_as(tile, std::false_type{});
+    };
+    const bool fast_fetch = table_in_lds && (uint64_t)a.page_stride * sizeof(float) < (1ull << 32);
     auto fetch = [&](int tile) {
-        if (table_in_lds)
-            fetch_with(tile, [&](int key) { return s_table[key >> 4]; });
+        if (fast_fetch)
+            fetch_lds(tile);
         else
             fetch_with(tile, [&](int key) {
                 const int pi = key >> 4;
