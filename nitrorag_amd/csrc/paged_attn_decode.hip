@@ -322,20 +322,19 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     const float* kbase = a.k_pool + a.layer_off + (size_t)kv_h * hd;
     const float* vbase = a.v_pool + a.layer_off + (size_t)kv_h * hd;
     // Fused append: the new row is read from k_new / v_new, and head
-    // sub-group 0 of the last split writes it into its page slot.
+    // sub-group 0 of the last split writes it into its page slot.  Nothing in
+    // the launch reads that slot (the row itself comes from k_new / v_new), so
+    // its values are loaded here and stored once the tiles are done: the
+    // copy's load latency stays off the tile loop.  (hd / 4 <= 64 <= threads:
+    // one float4 of K and one of V per thread at most.)
     const int new_row = a.k_new ? ctx - 1 : -1;
     const float* knew = a.k_new ? a.k_new + (size_t)b * a.kv_dim + (size_t)kv_h * hd : nullptr;
     const float* vnew = a.v_new ? a.v_new + (size_t)b * a.kv_dim + (size_t)kv_h * hd : nullptr;
-    if (knew && r == 0 && tile_end == n_tiles) {
-        const int page = s_pages[((ctx - 1) >> 4) - page_begin];
-        if (page >= 0) {
-            const size_t off = a.layer_off + (size_t)page * a.page_stride + (size_t)((ctx - 1) & 15) * a.kv_dim +
-                               (size_t)kv_h * hd;
-            for (int f = threadIdx.x; f < hd / 4; f += threads) {
-                reinterpret_cast<float4*>(a.k_pool + off)[f] = reinterpret_cast<const float4*>(knew)[f];
-                reinterpret_cast<float4*>(a.v_pool + off)[f] = reinterpret_cast<const float4*>(vnew)[f];
-            }
-        }
+    const bool appends = knew && r == 0 && tile_end == n_tiles && (int)threadIdx.x < hd / 4;
+    float4 k_app = make_float4(0.f, 0.f, 0.f, 0.f), v_app = k_app;
+    if (appends) {
+        k_app = reinterpret_cast<const float4*>(knew)[threadIdx.x];
+        v_app = reinterpret_cast<const float4*>(vnew)[threadIdx.x];
     }
 
     float m[QH], l[QH];
@@ -488,6 +487,15 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
                 store_coherent(part + hd, M);
                 store_coherent(part + hd + 1, L);
             }
+        }
+    }
+    if (appends) {
+        const int page = s_pages[((ctx - 1) >> 4) - page_begin];
+        if (page >= 0) {
+            const size_t off = a.layer_off + (size_t)page * a.page_stride + (size_t)((ctx - 1) & 15) * a.kv_dim +
+                               (size_t)kv_h * hd;
+            reinterpret_cast<float4*>(a.k_pool + off)[threadIdx.x] = k_app;
+            reinterpret_cast<float4*>(a.v_pool + off)[threadIdx.x] = v_app;
         }
     }
     if (splits_b == 1) return;  // uniform for the workgroup
