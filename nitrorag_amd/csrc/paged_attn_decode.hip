@@ -24,10 +24,11 @@
 //    wave take interleaved rows of a tile (64, 32, 16, 8 rows for HDP = 32,
 //    64, 128, 256); all 16 K/V float4 loads of a tile are issued before use.
 //  - q.k: HDP/LG FMAs per lane and row, then a DPP butterfly across LG lanes.
-//  - Softmax: every lane group keeps its own running (max, sum, acc) in base 2
-//    (q is pre-scaled by log2(e)/sqrt(hd)); groups (DPP and permlane swaps),
-//    then waves (through LDS), then splits are merged with the usual
-//    rescaling.  No score scratch.
+//  - Softmax in base 2 (q is pre-scaled by log2(e)/sqrt(hd)): a wave keeps one
+//    running max (each tile's maximum is taken across the lane groups), and
+//    every lane group its own running (sum, acc), so the groups' states just
+//    add up at the end (DPP and permlane swaps).  Waves (through LDS), then
+//    splits are merged with the usual rescaling.  No score scratch.
 //  - Split-K merge in the same launch: a split writes (acc[hd], m, l) per
 //    query head with device-coherent stores (global_store ... sc1, written
 //    through the XCD's L2), waits for them (vmcnt(0)) and bumps its (b, head
@@ -169,15 +170,12 @@ __device__ __forceinline__ void pair_values(float x, float& a, float& b) {
     }
 }
 
-// Online-softmax state (m, l, acc) of a lane merged with its pair's.
+// (l, acc) of a lane added to its pair's (both hold the same running max).
 template <int NF4, bool HALVES>
-__device__ __forceinline__ void merge_pair(float& m, float& l, float4 (&acc)[NF4]) {
-    float m0, m1, l0, l1;
-    pair_values<HALVES>(m, m0, m1);
-    pair_values<HALVES>(l, l0, l1);
-    const float mm = fmaxf(m0, m1);
-    const float f0 = scale_of(m0, mm), f1 = scale_of(m1, mm);
-    l = l0 * f0 + l1 * f1;
+__device__ __forceinline__ void sum_pair(float& l, float4 (&acc)[NF4]) {
+    float a, b;
+    pair_values<HALVES>(l, a, b);
+    l = a + b;
 #pragma unroll
     for (int j = 0; j < NF4; j++) {
         float x0, x1, y0, y1, z0, z1, w0, w1;
@@ -185,9 +183,20 @@ __device__ __forceinline__ void merge_pair(float& m, float& l, float4 (&acc)[NF4
         pair_values<HALVES>(acc[j].y, y0, y1);
         pair_values<HALVES>(acc[j].z, z0, z1);
         pair_values<HALVES>(acc[j].w, w0, w1);
-        acc[j] = make_float4(x0 * f0 + x1 * f1, y0 * f0 + y1 * f1, z0 * f0 + z1 * f1, w0 * f0 + w1 * f1);
+        acc[j] = make_float4(x0 + x1, y0 + y1, z0 + z1, w0 + w1);
     }
-    m = mm;
+}
+
+// Maximum of x over the lane groups of a wave (x is uniform within a group of
+// LG lanes; the result is in every lane).
+template <int LG>
+__device__ __forceinline__ float wave_max(float x) {
+    if constexpr (LG == 8) x = fmaxf(x, dpp_mov<0x128>(x));  // row_ror:8: the other group of the row
+    float a, b;
+    pair_values<false>(x, a, b);
+    x = fmaxf(a, b);
+    pair_values<true>(x, a, b);
+    return fmaxf(a, b);
 }
 
 // Device-coherent accesses of the split-K partials and arrival counters:
@@ -380,12 +389,14 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
                 }
             }
         }
-        // Rows are valid or not for the whole lane group (same rows), so this
-        // skip is uniform across the lanes that the DPP sums combine.
-        if (!any) continue;
+        // The running maximum is shared by the whole wave (the max below
+        // crosses lane groups), so a tile is skipped only when no lane of the
+        // wave holds a valid row.
+        if (__builtin_amdgcn_ballot_w64(any) == 0) continue;
 #pragma unroll
         for (int qi = 0; qi < QH; qi++) {
             float s[RL];
+            float mt = -INFINITY;
 #pragma unroll
             for (int i = 0; i < RL; i++) {
                 float d = 0.0f;
@@ -393,10 +404,9 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
                 for (int j = 0; j < NF4; j++) d = dot4(qv[qi][j], kr[i][j], d);
                 d = group_sum<LG>(d);
                 s[i] = valid[i] ? d : -INFINITY;
+                mt = fmaxf(mt, s[i]);
             }
-            float m_new = m[qi];
-#pragma unroll
-            for (int i = 0; i < RL; i++) m_new = fmaxf(m_new, s[i]);
+            const float m_new = fmaxf(m[qi], wave_max<LG>(mt));
             const float alpha = scale_of(m[qi], m_new);
             float p[RL];
             float psum = 0.0f;
@@ -423,29 +433,25 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
         }
     }
 
-    // Merge the lane groups of the wave (lanes with equal c, across g) on VALU
-    // permutes, no LDS round trips: lane l ^ 8 by DPP row_ror:8 (LG = 8), then
-    // l ^ 16 and l ^ 32 by gfx950's permlane16 / permlane32 swaps, each of
-    // which hands a lane both values of its pair.  Lanes of group 0 end up
-    // with the wave's (m, l, acc).
+    // Merge the lane groups of the wave (lanes with equal c, across g).  They
+    // share the running maximum, so their (l, acc) just add up: on VALU
+    // permutes, no LDS round trips, lane l ^ 8 by DPP row_ror:8 (LG = 8),
+    // then l ^ 16 and l ^ 32 by gfx950's permlane16 / permlane32 swaps, each
+    // of which hands a lane both values of its pair.  Every lane ends up with
+    // the wave's (m, l, acc).
 #pragma unroll
     for (int qi = 0; qi < QH; qi++) {
         if constexpr (LG == 8) {
-            const float mo = dpp_mov<0x128>(m[qi]), lo = dpp_mov<0x128>(l[qi]);
-            const float mm = fmaxf(m[qi], mo);
-            const float f = scale_of(m[qi], mm), fo = scale_of(mo, mm);
-            l[qi] = l[qi] * f + lo * fo;
+            l[qi] += dpp_mov<0x128>(l[qi]);
 #pragma unroll
-            for (int j = 0; j < NF4; j++) {
-                const float4 o = make_float4(dpp_mov<0x128>(acc[qi][j].x), dpp_mov<0x128>(acc[qi][j].y),
-                                             dpp_mov<0x128>(acc[qi][j].z), dpp_mov<0x128>(acc[qi][j].w));
-                acc[qi][j] = make_float4(acc[qi][j].x * f + o.x * fo, acc[qi][j].y * f + o.y * fo,
-                                         acc[qi][j].z * f + o.z * fo, acc[qi][j].w * f + o.w * fo);
-            }
-            m[qi] = mm;
+            for (int j = 0; j < NF4; j++)
+                acc[qi][j] = make_float4(acc[qi][j].x + dpp_mov<0x128>(acc[qi][j].x),
+                                         acc[qi][j].y + dpp_mov<0x128>(acc[qi][j].y),
+                                         acc[qi][j].z + dpp_mov<0x128>(acc[qi][j].z),
+                                         acc[qi][j].w + dpp_mov<0x128>(acc[qi][j].w));
         }
-        merge_pair<NF4, false>(m[qi], l[qi], acc[qi]);  // rows of 16 lanes: l ^ 16
-        merge_pair<NF4, true>(m[qi], l[qi], acc[qi]);   // halves of 32 lanes: l ^ 32
+        sum_pair<NF4, false>(l[qi], acc[qi]);  // rows of 16 lanes: l ^ 16
+        sum_pair<NF4, true>(l[qi], acc[qi]);   // halves of 32 lanes: l ^ 32
         if (g == 0) {
 #pragma unroll
             for (int j = 0; j < NF4; j++)
