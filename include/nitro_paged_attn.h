@@ -273,7 +273,10 @@ int nitro_q8_matmul(const void* w, const float* x, float* out, int32_t batch, in
  * rms_ffn f32, w1 w2 w3 Q8, rms_final f32, freq_cis_real, freq_cis_imag f32.
  * The weights are copied to the device; the caller may free the blob.  The
  * pool used with a model must have n_layers layers and kv_dim =
- * n_kv_heads * dim / n_heads.
+ * n_kv_heads * dim / n_heads.  The first forward with more than 4 rows of
+ * full-row products (NITRO_Q8_FULL_ROWS) allocates and builds a tile-layout
+ * copy of the Q8 matrices (1.125 bytes per weight) that those products read;
+ * a caller capturing such forwards into a graph runs one first.
  *
  * semantics selects the Q8 product (NITRO_Q8_*): forward_decode_batch and
  * forward_prefill_chunk compute their Q8 products with matmul_bulk

@@ -255,6 +255,9 @@ struct Q8Rope {
 struct Q8Tiled {
     const void* w[3] = {nullptr, nullptr, nullptr};
 };
+// Q8 products of up to this many activation rows run on VALU over the BlockQ8
+// rows; products of more full rows read the tile layout when there is one.
+constexpr int Q8_GEMV_MAX_BATCH = 4;
 inline size_t q8_tiled_bytes(size_t d, size_t n) { return (d + 15) / 16 * (n / 32) * 576; }
 // tiled = the tile layout of w (rows of BlockQ8, d x n)
 hipError_t launch_q8_tile(const void* w, void* tiled, int d, int n, hipStream_t stream);

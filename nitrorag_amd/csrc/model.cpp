@@ -26,8 +26,10 @@ struct nitro_model {
     size_t o_w1 = 0, o_w2 = 0, o_w3 = 0, o_rms_final = 0, o_freq_real = 0, o_freq_imag = 0;
     // the seven Q8 matrices again in the matrix-core tile layout (Q8Tiled),
     // each section holding every layer (rows are multiples of 16, so no tile
-    // spans two layers); read by the products over more than 4 rows
+    // spans two layers); read only by products over more than 4 rows of full
+    // rows, and built by the first forward that runs one (ensure_tiled)
     uint8_t* tiled = nullptr;
+    size_t tiled_bytes = 0;
     size_t t_wq = 0, t_wk = 0, t_wv = 0, t_wo = 0, t_w1 = 0, t_w2 = 0, t_w3 = 0;
     DeviceBuffer<float> x, attn, q, hb, last, ss;
     DeviceBuffer<int32_t> tokens;
@@ -38,13 +40,44 @@ struct nitro_model {
         return weights + off + (size_t)layer * rows * (cols / 32) * 36;
     }
     const uint8_t* q8t(size_t off, int layer, size_t rows, size_t cols) const {
-        return tiled + off + (size_t)layer * q8_tiled_bytes(rows, cols);
+        return tiled ? tiled + off + (size_t)layer * q8_tiled_bytes(rows, cols) : nullptr;
+    }
+    // (source offset, tiled offset, rows, cols) of each Q8 matrix
+    struct Mat {
+        size_t src, dst, rows, cols;
+    };
+    std::vector<Mat> q8_mats() const {
+        const size_t D = dim, Hd = hidden, KV = kv_dim;
+        return {{o_wq, t_wq, D, D}, {o_wk, t_wk, KV, D}, {o_wv, t_wv, KV, D}, {o_wo, t_wo, D, D},
+                {o_w1, t_w1, Hd, D}, {o_w2, t_w2, D, Hd}, {o_w3, t_w3, Hd, D}};
     }
 };
 
 namespace {
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Builds the tile-layout copy of the Q8 matrices (1.125 bytes per weight) on
+// the first forward that reads it, so a model that never runs more than 4
+// rows of full-row products never holds it.  Allocates: a caller capturing
+// such forwards into a HIP graph runs one of them before the capture.
+void ensure_tiled(nitro_model* m, hipStream_t s) {
+    if (m->tiled) return;
+    uint8_t* t = nullptr;
+    hip_check(hipMalloc((void**)&t, m->tiled_bytes), "hipMalloc(tiled weights)");
+    try {
+        for (const nitro_model::Mat& mt : m->q8_mats())
+            hip_check(launch_q8_tile(m->weights + mt.src, t + mt.dst, (int)(m->n_layers * mt.rows), (int)mt.cols, s),
+                      "q8 tile launch");
+        // built before any stream reads it, whichever stream a later forward uses
+        hip_check(hipStreamSynchronize(s), "q8 tile");
+    } catch (...) {
+        (void)hipStreamSynchronize(s);
+        (void)hipFree(t);
+        throw;
+    }
+    m->tiled = t;
+}
 
 void reserve_rows(nitro_model* m, int rows) {
     const size_t r = (size_t)rows;
@@ -86,6 +119,7 @@ void layers(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, int rows,
     const int dim = m->dim, kv = m->kv_dim, hid = m->hidden;
     const bool last = semantics == NITRO_Q8_LAST_BLOCK;
     const int parts = (dim + 15) / 16;  // partials per row left by wo / w2
+    if (!last && rows > Q8_GEMV_MAX_BATCH) ensure_tiled(m, s);
     hip_check(launch_embed_rows(m->f32(m->o_emb), tokens, m->x.ptr, rows, dim, m->vocab, pool->bad_pages.ptr,
                                 m->ss.ptr, s),
               "embed launch");
@@ -281,23 +315,16 @@ int nitro_model_create(const void* blob, uint64_t bytes, nitro_model** out) {
             hip_check(hipMalloc((void**)&m->weights, o), "hipMalloc(weights)");
             hip_check(hipMemcpy(m->weights, static_cast<const uint8_t*>(blob) + 28, o, hipMemcpyHostToDevice),
                       "hipMemcpy(weights)");
-            // the tile-layout copies, all layers of a matrix in one pass
-            struct Mat {
-                size_t src, *dst, rows, cols;
-            } mats[7] = {{m->o_wq, &m->t_wq, D, D},   {m->o_wk, &m->t_wk, KV, D}, {m->o_wv, &m->t_wv, KV, D},
-                         {m->o_wo, &m->t_wo, D, D},   {m->o_w1, &m->t_w1, Hd, D}, {m->o_w2, &m->t_w2, D, Hd},
-                         {m->o_w3, &m->t_w3, Hd, D}};
+            // offsets of the tile-layout copies (built by the first forward that
+            // reads them), all layers of a matrix together
             size_t t = 0;
-            for (Mat& mt : mats) {
-                *mt.dst = t;
-                t += L * q8_tiled_bytes(mt.rows, mt.cols);
+            size_t* dst[7] = {&m->t_wq, &m->t_wk, &m->t_wv, &m->t_wo, &m->t_w1, &m->t_w2, &m->t_w3};
+            const std::vector<nitro_model::Mat> mats = m->q8_mats();
+            for (int i = 0; i < 7; i++) {
+                *dst[i] = t;
+                t += L * q8_tiled_bytes(mats[i].rows, mats[i].cols);
             }
-            hip_check(hipMalloc((void**)&m->tiled, t), "hipMalloc(tiled weights)");
-            for (const Mat& mt : mats)
-                hip_check(launch_q8_tile(m->weights + mt.src, m->tiled + *mt.dst, (int)(L * mt.rows), (int)mt.cols,
-                                         nullptr),
-                          "q8 tile launch");
-            hip_check(hipDeviceSynchronize(), "q8 tile");
+            m->tiled_bytes = t;
         } catch (...) {
             if (m->tiled) (void)hipFree(m->tiled);
             if (m->weights) (void)hipFree(m->weights);

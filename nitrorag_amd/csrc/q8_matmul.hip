@@ -59,7 +59,6 @@ constexpr int Q8_BLOCK_BYTES = 36;   // float scale + 32 int8
 constexpr int Q8_WAVES = 4;
 constexpr int Q8_MAX_BTILES = 4;     // batch tiles of 16 per launch row (batch <= 64 per grid.y)
 constexpr int Q8_UNROLL = 4;         // 64-weight chunks whose loads a wave issues together
-constexpr int Q8_GEMV_MAX_BATCH = 4;
 
 // The 16 int8 weights and the scale a lane feeds for one 64-k chunk.
 struct Q8Slice {
