@@ -95,9 +95,6 @@ struct DecodeArgItems {
     int4 item[DECODE_ARG_ITEMS];
 };
 
-// Head sizes the model step's fused kernels take.
-inline bool supported_head_dim(int hd) { return hd == 32 || hd == 64 || hd == 128 || hd == 256; }
-
 struct DecodeBatch {
     int32_t batch = 0, max_pages = 0;
     bool shared_pages = false;       // some page id is read by more than one sequence

@@ -290,7 +290,8 @@ int nitro_model_create(const void* blob, uint64_t bytes, nitro_model** out) {
                     "dim must split into heads and heads into KV groups");
             m->head_size = m->dim / m->n_heads;
             m->kv_dim = m->n_kv_heads * m->head_size;
-            require(supported_head_dim(m->head_size), ERR_UNSUPPORTED, "head_size must be 32, 64, 128 or 256");
+            require(attention_head_dim(m->head_size), ERR_UNSUPPORTED,
+                    "head_size must be a multiple of 4 from 4 to 256");
             require(m->dim % 64 == 0 && m->hidden % 32 == 0 && m->kv_dim % 32 == 0, ERR_UNSUPPORTED,
                     "dim must be a multiple of 64, hidden_dim and kv_dim of 32");
             const size_t L = m->n_layers, D = m->dim, Hd = m->hidden, KV = m->kv_dim, V = m->vocab;

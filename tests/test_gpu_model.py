@@ -128,10 +128,14 @@ MODELS = {
     # rows of >= 2048 k: the flat products with rms_norm, RoPE + K/V append,
     # SwiGLU and residual epilogues (3 decode rows)
     "gqa_hd128_wide_l1": (2048, 2304, 1, 16, 4, 500, 128),
+    # head sizes other than 32/64/128/256 (attention on the padded kernels)
+    "gqa_hd96_l2": (384, 512, 2, 4, 2, 400, 160),
+    "mha_hd80_l1": (320, 384, 1, 4, 4, 300, 160),
+    "gqa_hd48_l2": (192, 256, 2, 4, 2, 300, 160),
 }
 
 
-@pytest.mark.parametrize("name", ["mha_hd64_l3", "gqa_hd128_l2", "gqa_hd32_l2"])
+@pytest.mark.parametrize("name", ["mha_hd64_l3", "gqa_hd128_l2", "gqa_hd32_l2", "gqa_hd96_l2"])
 def test_full_row_products_over_many_rows(name):
     """Full-row products over more than 4 activation rows take the bf16
     matrix-core kernel over the tile-layout weights, with rms_norm, RoPE + K/V
