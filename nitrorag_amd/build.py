@@ -34,6 +34,10 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"-I{INCLUDE}", f"-I{CSRC}", "-Wall"]
 # as by /opt/rocm's (7.2), whichever of the two the process has loaded.
 HIP_FLAGS = [f"--offload-arch={ARCH}", "-mcode-object-version=5", "-Xclang", "-target-feature",
              "-Xclang", "-packed-fp32-ops"]
+# The decode kernel's first arguments (the scalars that locate a workgroup's
+# block-table slice) are preloaded into SGPRs, so its first loads do not wait
+# for a load of the kernel arguments.
+SOURCE_FLAGS = {"paged_attn_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=10"]}
 
 
 def _run(cmd):
@@ -49,7 +53,7 @@ def _compile(src: str) -> str:
     if src in HOST_SOURCES:
         cmd = ["g++", *COMMON, "-c", path, "-o", obj]
     elif src.endswith(".hip"):
-        cmd = [HIPCC, *COMMON, *HIP_FLAGS, "-x", "hip", "-c", path, "-o", obj]
+        cmd = [HIPCC, *COMMON, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), "-x", "hip", "-c", path, "-o", obj]
     else:
         cmd = [HIPCC, *COMMON, *HIP_FLAGS, "-c", path, "-o", obj]
     _run(cmd)

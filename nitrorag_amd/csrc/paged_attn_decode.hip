@@ -217,9 +217,18 @@ __device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcn
 // row is loaded once and scored against all QH queries.  QH > 1 needs about
 // twice the registers, so those workgroups hold at most 8 waves.  FULL: the
 // head size is HDP (no column masks).
+//
+// The scalars that locate a workgroup's item and its block-table slice come
+// first in the argument list, so that the build preloads them into SGPRs
+// (-mllvm -amdgpu-kernarg-preload-count=10): the table and position loads go
+// out at once, while the loads of the other arguments are still in flight.
+// flags: bit 0 XCD work order, bit 1 items from arg_items.  waves and
+// nblocks stand for blockDim.x / 64 and gridDim.x, which are read from memory.
 template <int HDP, int QH, bool STREAM, bool FULL>
 __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged_attn_decode_kernel(
-    DecodeLaunch a, DecodeArgItems arg_items) {
+    const int32_t* __restrict__ tables, const int32_t* __restrict__ positions, int32_t max_pages,
+    int32_t num_splits, int32_t tiles_per_split, int32_t n_heads, int32_t kv_mul, int32_t flags,
+    int32_t waves, int32_t nblocks, DecodeLaunch a, DecodeArgItems arg_items) {
     using G = DecodeGeom<HDP>;
     constexpr int LG = G::LG, NF4 = G::NF4, RL = G::RL, GROUPS = G::GROUPS, TILE = G::TILE;
     constexpr int MAXW = QH == 1 ? MAX_WAVES : MAX_WAVES / 2;
@@ -228,8 +237,7 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     __shared__ float s_m[MAXW][QH], s_l[MAXW][QH];
     __shared__ int s_last;
     const int hd = FULL ? HDP : a.head_dim;
-    const int waves = blockDim.x >> 6;
-    const int threads = blockDim.x;
+    const int threads = waves * 64;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -243,53 +251,61 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     // eighth of that order: workgroups sharing a K/V range run together on
     // one XCD and re-read it from its L2.
     int w = blockIdx.x;
-    if (a.xcd_remap) {
-        const int n = gridDim.x, per = n >> 3, rem = n & 7;
+    if ((flags & 1)) {
+        const int n = nblocks, per = n >> 3, rem = n & 7;
         const int x = w & 7;
         w = x * per + min(x, rem) + (w >> 3);
     }
-    const int hsubs = a.kv_mul / QH;
-    const int n_kv = a.n_heads / a.kv_mul;
+    const int hsubs = kv_mul / QH;
+    const int n_kv = n_heads / kv_mul;
     const int r = w % hsubs;
     const int rest = w / hsubs;
     const int kv_h = rest % n_kv;
     const int item = rest / n_kv;
     const int hg = kv_h * hsubs + r;  // head group of the sequence (arrival counter)
-    const int bh_in_seq = kv_h * a.kv_mul + r * QH;
+    const int bh_in_seq = kv_h * kv_mul + r * QH;
 
     // The item: from the work list {b, split, first partial slot of b, ctx},
     // or implied by the block id (then the position load goes out together
     // with the block-table slice and q below).
-    int b, split, pslot0, ctx;
-    if (a.arg_items) {
-        // the list rides in the kernel arguments, fetched with the rest of
-        // them: no load precedes the table and q loads
+    const bool listed = flags & 2;
+    int b, split, pslot0, ctx = 0;
+    if (listed) {
+        // the list rides in the kernel arguments: one scalar load of the
+        // item precedes the table and q loads
         const int4 it = arg_items.item[item];
         b = it.x;
         split = it.y;
         pslot0 = it.z;
         ctx = it.w;
     } else {
-        b = item / a.num_splits;
-        split = item - b * a.num_splits;
-        pslot0 = b * a.num_splits;
-        ctx = a.positions[b] + 1;
+        b = item / num_splits;
+        split = item - b * num_splits;
+        pslot0 = b * num_splits;
     }
-    const int bh0 = b * a.n_heads + bh_in_seq;
+    const int bh0 = b * n_heads + bh_in_seq;
     // The split's block-table slice is read speculatively over the split's
     // whole page range (clipped to the table row); only the entries below the
     // context length are validated and used.
     constexpr int TBL_PER_THREAD = DECODE_MAX_SPLIT_PAGES / 256;  // >= 4 waves per workgroup
-    const int tile_begin = split * a.tiles_per_split;
+    const int tile_begin = split * tiles_per_split;
     const int page_begin = (tile_begin * TILE) >> 4;
-    const int spec_end = min(a.max_pages, ((tile_begin + a.tiles_per_split) * TILE + 15) >> 4);
-    const int32_t* trow = a.tables + (size_t)b * a.max_pages;
+    const int spec_end = min(max_pages, ((tile_begin + tiles_per_split) * TILE + 15) >> 4);
+    const int32_t* trow = tables + (size_t)b * max_pages;
     int tv[TBL_PER_THREAD];
 #pragma unroll
     for (int k = 0; k < TBL_PER_THREAD; k++) {
         const int i = threadIdx.x + k * threads;
         tv[k] = i < spec_end - page_begin ? trow[page_begin + i] : -1;
     }
+
+    // The position (implied items), then the other arguments the prologue
+    // and the first tile use, loaded here together: one round trip, which
+    // overlaps the table loads above, rather than one where each is first
+    // used.  (A vector load of the position measured slower.)
+    if (!listed) ctx = positions[b] + 1;
+    asm volatile("" ::"s"(a.q), "s"(a.qscale), "s"(a.ctx_limit), "s"(a.num_pages), "s"(a.k_pool), "s"(a.v_pool),
+                 "s"(a.layer_off), "s"(a.page_stride), "s"(a.k_new), "s"(a.v_new), "s"(a.kv_dim));
 
     // q slices of this lane, pre-scaled to base-2 logits (columns past the
     // head size are zero).
@@ -309,8 +325,8 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     ctx = max(0, min(ctx, a.ctx_limit));  // a position past the table (or the splits) reads no further
     const int n_tiles = (ctx + TILE - 1) / TILE;
     if (tile_begin >= n_tiles) return;  // uniform for the workgroup (implied items only)
-    const int tile_end = min(n_tiles, tile_begin + a.tiles_per_split);
-    const int splits_b = (n_tiles + a.tiles_per_split - 1) / a.tiles_per_split;
+    const int tile_end = min(n_tiles, tile_begin + tiles_per_split);
+    const int splits_b = (n_tiles + tiles_per_split - 1) / tiles_per_split;
 
     // Used part of the slice -> LDS (page ids checked against the pool size).
     const int page_end = ((min(ctx, tile_end * TILE) - 1) >> 4) + 1;
@@ -487,7 +503,7 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
         if (splits_b == 1) {
             a.out[(size_t)bh * hd + d] = A / L;
         } else {
-            float* part = a.partials + ((size_t)(pslot0 + split) * a.n_heads + bh - b * a.n_heads) * a.pstride;
+            float* part = a.partials + ((size_t)(pslot0 + split) * n_heads + bh - b * n_heads) * a.pstride;
             store_coherent(part + d, A);
             if (d == 0) {
                 store_coherent(part + hd, M);
@@ -510,7 +526,7 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     wait_vector_memory();
     __syncthreads();
     if (threadIdx.x == 0) {
-        int* counter = a.counters + (size_t)b * (a.n_heads / QH) + hg;
+        int* counter = a.counters + (size_t)b * (n_heads / QH) + hg;
         const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = before == splits_b - 1;
         if (before == splits_b - 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -529,7 +545,7 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
 #pragma unroll
             for (int j = 0; j < MERGE_BATCH; j++) {
                 const int sp = min(sp0 + j, splits_b - 1);  // past the last split: a repeat, unused
-                const float* part = a.partials + ((size_t)(pslot0 + sp) * a.n_heads + h) * a.pstride;
+                const float* part = a.partials + ((size_t)(pslot0 + sp) * n_heads + h) * a.pstride;
                 ms[j] = load_coherent(part + hd);
                 ls[j] = load_coherent(part + hd + 1);
                 as[j] = load_coherent(part + d);
@@ -571,12 +587,16 @@ int decode_tile_rows(int head_dim) {
 template <int HDP, int QH>
 static void launch_main(const DecodeLaunch& a, const DecodeArgItems& it, dim3 grid, hipStream_t stream) {
     const dim3 block(64 * a.waves);
+    const int32_t flags = (a.xcd_remap ? 1 : 0) | (a.arg_items ? 2 : 0);
+#define NITRO_DECODE_ARGS a.tables, a.positions, a.max_pages, a.num_splits, a.tiles_per_split, a.n_heads, a.kv_mul, \
+                          flags, a.waves, (int32_t)grid.x, a, it
     if (a.head_dim != HDP)  // padded head: plain loads
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, false>), grid, block, 0, stream, a, it);
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, false>), grid, block, 0, stream, NITRO_DECODE_ARGS);
     else if (a.stream_kv)
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, true, true>), grid, block, 0, stream, a, it);
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, true, true>), grid, block, 0, stream, NITRO_DECODE_ARGS);
     else
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, true>), grid, block, 0, stream, a, it);
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, true>), grid, block, 0, stream, NITRO_DECODE_ARGS);
+#undef NITRO_DECODE_ARGS
 }
 
 template <int HDP>
