@@ -569,3 +569,57 @@ def test_decode_graph_replays_match_eager(name, tiles, monkeypatch):
         assert torch.equal(eager, want), f"eager call after replay {i}"
     del graph
     assert c.pool.take_device_errors() == 0
+
+
+@pytest.mark.parametrize("max_context_split", [False, True])
+def test_decode_counts_and_skips_page_ids_outside_the_pool(max_context_split):
+    """Tables handed to the kernel directly (nitro_paged_attn_decode_static
+    takes device tables, with no host validation) may hold page ids outside
+    the pool: the kernel counts them (nitro_kvpool_take_device_errors) and
+    skips their rows without reading them.  The other sequences' outputs are
+    bit-identical to a launch with clean tables, and the damaged sequence
+    attends exactly its rows on valid pages (fp64 closed form).  With
+    max_context_split the launch splits, so the skipped rows fall in split
+    partials that are merged."""
+    import torch
+
+    import nitrorag_amd as na
+    from nitrorag_amd import _native as N
+    from oracle import closed_form as cf
+
+    say(f"bad page ids, split={max_context_split}")
+    rng = np.random.default_rng(91)
+    H, Hkv, hd, pages = 4, 4, 64, 600
+    ctx = np.array([50, 37, 64] if not max_context_split else [3000, 2100, 64])
+    tables = random_tables(rng, ctx, pages)
+    positions = (ctx - 1).astype(np.int32)
+    k = rng.standard_normal((pages, 1, 16, Hkv * hd)).astype(np.float32)
+    v = rng.standard_normal((pages, 1, 16, Hkv * hd)).astype(np.float32)
+    q = rng.standard_normal((len(ctx), H * hd)).astype(np.float32)
+    pool = na.KVPool.wrap(to_gpu(k), to_gpu(v))
+    dq, pos_d = to_gpu(q), to_gpu(positions)
+
+    def run(tab):
+        out = torch.full_like(dq, float("nan"))
+        tab_d = to_gpu(tab)
+        st = N.lib().nitro_paged_attn_decode_static(
+            pool.handle, 0, ctypes.c_void_p(dq.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+            ctypes.c_void_p(tab_d.data_ptr()), ctypes.c_void_p(pos_d.data_ptr()), len(ctx),
+            tab.shape[1], int(ctx.max()), H, Hkv, hd, None)
+        assert st == N.OK, N.last_error()
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+    clean = run(tables)
+    assert pool.take_device_errors() == 0
+    bad = tables.copy()
+    bad[1, 1] = pages + 7  # past the pool
+    bad[1, 2] = -3         # negative
+    got = run(bad)
+    assert pool.take_device_errors() > 0
+    assert np.array_equal(got[0], clean[0]) and np.array_equal(got[2], clean[2])
+    rows = np.arange(ctx[1])
+    keep = rows[(rows // 16 != 1) & (rows // 16 != 2)]
+    pg = tables[1][keep // 16].astype(np.int64)
+    want = cf.attention_f64(q[1], k[pg, 0, keep % 16], v[pg, 0, keep % 16], H, Hkv, hd)
+    assert_parity(got[1:2], want[None, :].astype(np.float32), "sequence with bad page ids")
