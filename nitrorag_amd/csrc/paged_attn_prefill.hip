@@ -259,15 +259,21 @@ __global__ __launch_bounds__(THREADS) void paged_attn_prefill_kernel(PrefillLaun
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// The larger of a and b, NaN if either is (v_maximum3_f32).  fmaxf ignores a
+// NaN operand, so in IEEE mode the compiler first quiets each operand that is
+// not the result of arithmetic (an MFMA or permute result) with an extra
+// v_max_f32 x, x.  A NaN score makes the softmax NaN either way.
+__device__ __forceinline__ float max_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Max / sum over the four lanes l%16 + 16g (g = 0..3) of a wave, on gfx950's
 // row-swap permutes (VALU only; no LDS round trip).  permlane16_swap(x, x)
 // returns rows (0,0,2,2) and (1,1,3,3); permlane32_swap(y, y) returns halves
 // (lo,lo) and (hi,hi).
 __device__ __forceinline__ float max_over_rows(float x) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const float y = max_nan(__uint_as_float(a[0]), __uint_as_float(a[1]));
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    return max_nan(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ float sum_over_rows(float x) {
@@ -637,6 +643,17 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
     const size_t dim = (size_t)a.n_heads * HD;
     const size_t qrow = (size_t)(a.row_off[seq] + q0 + min(row, qcount - 1));
 
+    // This lane's query at d = 32c + 8g .. +8, loaded before the table so the
+    // two loads' latencies overlap; it is scaled and split into parts once
+    // the first tile's K/V loads are in flight.
+    float4 qraw[NC][2];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const float4* src = reinterpret_cast<const float4*>(a.q + qrow * dim + (size_t)h * HD + 32 * c + 8 * g);
+        qraw[c][0] = src[0];
+        qraw[c][1] = src[1];
+    }
+
     // The LDS copy of the table holds -1 for an id outside the pool (counted
     // here, once per workgroup), so the tile fetch checks only the sign.
     const int n_pages = min((last_pos >> 4) + 1, TABLE_LDS);
@@ -650,16 +667,6 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
     }
     __syncthreads();
 
-    // Q (pre-scaled) of this lane's query at d = 32c + 8g .. +8, in parts
-    bf16x8 qp[3][NC];
-#pragma unroll
-    for (int c = 0; c < NC; c++) {
-        const float4* src = reinterpret_cast<const float4*>(a.q + qrow * dim + (size_t)h * HD + 32 * c + 8 * g);
-        const float4 u = src[0], w = src[1];
-        const float v[8] = {u.x * a.qscale, u.y * a.qscale, u.z * a.qscale, u.w * a.qscale,
-                            w.x * a.qscale, w.y * a.qscale, w.z * a.qscale, w.w * a.qscale};
-        split3(v, qp[0][c], qp[1][c], qp[2][c]);
-    }
     f32x4 acc[NB];
 #pragma unroll
     for (int n = 0; n < NB; n++) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -778,6 +785,14 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
     };
 
     fetch(0);
+    bf16x8 qp[3][NC];  // Q (pre-scaled) in parts
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const float4 u = qraw[c][0], w = qraw[c][1];
+        const float v[8] = {u.x * a.qscale, u.y * a.qscale, u.z * a.qscale, u.w * a.qscale,
+                            w.x * a.qscale, w.y * a.qscale, w.z * a.qscale, w.w * a.qscale};
+        split3(v, qp[0][c], qp[1][c], qp[2][c]);
+    }
     for (int tile = 0; tile < n_tiles; tile++) {
         __syncthreads();  // previous tile fully consumed
         // four values as three bf16 planes, one 8-byte store each
@@ -848,13 +863,13 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
             const int last_key0 = tile * BNM + (kg + (nvb - 1) * KSPLIT) * 16;
             float p[NBW][4];
             if (nvb == NBW && last_key0 + 15 <= wave_first) {
-                float bmax = fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3]));
+                float bmax = max_nan(max_nan(st[0][0], st[0][1]), max_nan(st[0][2], st[0][3]));
 #pragma unroll
                 for (int j = 1; j < NBW; j++)
-                    bmax = fmaxf(bmax, fmaxf(fmaxf(st[j][0], st[j][1]), fmaxf(st[j][2], st[j][3])));
+                    bmax = max_nan(bmax, max_nan(max_nan(st[j][0], st[j][1]), max_nan(st[j][2], st[j][3])));
                 bmax = max_over_rows(bmax);
                 if (__builtin_amdgcn_ballot_w64(bmax > m + kLazyRescaleLog2) != 0) {  // wave-uniform
-                    const float m_new = fmaxf(m, bmax);
+                    const float m_new = max_nan(m, bmax);
                     const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // m = -inf: 0
                     lsum *= alpha;
 #pragma unroll
@@ -874,11 +889,11 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         sm[j][r] = (j < nvb && kj + r <= my_pos) ? st[j][r] : -INFINITY;
-                        bmax = fmaxf(bmax, sm[j][r]);
+                        bmax = max_nan(bmax, sm[j][r]);
                     }
                 }
                 bmax = max_over_rows(bmax);
-                const float m_new = fmaxf(m, bmax);
+                const float m_new = max_nan(m, bmax);
                 const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - m_new);
 #pragma unroll
                 for (int j = 0; j < NBW; j++)
