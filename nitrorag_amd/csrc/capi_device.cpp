@@ -80,6 +80,48 @@ bool any_page_shared(const nitro_kvpool* pool, DecodeBatch& d, const int32_t* ta
     return shared;
 }
 
+// Shared prefixes: at least kPrefixMinPages pages, in whole multiples of
+// kPrefixPageQuantum pages (64 rows: a whole number of decode tiles at every
+// head size, so a sequence's own rows start on a tile).
+constexpr int kPrefixMinPages = 4;
+constexpr int kPrefixPageQuantum = 4;
+
+// Groups of two or more sequences whose first pages are the same physical
+// pages (prefix-cache hits): sequences with equal first page ids, and the
+// longest run of pages all of them share, kept below every member's newest
+// row (pos_b >= 16 * pages, so each member keeps at least that row as its own).
+std::vector<DecodeBatch::PrefixGroup> find_prefix_groups(const int32_t* tables, const int32_t* positions,
+                                                         int batch, int max_pages) {
+    std::vector<DecodeBatch::PrefixGroup> groups;
+    std::vector<std::pair<int32_t, int32_t>> first;  // (first page id, b)
+    for (int b = 0; b < batch; b++)
+        if (positions[b] >= BLOCK_SIZE * kPrefixMinPages) first.push_back({tables[(size_t)b * max_pages], b});
+    std::sort(first.begin(), first.end());
+    for (size_t i = 0; i < first.size();) {
+        size_t j = i;
+        while (j < first.size() && first[j].first == first[i].first) j++;
+        if (j - i >= 2) {
+            DecodeBatch::PrefixGroup g;
+            int cap = max_pages;
+            for (size_t k = i; k < j; k++) {
+                g.members.push_back(first[k].second);
+                cap = std::min(cap, positions[first[k].second] / BLOCK_SIZE);
+            }
+            const int32_t* row0 = tables + (size_t)g.members[0] * max_pages;
+            int pages = 0;
+            for (; pages < cap; pages++) {
+                bool same = true;
+                for (int m : g.members) same &= tables[(size_t)m * max_pages + pages] == row0[pages];
+                if (!same) break;
+            }
+            g.pages = pages - pages % kPrefixPageQuantum;
+            if (g.pages >= kPrefixMinPages) groups.push_back(std::move(g));
+        }
+        i = j;
+    }
+    return groups;
+}
+
 void check_shape(const nitro_kvpool* pool, int layer, int n_heads, int n_kv_heads, int head_dim) {
     require(layer >= 0 && layer < pool->num_layers, ERR_INVALID_ARGUMENT, "layer out of range");
     require(n_heads > 0 && n_kv_heads > 0, ERR_INVALID_ARGUMENT, "head counts must be positive");
@@ -218,11 +260,169 @@ DecodeLaunch decode_launch_base(const nitro_kvpool* pool, int layer, const float
     return a;
 }
 
+// Shared prefixes (prefix-cache hits): the rows that every member of a group
+// shares are streamed once per set of W members (W = waves per workgroup),
+// not once per member.  The launch's work list puts member items first: a
+// workgroup whose W waves each take one member of the set over the same
+// chunk of shared rows (so they read each row at about the same time,
+// through one L1), each wave writing its member's partial of the chunk.  The
+// sequences' own rows follow as usual splits, and every (sequence, head)
+// merges its partials, the member items' first, whoever arrives last.  The
+// list rides in the kernel arguments; a batch whose list does not fit, or
+// that groups query heads per workgroup (GQA), is launched as usual.
+
+// Builds that list into d.arg_list for the uploaded batch; false when it does
+// not fit the kernel arguments or the item fields.
+bool plan_prefix(nitro_kvpool* pool, int n_heads, int n_kv_heads, int head_dim) {
+    DecodeBatch& d = pool->decode;
+    const int B = d.batch;
+    const int tile = decode_tile_rows(head_dim);
+    std::vector<int> shared_rows(B, 0), group(B, -1);
+    for (size_t g = 0; g < d.groups.size(); g++)
+        for (int b : d.groups[g].members) {
+            shared_rows[b] = d.groups[g].pages * BLOCK_SIZE;
+            group[b] = (int)g;
+        }
+    auto ctx = [&](int b) { return d.positions[b] + 1; };
+    auto own = [&](int b) { return ctx(b) - shared_rows[b]; };
+    const DecodeShape sh = plan_decode_shape(pool, B, own, n_heads, n_kv_heads, head_dim);
+    if (sh.qh != 1) return false;
+    const int max_tps = (DECODE_MAX_SPLIT_PAGES - 2) * BLOCK_SIZE / tile;
+    const int W = sh.waves;
+    auto sets = [&](const DecodeBatch::PrefixGroup& g) { return ((int)g.members.size() + W - 1) / W; };
+    auto own_tiles = [&](int b) { return (ctx(b) + tile - 1) / tile - shared_rows[b] / tile; };
+    auto splits = [&](int b) { return (own_tiles(b) + sh.tps - 1) / sh.tps; };
+    long long main_items = 0;
+    for (int b = 0; b < B; b++) main_items += splits(b);
+
+    // Chunks of ch tiles of shared rows per member item, which a member's
+    // wave streams one after another.  Shorter chunks mean more items and
+    // more partials to merge, longer ones a longer wave: the shared rows of
+    // the longest group in about three chunks, at least a split's tiles per
+    // wave and at most 8 tiles (measured on 48 sequences sharing 512 rows,
+    // 12 x 64: 26.0-26.5 us at 6-7 tiles, 27.7 at 5, 28.3 at 10, 36.4 at 16;
+    // 29.1 us reading every sequence's rows), more when the list would not
+    // fit.  A chunk starts on a page.
+    int longest = 0;
+    for (const auto& g : d.groups) longest = std::max(longest, g.pages * BLOCK_SIZE / tile);
+    int ch = std::min(8, std::max((sh.tps + W - 1) / W, (longest + 2) / 3));
+    if (env_int("NITRO_DECODE_PREFIX_CHUNK", 0) > 0) ch = env_int("NITRO_DECODE_PREFIX_CHUNK", 0);
+    while ((ch * tile) % BLOCK_SIZE) ch++;
+    long long member_items = 0, entries = 0;
+    for (;; ch *= 2) {
+        member_items = entries = 0;
+        for (const auto& g : d.groups) {
+            member_items += (long long)sets(g) * ((g.pages * BLOCK_SIZE / tile + ch - 1) / ch);
+            for (int k = 0; k < sets(g); k++) entries += (std::min(W, (int)g.members.size() - k * W) + 1) / 2;
+        }
+        if (member_items + main_items + entries <= DECODE_ARG_ITEMS) break;
+        if (ch * 2 > max_tps) return false;
+    }
+    auto chunks_of = [&](int g) { return (d.groups[g].pages * BLOCK_SIZE / tile + ch - 1) / ch; };
+
+    // Partial slots: per sequence its member parts, then its splits.
+    std::vector<int> first_slot(B), parts(B);
+    int slot0 = 0;
+    for (int b = 0; b < B; b++) {
+        parts[b] = (group[b] >= 0 ? chunks_of(group[b]) : 0) + splits(b);
+        if (splits(b) > 255 || shared_rows[b] / tile >= (1 << 23) || parts[b] >= (1 << 15) || slot0 >= (1 << 16))
+            return false;
+        first_slot[b] = slot0;
+        slot0 += parts[b];
+    }
+
+    // Member items {-1 - first entry, members | part << 8, first tile,
+    // tiles}; entries {b, first slot | parts << 16, b', ...} after the items.
+    int n = 0, at = (int)(member_items + main_items);
+    for (size_t g = 0; g < d.groups.size(); g++) {
+        const auto& members = d.groups[g].members;
+        const int tiles = d.groups[g].pages * BLOCK_SIZE / tile;
+        for (int k = 0; k < sets(d.groups[g]); k++) {
+            const int count = std::min(W, (int)members.size() - k * W);
+            const int base = at;
+            for (int j = 0; j < count; j += 2) {
+                const int b0 = members[k * W + j], b1 = members[k * W + std::min(j + 1, count - 1)];
+                d.arg_list.item[at++] = make_int4(b0, first_slot[b0] | (parts[b0] << 16), b1,
+                                                  first_slot[b1] | (parts[b1] << 16));
+            }
+            for (int c = 0; c < chunks_of((int)g); c++)
+                d.arg_list.item[n++] =
+                    make_int4(-1 - base, count | (c << 8), c * ch, std::min(ch, tiles - c * ch));
+        }
+    }
+    // The splits of each sequence's own rows, shortest first.
+    std::vector<std::pair<int, int4>> order;  // (tiles, item)
+    for (int b = 0; b < B; b++) {
+        const int first_tile = shared_rows[b] / tile;
+        const int n_pre = parts[b] - splits(b);
+        for (int x = 0; x < splits(b); x++)
+            order.push_back({std::min(sh.tps, own_tiles(b) - x * sh.tps),
+                             make_int4(b, x | (first_tile << 8), first_slot[b] | (parts[b] << 16), ctx(b))});
+        (void)n_pre;
+    }
+    std::stable_sort(order.begin(), order.end(), [](const auto& x, const auto& y) { return x.first < y.first; });
+    for (const auto& o : order) d.arg_list.item[n++] = o.second;
+    d.main_items = n;
+    d.main_tps = sh.tps;
+    d.main_waves = W;
+    d.prefix_slots = slot0;
+    d.work_generation = ~0ull;  // arg_list now holds this list, not the usual one
+    return true;
+}
+
+// The shared-prefix form of a decode launch, when the batch has prefix
+// groups and its list fits; false otherwise (nothing launched).
+bool launch_decode_prefix(nitro_kvpool* pool, int layer, const float* q, float* out, const float* k_new,
+                          const float* v_new, int n_heads, int n_kv_heads, int head_dim, hipStream_t s) {
+    DecodeBatch& d = pool->decode;
+    const int32_t key = (n_heads << 16) ^ (n_kv_heads << 9) ^ head_dim;
+    if (d.prefix_generation != d.generation || d.prefix_heads != key ||
+        (d.prefix_ok && d.work_generation == d.generation)) {  // arg_list since taken by the usual list
+        d.prefix_generation = d.generation;
+        d.prefix_heads = key;
+        d.prefix_ok = plan_prefix(pool, n_heads, n_kv_heads, head_dim) ? 1 : 0;
+    }
+    if (!d.prefix_ok) return false;
+    DecodeShape sh;
+    sh.qh = 1;
+    sh.waves = d.main_waves;
+    sh.tps = d.main_tps;
+    DecodeLaunch a = decode_launch_base(pool, layer, q, out, n_heads, n_kv_heads, head_dim, sh, true);
+    pool->partials.reserve((size_t)d.prefix_slots * n_heads * a.pstride);
+    if (pool->counters.reserve((size_t)d.batch * n_heads))
+        hip_check(hipMemset(pool->counters.ptr, 0, pool->counters.count * sizeof(int32_t)), "hipMemset");
+    a.tables = d.tables.ptr;
+    a.positions = d.pos.ptr;
+    a.partials = pool->partials.ptr;
+    a.counters = pool->counters.ptr;
+    a.batch = d.batch;
+    a.max_pages = d.max_pages;
+    a.num_splits = 0;
+    a.arg_items = 1;
+    a.members = 1;
+    a.work_items = d.main_items;
+    a.ctx_limit = d.max_pages * BLOCK_SIZE;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    // each row past the shared ones is read once when no such page is read
+    // twice: non-temporal loads, as without sharing (the shared rows are
+    // re-read by the member sets, through plain loads of the same kernel
+    // only in that case: NITRO_DECODE_STREAM overrides)
+    a.stream_kv = env_int("NITRO_DECODE_STREAM", -1) >= 0 ? env_int("NITRO_DECODE_STREAM", -1) != 0
+                                                         : d.own_rows_private && a.kv_mul == 1;
+    hip_check(launch_paged_attn_decode(a, s, &d.arg_list), "paged_attn_decode launch");
+    pool->last_stream = s;
+    return true;
+}
+
 // One decode launch over the pool's uploaded batch (k_new / v_new: the fused
 // append, used by the caller only where it is safe).
 void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, const float* k_new,
                    const float* v_new, int n_heads, int n_kv_heads, int head_dim, hipStream_t s) {
     DecodeBatch& d = pool->decode;
+    if (!d.groups.empty() && env_int("NITRO_DECODE_PREFIX", 1) != 0 &&
+        launch_decode_prefix(pool, layer, q, out, k_new, v_new, n_heads, n_kv_heads, head_dim, s))
+        return;
     const int B = d.batch;
     auto ctx = [&](int b) { return d.positions[b] + 1; };
     const DecodeShape sh = plan_decode_shape(pool, B, ctx, n_heads, n_kv_heads, head_dim);
@@ -256,7 +456,7 @@ void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, co
         for (int b = 0; b < B; b++) {
             const int nt = (ctx(b) + tile - 1) / tile;
             for (int x = 0; x < splits(b); x++)
-                order.push_back({std::min(sh.tps, nt - x * sh.tps), make_int4(b, x, slot0, ctx(b))});
+                order.push_back({std::min(sh.tps, nt - x * sh.tps), make_int4(b, x, slot0 | (splits(b) << 16), ctx(b))});
             slot0 += splits(b);
         }
         std::stable_sort(order.begin(), order.end(),
@@ -308,6 +508,7 @@ void set_device_decode_batch(nitro_kvpool* pool, int batch, int max_pages, const
     *device_slots = d.slots.ptr;
     d.positions.assign(positions, positions + batch);
     d.shared_pages = shared_pages;
+    d.groups.clear();  // no host tables to find them in
     d.new_rows_private = false;
     d.generation++;
     d.batch = batch;
@@ -432,6 +633,20 @@ int nitro_decode_batch_upload(nitro_kvpool* pool, const int32_t* tables, const i
         st.finish(s);
         d.positions.assign(positions, positions + batch);
         d.shared_pages = any_page_shared(pool, d, tables, positions, batch, max_pages);
+        d.groups = d.shared_pages ? find_prefix_groups(tables, positions, batch, max_pages)
+                                  : std::vector<DecodeBatch::PrefixGroup>{};
+        d.own_rows_private = true;
+        if (!d.groups.empty()) {
+            std::vector<int> shared(batch, 0);
+            for (const auto& g : d.groups)
+                for (int b : g.members) shared[b] = g.pages;
+            for (int b = 0; b < batch && d.own_rows_private; b++)
+                for (int i = shared[b]; i <= (positions[b] >> 4); i++)
+                    if (d.page_multi[tables[(size_t)b * max_pages + i]] == d.stamp) {
+                        d.own_rows_private = false;
+                        break;
+                    }
+        }
         d.generation++;
         d.batch = batch;
         d.max_pages = max_pages;

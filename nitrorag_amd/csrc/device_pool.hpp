@@ -110,6 +110,19 @@ struct DecodeBatch {
     DecodeArgItems arg_list;
     uint64_t work_generation = ~0ull;
     int32_t work_tile = 0, work_tps = 0, work_items = 0;
+    // Sequences whose first `pages` pages are the same physical pages
+    // (prefix-cache hits), found at upload from the host tables.
+    struct PrefixGroup {
+        int32_t pages = 0;
+        std::vector<int32_t> members;
+    };
+    std::vector<PrefixGroup> groups;
+    bool own_rows_private = false;   // no page past a group's shared pages is read by two rows
+    // The shared-prefix plan last built (see launch_decode_prefix; its list
+    // is in arg_list) and what it was built for.
+    uint64_t prefix_generation = ~0ull;
+    int32_t prefix_heads = 0, prefix_ok = 0;
+    int32_t main_tps = 0, main_waves = 0, main_items = 0, prefix_slots = 0;
 };
 
 struct PrefillBatch {
@@ -179,6 +192,10 @@ struct DecodeLaunch {
     int32_t stream_kv;  // non-temporal K/V loads (lines read once per launch)
     int32_t xcd_remap;  // keep the workgroups that read one K/V range on one XCD
     int32_t heads_per_wg;  // query heads of one KV head per workgroup (divides kv_mul)
+    // Shared-prefix launch (heads_per_wg 1, work list in the arguments): the
+    // list may hold member items, whose waves each take one sequence of a
+    // prefix group over a chunk of its shared rows; see the decode kernel.
+    int32_t members;
     float qscale;
 };
 // Head sizes attention takes: multiples of 4 up to 256 (kernels are built for

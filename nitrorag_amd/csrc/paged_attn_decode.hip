@@ -13,7 +13,8 @@
 //    a work list the host hands out only real items (shortest first), and
 //    long sequences are split into equal runs, so no workgroup streams more
 //    than one split's tiles whatever the mix of context lengths.  The list
-//    (up to DECODE_ARG_ITEMS items) rides in the kernel arguments.  Without
+//    (up to DECODE_ARG_ITEMS items) rides in the kernel arguments; an item
+//    may start past a sequence's shared rows (below).  Without
 //    one, item i is split i % num_splits of sequence i / num_splits and
 //    workgroups past a sequence's last split exit at once.
 //  - Lane layout: LG = 8 lanes share one K/V row (16 for a 256-wide head) so
@@ -45,6 +46,16 @@
 //    i.e. forward_decode_batch's memcpy (src/model_q8.cpp:616-623) and its
 //    attention in one launch.  The host uses it only when no other row of the
 //    batch reads that page.
+//  - Shared prefixes (MEMBERS instances; the host finds sequences whose first
+//    pages are the same physical pages): the work list starts with member
+//    items, each a set of up to W member sequences over a chunk of the shared
+//    rows.  Wave w takes member w and streams the whole chunk, so the
+//    workgroup's waves read each shared row at about the same time through
+//    one L1 and the row leaves L2 once per set, not once per sequence.  The
+//    wave writes its member's partial and counts it in like a split.  The
+//    sequences' own rows follow as ordinary split items.  Every (sequence,
+//    head) then has partials from both, merged in slot order (member chunks
+//    first) by whichever workgroup or wave arrives last.
 //  - The item's block-table slice is staged in LDS once; page ids outside the
 //    pool are counted in *bad_pages and their rows skipped (no fault).
 #include <hip/hip_runtime.h>
@@ -213,6 +224,41 @@ __device__ __forceinline__ float load_coherent(const float* p) {
 // stores have completed.
 __device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Split-K merge of one (sequence, query head h): its partials in slots
+// slot0 .. slot0 + parts - 1, combined in slot order (so the result does not
+// depend on arrival order), output columns first, first + stride, ... (a
+// workgroup's or a wave's threads).  Every part's (m, l, acc[d]) loads go out
+// together, MB parts at a time.
+constexpr int MERGE_BATCH = 8;
+template <int MB>
+__device__ __forceinline__ void merge_parts(const DecodeLaunch& a, int slot0, int parts, int n_heads, int h, int hd,
+                                            int first, int stride, size_t out_row) {
+    for (int d = first; d < hd; d += stride) {
+        float M = -INFINITY, L = 0.0f, A = 0.0f;
+        for (int sp0 = 0; sp0 < parts; sp0 += MB) {
+            float ms[MB], ls[MB], as[MB];
+#pragma unroll
+            for (int j = 0; j < MB; j++) {
+                const int sp = min(sp0 + j, parts - 1);  // past the last part: a repeat, unused
+                const float* part = a.partials + ((size_t)(slot0 + sp) * n_heads + h) * a.pstride;
+                ms[j] = load_coherent(part + hd);
+                ls[j] = load_coherent(part + hd + 1);
+                as[j] = load_coherent(part + d);
+            }
+#pragma unroll
+            for (int j = 0; j < MB; j++) {
+                if (sp0 + j >= parts) break;
+                const float mm = fmaxf(M, ms[j]);
+                const float f = scale_of(M, mm), fs = scale_of(ms[j], mm);
+                L = L * f + ls[j] * fs;
+                A = A * f + as[j] * fs;
+                M = mm;
+            }
+        }
+        a.out[out_row * hd + d] = A / L;
+    }
+}
+
 // QH query heads of one KV head per workgroup (QH = 1 for MHA): each K/V
 // row is loaded once and scored against all QH queries.  QH > 1 needs about
 // twice the registers, so those workgroups hold at most 8 waves.  FULL: the
@@ -224,7 +270,7 @@ __device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcn
 // out at once, while the loads of the other arguments are still in flight.
 // flags: bit 0 XCD work order, bit 1 items from arg_items.  waves and
 // nblocks stand for blockDim.x / 64 and gridDim.x, which are read from memory.
-template <int HDP, int QH, bool STREAM, bool FULL>
+template <int HDP, int QH, bool STREAM, bool FULL, bool MEMBERS>
 __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged_attn_decode_kernel(
     const int32_t* __restrict__ tables, const int32_t* __restrict__ positions, int32_t max_pages,
     int32_t num_splits, int32_t tiles_per_split, int32_t n_heads, int32_t kv_mul, int32_t flags,
@@ -265,19 +311,45 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     const int hg = kv_h * hsubs + r;  // head group of the sequence (arrival counter)
     const int bh_in_seq = kv_h * kv_mul + r * QH;
 
-    // The item: from the work list {b, split, first partial slot of b, ctx},
-    // or implied by the block id (then the position load goes out together
-    // with the block-table slice and q below).
+    // The item: from the work list {b, split | first tile << 8, first partial
+    // slot of b | partials of b << 16, ctx}, or implied by the block id (then
+    // the position load goes out together with the block-table slice and q
+    // below).  With MEMBERS the list may also hold member items (x < 0):
+    // {-1 - first member entry, members | part << 8, first tile, tiles}, the
+    // entries {b, first slot | partials << 16, b', ...} two to an int4.
     const bool listed = flags & 2;
-    int b, split, pslot0, ctx = 0;
+    int b, split, pslot0, ctx = 0, first_tile = 0, parts_b = 0;
+    bool member = false;
+    int mem_count = 0, mem_part = 0, mem_b = 0, mem_slot = 0, mem_parts = 0, mem_tiles = 0;
     if (listed) {
         // the list rides in the kernel arguments: one scalar load of the
         // item precedes the table and q loads
         const int4 it = arg_items.item[item];
-        b = it.x;
-        split = it.y;
-        pslot0 = it.z;
-        ctx = it.w;
+        member = MEMBERS && it.x < 0;
+        if (member) {
+            mem_count = it.y & 0xFF;
+            mem_part = it.y >> 8;
+            first_tile = it.z;
+            mem_tiles = it.w;
+            const int4 e0 = arg_items.item[-1 - it.x];  // member 0: its table row holds the shared pages
+            b = e0.x;
+            const int mine = min(wave, mem_count - 1);
+            const int4 e = arg_items.item[-1 - it.x + mine / 2];
+            mem_b = (mine & 1) ? e.z : e.x;
+            const int sp = (mine & 1) ? e.w : e.y;
+            mem_slot = sp & 0xFFFF;
+            mem_parts = sp >> 16;
+            split = 0;
+            pslot0 = 0;
+            ctx = (first_tile + mem_tiles) * TILE;
+        } else {
+            b = it.x;
+            split = it.y & 0xFF;
+            first_tile = it.y >> 8;
+            pslot0 = it.z & 0xFFFF;
+            parts_b = it.z >> 16;
+            ctx = it.w;
+        }
     } else {
         b = item / num_splits;
         split = item - b * num_splits;
@@ -288,9 +360,10 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     // whole page range (clipped to the table row); only the entries below the
     // context length are validated and used.
     constexpr int TBL_PER_THREAD = DECODE_MAX_SPLIT_PAGES / 256;  // >= 4 waves per workgroup
-    const int tile_begin = split * tiles_per_split;
+    const int tile_begin = first_tile + split * tiles_per_split;
     const int page_begin = (tile_begin * TILE) >> 4;
-    const int spec_end = min(max_pages, ((tile_begin + tiles_per_split) * TILE + 15) >> 4);
+    const int span = member ? mem_tiles : tiles_per_split;  // tiles of the item at most
+    const int spec_end = min(max_pages, ((tile_begin + span) * TILE + 15) >> 4);
     const int32_t* trow = tables + (size_t)b * max_pages;
     int tv[TBL_PER_THREAD];
 #pragma unroll
@@ -308,11 +381,12 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
                  "s"(a.layer_off), "s"(a.page_stride), "s"(a.k_new), "s"(a.v_new), "s"(a.kv_dim));
 
     // q slices of this lane, pre-scaled to base-2 logits (columns past the
-    // head size are zero).
+    // head size are zero).  A member item's wave takes its member's query.
     float4 qv[QH][NF4];
 #pragma unroll
     for (int qi = 0; qi < QH; qi++) {
-        const float* qp = a.q + (size_t)(bh0 + qi) * hd;
+        const size_t qrow = member ? (size_t)mem_b * n_heads + bh_in_seq : (size_t)(bh0 + qi);
+        const float* qp = a.q + qrow * hd;
 #pragma unroll
         for (int j = 0; j < NF4; j++) {
             const int col = (c + j * LG) * 4;
@@ -325,8 +399,15 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     ctx = max(0, min(ctx, a.ctx_limit));  // a position past the table (or the splits) reads no further
     const int n_tiles = (ctx + TILE - 1) / TILE;
     if (tile_begin >= n_tiles) return;  // uniform for the workgroup (implied items only)
-    const int tile_end = min(n_tiles, tile_begin + tiles_per_split);
-    const int splits_b = (n_tiles + tiles_per_split - 1) / tiles_per_split;
+    // the tiles this workgroup streams: a member item's whole chunk, or the
+    // split's run
+    const int tile_end = member ? first_tile + mem_tiles : min(n_tiles, tile_begin + tiles_per_split);
+    // this sequence's splits, its partials in all (a listed item carries the
+    // count, which includes the member items' partials of its shared rows;
+    // those take the first slots), and this split's slot
+    const int splits_b = (n_tiles - first_tile + tiles_per_split - 1) / tiles_per_split;
+    const int parts = listed ? parts_b : splits_b;
+    const int my_slot = pslot0 + parts - splits_b + split;
 
     // Used part of the slice -> LDS (page ids checked against the pool size).
     const int page_end = ((min(ctx, tile_end * TILE) - 1) >> 4) + 1;
@@ -352,10 +433,12 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     // its values are loaded here and stored once the tiles are done: the
     // copy's load latency stays off the tile loop.  (hd / 4 <= 64 <= threads:
     // one float4 of K and one of V per thread at most.)
-    const int new_row = a.k_new ? ctx - 1 : -1;
-    const float* knew = a.k_new ? a.k_new + (size_t)b * a.kv_dim + (size_t)kv_h * hd : nullptr;
-    const float* vnew = a.v_new ? a.v_new + (size_t)b * a.kv_dim + (size_t)kv_h * hd : nullptr;
-    const bool appends = knew && r == 0 && tile_end == n_tiles && (int)threadIdx.x < hd / 4;
+    // (A member item's rows are all shared rows, older than any new row.)
+    const bool fused = a.k_new && !member;
+    const int new_row = fused ? ctx - 1 : -1;
+    const float* knew = fused ? a.k_new + (size_t)b * a.kv_dim + (size_t)kv_h * hd : nullptr;
+    const float* vnew = fused ? a.v_new + (size_t)b * a.kv_dim + (size_t)kv_h * hd : nullptr;
+    const bool appends = fused && r == 0 && tile_end == n_tiles && (int)threadIdx.x < hd / 4;
     float4 k_app = make_float4(0.f, 0.f, 0.f, 0.f), v_app = k_app;
     if (appends) {
         k_app = reinterpret_cast<const float4*>(knew)[threadIdx.x];
@@ -372,7 +455,12 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
         for (int j = 0; j < NF4; j++) acc[qi][j] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
-    for (int t = tile_begin + wave; t < tile_end; t += waves) {
+    // Waves take the split's tiles in turn; in a member item every wave with
+    // a member streams the whole chunk (the workgroup's waves read the same
+    // rows at about the same time, through one L1).
+    const int t_first = member ? (wave < mem_count ? tile_begin : tile_end) : tile_begin + wave;
+    const int t_step = member ? 1 : waves;
+    for (int t = t_first; t < tile_end; t += t_step) {
         float4 kr[RL][NF4], vr[RL][NF4];
         bool valid[RL];
         bool any = false;
@@ -391,8 +479,9 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
                 for (int j = 0; j < NF4; j++) {
                     const int col = (c + j * LG) * 4;
                     if (FULL || col < hd) {
-                        kr[i][j] = load_kv<STREAM>(kp + col);
-                        vr[i][j] = load_kv<STREAM>(vp + col);
+                        // member items re-read shared rows: plain loads
+                        kr[i][j] = member ? load_kv<false>(kp + col) : load_kv<STREAM>(kp + col);
+                        vr[i][j] = member ? load_kv<false>(vp + col) : load_kv<STREAM>(vp + col);
                     } else {
                         kr[i][j] = vr[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
                     }
@@ -468,7 +557,7 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
         }
         sum_pair<NF4, false>(l[qi], acc[qi]);  // rows of 16 lanes: l ^ 16
         sum_pair<NF4, true>(l[qi], acc[qi]);   // halves of 32 lanes: l ^ 32
-        if (g == 0) {
+        if (g == 0 && !member) {
 #pragma unroll
             for (int j = 0; j < NF4; j++)
                 *reinterpret_cast<float4*>(&s_acc[wave][qi][(c + j * LG) * 4]) = acc[qi][j];
@@ -477,6 +566,43 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
                 s_l[wave][qi] = l[qi];
             }
         }
+    }
+    if (member) {
+        // A member item's wave owns its member's result over the chunk: it
+        // writes that partial, then counts it in like a split, and merges
+        // the sequence's partials if it arrives last.  (Uniform for the
+        // workgroup; no workgroup barrier follows.)
+        if (wave < mem_count) {
+            float* part = a.partials + ((size_t)(mem_slot + mem_part) * n_heads + bh_in_seq) * a.pstride;
+            if (g == 0) {
+#pragma unroll
+                for (int j = 0; j < NF4; j++) {
+                    const int col = (c + j * LG) * 4;
+                    if (FULL || col < hd) {
+                        store_coherent(part + col, acc[0][j].x);
+                        store_coherent(part + col + 1, acc[0][j].y);
+                        store_coherent(part + col + 2, acc[0][j].z);
+                        store_coherent(part + col + 3, acc[0][j].w);
+                    }
+                }
+                if (c == 0) {
+                    store_coherent(part + hd, m[0]);
+                    store_coherent(part + hd + 1, l[0]);
+                }
+            }
+            wait_vector_memory();
+            int last = 0;
+            if (lane == 0) {
+                int* counter = a.counters + (size_t)mem_b * (n_heads / QH) + hg;
+                const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                last = before == mem_parts - 1;
+                if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (__builtin_amdgcn_readfirstlane(last))
+                merge_parts<MERGE_BATCH>(a, mem_slot, mem_parts, n_heads, bh_in_seq, hd, lane, 64,
+                                          (size_t)mem_b * n_heads + bh_in_seq);
+        }
+        return;
     }
     __syncthreads();
 
@@ -500,10 +626,10 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
             }
         }
         const int bh = bh0 + qi;
-        if (splits_b == 1) {
+        if (parts == 1) {
             a.out[(size_t)bh * hd + d] = A / L;
         } else {
-            float* part = a.partials + ((size_t)(pslot0 + split) * n_heads + bh - b * n_heads) * a.pstride;
+            float* part = a.partials + ((size_t)my_slot * n_heads + bh - b * n_heads) * a.pstride;
             store_coherent(part + d, A);
             if (d == 0) {
                 store_coherent(part + hd, M);
@@ -520,7 +646,7 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
             reinterpret_cast<float4*>(a.v_pool + off)[threadIdx.x] = v_app;
         }
     }
-    if (splits_b == 1) return;  // uniform for the workgroup
+    if (parts == 1) return;  // uniform for the workgroup
 
     // Split-K: the last workgroup of this (b, head group) to arrive merges.
     wait_vector_memory();
@@ -528,40 +654,15 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     if (threadIdx.x == 0) {
         int* counter = a.counters + (size_t)b * (n_heads / QH) + hg;
         const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = before == splits_b - 1;
-        if (before == splits_b - 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = before == parts - 1;
+        if (before == parts - 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!s_last) return;
-    // Every split's (m, l, acc[d]) loads go out together, MERGE_BATCH splits
-    // at a time, then they are combined in split order.
-    constexpr int MERGE_BATCH = 8;
-    for (int o = threadIdx.x; o < QH * hd; o += threads) {
-        const int qi = o / hd, d = o - qi * hd;
-        const int h = bh_in_seq + qi;
-        float M = -INFINITY, L = 0.0f, A = 0.0f;
-        for (int sp0 = 0; sp0 < splits_b; sp0 += MERGE_BATCH) {
-            float ms[MERGE_BATCH], ls[MERGE_BATCH], as[MERGE_BATCH];
 #pragma unroll
-            for (int j = 0; j < MERGE_BATCH; j++) {
-                const int sp = min(sp0 + j, splits_b - 1);  // past the last split: a repeat, unused
-                const float* part = a.partials + ((size_t)(pslot0 + sp) * n_heads + h) * a.pstride;
-                ms[j] = load_coherent(part + hd);
-                ls[j] = load_coherent(part + hd + 1);
-                as[j] = load_coherent(part + d);
-            }
-#pragma unroll
-            for (int j = 0; j < MERGE_BATCH; j++) {
-                if (sp0 + j >= splits_b) break;
-                const float mm = fmaxf(M, ms[j]);
-                const float f = scale_of(M, mm), fs = scale_of(ms[j], mm);
-                L = L * f + ls[j] * fs;
-                A = A * f + as[j] * fs;
-                M = mm;
-            }
-        }
-        a.out[(size_t)(bh0 + qi) * hd + d] = A / L;
-    }
+    for (int qi = 0; qi < QH; qi++)
+        merge_parts<MERGE_BATCH>(a, pslot0, parts, n_heads, bh_in_seq + qi, hd, (int)threadIdx.x, threads,
+                                 (size_t)(bh0 + qi));
 }
 
 }  // namespace
@@ -590,20 +691,30 @@ static void launch_main(const DecodeLaunch& a, const DecodeArgItems& it, dim3 gr
     const int32_t flags = (a.xcd_remap ? 1 : 0) | (a.arg_items ? 2 : 0);
 #define NITRO_DECODE_ARGS a.tables, a.positions, a.max_pages, a.num_splits, a.tiles_per_split, a.n_heads, a.kv_mul, \
                           flags, a.waves, (int32_t)grid.x, a, it
+    if constexpr (QH == 1) {
+        if (a.members) {  // the list holds member items (shared prefixes)
+            if (a.head_dim != HDP)
+                hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, 1, false, false, true>), grid, block, 0, stream, NITRO_DECODE_ARGS);
+            else if (a.stream_kv)
+                hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, 1, true, true, true>), grid, block, 0, stream, NITRO_DECODE_ARGS);
+            else
+                hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, 1, false, true, true>), grid, block, 0, stream, NITRO_DECODE_ARGS);
+            return;
+        }
+    }
     if (a.head_dim != HDP)  // padded head: plain loads
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, false>), grid, block, 0, stream, NITRO_DECODE_ARGS);
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, false, false>), grid, block, 0, stream, NITRO_DECODE_ARGS);
     else if (a.stream_kv)
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, true, true>), grid, block, 0, stream, NITRO_DECODE_ARGS);
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, true, true, false>), grid, block, 0, stream, NITRO_DECODE_ARGS);
     else
-        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, true>), grid, block, 0, stream, NITRO_DECODE_ARGS);
+        hipLaunchKernelGGL((paged_attn_decode_kernel<HDP, QH, false, true, false>), grid, block, 0, stream, NITRO_DECODE_ARGS);
 #undef NITRO_DECODE_ARGS
 }
 
 template <int HDP>
 static hipError_t launch_hd(const DecodeLaunch& a, const DecodeArgItems& it, hipStream_t stream) {
-    if (a.heads_per_wg < 1 || a.kv_mul % a.heads_per_wg != 0 ||
-        a.heads_per_wg > decode_max_heads_per_wg(HDP) ||
-        (a.heads_per_wg > 1 && a.waves > MAX_WAVES / 2))
+    if (a.heads_per_wg < 1 || a.kv_mul % a.heads_per_wg != 0 || a.heads_per_wg > decode_max_heads_per_wg(HDP) ||
+        (a.heads_per_wg > 1 && a.waves > MAX_WAVES / 2) || (a.members && (!a.arg_items || a.heads_per_wg != 1)))
         return hipErrorInvalidValue;
     const size_t items = a.arg_items ? (size_t)a.work_items : (size_t)a.batch * a.num_splits;
     const dim3 grid((unsigned)(items * (a.n_heads / a.heads_per_wg)));
