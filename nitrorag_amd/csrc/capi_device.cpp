@@ -295,17 +295,17 @@ bool plan_prefix(nitro_kvpool* pool, int n_heads, int n_kv_heads, int head_dim) 
     long long main_items = 0;
     for (int b = 0; b < B; b++) main_items += splits(b);
 
-    // Chunks of ch tiles of shared rows per member item, which a member's
-    // wave streams one after another.  Shorter chunks mean more items and
-    // more partials to merge, longer ones a longer wave: the shared rows of
-    // the longest group in about three chunks, at least a split's tiles per
-    // wave and at most 8 tiles (measured on 48 sequences sharing 512 rows,
-    // 12 x 64: 26.0-26.5 us at 6-7 tiles, 27.7 at 5, 28.3 at 10, 36.4 at 16;
-    // 29.1 us reading every sequence's rows), more when the list would not
-    // fit.  A chunk starts on a page.
+    // Chunks of ch tiles of shared rows per member item, which its workgroup
+    // stages one tile after another.  Shorter chunks mean more items and
+    // more partials to merge, longer ones a longer workgroup: the shared rows
+    // of the longest group in two chunks, at least a split's tiles per wave
+    // and at most 16 tiles (measured on 48 sequences sharing 512 rows,
+    // 12 x 64: 23.2-23.4 us at 8 tiles, 23.5 at 10, 24.1 at 12, 24.9 at 7,
+    // 25.9 at 16, 26.9 at 4; 29.2 us reading every sequence's rows), more when
+    // the list would not fit.  A chunk starts on a page.
     int longest = 0;
     for (const auto& g : d.groups) longest = std::max(longest, g.pages * BLOCK_SIZE / tile);
-    int ch = std::min(8, std::max((sh.tps + W - 1) / W, (longest + 2) / 3));
+    int ch = std::min(16, std::max((sh.tps + W - 1) / W, (longest + 1) / 2));
     if (env_int("NITRO_DECODE_PREFIX_CHUNK", 0) > 0) ch = env_int("NITRO_DECODE_PREFIX_CHUNK", 0);
     while ((ch * tile) % BLOCK_SIZE) ch++;
     long long member_items = 0, entries = 0;

@@ -279,6 +279,12 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     constexpr int LG = G::LG, NF4 = G::NF4, RL = G::RL, GROUPS = G::GROUPS, TILE = G::TILE;
     constexpr int MAXW = QH == 1 ? MAX_WAVES : MAX_WAVES / 2;
     __shared__ int32_t s_pages[DECODE_MAX_SPLIT_PAGES];
+    // member items: one staged tile of K and V, rows STAGE_ROW floats apart
+    // (32 floats of padding where that puts a wave's two rows of one 16-lane
+    // read on different banks)
+    constexpr int STAGE_ROW = HDP == 64 || HDP == 128 ? HDP + 32 : HDP;
+    __shared__ __attribute__((aligned(16))) float s_stage_k[MEMBERS ? TILE * STAGE_ROW : 4];
+    __shared__ __attribute__((aligned(16))) float s_stage_v[MEMBERS ? TILE * STAGE_ROW : 4];
     __shared__ float s_acc[MAXW][QH][HDP];
     __shared__ float s_m[MAXW][QH], s_l[MAXW][QH];
     __shared__ int s_last;
@@ -455,49 +461,9 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
         for (int j = 0; j < NF4; j++) acc[qi][j] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
-    // Waves take the split's tiles in turn; in a member item every wave with
-    // a member streams the whole chunk (the workgroup's waves read the same
-    // rows at about the same time, through one L1).
-    const int t_first = member ? (wave < mem_count ? tile_begin : tile_end) : tile_begin + wave;
-    const int t_step = member ? 1 : waves;
-    for (int t = t_first; t < tile_end; t += t_step) {
-        float4 kr[RL][NF4], vr[RL][NF4];
-        bool valid[RL];
-        bool any = false;
-#pragma unroll
-        for (int i = 0; i < RL; i++) {
-            const int row = t * TILE + g + i * GROUPS;
-            int page = row < ctx ? s_pages[(row >> 4) - page_begin] : -1;
-            valid[i] = page >= 0;
-            any |= valid[i];
-            if (valid[i]) {
-                const size_t off = (size_t)page * a.page_stride + (size_t)(row & 15) * a.kv_dim;
-                const bool fresh = row == new_row;
-                const float* kp = fresh ? knew : kbase + off;
-                const float* vp = fresh ? vnew : vbase + off;
-#pragma unroll
-                for (int j = 0; j < NF4; j++) {
-                    const int col = (c + j * LG) * 4;
-                    if (FULL || col < hd) {
-                        // member items re-read shared rows: plain loads
-                        kr[i][j] = member ? load_kv<false>(kp + col) : load_kv<STREAM>(kp + col);
-                        vr[i][j] = member ? load_kv<false>(vp + col) : load_kv<STREAM>(vp + col);
-                    } else {
-                        kr[i][j] = vr[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < NF4; j++) {
-                    kr[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    vr[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                }
-            }
-        }
-        // The running maximum is shared by the whole wave (the max below
-        // crosses lane groups), so a tile is skipped only when no lane of the
-        // wave holds a valid row.
-        if (__builtin_amdgcn_ballot_w64(any) == 0) continue;
+    // One tile's rows of this lane (kr, vr; valid: the row is real) into the
+    // running (m, l, acc) of each query.
+    auto consume = [&](const float4 (&kr)[RL][NF4], const float4 (&vr)[RL][NF4], const bool (&valid)[RL]) {
 #pragma unroll
         for (int qi = 0; qi < QH; qi++) {
             float s[RL];
@@ -535,6 +501,110 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
                 acc[qi][j] = o;
             }
             m[qi] = m_new;
+        }
+    };
+
+    if (MEMBERS && member) {
+        // A member item: the workgroup stages each tile of the chunk in LDS,
+        // and wave w scores its member against every row.  Each thread loads
+        // its share of the next tile into registers while the waves work on
+        // the current one.  Staged rows are STAGE_ROW floats apart, so that a
+        // wave's 16-byte reads of one column slice hit distinct banks.
+        constexpr int F4_ROW = HDP / 4;
+        constexpr int SHARE = TILE * F4_ROW / 256;  // float4 of K (and of V) per thread, >= 4 waves
+        float4 sk[SHARE], sv[SHARE];
+        auto stage_load = [&](int t) {
+#pragma unroll
+            for (int k = 0; k < SHARE; k++) {
+                const int f = threadIdx.x + k * threads;
+                const int row = f / F4_ROW, col = (f % F4_ROW) * 4;
+                const int abs_row = t * TILE + row;
+                const int page = f < TILE * F4_ROW ? s_pages[(abs_row >> 4) - page_begin] : -1;
+                sk[k] = sv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (page >= 0 && (FULL || col < hd)) {
+                    const size_t off = (size_t)page * a.page_stride + (size_t)(abs_row & 15) * a.kv_dim + col;
+                    sk[k] = *reinterpret_cast<const float4*>(kbase + off);
+                    sv[k] = *reinterpret_cast<const float4*>(vbase + off);
+                }
+            }
+        };
+        // (At hd 128 and 256 the next tile's registers would spill: there the
+        // tile is loaded after the previous one is consumed.)
+        constexpr bool PREFETCH = HDP <= 64;
+        if (PREFETCH) stage_load(tile_begin);
+        for (int t = tile_begin; t < tile_end; t++) {
+            __syncthreads();  // every wave is done with the previous tile
+            if (!PREFETCH) stage_load(t);
+#pragma unroll
+            for (int k = 0; k < SHARE; k++) {
+                const int f = threadIdx.x + k * threads;
+                if (f < TILE * F4_ROW) {
+                    const int at = (f / F4_ROW) * STAGE_ROW + (f % F4_ROW) * 4;
+                    *reinterpret_cast<float4*>(&s_stage_k[at]) = sk[k];
+                    *reinterpret_cast<float4*>(&s_stage_v[at]) = sv[k];
+                }
+            }
+            __syncthreads();
+            if (PREFETCH && t + 1 < tile_end) stage_load(t + 1);
+            if (wave < mem_count) {
+                float4 kr[RL][NF4], vr[RL][NF4];
+                bool valid[RL];
+                bool any = false;
+#pragma unroll
+                for (int i = 0; i < RL; i++) {
+                    const int row = t * TILE + g + i * GROUPS;
+                    valid[i] = s_pages[(row >> 4) - page_begin] >= 0;
+                    any |= valid[i];
+#pragma unroll
+                    for (int j = 0; j < NF4; j++) {
+                        const int at = (g + i * GROUPS) * STAGE_ROW + (c + j * LG) * 4;
+                        kr[i][j] = *reinterpret_cast<const float4*>(&s_stage_k[at]);
+                        vr[i][j] = *reinterpret_cast<const float4*>(&s_stage_v[at]);
+                    }
+                }
+                if (__builtin_amdgcn_ballot_w64(any) != 0) consume(kr, vr, valid);
+            }
+        }
+    } else {
+        // Waves take the split's tiles in turn.
+        for (int t = tile_begin + wave; t < tile_end; t += waves) {
+            float4 kr[RL][NF4], vr[RL][NF4];
+            bool valid[RL];
+            bool any = false;
+#pragma unroll
+            for (int i = 0; i < RL; i++) {
+                const int row = t * TILE + g + i * GROUPS;
+                int page = row < ctx ? s_pages[(row >> 4) - page_begin] : -1;
+                valid[i] = page >= 0;
+                any |= valid[i];
+                if (valid[i]) {
+                    const size_t off = (size_t)page * a.page_stride + (size_t)(row & 15) * a.kv_dim;
+                    const bool fresh = row == new_row;
+                    const float* kp = fresh ? knew : kbase + off;
+                    const float* vp = fresh ? vnew : vbase + off;
+#pragma unroll
+                    for (int j = 0; j < NF4; j++) {
+                        const int col = (c + j * LG) * 4;
+                        if (FULL || col < hd) {
+                            kr[i][j] = load_kv<STREAM>(kp + col);
+                            vr[i][j] = load_kv<STREAM>(vp + col);
+                        } else {
+                            kr[i][j] = vr[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < NF4; j++) {
+                        kr[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                        vr[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
+                }
+            }
+            // The running maximum is shared by the whole wave (the max below
+            // crosses lane groups), so a tile is skipped only when no lane of
+            // the wave holds a valid row.
+            if (__builtin_amdgcn_ballot_w64(any) == 0) continue;
+            consume(kr, vr, valid);
         }
     }
 
