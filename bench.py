@@ -809,8 +809,13 @@ def kernel_name(w) -> str:
         qh = 1
         while qh * 2 <= (8 if w.hd <= 64 else 4 if w.hd == 128 else 2) and kv_mul % (qh * 2) == 0:
             qh *= 2
+        if w.shared_pages and qh == 1:
+            # shared prefixes: member items first in the list, the own rows
+            # streamed (its pages are read once each)
+            return (f"paged_attn_decode_kernel<{w.hd}, 1, true, true, true> "
+                    "(append fused; shared prefixes read once per member set)")
         stream = qh == kv_mul and not w.shared_pages
-        return f"paged_attn_decode_kernel<{w.hd}, {qh}, {str(stream).lower()}, true> (append fused)"
+        return f"paged_attn_decode_kernel<{w.hd}, {qh}, {str(stream).lower()}, true, false> (append fused)"
     kern = os.environ.get("NITRO_PREFILL_KERNEL")
     if w.hd == 256 or kern == "valu":
         return f"paged_attn_prefill_kernel<{w.hd}> (VALU)"
