@@ -308,6 +308,7 @@ bool plan_prefix(nitro_kvpool* pool, int n_heads, int n_kv_heads, int head_dim) 
     int ch = std::min(16, std::max((sh.tps + W - 1) / W, (longest + 1) / 2));
     if (env_int("NITRO_DECODE_PREFIX_CHUNK", 0) > 0) ch = env_int("NITRO_DECODE_PREFIX_CHUNK", 0);
     while ((ch * tile) % BLOCK_SIZE) ch++;
+    if (ch > max_tps) return false;  // a chunk's pages must fit the table slice
     long long member_items = 0, entries = 0;
     for (;; ch *= 2) {
         member_items = entries = 0;
@@ -354,11 +355,9 @@ bool plan_prefix(nitro_kvpool* pool, int n_heads, int n_kv_heads, int head_dim) 
     std::vector<std::pair<int, int4>> order;  // (tiles, item)
     for (int b = 0; b < B; b++) {
         const int first_tile = shared_rows[b] / tile;
-        const int n_pre = parts[b] - splits(b);
         for (int x = 0; x < splits(b); x++)
             order.push_back({std::min(sh.tps, own_tiles(b) - x * sh.tps),
                              make_int4(b, x | (first_tile << 8), first_slot[b] | (parts[b] << 16), ctx(b))});
-        (void)n_pre;
     }
     std::stable_sort(order.begin(), order.end(), [](const auto& x, const auto& y) { return x.first < y.first; });
     for (const auto& o : order) d.arg_list.item[n++] = o.second;
