@@ -143,7 +143,10 @@ int nitro_kvpool_shape(const nitro_kvpool* pool, int32_t* num_pages, int32_t* nu
  * host tables[batch][max_pages] and positions[batch] (pos_b = the sequence's
  * logical_token_count before this step's token, src/pagedMemory.hpp:334-341).
  * Validated on the host (every page id of pages 0..pos/16 inside the pool),
- * then copied to device memory owned by the pool, on `stream`. */
+ * then copied to device memory owned by the pool, on `stream`.  Sequences whose
+ * first pages (4 or more) are the same physical pages (prefix-cache hits) are
+ * noted here, and MHA decode launches over the batch read those shared rows
+ * once per set of sequences instead of once per sequence. */
 int nitro_decode_batch_upload(nitro_kvpool* pool, const int32_t* tables, const int32_t* positions,
                               int32_t batch, int32_t max_pages, void* stream);
 
