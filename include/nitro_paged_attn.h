@@ -145,8 +145,10 @@ int nitro_kvpool_shape(const nitro_kvpool* pool, int32_t* num_pages, int32_t* nu
  * Validated on the host (every page id of pages 0..pos/16 inside the pool),
  * then copied to device memory owned by the pool, on `stream`.  Sequences whose
  * first pages (4 or more) are the same physical pages (prefix-cache hits) are
- * noted here, and MHA decode launches over the batch read those shared rows
- * once per set of sequences instead of once per sequence. */
+ * noted here.  MHA decode launches over such a batch read those shared rows
+ * once per set of sequences instead of once per sequence when the batch's
+ * K/V rows add up to at least 128 MB; below that, reading each sequence's
+ * rows from the caches measured faster. */
 int nitro_decode_batch_upload(nitro_kvpool* pool, const int32_t* tables, const int32_t* positions,
                               int32_t batch, int32_t max_pages, void* stream);
 
@@ -417,6 +419,15 @@ int nitro_server_step(nitro_server* server, void* stream, int32_t* active);
  * clears that record (synchronising the pool's last stream): *bad_pages = 0
  * when no kernel saw a bad id. */
 int nitro_kvpool_take_device_errors(nitro_kvpool* pool, int32_t* bad_pages);
+
+/* Decode launches this pool has run over its current and earlier batches
+ * (nitro_paged_attn_decode, nitro_paged_attn_decode_append and the
+ * scheduler step's attention), and how many of them took the shared-prefix
+ * form, where sequences that begin with the same physical pages read those
+ * rows once per set of members.  No counterpart in the reference, which
+ * reads every sequence's pages on its own: it is for callers that check
+ * whether their prefix-cache hits are shared on the GPU. */
+int nitro_kvpool_decode_counts(nitro_kvpool* pool, int64_t* launches, int64_t* shared_prefix_launches);
 
 #ifdef __cplusplus
 }

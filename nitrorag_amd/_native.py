@@ -125,6 +125,7 @@ SIGNATURES = {
     "nitro_server_accept_fd": [_vp, _i32, _i32p],
     "nitro_server_step": [_vp, _vp, _i32p],
     "nitro_kvpool_take_device_errors": [_vp, _i32p],
+    "nitro_kvpool_decode_counts": [_vp, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)],
 }
 _RESTYPES = {
     "nitro_status_string": ctypes.c_char_p,

@@ -185,3 +185,9 @@ class KVPool:
         out = ctypes.c_int32()
         N.call("nitro_kvpool_take_device_errors", self._h, ctypes.byref(out))
         return out.value
+
+    def decode_counts(self) -> tuple:
+        """(decode launches so far, how many took the shared-prefix form)."""
+        n, shared = ctypes.c_int64(), ctypes.c_int64()
+        N.call("nitro_kvpool_decode_counts", self._h, ctypes.byref(n), ctypes.byref(shared))
+        return n.value, shared.value

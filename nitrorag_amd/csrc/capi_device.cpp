@@ -122,6 +122,28 @@ std::vector<DecodeBatch::PrefixGroup> find_prefix_groups(const int32_t* tables, 
     return groups;
 }
 
+// Page sharing of a decode batch from the host's copy of its tables: whether
+// any page is read by two rows, the prefix groups, and whether every row's
+// own rows (past its group's shared pages) are read by that row alone.
+void find_decode_groups(const nitro_kvpool* pool, DecodeBatch& d, const int32_t* tables, const int32_t* positions,
+                        int batch, int max_pages) {
+    d.shared_pages = any_page_shared(pool, d, tables, positions, batch, max_pages);
+    d.groups = d.shared_pages ? find_prefix_groups(tables, positions, batch, max_pages)
+                              : std::vector<DecodeBatch::PrefixGroup>{};
+    d.own_rows_private = true;
+    if (!d.groups.empty()) {
+        std::vector<int> shared(batch, 0);
+        for (const auto& g : d.groups)
+            for (int b : g.members) shared[b] = g.pages;
+        for (int b = 0; b < batch && d.own_rows_private; b++)
+            for (int i = shared[b]; i <= (positions[b] >> 4); i++)
+                if (d.page_multi[tables[(size_t)b * max_pages + i]] == d.stamp) {
+                    d.own_rows_private = false;
+                    break;
+                }
+    }
+}
+
 void check_shape(const nitro_kvpool* pool, int layer, int n_heads, int n_kv_heads, int head_dim) {
     require(layer >= 0 && layer < pool->num_layers, ERR_INVALID_ARGUMENT, "layer out of range");
     require(n_heads > 0 && n_kv_heads > 0, ERR_INVALID_ARGUMENT, "head counts must be positive");
@@ -299,13 +321,14 @@ bool plan_prefix(nitro_kvpool* pool, int n_heads, int n_kv_heads, int head_dim) 
     // stages one tile after another.  Shorter chunks mean more items and
     // more partials to merge, longer ones a longer workgroup: the shared rows
     // of the longest group in two chunks, at least a split's tiles per wave
-    // and at most 16 tiles (measured on 48 sequences sharing 512 rows,
-    // 12 x 64: 23.2-23.4 us at 8 tiles, 23.5 at 10, 24.1 at 12, 24.9 at 7,
-    // 25.9 at 16, 26.9 at 4; 29.2 us reading every sequence's rows), more when
-    // the list would not fit.  A chunk starts on a page.
+    // and at most 256 rows, more when the list would not fit.  A chunk starts
+    // on a page.  Measured on 48 sequences sharing 512 rows, 12 x 64: 23.2-23.4
+    // us at 8 tiles (256 rows), 23.5 at 10, 24.1 at 12, 24.9 at 7, 25.9 at 16,
+    // 26.9 at 4; 29.2 us reading every sequence's rows.  Over 1024 shared rows
+    // at 12 x 64 and 2048 at 32 x 128 the best chunk was also 256 rows.
     int longest = 0;
     for (const auto& g : d.groups) longest = std::max(longest, g.pages * BLOCK_SIZE / tile);
-    int ch = std::min(16, std::max((sh.tps + W - 1) / W, (longest + 1) / 2));
+    int ch = std::min(256 / tile, std::max((sh.tps + W - 1) / W, (longest + 1) / 2));
     if (env_int("NITRO_DECODE_PREFIX_CHUNK", 0) > 0) ch = env_int("NITRO_DECODE_PREFIX_CHUNK", 0);
     while ((ch * tile) % BLOCK_SIZE) ch++;
     if (ch > max_tps) return false;  // a chunk's pages must fit the table slice
@@ -369,6 +392,25 @@ bool plan_prefix(nitro_kvpool* pool, int n_heads, int n_kv_heads, int head_dim) 
     return true;
 }
 
+// Whether the shared-prefix form is worth taking for the uploaded batch.  It
+// cuts the rows the launch moves from L2 and HBM, but its member workgroups
+// stage their chunk tile by tile, a longer chain than the usual splits: it
+// pays where the usual launch is bound by the bytes it moves, not by that
+// chain.  Measured (per launch, the form against the usual one): 32 sequences
+// sharing 256 rows at 12 x 64 (51 MB of K/V rows in all) 8.0-8.9 vs 7.0 us in
+// the continuous-batching run; 48 sharing 512 rows (236 MB) 22.6 vs 24.2 us
+// warm, 26.7 vs 32.8 flushed; at 32 x 128, 16 sharing 2048 rows (1.1 GB)
+// 38.3 vs 49.7 us, 64 sharing 1024 (2.5 GB) 157 vs 172 us, 32 sharing 256
+// (272 MB) equal; 8 sharing 4096 (1.1 GB) 61 vs 52 us, the one loss above the
+// threshold.
+constexpr double kPrefixFormMinBytes = 128e6;
+bool prefix_form_pays(const nitro_kvpool* pool) {
+    const DecodeBatch& d = pool->decode;
+    double rows = 0;
+    for (int b = 0; b < d.batch; b++) rows += d.positions[b] + 1;
+    return rows * pool->kv_dim * 2 * sizeof(float) >= kPrefixFormMinBytes;
+}
+
 // The shared-prefix form of a decode launch, when the batch has prefix
 // groups and its list fits; false otherwise (nothing launched).
 bool launch_decode_prefix(nitro_kvpool* pool, int layer, const float* q, float* out, const float* k_new,
@@ -419,9 +461,13 @@ bool launch_decode_prefix(nitro_kvpool* pool, int layer, const float* q, float* 
 void launch_decode(nitro_kvpool* pool, int layer, const float* q, float* out, const float* k_new,
                    const float* v_new, int n_heads, int n_kv_heads, int head_dim, hipStream_t s) {
     DecodeBatch& d = pool->decode;
-    if (!d.groups.empty() && env_int("NITRO_DECODE_PREFIX", 1) != 0 &&
-        launch_decode_prefix(pool, layer, q, out, k_new, v_new, n_heads, n_kv_heads, head_dim, s))
+    d.launches++;
+    const int prefix_mode = env_int("NITRO_DECODE_PREFIX", 1);  // 0 off, 1 where it pays, 2 always
+    if (!d.groups.empty() && prefix_mode != 0 && (prefix_mode == 2 || prefix_form_pays(pool)) &&
+        launch_decode_prefix(pool, layer, q, out, k_new, v_new, n_heads, n_kv_heads, head_dim, s)) {
+        d.prefix_launches++;
         return;
+    }
     const int B = d.batch;
     auto ctx = [&](int b) { return d.positions[b] + 1; };
     const DecodeShape sh = plan_decode_shape(pool, B, ctx, n_heads, n_kv_heads, head_dim);
@@ -514,6 +560,15 @@ void set_device_decode_batch(nitro_kvpool* pool, int batch, int max_pages, const
     d.max_pages = max_pages;
     *tables = d.tables.ptr;
     *device_positions = d.pos.ptr;
+}
+
+void set_device_decode_groups(nitro_kvpool* pool, const int32_t* tables, int max_pages) {
+    require_pool(pool);
+    DecodeBatch& d = pool->decode;
+    require(d.batch > 0 && max_pages == d.max_pages, ERR_INVALID_ARGUMENT,
+            "the host tables must be the rows of the batch just set");
+    for (int b = 0; b < d.batch; b++) check_table_rows(pool, tables, b, max_pages, d.positions[b]);
+    find_decode_groups(pool, d, tables, d.positions.data(), d.batch, max_pages);
 }
 
 }  // namespace nitro
@@ -631,21 +686,7 @@ int nitro_decode_batch_upload(nitro_kvpool* pool, const int32_t* tables, const i
         st.copy(d.slots.ptr, h + nt + batch, batch, s);
         st.finish(s);
         d.positions.assign(positions, positions + batch);
-        d.shared_pages = any_page_shared(pool, d, tables, positions, batch, max_pages);
-        d.groups = d.shared_pages ? find_prefix_groups(tables, positions, batch, max_pages)
-                                  : std::vector<DecodeBatch::PrefixGroup>{};
-        d.own_rows_private = true;
-        if (!d.groups.empty()) {
-            std::vector<int> shared(batch, 0);
-            for (const auto& g : d.groups)
-                for (int b : g.members) shared[b] = g.pages;
-            for (int b = 0; b < batch && d.own_rows_private; b++)
-                for (int i = shared[b]; i <= (positions[b] >> 4); i++)
-                    if (d.page_multi[tables[(size_t)b * max_pages + i]] == d.stamp) {
-                        d.own_rows_private = false;
-                        break;
-                    }
-        }
+        find_decode_groups(pool, d, tables, positions, batch, max_pages);
         d.generation++;
         d.batch = batch;
         d.max_pages = max_pages;
@@ -989,6 +1030,16 @@ int nitro_q8_matmul(const void* w, const float* x, float* out, int32_t batch, in
         hip_check(launch_q8_matmul(w, x, out, batch, n, d, semantics == NITRO_Q8_LAST_BLOCK,
                                    as_stream(stream)),
                   "q8_matmul launch");
+    });
+}
+
+int nitro_kvpool_decode_counts(nitro_kvpool* pool, int64_t* launches, int64_t* shared_prefix_launches) {
+    return guarded([&] {
+        require_pool(pool);
+        require(launches != nullptr && shared_prefix_launches != nullptr, ERR_INVALID_ARGUMENT,
+                "null output pointer");
+        *launches = (int64_t)pool->decode.launches;
+        *shared_prefix_launches = (int64_t)pool->decode.prefix_launches;
     });
 }
 

@@ -123,6 +123,9 @@ struct DecodeBatch {
     uint64_t prefix_generation = ~0ull;
     int32_t prefix_heads = 0, prefix_ok = 0;
     int32_t main_tps = 0, main_waves = 0, main_items = 0, prefix_slots = 0;
+    // Launches over uploaded or device-set batches so far, and how many took
+    // the shared-prefix form (nitro_kvpool_decode_counts).
+    uint64_t launches = 0, prefix_launches = 0;
 };
 
 struct PrefillBatch {
@@ -363,6 +366,10 @@ namespace nitro {
 void set_device_decode_batch(nitro_kvpool* pool, int batch, int max_pages, const int32_t* positions,
                              bool shared_pages, int32_t** tables, int32_t** device_positions,
                              int32_t** device_slots);
+// Hands over the host's copy of that batch's tables ([batch][max_pages], the
+// same rows the caller writes on the device) so that its decode launches can
+// read shared prefixes once per member set, as after an upload.
+void set_device_decode_groups(nitro_kvpool* pool, const int32_t* tables, int max_pages);
 
 // One forward over prefill rows [0, prefill_rows) and decode rows
 // [prefill_rows, prefill_rows + decode_rows), tokens on the device.  With

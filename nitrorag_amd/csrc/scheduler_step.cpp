@@ -41,6 +41,7 @@ struct SchedDevice {
     int vocab = 0;
     std::vector<uint32_t> page_mark;    // shared-page scan stamps
     uint32_t stamp = 0;
+    std::vector<int32_t> host_tables;   // the decode batch's tables, when pages are shared
 
     ~SchedDevice() {
         if (readback) (void)hipHostFree(readback);
@@ -246,6 +247,20 @@ int nitro_sched_step(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* p
             const bool shared = c0 > 0 || rows_share_pages(d, p, pool->num_pages);
             set_device_decode_batch(pool, R, max_pages, positions.data(), shared, &d_tables, &d_positions,
                                     &d_slots);
+            if (shared && R > 1) {
+                // The host holds every row's table too: sequences that begin
+                // with the same pages (a shared prompt, the rows of one chunk)
+                // then read those rows once per member set in each layer.
+                d.host_tables.assign((size_t)R * max_pages, 0);
+                for (int i = 0; i < R; i++) {
+                    const std::vector<int32_t>& t =
+                        i < c0 ? p.prefill->seq.block_table : p.decode[i - c0]->seq.block_table;
+                    const int n = positions[i] / BLOCK_SIZE + 1;
+                    require((int)t.size() >= n, ERR_BAD_BLOCK_TABLE, "a row's table ends before its position");
+                    std::copy(t.begin(), t.begin() + n, d.host_tables.begin() + (size_t)i * max_pages);
+                }
+                set_device_decode_groups(pool, d.host_tables.data(), max_pages);
+            }
         }
         hip_check(launch_sched_tables(d.store.ptr, d.row_stride, d_desc, d_other, n_other, d_chunk_table,
                                       d_tables, d_positions, d_slots, R, max_pages, s),

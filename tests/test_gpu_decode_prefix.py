@@ -5,9 +5,11 @@ launch streams those rows once per set of member sequences (member items) and
 each sequence's own rows as usual, then merges the two kinds of partial.  The
 reference reads every sequence's pages independently
 (src/model_q8.cpp:625-662); the outputs must match the oracle at the parity
-bar whichever way the rows are read.  Every case also runs with the shared-
-prefix form switched off (NITRO_DECODE_PREFIX=0), and the two results must
-agree at the same bar."""
+bar whichever way the rows are read.  These batches are far below the size
+where the library takes the form by itself, so every case forces it
+(NITRO_DECODE_PREFIX=2) and also runs with it switched off (=0); the two
+results must agree at the same bar, and the launch counts show which form
+ran."""
 import sys
 import zlib
 
@@ -84,7 +86,7 @@ def test_shared_prefix_decode_matches_oracle(name, monkeypatch):
     pool = na.KVPool.wrap(dk, dv)
     pool.upload_decode_batch(tables, positions)
     outs = []
-    for prefix in ("1", "0"):
+    for prefix in ("2", "0"):
         monkeypatch.setenv("NITRO_DECODE_PREFIX", prefix)
         for rep in range(2):  # twice: the arrival counters are left at zero
             out = torch.full_like(dq, float("nan"))
@@ -93,10 +95,13 @@ def test_shared_prefix_decode_matches_oracle(name, monkeypatch):
             assert_parity(out.cpu().numpy(), want, f"{name} prefix={prefix} rep={rep}")
         outs.append(out.cpu().numpy())
     assert_parity(outs[0], outs[1], f"{name}: shared-prefix vs usual launch")
+    # GQA runs the usual launch; a list too long for the kernel arguments too
+    takes_form = name not in ("gqa_uses_the_usual_launch", "list_too_long")
+    assert pool.decode_counts() == (4, 2 if takes_form else 0)
     assert pool.take_device_errors() == 0
 
 
-@pytest.mark.parametrize("prefix", ["1", "0"])
+@pytest.mark.parametrize("prefix", ["2", "0"])
 def test_shared_prefix_decode_append(prefix, monkeypatch):
     """decode_append over a batch with a shared prefix: the appended rows are
     each sequence's own (the shared pages end below every newest row), so the
@@ -132,4 +137,5 @@ def test_shared_prefix_decode_append(prefix, monkeypatch):
     pool.decode_append(0, to_gpu(q), to_gpu(knew), to_gpu(vnew), out, H, H, hd)
     torch.cuda.synchronize()
     assert_parity(out.cpu().numpy(), want, "shared-prefix decode_append")
+    assert pool.decode_counts() == (1, 1 if prefix == "2" else 0)
     assert np.array_equal(dk.cpu().numpy(), k2) and np.array_equal(dv.cpu().numpy(), v2)

@@ -145,3 +145,46 @@ def test_device_argmax_quirks():
         got = argmax(torch.from_numpy(rows).cuda()).cpu().numpy()
         want = [sc.argmax(r) for r in rows]
         assert got.tolist() == want, (vocab, got.tolist(), want)
+
+
+def test_scheduler_reads_shared_prompts_once(monkeypatch):
+    """Requests whose prompts are prefix-cache hits begin with the same pages,
+    and the scheduler step hands its host tables to the decode batch, so its
+    attention takes the shared-prefix form (those rows read once per member
+    set).  An MHA model (the form's case) serves 8 requests of one 128-token
+    prompt (8 shared pages) and 2 others, with the form forced on (these
+    batches are far below the size where the library takes it by itself) and
+    off: every step must leave the same scheduler state (hence the same
+    tokens) and logits within 1e-4 + 1e-3|x|, and the form must have run."""
+    import nitrorag_amd as na
+    from nitrorag_amd.model import LAST_BLOCK, synthetic_model_file
+
+    dim, hid, L, H, V, S = 128, 256, 2, 4, 200, 256
+    blob = synthetic_model_file(dim, hid, L, H, H, V, S, seed=23)
+    rng = np.random.default_rng(23)
+    shared = rng.integers(0, V, 128).astype(np.int32)
+    prompts = [shared] * 8 + [rng.integers(0, V, 70).astype(np.int32), rng.integers(0, V, 130).astype(np.int32)]
+    runs = {}
+    for form in ("2", "0"):
+        monkeypatch.setenv("NITRO_DECODE_PREFIX", form)
+        say(f"scheduler over shared prompts, shared-prefix form {form}")
+        model = na.Model(blob)
+        pool = na.KVPool(300, L, model.kv_dim)
+        sched = na.ContinuousScheduler(na.BlockManager(300), 256, 12)
+        for rid, pr in enumerate(prompts):
+            sched.add_request(rid, pr)
+        steps = []
+        while sched.has_active_requests():
+            sched.step(model, pool, LAST_BLOCK)
+            steps.append((sched.state_words(), sched.last_logits().copy()))
+            assert len(steps) < 200
+        runs[form] = (steps, pool.decode_counts())
+        assert pool.take_device_errors() == 0
+        sched.close()
+        pool.close()
+    (on, (n_on, shared_on)), (off, (n_off, shared_off)) = runs["2"], runs["0"]
+    assert shared_on > 0 and shared_off == 0 and n_on == n_off, (n_on, shared_on, n_off, shared_off)
+    assert len(on) == len(off)
+    for t, ((w1, l1), (w0, l0)) in enumerate(zip(on, off)):
+        assert w1 == w0, t
+        assert l1.shape == l0.shape and np.all(np.abs(l1 - l0) <= 1e-4 + 1e-3 * np.abs(l0)), t
