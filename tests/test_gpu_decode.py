@@ -623,3 +623,26 @@ def test_decode_counts_and_skips_page_ids_outside_the_pool(max_context_split):
     pg = tables[1][keep // 16].astype(np.int64)
     want = cf.attention_f64(q[1], k[pg, 0, keep % 16], v[pg, 0, keep % 16], H, Hkv, hd)
     assert_parity(got[1:2], want[None, :].astype(np.float32), "sequence with bad page ids")
+
+
+def test_decode_random_shapes():
+    """Thirty seeded random batches: 1-9 sequences of 1-2500 tokens, MHA and GQA
+    (groups of 1-8 query heads), head sizes that are any multiple of 4 up to
+    256, 1-2 layers; every one against the oracle at the parity bar, and a
+    second launch bit-identical to the first."""
+    rng = np.random.default_rng(20261202)
+    for i in range(30):
+        B = int(rng.integers(1, 10))
+        kv_mul = int(rng.choice([1, 1, 2, 3, 4, 8]))
+        hd = 4 * int(rng.integers(1, 65))
+        Hkv = int(rng.integers(1, max(2, min(8, 1024 // hd)) + 1))
+        layers = int(rng.integers(1, 3))
+        ctx = rng.integers(1, 2501, size=B)
+        pages = int(((ctx + 15) // 16).sum()) + int(rng.integers(0, 9))
+        say(f"random decode {i}: B={B} H={Hkv * kv_mul} Hkv={Hkv} hd={hd} layers={layers} "
+            f"ctx={ctx.min()}..{ctx.max()}")
+        c = DecodeCase(rng, ctx, Hkv * kv_mul, Hkv, hd, pages, layers, int(rng.integers(0, layers)))
+        first = c.run_gpu()
+        assert_parity(first, c.run_oracle(), f"random decode {i}")
+        assert np.array_equal(c.run_gpu(), first)
+        assert c.pool.take_device_errors() == 0
