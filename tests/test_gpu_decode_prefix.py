@@ -139,3 +139,50 @@ def test_shared_prefix_decode_append(prefix, monkeypatch):
     assert_parity(out.cpu().numpy(), want, "shared-prefix decode_append")
     assert pool.decode_counts() == (1, 1 if prefix == "2" else 0)
     assert np.array_equal(dk.cpu().numpy(), k2) and np.array_equal(dv.cpu().numpy(), v2)
+
+
+def test_shared_prefix_decode_random_groups(monkeypatch):
+    """Fifteen seeded random batches of prefix groups (2-40 members sharing 4-40
+    pages, own rows 1-300) and loners, MHA at head sizes 32-256: with the form
+    forced on and off, each against the oracle at the parity bar, bit-identical
+    on a second launch, and the counts show the form ran wherever the list fit
+    the kernel arguments."""
+    import torch
+
+    import nitrorag_amd as na
+
+    rng = np.random.default_rng(20261204)
+    took_form = 0
+    for i in range(15):
+        hd = int(rng.choice([32, 48, 64, 96, 128, 256]))
+        H = int(rng.integers(1, max(2, 1024 // hd // 2) + 1))
+        groups = [(int(rng.integers(2, 41)), int(rng.integers(4, 41)), 1, int(rng.integers(1, 301)))
+                  for _ in range(int(rng.integers(1, 4)))]
+        loners = [int(n) for n in rng.integers(1, 800, size=int(rng.integers(0, 4)))]
+        pages = sum(m * ((s * 16 + hi + 15) // 16) for m, s, _, hi in groups) + sum((n + 15) // 16 for n in loners) + 4
+        tables, positions = shared_tables(rng, groups, loners, pages)
+        say(f"random shared-prefix decode {i}: H={H} hd={hd} groups={[(m, s) for m, s, _, _ in groups]} "
+            f"loners={len(loners)}")
+        k = rng.standard_normal((pages, 1, 16, H * hd)).astype(np.float32)
+        v = rng.standard_normal((pages, 1, 16, H * hd)).astype(np.float32)
+        q = rng.standard_normal((len(positions), H * hd)).astype(np.float32)
+        want = attn.decode_batch(k, v, 0, q, tables, positions, H, H, hd)
+        dq = to_gpu(q)
+        pool = na.KVPool.wrap(to_gpu(k), to_gpu(v))
+        pool.upload_decode_batch(tables, positions)
+        for prefix in ("2", "0"):
+            monkeypatch.setenv("NITRO_DECODE_PREFIX", prefix)
+            out = torch.full_like(dq, float("nan"))
+            pool.decode(0, dq, out, H, H, hd)
+            torch.cuda.synchronize()
+            first = out.cpu().numpy()
+            assert_parity(first, want, f"random shared-prefix {i} prefix={prefix}")
+            pool.decode(0, dq, out, H, H, hd)
+            torch.cuda.synchronize()
+            assert np.array_equal(out.cpu().numpy(), first)
+        n, shared = pool.decode_counts()
+        assert n == 4 and shared in (0, 2)
+        took_form += shared == 2
+        assert pool.take_device_errors() == 0
+        pool.close()
+    assert took_form >= 10, took_form  # the others' lists exceed the kernel arguments
