@@ -112,3 +112,23 @@ def test_q8_argument_errors():
     assert st == N.INVALID_ARGUMENT  # unknown semantics
     st = lib.nitro_q8_matmul(w.data_ptr(), x.data_ptr() + 4, out.data_ptr(), 1, 32, 4, 0, None)
     assert st == N.INVALID_ARGUMENT  # x not 16-byte aligned
+
+
+def test_q8_random_shapes():
+    """Twenty-five seeded random products over every kernel the shape selects
+    (slab, flat, row-streaming, bf16 matrix cores): rows of 32-12288 k, 1-2100
+    output rows, 1-40 activation rows, weights at random scales; both
+    semantics against the oracle."""
+    from nitrorag_amd.q8 import FULL_ROWS, LAST_BLOCK
+
+    rng = np.random.default_rng(20261205)
+    for i in range(25):
+        n = 32 * int(rng.integers(1, 385))
+        d = int(rng.integers(1, 2101))
+        batch = int(rng.choice([1, 2, 3, 4, int(rng.integers(5, 41))]))
+        say(f"q8 random {i}: n={n} d={d} batch={batch}")
+        s, q = om.quantize_q8((rng.standard_normal((d, n)) * float(rng.choice([0.01, 0.05, 0.3]))).astype(np.float32))
+        w = om.pack_q8(s, q)
+        x = rng.standard_normal((batch, n)).astype(np.float32)
+        assert_parity(run_gpu(w, x, d, FULL_ROWS), om.q8_matmul(w, x, n, d), f"random full {i}")
+        assert_parity(run_gpu(w, x, d, LAST_BLOCK), om.q8_matmul_bulk(w, x, n, d), f"random last {i}")
