@@ -34,6 +34,9 @@ Q8 products and the serving loop):
   decode-b32-mixed       B=32, 12x64, ctx ~ U[16,1024], 4096-page pool (12 layers, one timed)
   decode-prefix-shared   B=48, 12x64, 512 shared prefix tokens (32 pages, FNV-1a cache
                          hits) + private suffixes ~ U[64,512]
+  decode-long-131072-32x128  one sequence of 131072 tokens, 32x128 (a long retrieved context)
+  prefill-long-16384-32x128  one 16384-token prompt, 32x128 (its CPU baseline runs the whole
+                         prompt: minutes; --no-cpu-baseline skips it)
   prefill-b8-12x64       B=8 prompts, lengths ~ U[128,1024], 12x64, KV scattered into
                          fresh pages then attended causally; FLOPs = sum 2*H*hd*L(L+1)
   q8-gemv-7b-ffn         Q8_0 product, W 11008 x 4096 BlockQ8, 1 activation row
@@ -733,6 +736,15 @@ def make_workload(name, seed):
                                       ", the 12 launches replayed as one HIP graph")))
         w.graph = not flushed
         return w
+    if name == "decode-long-131072-32x128":
+        return DecodeWorkload(name, 1, 32, 32, 128, 131072 // 16 + 8, 1, [0], [131072], False, seed,
+                              describe=("paged-attention decode of one 131072-token sequence (a long "
+                                        "retrieved context), 32 heads x 128, one layer, append + attend "
+                                        "per step"))
+    if name == "prefill-long-16384-32x128":
+        return PrefillWorkload(name, 1, 32, 32, 128, np.array([16384]), seed,
+                               describe=("causal prefill of one 16384-token prompt (a long retrieved "
+                                         "context), 32 heads x 128, fresh 16-token pages"))
     if name == "decode-b32-mixed":
         rng = np.random.default_rng(seed)
         return DecodeWorkload(name, 32, 12, 12, 64, 4096, 12, [0], rng.integers(16, 1025, size=32),
@@ -788,12 +800,15 @@ TRAFFIC_PROFILES = {
     "decode-single-110m-flushed": "paged_attn_decode_single_ctx256_12x64.md",
     "decode-b32-mixed": "paged_attn_decode_b32_mixed_12x64.md",
     "decode-prefix-shared": "paged_attn_decode_prefix_shared_b48_12x64.md",
+    "decode-long-131072-32x128": "paged_attn_decode_long_131072_32x128.md",
     "prefill-b8-12x64": "paged_attn_prefill_b8_12x64.md",
+    "prefill-long-16384-32x128": "paged_attn_prefill_long_16384_32x128.md",
     "model-7b-decode-b1": "model_7b_decode_b1.md",
 }
 
 WORKLOADS = ["decode-b64-ctx4096", "decode-single-110m", "decode-single-110m-flushed", "decode-b32-mixed",
-             "decode-prefix-shared", "prefill-b8-12x64", "q8-gemv-7b-ffn", "q8-matmul-110m-b32",
+             "decode-prefix-shared", "decode-long-131072-32x128", "prefill-b8-12x64",
+             "prefill-long-16384-32x128", "q8-gemv-7b-ffn", "q8-matmul-110m-b32",
              "model-110m-decode-b32", "model-7b-decode-b1", "model-7b-decode-b2", "model-7b-decode-b8", "serve-110m-u1", "serve-110m-u4", "serve-110m-u8",
              "serve-110m-u16", "serve-110m-u32"]
 
