@@ -253,7 +253,8 @@ class DecodeWorkload:
 
 
 class PrefillWorkload:
-    """Causal paged prefill: scatter the chunk's K/V rows, then attend.  Rates are
+    """Causal paged prefill: the scatter of the chunk's K/V rows into the pool and
+    the attention, in one launch (nitro_paged_attn_prefill_append).  Rates are
     the algorithmic fp32 FLOPs (QK^T and PV) against the fp32 matrix-core peak; the
     default kernel reaches fp32 accuracy on the bf16 matrix cores (split operands)."""
 
@@ -294,10 +295,10 @@ class PrefillWorkload:
         self.pool.upload_prefill_batch(self.tables, self.starts, self.lens)
 
     def step(self, stream, events=None):
-        self.pool.kv_append_prefill(0, self.kc, self.vc, stream)
         if events is not None:
             events[0][0].record(stream)
-        self.pool.prefill(0, self.q, self.out, self.H, self.Hkv, self.hd, stream)
+        self.pool.prefill_append(0, self.q, self.kc, self.vc, self.out, self.H, self.Hkv, self.hd,
+                                 stream)
         if events is not None:
             events[0][1].record(stream)
 
@@ -314,6 +315,9 @@ class PrefillWorkload:
         import torch
 
         assert torch.isfinite(self.out).all().item(), "non-finite prefill output"
+        calls, one_launch = self.pool.prefill_counts()
+        if os.environ.get("NITRO_PREFILL_APPEND", "1") != "0":
+            assert one_launch == calls, "a prefill step ran the scatter as a launch of its own"
 
     def cpu_baseline(self, seconds, sample):
         from oracle import attn

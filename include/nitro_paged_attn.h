@@ -226,6 +226,22 @@ int nitro_kv_append_prefill(nitro_kvpool* pool, int32_t layer, const float* k, c
 int nitro_paged_attn_prefill(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
                              int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void* stream);
 
+/* KV scatter and causal prefill attention of the batch in one call — the
+ * reference's prefill layer step, src/model_q8.cpp:473-484 then :485-523
+ * (nitro_kv_append_prefill followed by nitro_paged_attn_prefill, with the same
+ * pool contents and output).  k, v: device [total_tokens][kv_dim].  With the
+ * matrix-core kernel (head_dim 32, 64, 128), a batch of fresh prompts (every
+ * start_pos 0, positions below 32768) and no page written from two table
+ * entries (checked at upload), one launch reads the keys from k / v and
+ * appends them; otherwise the scatter and the attention run as two launches. */
+int nitro_paged_attn_prefill_append(nitro_kvpool* pool, int32_t layer, const float* q, const float* k,
+                                    const float* v, float* out, int32_t n_heads, int32_t n_kv_heads,
+                                    int32_t head_dim, void* stream);
+
+/* No counterpart in the reference: how many nitro_paged_attn_prefill_append
+ * calls the pool has run, and how many of them ran as one launch. */
+int nitro_kvpool_prefill_counts(nitro_kvpool* pool, int64_t* calls, int64_t* one_launch);
+
 /* ------------------------------- RoPE --------------------------------------
  * RoPE fused with the KV append, as the reference does it in one loop: each
  * pair (j, j+1) of q (all heads) and of k (kv heads) is rotated in place by

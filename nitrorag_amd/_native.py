@@ -89,6 +89,7 @@ SIGNATURES = {
     "nitro_prefill_batch_upload": [_vp, _i32p, _i32p, _i32p, _i32, _i32, _vp],
     "nitro_kv_append_prefill": [_vp, _i32, _fp, _fp, _vp],
     "nitro_paged_attn_prefill": [_vp, _i32, _fp, _fp, _i32, _i32, _i32, _vp],
+    "nitro_paged_attn_prefill_append": [_vp, _i32, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _vp],
     "nitro_rope_kv_append": [_vp, _i32, _fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32, _vp],
     "nitro_rope_kv_append_prefill": [_vp, _i32, _fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32,
                                      _vp],
@@ -126,6 +127,7 @@ SIGNATURES = {
     "nitro_server_step": [_vp, _vp, _i32p],
     "nitro_kvpool_take_device_errors": [_vp, _i32p],
     "nitro_kvpool_decode_counts": [_vp, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)],
+    "nitro_kvpool_prefill_counts": [_vp, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)],
 }
 _RESTYPES = {
     "nitro_status_string": ctypes.c_char_p,

@@ -154,6 +154,23 @@ class KVPool:
         N.call("nitro_paged_attn_prefill", self._h, layer, _dev(q, "q"), _dev(out, "out"), n_heads,
                n_kv_heads, head_dim, _stream_ptr(stream))
 
+    def prefill_append(self, layer: int, q, k, v, out, n_heads: int, n_kv_heads: int,
+                       head_dim: int, stream=None) -> None:
+        """kv_append_prefill then prefill (src/model_q8.cpp:473-523), in one
+        launch where the batch allows it."""
+        self._need(q, self.prefill_rows * n_heads * head_dim, "q")
+        self._need(k, self.prefill_rows * self.kv_dim, "k")
+        self._need(v, self.prefill_rows * self.kv_dim, "v")
+        self._need(out, self.prefill_rows * n_heads * head_dim, "out")
+        N.call("nitro_paged_attn_prefill_append", self._h, layer, _dev(q, "q"), _dev(k, "k"),
+               _dev(v, "v"), _dev(out, "out"), n_heads, n_kv_heads, head_dim, _stream_ptr(stream))
+
+    def prefill_counts(self) -> tuple:
+        """(prefill_append calls so far, how many ran as one launch)."""
+        n, one = ctypes.c_int64(), ctypes.c_int64()
+        N.call("nitro_kvpool_prefill_counts", self._h, ctypes.byref(n), ctypes.byref(one))
+        return n.value, one.value
+
     # ------------------------------------------------------------------ RoPE
     def rope_kv_append(self, layer: int, q, k, v, freq_real, freq_imag, n_heads: int,
                        n_kv_heads: int, head_dim: int, stream=None) -> None:

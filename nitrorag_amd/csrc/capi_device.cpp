@@ -8,6 +8,8 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "capi_common.hpp"
@@ -794,6 +796,25 @@ int nitro_paged_attn_decode_append(nitro_kvpool* pool, int32_t layer, const floa
     });
 }
 
+// Whether attention may read a prefill batch's keys from the new rows while
+// the same launch writes them into the pool: every chunk starts at position 0
+// (a fresh prompt: no cached keys are read) and no page is written from two
+// table entries.
+static bool fresh_prompts_unshared(const int32_t* tables, const int32_t* start_pos,
+                                 const int32_t* num_tokens, int batch, int max_pages) {
+    std::unordered_map<int32_t, std::pair<int, int>> written;  // page -> (seq, table index)
+    for (int b = 0; b < batch; b++) {
+        if (num_tokens[b] == 0) continue;
+        if (start_pos[b] != 0) return false;
+        const int32_t* row = tables + (size_t)b * max_pages;
+        for (int i = start_pos[b] >> 4; i <= (start_pos[b] + num_tokens[b] - 1) >> 4; i++) {
+            const auto at = written.emplace(row[i], std::make_pair(b, i));
+            if (!at.second) return false;
+        }
+    }
+    return true;
+}
+
 int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const int32_t* start_pos,
                                const int32_t* num_tokens, int32_t batch, int32_t max_pages,
                                void* stream) {
@@ -892,6 +913,7 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
         for (int b = 0; b < batch; b++)
             if (num_tokens[b] > 0) max_pos = std::max(max_pos, start_pos[b] + num_tokens[b] - 1);
         p.max_pos = max_pos;
+        p.append_in_launch = fresh_prompts_unshared(tables, start_pos, num_tokens, batch, max_pages);
         p.work_items = (int32_t)items.size();
         p.work_block_m = bm;
         p.work_items_wide = (int32_t)wide.size();
@@ -918,51 +940,94 @@ int nitro_kv_append_prefill(nitro_kvpool* pool, int32_t layer, const float* k, c
     });
 }
 
+static PrefillLaunch prefill_args(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
+                                  int32_t n_heads, int32_t n_kv_heads, int32_t head_dim) {
+    require_pool(pool);
+    require(q != nullptr && out != nullptr, ERR_INVALID_ARGUMENT, "null q/out");
+    check_shape(pool, layer, n_heads, n_kv_heads, head_dim);
+    const PrefillBatch& p = pool->prefill;
+    require(p.batch > 0, ERR_NO_BATCH, "no prefill batch uploaded");
+    PrefillLaunch a{};
+    a.q = q;
+    a.out = out;
+    a.k_pool = pool->k;
+    a.v_pool = pool->v;
+    a.tables = p.tables.ptr;
+    a.start_pos = p.d_start.ptr;
+    a.num_tokens = p.d_len.ptr;
+    a.row_off = p.d_row_off.ptr;
+    a.work = p.work.ptr;
+    a.bad_pages = pool->bad_pages.ptr;
+    a.page_stride = pool->page_stride();
+    a.layer_off = pool->layer_offset(layer);
+    a.kv_dim = pool->kv_dim;
+    a.n_heads = n_heads;
+    a.kv_mul = n_heads / n_kv_heads;
+    a.head_dim = head_dim;
+    a.max_pages = p.max_pages;
+    a.num_pages = pool->num_pages;
+    a.work_items = p.work_items;
+    a.max_pos = p.max_pos;
+    a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+    // NITRO_PREFILL_KERNEL=valu / mfma32 selects the VALU / fp32 matrix-core
+    // kernel (A/B counter comparisons).
+    const char* kern = std::getenv("NITRO_PREFILL_KERNEL");
+    a.kernel = !kern                                ? PREFILL_KERNEL_DEFAULT
+               : std::strcmp(kern, "valu") == 0     ? PREFILL_KERNEL_VALU
+               : std::strcmp(kern, "mfma32") == 0   ? PREFILL_KERNEL_MFMA_F32
+                                                    : PREFILL_KERNEL_DEFAULT;
+    a.item_rows = p.work_block_m;
+    if (prefill_uses_wide_items(a.kernel, head_dim)) {
+        a.work = p.work_wide.ptr;
+        a.work_items = p.work_items_wide;
+        a.item_rows = PREFILL_WIDE_ROWS;
+    }
+    return a;
+}
+
 int nitro_paged_attn_prefill(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
                              int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, void* stream) {
     return guarded([&] {
-        require_pool(pool);
-        require(q != nullptr && out != nullptr, ERR_INVALID_ARGUMENT, "null q/out");
-        check_shape(pool, layer, n_heads, n_kv_heads, head_dim);
-        const PrefillBatch& p = pool->prefill;
-        require(p.batch > 0, ERR_NO_BATCH, "no prefill batch uploaded");
-        PrefillLaunch a{};
-        a.q = q;
-        a.out = out;
-        a.k_pool = pool->k;
-        a.v_pool = pool->v;
-        a.tables = p.tables.ptr;
-        a.start_pos = p.d_start.ptr;
-        a.num_tokens = p.d_len.ptr;
-        a.row_off = p.d_row_off.ptr;
-        a.work = p.work.ptr;
-        a.bad_pages = pool->bad_pages.ptr;
-        a.page_stride = pool->page_stride();
-        a.layer_off = pool->layer_offset(layer);
-        a.kv_dim = pool->kv_dim;
-        a.n_heads = n_heads;
-        a.kv_mul = n_heads / n_kv_heads;
-        a.head_dim = head_dim;
-        a.max_pages = p.max_pages;
-        a.num_pages = pool->num_pages;
-        a.work_items = p.work_items;
-        a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
-        // NITRO_PREFILL_KERNEL=valu / mfma32 selects the VALU / fp32 matrix-core
-        // kernel (A/B counter comparisons).
-        const char* kern = std::getenv("NITRO_PREFILL_KERNEL");
-        a.kernel = !kern                                ? PREFILL_KERNEL_DEFAULT
-                   : std::strcmp(kern, "valu") == 0     ? PREFILL_KERNEL_VALU
-                   : std::strcmp(kern, "mfma32") == 0   ? PREFILL_KERNEL_MFMA_F32
-                                                        : PREFILL_KERNEL_DEFAULT;
-        a.item_rows = p.work_block_m;
-        if (prefill_uses_wide_items(a.kernel, head_dim)) {
-            a.work = p.work_wide.ptr;
-            a.work_items = p.work_items_wide;
-            a.item_rows = PREFILL_WIDE_ROWS;
-        }
+        const PrefillLaunch a = prefill_args(pool, layer, q, out, n_heads, n_kv_heads, head_dim);
         hipStream_t s = as_stream(stream);
         hip_check(launch_paged_attn_prefill(a, s), "paged_attn_prefill launch");
         pool->last_stream = s;
+    });
+}
+
+int nitro_paged_attn_prefill_append(nitro_kvpool* pool, int32_t layer, const float* q, const float* k,
+                                    const float* v, float* out, int32_t n_heads, int32_t n_kv_heads,
+                                    int32_t head_dim, void* stream) {
+    return guarded([&] {
+        PrefillLaunch a = prefill_args(pool, layer, q, out, n_heads, n_kv_heads, head_dim);
+        require(k != nullptr && v != nullptr, ERR_INVALID_ARGUMENT, "null k/v");
+        PrefillBatch& p = pool->prefill;
+        hipStream_t s = as_stream(stream);
+        p.append_launches++;
+        // NITRO_PREFILL_APPEND=0: always the scatter, then attention (A/B)
+        if (p.append_in_launch && prefill_appends_in_launch(a.kernel, head_dim, p.max_pos, a.page_stride) &&
+            env_int("NITRO_PREFILL_APPEND", 1) != 0) {
+            a.k_new = k;
+            a.v_new = v;
+            hip_check(launch_paged_attn_prefill(a, s), "paged_attn_prefill append launch");
+            p.fused_launches++;
+        } else {
+            hip_check(launch_kv_scatter_rows(pool->k, pool->v, k, v, p.slots.ptr, p.total_rows,
+                                             pool->kv_dim, pool->page_stride(), pool->layer_offset(layer),
+                                             pool->num_pages, pool->bad_pages.ptr, s),
+                      "kv_scatter launch");
+            hip_check(launch_paged_attn_prefill(a, s), "paged_attn_prefill launch");
+        }
+        pool->last_stream = s;
+    });
+}
+
+int nitro_kvpool_prefill_counts(nitro_kvpool* pool, int64_t* calls, int64_t* one_launch) {
+    return guarded([&] {
+        require_pool(pool);
+        require(calls != nullptr && one_launch != nullptr, ERR_INVALID_ARGUMENT, "null output");
+        *calls = (int64_t)pool->prefill.append_launches;
+        *one_launch = (int64_t)pool->prefill.fused_launches;
     });
 }
 

@@ -140,6 +140,11 @@ struct PrefillBatch {
     DeviceBuffer<int32_t> work_wide;  // the same for items of PREFILL_WIDE_ROWS rows
     int32_t work_items_wide = 0;
     int32_t max_pos = 0;              // largest position of any row
+    // Every chunk starts at position 0 and no page is written from two table
+    // entries: attention may then read the keys from the new rows while the
+    // same launch writes them into the pool.
+    bool append_in_launch = false;
+    uint64_t append_launches = 0, fused_launches = 0;  // nitro_paged_attn_prefill_append calls / one-launch form
 };
 
 }  // namespace nitro
@@ -331,8 +336,14 @@ hipError_t launch_argmax_rows(const float* logits, int32_t* next, int rows, int 
 struct PrefillLaunch {
     const float* q;
     float* out;
-    const float* k_pool;
-    const float* v_pool;
+    float* k_pool;  // read, and written by the appending form
+    float* v_pool;
+    // Appending form (bf16 matrix-core kernel only): the chunk's new K/V rows
+    // [rows][kv_dim]; its keys are read from here and copied into the pool by
+    // the same launch.  nullptr: every key is read from the pool.
+    const float* k_new;
+    const float* v_new;
+    int32_t max_pos;  // largest position of the batch
     const int32_t* tables;
     const int32_t* start_pos;
     const int32_t* num_tokens;
@@ -349,6 +360,9 @@ struct PrefillLaunch {
 constexpr int32_t PREFILL_WIDE_ROWS = 128;
 // Whether a launch of this kernel / head_dim takes the wide work list.
 bool prefill_uses_wide_items(int32_t kernel, int32_t head_dim);
+// Whether this kernel / head_dim has the appending form (PrefillLaunch::k_new)
+// for a batch whose largest position is max_pos (its table rows fit in LDS).
+bool prefill_appends_in_launch(int32_t kernel, int32_t head_dim, int32_t max_pos, int64_t page_stride);
 constexpr int32_t PREFILL_KERNEL_DEFAULT = 0;   // bf16 matrix cores at fp32 accuracy (hd <= 128)
 constexpr int32_t PREFILL_KERNEL_VALU = 1;      // fp32 VALU FMAs
 constexpr int32_t PREFILL_KERNEL_MFMA_F32 = 2;  // fp32 matrix cores (v_mfma_f32_16x16x4_f32)

@@ -596,7 +596,15 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_mfma_kern
 // per thread; V one d of four consecutive keys per thread (a wave's lanes
 // cover consecutive d of a row, so the loads coalesce), which becomes one
 // 8-byte store per plane into the transposed tile.
-template <int HD, int QT, int KSPLIT, int BNM>
+// APPEND: the launch also appends the chunk, for a batch of fresh prompts
+// (every chunk starts at position 0).  The keys are read from the new rows
+// k_new / v_new (the same values, so the output is the same as after a
+// separate scatter), and the workgroup of
+// the first head of each kv group stores its query rows' K/V into the pool
+// from the registers the tile loads left them in.  No workgroup reads those
+// pool rows: the host takes this form only when no sequence reads a page a
+// chunk row lands on.
+template <int HD, int QT, int KSPLIT, int BNM, bool APPEND>
 // Up to hd 64 two workgroups share a CU (LDS), which takes at most 128
 // VGPRs (4 waves per SIMD); hd 128 runs one workgroup per CU.
 __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn_prefill_x3_kernel(PrefillLaunch a) {
@@ -737,25 +745,58 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
     const size_t vrow_b = (size_t)a.kv_dim * sizeof(float);
     // FULL: every key of the tile is at most last_pos (wave-uniform), so
     // only the page ids decide validity and no index needs clamping.
-    auto fetch_lds_as = [&](int tile, auto full) {
+    // SRC: the keys are read from the pool (POOL) or, in an APPEND launch
+    // (every chunk starts at position 0), from the new rows (NEW), where the
+    // sequence's row j holds position start + j.  A key at page index p and
+    // the thread's fixed row is new row 16 p + row - start, i.e. at kb + dk +
+    // p * 16 rows: the same per-thread pointer plus a workgroup-uniform
+    // offset, so the new rows cost no registers of their own.  (A form that
+    // also reads cached keys from the pool in the same launch pushed the
+    // kernel past 128 VGPRs into spills and measured slower than the scatter
+    // and the attention as two launches.)
+    constexpr int POOL = 0, NEW = 1;
+    const bool appends = APPEND && h % a.kv_mul == 0;
+    const int own_first = start + q0;
+    const size_t rows16_b = 16 * vrow_b;
+    const size_t dk = APPEND ? (size_t)(reinterpret_cast<uintptr_t>(a.k_new + (size_t)a.row_off[seq] * a.kv_dim) -
+                                        reinterpret_cast<uintptr_t>(a.k_pool + a.layer_off)) -
+                                   (size_t)start * vrow_b
+                             : 0;
+    const size_t dv = APPEND ? (size_t)(reinterpret_cast<uintptr_t>(a.v_new + (size_t)a.row_off[seq] * a.kv_dim) -
+                                        reinterpret_cast<uintptr_t>(a.v_pool + a.layer_off)) -
+                                   (size_t)start * vrow_b
+                             : 0;
+    auto fetch_lds_as = [&](int tile, auto full, auto src) __attribute__((always_inline)) {
         constexpr bool FULL = decltype(full)::value;
+        constexpr int SRC = decltype(src)::value;
         kmask = vmask = 0;
 #pragma unroll
         for (int i = 0; i < LOADS; i++) {
             const int key = tile * BNM + (int)(threadIdx.x + i * NT) / F4;
-            const int page = s_table[(FULL ? key : min(key, last_pos)) >> 4];  // -1: outside the pool
+            const int kc = FULL ? key : min(key, last_pos);
+            const int page = s_table[kc >> 4];  // -1: outside the pool
             const bool ok = (FULL || key <= last_pos) && page >= 0;
             kmask |= (uint32_t)ok << i;
-            kreg[i] = *reinterpret_cast<const float4*>(kb + (size_t)(uint32_t)(ok ? page : 0) * stride_b);
+            const size_t pool_off = (size_t)(uint32_t)(ok ? page : 0) * stride_b;
+            const size_t new_off = dk + (size_t)(uint32_t)(kc >> 4) * rows16_b;
+            const size_t off = SRC == POOL ? pool_off : (ok ? new_off : 0);
+            kreg[i] = *reinterpret_cast<const float4*>(kb + off);
         }
 #pragma unroll
         for (int i = 0; i < VSLOTS; i++) {
             const int key0 = tile * BNM + 4 * ((int)(threadIdx.x + i * NT) / HD);  // 4 keys, one page
-            const int page = s_table[(FULL ? key0 : min(key0, last_pos)) >> 4];
+            const int kc = FULL ? key0 : min(key0, last_pos);
+            const int page = s_table[kc >> 4];
             const bool ok = (FULL || key0 <= last_pos) && page >= 0;
             const char* vp = vb + (size_t)(uint32_t)(ok ? page : 0) * stride_b;
+            const char* vn = vb + (ok ? dv + (size_t)(uint32_t)(kc >> 4) * rows16_b : 0);
 #pragma unroll
-            for (int e = 0; e < 4; e++) vreg[i][e] = *reinterpret_cast<const float*>(vp + e * vrow_b);
+            for (int e = 0; e < 4; e++) {
+                // a new row past last_pos is not read (the sequence's rows end there)
+                const int ec = FULL ? e : max(0, min(e, last_pos - key0));
+                const char* p = SRC == POOL ? vp + e * vrow_b : vn + ec * vrow_b;
+                vreg[i][e] = *reinterpret_cast<const float*>(p);
+            }
             if (FULL) {
                 vmask |= (ok ? 0xFu : 0u) << (4 * i);
             } else {
@@ -764,21 +805,26 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
             }
         }
     };
-    auto fetch_lds = [&](int tile) {
+    auto fetch_lds = [&](int tile, auto src) __attribute__((always_inline)) {
         if (tile * BNM + BNM - 1 <= last_pos)
-            fetch_lds_as(tile, std::true_type{});
+            fetch_lds_as(tile, std::true_type{}, src);
         else
-            fetch_lds_as(tile, std::false_type{});
+            fetch_lds_as(tile, std::false_type{}, src);
     };
+    // APPEND launches are taken only where this holds (host).
     const bool fast_fetch = table_in_lds && (uint64_t)a.page_stride * sizeof(float) < (1ull << 32);
-    auto fetch = [&](int tile) {
-        if (fast_fetch)
-            fetch_lds(tile);
-        else
+    // inlined: as a call (several forms, two call sites) it measured 4x slower
+    auto fetch = [&](int tile) __attribute__((always_inline)) {
+        if constexpr (APPEND) {
+            fetch_lds(tile, std::integral_constant<int, NEW>{});
+        } else if (fast_fetch) {
+            fetch_lds(tile, std::integral_constant<int, POOL>{});
+        } else {
             fetch_with(tile, [&](int key) {
                 const int pi = key >> 4;
                 return pi < TABLE_LDS ? s_table[pi] : trow[pi];
             });
+        }
     };
     auto mfma = [](const bf16x8& x, const bf16x8& y, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, c, 0, 0, 0);
@@ -839,6 +885,43 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
             stage_tile(true);
         else
             stage_tile(false);
+        if constexpr (APPEND) {
+            // The append, by the workgroup of the first head of each kv group:
+            // the tile's keys that are this item's query rows (positions
+            // own_first .. last_pos) are stored from the registers they were
+            // just loaded into, at the pool address the pool form reads them
+            // from, as streaming stores (nothing in the launch reads them; 0.6
+            // us of 57 on 8 prompts of 128-1024 tokens at 12 x 64).  A row on a
+            // page outside the pool is counted once (kv head 0, its first
+            // column) and skipped, as the scatter does.
+            if (appends && tile * BNM + BNM > own_first) {  // block-uniform
+                char* const kw = const_cast<char*>(kb);
+                char* const vw = const_cast<char*>(vb);
+#pragma unroll
+                for (int i = 0; i < LOADS; i++) {
+                    const int f = threadIdx.x + i * NT;
+                    const int key = tile * BNM + f / F4;
+                    if (key >= own_first && key <= last_pos) {
+                        const int page = s_table[key >> 4];
+                        if (page >= 0)
+                            __builtin_nontemporal_store(f32x4{kreg[i].x, kreg[i].y, kreg[i].z, kreg[i].w},
+                                                        reinterpret_cast<f32x4*>(kw + (size_t)(uint32_t)page * stride_b));
+                        else if (kv_h == 0 && f % F4 == 0)
+                            atomicAdd(a.bad_pages, 1);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < VSLOTS; i++) {
+                    const int key0 = tile * BNM + 4 * ((int)(threadIdx.x + i * NT) / HD);  // 4 keys, one page
+                    const int page = s_table[min(key0, last_pos) >> 4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (key0 + e >= own_first && key0 + e <= last_pos && page >= 0)
+                            __builtin_nontemporal_store(
+                                vreg[i][e], reinterpret_cast<float*>(vw + (size_t)(uint32_t)page * stride_b + e * vrow_b));
+                }
+            }
+        }
         __syncthreads();
         if (tile + 1 < n_tiles) fetch(tile + 1);
         __builtin_amdgcn_s_setprio(0);
@@ -1010,16 +1093,32 @@ bool prefill_uses_wide_items(int32_t kernel, int32_t head_dim) {
     return kernel == PREFILL_KERNEL_DEFAULT && head_dim == 128;
 }
 
+bool prefill_appends_in_launch(int32_t kernel, int32_t head_dim, int32_t max_pos, int64_t page_stride) {
+    return kernel == PREFILL_KERNEL_DEFAULT && (head_dim == 32 || head_dim == 64 || head_dim == 128) &&
+           (max_pos >> 4) < TABLE_LDS && (uint64_t)page_stride * sizeof(float) < (1ull << 32);
+}
+
 hipError_t launch_paged_attn_prefill(const PrefillLaunch& a, hipStream_t stream) {
     const dim3 grid((unsigned)((size_t)a.work_items * a.n_heads));
     const bool wide = a.item_rows == PREFILL_WIDE_ROWS;
     if (wide != prefill_uses_wide_items(a.kernel, a.head_dim) || (!wide && a.item_rows != BM))
         return hipErrorInvalidValue;  // the work list must match the kernel's rows per item
+    if ((a.k_new != nullptr) != (a.v_new != nullptr) ||
+        (a.k_new && !prefill_appends_in_launch(a.kernel, a.head_dim, a.max_pos, a.page_stride)))
+        return hipErrorInvalidValue;  // only the bf16 matrix-core kernel appends, with the table in LDS
+    if (a.kernel == PREFILL_KERNEL_DEFAULT && a.k_new) {
+        switch (a.head_dim) {
+            case 32: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<32, 4, 2, 64, true>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 64: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<64, 4, 2, 64, true>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 128: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<128, 8, 1, 32, true>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            default: return hipErrorInvalidValue;
+        }
+    }
     if (a.kernel == PREFILL_KERNEL_DEFAULT) {
         switch (a.head_dim) {
-            case 32: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<32, 4, 2, 64>), grid, dim3(512), 0, stream, a); return hipGetLastError();
-            case 64: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<64, 4, 2, 64>), grid, dim3(512), 0, stream, a); return hipGetLastError();
-            case 128: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<128, 8, 1, 32>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 32: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<32, 4, 2, 64, false>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 64: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<64, 4, 2, 64, false>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 128: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<128, 8, 1, 32, false>), grid, dim3(512), 0, stream, a); return hipGetLastError();
             default: break;  // other head sizes: VALU kernel
         }
     }
