@@ -840,7 +840,9 @@ def kernel_name(w) -> str:
         return f"paged_attn_prefill_kernel<{w.hd}> (VALU)"
     if kern == "mfma32":
         return f"paged_attn_prefill_mfma_kernel<{w.hd}> (fp32 matrix cores)"
-    return f"paged_attn_prefill_x3_kernel<{w.hd}> (bf16 matrix cores, three-part splits)"
+    append = os.environ.get("NITRO_PREFILL_APPEND", "1") != "0" and bool((w.starts == 0).all())
+    return (f"paged_attn_prefill_x3_kernel<{w.hd}> (bf16 matrix cores, three-part splits"
+            + (", KV scatter inside the launch)" if append else ")"))
 
 
 def host_cpu():
