@@ -19,6 +19,15 @@ Reported:
                     per launch measured with rocprofv3 (profiles/)
   cpu_baseline      the CPU oracle (C restatement of the reference's OpenMP
                     loops, all host cores) on a sample of the same workload
+  parity            after the timed steps, the first and the last sequence's
+                    outputs against the oracle (1e-4 + 1e-3|cpu|) and all 64
+                    appended K/V rows bit for bit; a mismatch ends the run with
+                    exit status 3 and no line
+  configs           the four other configurations of the metric, each measured
+                    in this process the way its own --workload run measures it,
+                    with its roofline and its own oracle check (no CPU baseline):
+                    decode-single-110m, decode-b32-mixed, prefill-b8-12x64,
+                    decode-prefix-shared (--no-configs leaves them out)
 Algorithmic bytes per decode launch (append fused): sum_b ctx_b*Hkv*hd*4*2 (K
 and V, the new row read from the appended k/v) + B*H*hd*4*2 (q in, out) +
 sum_b ceil(ctx_b/16)*4 (block-table entries) + B*Hkv*hd*4*2 (the new rows
@@ -31,24 +40,30 @@ Q8 products and the serving loop):
                          the 12 launches replayed as one HIP graph (decode-single-110m-
                          flushed: eager, 1 GiB read before each layer's launch, only the
                          launches timed)
-  decode-b32-mixed       B=32, 12x64, ctx ~ U[16,1024], 4096-page pool (12 layers, one timed)
+  decode-b32-mixed       B=32, 12x64, ctx ~ U[16,1024], 4096-page pool of 12 layers; a step
+                         is the 12 layers' launches, one HIP graph
   decode-prefix-shared   B=48, 12x64, 512 shared prefix tokens (32 pages, FNV-1a cache
-                         hits) + private suffixes ~ U[64,512]
+                         hits) + private suffixes ~ U[64,512], 12 layers, one HIP graph
   decode-long-131072-32x128  one sequence of 131072 tokens, 32x128 (a long retrieved context)
   prefill-long-16384-32x128  one 16384-token prompt, 32x128 (its CPU baseline runs the whole
                          prompt: minutes; --no-cpu-baseline skips it)
   prefill-b8-12x64       B=8 prompts, lengths ~ U[128,1024], 12x64, KV scattered into
-                         fresh pages then attended causally; FLOPs = sum 2*H*hd*L(L+1)
+                         fresh pages then attended causally, in one launch per layer,
+                         12 layers as one HIP graph; FLOPs = sum 2*H*hd*L(L+1)
   q8-gemv-7b-ffn         Q8_0 product, W 11008 x 4096 BlockQ8, 1 activation row
   q8-matmul-110m-b32     Q8_0 product, W 2048 x 768 BlockQ8, 32 activation rows
   model-110m-decode-b32  one decode step of a 110M-shaped Q8 model, B=32 at context 512
   model-7b-decode-bN     one decode step of a Llama-2-7B-shaped Q8 model, N = 1, 2 or 8
                          sequences at context 1024
   serve-110m-uN          the reference's continuous-batching experiment, N users
-The mixed-length and prefix-shared decode workloads fit in the 256 MB Infinity
-Cache, so a 1 GiB buffer is read before every timed launch and only the launch
-itself is timed (events).  Elsewhere the K steps run back to back under the wall
-clock, and a second pass of K steps times every launch between its own events.
+Short launches are timed as HIP graphs of a step's launches: K replays back to
+back under the wall clock, then K more between one pair of events (kernel time
+= their time / launches).  One layer of the mixed-length or prefix-shared batch
+fits in the 256 MB Infinity Cache, but a step's 12 layers are 1.1-1.2 GB of
+distinct rows, so every launch reads rows the cache no longer holds.  Long
+launches (the headline) run K steps back to back under the wall clock, then K
+more with an event pair around every launch.  The -flushed single-sequence form
+reads 1 GiB before every launch and times each launch between its own events.
 """
 from __future__ import annotations
 
@@ -125,10 +140,27 @@ def time_cpu(fn, seconds: float, warmup: int = 2, min_reps: int = 5):
     return float(np.median(times)), len(times), time.perf_counter() - t0
 
 
+class ParityError(AssertionError):
+    pass
+
+
+def check_parity(got, want, what):
+    """|gpu - cpu| <= 1e-4 + 1e-3 |cpu| elementwise (the path's fp32 bar); raises ParityError."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    if got.shape != want.shape or not np.all(np.isfinite(got)):
+        raise ParityError(f"{what}: shape {got.shape} vs {want.shape}, or non-finite output")
+    excess = np.abs(got - want) - (1e-4 + 1e-3 * np.abs(want))
+    if excess.max() > 0:
+        i = np.unravel_index(np.argmax(excess), excess.shape)
+        raise ParityError(f"{what}: |gpu-cpu| exceeds 1e-4 + 1e-3|cpu| at {i}: gpu={got[i]} cpu={want[i]}")
+
+
 class DecodeWorkload:
     """Paged decode: per layer, append every sequence's new K/V row, then attend."""
 
     bound = "hbm"
+    graph = False
 
     def __init__(self, name, B, H, Hkv, hd, pages, layers, steps_layers, ctx, flush, seed,
                  tables=None, shared_pages=False, describe=""):
@@ -207,6 +239,41 @@ class DecodeWorkload:
         torch.cuda.synchronize()
         assert torch.equal(self.out, self.eager_out), "graph replay differs from the eager step"
 
+    def verify(self, sample=None, layers=None):
+        """After the timed steps: the outputs of `sample` sequences (all by
+        default) in the step's layers `layers` (all by default) against the
+        oracle at the parity bar, over host copies of just their pages, and
+        every sampled sequence's appended K/V row in its page bit for bit."""
+        import torch
+
+        from oracle import attn
+
+        sel = np.arange(self.B) if sample is None else np.asarray(sample)
+        steps = range(len(self.steps_layers)) if layers is None else layers
+        n_pages = self.tables.shape[1]
+        idx = torch.from_numpy(self.tables[sel].reshape(-1).astype(np.int64)).to(self.k.device)
+        local = np.arange(len(sel) * n_pages, dtype=np.int32).reshape(len(sel), n_pages)
+        pos = self.positions[sel]
+        new_page = local[np.arange(len(sel)), pos >> 4]
+        for i in steps:
+            layer = self.steps_layers[i]
+            kh = self.k[:, layer].index_select(0, idx).cpu().numpy()[:, None]
+            vh = self.v[:, layer].index_select(0, idx).cpu().numpy()[:, None]
+            for pool, new, what in ((kh, self.knew, "K"), (vh, self.vnew, "V")):
+                if not np.array_equal(pool[new_page, 0, pos & 15], new[i, torch.from_numpy(sel)].cpu().numpy()):
+                    raise ParityError(f"{self.name} layer {layer}: an appended {what} row differs from its input")
+            want = attn.decode_batch(kh, vh, 0, self.q[i, torch.from_numpy(sel)].cpu().numpy(), local, pos,
+                                     self.H, self.Hkv, self.hd)
+            check_parity(self.out[i, torch.from_numpy(sel)].cpu().numpy(), want, f"{self.name} layer {layer}")
+        return (f"{len(sel)} of {self.B} sequences x {len(steps)} of {len(self.steps_layers)} layers vs the "
+                f"oracle within 1e-4 + 1e-3|cpu|; their appended K/V rows bit-exact")
+
+    def release(self):
+        self.pool.close()
+        for name in ("k", "v", "q", "knew", "vnew", "out", "scratch", "eager_out"):
+            if hasattr(self, name):
+                delattr(self, name)
+
     def cpu_baseline(self, seconds, sample):
         """Oracle append + decode on `sample` sequences (their pages copied to a compact pool)."""
         import torch
@@ -261,10 +328,13 @@ class PrefillWorkload:
     bound = "mfma"
     flush = False
 
-    def __init__(self, name, B, H, Hkv, hd, lens, seed, describe):
+    def __init__(self, name, B, H, Hkv, hd, lens, seed, describe, layers=1):
         import nitrorag_amd as na
 
         self.name, self.B, self.H, self.Hkv, self.hd = name, B, H, Hkv, hd
+        # a step runs the prefill of every layer of the pool, each with its own q/k/v
+        self.layers = layers
+        self.graph = layers > 1
         self.lens = np.asarray(lens, dtype=np.int64)
         self.starts = np.zeros(B, np.int32)
         self.seed, self.describe = seed, describe
@@ -285,25 +355,67 @@ class PrefillWorkload:
 
         kv_dim = self.Hkv * self.hd
         total = int(self.lens.sum())
-        self.k = torch.zeros((self.pages, 1, 16, kv_dim), device=dev)
+        L = self.layers
+        self.k = torch.zeros((self.pages, L, 16, kv_dim), device=dev)
         self.v = torch.zeros_like(self.k)
-        self.q = torch.randn((total, self.H * self.hd), device=dev, generator=g)
-        self.kc = torch.randn((total, kv_dim), device=dev, generator=g)
-        self.vc = torch.randn((total, kv_dim), device=dev, generator=g)
+        self.q = torch.randn((L, total, self.H * self.hd), device=dev, generator=g)
+        self.kc = torch.randn((L, total, kv_dim), device=dev, generator=g)
+        self.vc = torch.randn((L, total, kv_dim), device=dev, generator=g)
         self.out = torch.empty_like(self.q)
         self.pool = na.KVPool.wrap(self.k, self.v)
         self.pool.upload_prefill_batch(self.tables, self.starts, self.lens)
 
     def step(self, stream, events=None):
-        if events is not None:
-            events[0][0].record(stream)
-        self.pool.prefill_append(0, self.q, self.kc, self.vc, self.out, self.H, self.Hkv, self.hd,
-                                 stream)
-        if events is not None:
-            events[0][1].record(stream)
+        for layer in range(self.layers):
+            if events is not None:
+                events[layer][0].record(stream)
+            self.pool.prefill_append(layer, self.q[layer], self.kc[layer], self.vc[layer], self.out[layer],
+                                     self.H, self.Hkv, self.hd, stream)
+            if events is not None:
+                events[layer][1].record(stream)
 
     def launches_per_step(self):
-        return 1
+        return self.layers
+
+    def check_graph_replay(self):
+        import torch
+
+        torch.cuda.synchronize()
+        assert torch.equal(self.out, self.eager_out), "graph replay differs from the eager step"
+
+    def verify(self, sample=None, layers=None):
+        """After the timed steps: every prompt's K/V rows in its pages bit for
+        bit (all layers), and the attention outputs of `sample` prompts (all by
+        default) in `layers` (the last layer by default) against the oracle's
+        causal prefill at the parity bar."""
+        from oracle import attn
+
+        sel = range(self.B) if sample is None else sample
+        layers = [self.layers - 1] if layers is None else layers
+        off = np.concatenate([[0], np.cumsum(self.lens)])
+        k, v = self.k.cpu().numpy(), self.v.cpu().numpy()
+        kc, vc = self.kc.cpu().numpy(), self.vc.cpu().numpy()
+        for b in range(self.B):
+            t = np.arange(int(self.lens[b]))
+            pg = self.tables[b][t >> 4]
+            rows = slice(int(off[b]), int(off[b + 1]))
+            if not (np.array_equal(k[pg, :, t & 15].transpose(1, 0, 2), kc[:, rows]) and
+                    np.array_equal(v[pg, :, t & 15].transpose(1, 0, 2), vc[:, rows])):
+                raise ParityError(f"{self.name}: prompt {b}'s K/V rows in its pages differ from its input")
+        for layer in layers:
+            q, out = self.q[layer].cpu().numpy(), self.out[layer].cpu().numpy()
+            for b in sel:
+                rows = slice(int(off[b]), int(off[b + 1]))
+                want = attn.prefill_chunk(k, v, layer, q[rows], self.tables[b], 0, self.H, self.Hkv, self.hd)
+                check_parity(out[rows], want, f"{self.name} prompt {b} layer {layer}")
+        return (f"{len(sel)} of {self.B} prompts x {len(layers)} of {self.layers} layer(s) vs the oracle "
+                f"within 1e-4 + 1e-3|cpu|; every prompt's K/V rows in its pages bit-exact")
+
+    def release(self):
+        self.pool.close()
+        for name in ("k", "v", "q", "kc", "vc", "out", "eager_out"):
+            if hasattr(self, name):
+                delattr(self, name)
 
     def work_per_launch(self):
         return int((2 * self.H * self.hd * self.lens * (self.lens + 1)).sum())
@@ -323,10 +435,10 @@ class PrefillWorkload:
         from oracle import attn
 
         sample = min(sample, self.B)
-        k = self.k.cpu().numpy()
-        v = self.v.cpu().numpy()
-        q = self.q.cpu().numpy()
-        kc, vc = self.kc.cpu().numpy(), self.vc.cpu().numpy()
+        k = self.k[:, :1].cpu().numpy()
+        v = self.v[:, :1].cpu().numpy()
+        q = self.q[0].cpu().numpy()
+        kc, vc = self.kc[0].cpu().numpy(), self.vc[0].cpu().numpy()
         off = np.concatenate([[0], np.cumsum(self.lens)])
         threads = attn.max_threads()
 
@@ -716,11 +828,14 @@ def prefix_shared_workload(seed):
     for s in seqs:
         s.allocate_next_token(7, bm)
     tables = na.pack_block_tables(seqs)
-    return DecodeWorkload("decode-prefix-shared", B, 12, 12, 64, pages, 1, [0], positions + 1,
-                          True, seed, tables=tables, shared_pages=True,
-                          describe=(f"prefix-shared decode, B=48, 12 heads x 64, 512 shared tokens "
-                                    f"(32 pages, ref_count 48) + private suffixes U[64,512], "
-                                    f"{pages}-page pool, one layer, Infinity Cache flushed per launch"))
+    w = DecodeWorkload("decode-prefix-shared", B, 12, 12, 64, pages, 12, list(range(12)), positions + 1,
+                       False, seed, tables=tables, shared_pages=True,
+                       describe=(f"prefix-shared decode, B=48, 12 heads x 64, 512 shared tokens "
+                                 f"(32 pages, ref_count 48) + private suffixes U[64,512], "
+                                 f"{pages}-page pool of 12 layers; a step is one decode token through "
+                                 f"the 12 layers (append + attend), one HIP graph"))
+    w.graph = True
+    return w
 
 
 def make_workload(name, seed):
@@ -751,18 +866,22 @@ def make_workload(name, seed):
                                          "context), 32 heads x 128, fresh 16-token pages"))
     if name == "decode-b32-mixed":
         rng = np.random.default_rng(seed)
-        return DecodeWorkload(name, 32, 12, 12, 64, 4096, 12, [0], rng.integers(16, 1025, size=32),
-                              True, seed,
-                              describe=("batched decode, B=32, 12 heads x 64, ctx ~ U[16,1024], "
-                                        "4096-page pool of 12 layers (layer 0 timed), "
-                                        "Infinity Cache flushed per launch"))
+        w = DecodeWorkload(name, 32, 12, 12, 64, 4096, 12, list(range(12)), rng.integers(16, 1025, size=32),
+                           False, seed,
+                           describe=("batched decode, B=32, 12 heads x 64, ctx ~ U[16,1024], "
+                                     "4096-page pool of 12 layers; a step is one decode token through "
+                                     "the 12 layers (append + attend), one HIP graph"))
+        w.graph = True
+        return w
     if name == "decode-prefix-shared":
         return prefix_shared_workload(seed)
     if name == "prefill-b8-12x64":
         rng = np.random.default_rng(seed)
         return PrefillWorkload(name, 8, 12, 12, 64, rng.integers(128, 1025, size=8), seed,
                                describe=("causal prefill, B=8 prompts, lengths ~ U[128,1024], "
-                                         "12 heads x 64, fresh 16-token pages (LIFO ids)"))
+                                         "12 heads x 64, fresh 16-token pages (LIFO ids) of a 12-layer "
+                                         "pool; a step is the 12 layers' prefill (KV scatter + attention "
+                                         "per layer), one HIP graph"), layers=12)
     if name == "model-110m-decode-b32":
         return ModelDecodeWorkload(name, (768, 2048, 12, 12, 12, 32000, 1024), 32, 512, seed,
                                    describe=("one decode step of a Llama-2-110M-shaped model "
@@ -907,6 +1026,143 @@ def capture_step(torch, w):
     return graph
 
 
+# Configurations of the benchmark's headline metric the default run measures
+# beside it, in the order they are listed for it: single-sequence decode,
+# batched mixed-length decode, causal prefill, prefix-shared decode (the
+# headline itself is the fifth, B=64 at ctx 4096).
+CONFIG_WORKLOADS = ["decode-single-110m", "decode-b32-mixed", "prefill-b8-12x64", "decode-prefix-shared"]
+
+
+def measure(torch, w, dev, g, steps, warmup):
+    """Sets the workload up, runs `warmup` untimed steps, then the timed ones.
+
+    Three forms, by workload:
+      graph  a step's launches captured as one HIP graph (many short launches):
+             `steps` replays back to back under the wall clock (ms_per_step),
+             each checked bit for bit against the eager step; then, behind a
+             spin kernel that lets the host enqueue every replay first, another
+             `steps` replays between one pair of HIP events on the launch
+             stream: kernel_ms = that time / (steps * launches per step)
+      flush  a cache flush before every launch, and an event pair around each
+             launch (only the launches are timed)
+      eager  `steps` steps back to back under the wall clock, then `steps` more
+             behind a spin kernel with an event pair around every launch
+             (kernel_ms = their mean)
+    Returns (ms_per_step, kernel_ms, form)."""
+    w.setup(dev, g)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        w.step(stream)
+    torch.cuda.synchronize()
+    nl = w.launches_per_step()
+    if getattr(w, "graph", False) and not w.flush:
+        graph = capture_step(torch, w)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        ms_per_step = (time.perf_counter() - t0) / steps * 1e3
+        w.check_graph_replay()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(spin_cycles(torch, 5.0 + 0.05 * steps))
+        a.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        w.check_graph_replay()
+        del graph
+        return ms_per_step, a.elapsed_time(b) / (steps * nl), "graph"
+    events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(nl)] for _ in range(steps)]
+    if w.flush:
+        # the flushes between launches are not part of the step: only the
+        # launches, each between its own pair of events, are timed
+        for i in range(steps):
+            w.step(stream, events[i])
+        torch.cuda.synchronize()
+        kernel_ms = float(np.mean([a.elapsed_time(b) for ev in events for a, b in ev]))
+        return kernel_ms * nl, kernel_ms, "flush"
+    if not getattr(w, "event_pass", True):
+        # a step that is a whole serving run: its events bracket the run
+        t0 = time.perf_counter()
+        for i in range(steps):
+            w.step(stream, events[i])
+        torch.cuda.synchronize()
+        ms_per_step = (time.perf_counter() - t0) / steps * 1e3
+        return ms_per_step, float(np.mean([a.elapsed_time(b) for ev in events for a, b in ev])), "run"
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        w.step(stream)
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) / steps * 1e3
+    spin = spin_cycles(torch, 1.0)
+    for i in range(steps):
+        torch.cuda._sleep(spin)
+        w.step(stream, events[i])
+    torch.cuda.synchronize()
+    return ms_per_step, float(np.mean([a.elapsed_time(b) for ev in events for a, b in ev])), "eager"
+
+
+TIMING = {
+    "graph": "one HIP graph per step; kernel_ms = the time of {steps} back-to-back replays between "
+             "one event pair on the launch stream / ({steps} x {nl} launches)",
+    "flush": "an event pair around each launch, a 1 GiB read before it (not timed)",
+    "run": "an event pair around each run",
+    "eager": "an event pair around each launch, the launches queued behind a spin kernel",
+}
+
+
+def rates(w, ms_per_step, kernel_ms):
+    """(unit, peak, step rate, kernel rate, algorithmic work per launch for the roofline)."""
+    work = w.work_per_launch()
+    hbm_work = w.hbm_bytes_per_launch() if hasattr(w, "hbm_bytes_per_launch") else work
+    if w.bound == "hbm":
+        unit, scale, peak = "GB/s", 1e9, HBM_PEAK_GBPS
+    else:
+        unit, scale, peak = "TFLOP/s", 1e12, FP32_PEAK_TFLOPS
+    step_rate = work * w.launches_per_step() / (ms_per_step * 1e-3) / scale
+    kernel_rate = hbm_work / (kernel_ms * 1e-3) / scale
+    return unit, peak, step_rate, kernel_rate, hbm_work
+
+
+def config_entry(torch, name, dev, args):
+    """One configuration's numbers, measured in this process (no CPU baseline)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    w = make_workload(name, args.seed)
+    ms_per_step, kernel_ms, form = measure(torch, w, dev, g, args.steps, args.warmup)
+    w.check()
+    assert w.pool.take_device_errors() == 0, f"{name}: a kernel saw a page id outside the pool"
+    parity = w.verify()
+    unit, peak, step_rate, kernel_rate, hbm_work = rates(w, ms_per_step, kernel_ms)
+    nl = w.launches_per_step()
+    entry = {
+        "workload": w.describe,
+        "kernel": kernel_name(w),
+        "kernel_ms": round(kernel_ms, 5),
+        "launches_per_step": nl,
+        "ms_per_step": round(ms_per_step, 4),
+        ("bytes_per_launch" if w.bound == "hbm" else "flops_per_launch"): hbm_work,
+        "achieved": round(kernel_rate, 2 if unit == "GB/s" else 4),
+        "peak": peak,
+        "unit": unit,
+        "frac": round(kernel_rate / peak, 4),
+        "traffic": (measured_traffic(os.path.join(ROOT, "profiles", TRAFFIC_PROFILES[name]))
+                    if name in TRAFFIC_PROFILES else None),
+        "step_rate": round(step_rate, 2 if unit == "GB/s" else 4),
+        "tokens_per_s": round(w.tokens_per_step() / (ms_per_step * 1e-3), 1),
+        "timing": TIMING[form].format(steps=args.steps, nl=nl),
+        "parity": parity,
+    }
+    entry.update(w.extra(kernel_ms * 1e-3))
+    w.release()
+    del w
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return entry
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -917,6 +1173,8 @@ def main():
     ap.add_argument("--cpu-sample", type=int, default=8,
                     help="sequences (prompts) of the workload the CPU baseline runs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="default workload only: leave out the other four configurations")
     ap.add_argument("--seed", type=int, default=0x4E49545205)
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="also run a plain device-to-device copy of this many MiB three times "
@@ -931,6 +1189,12 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    from oracle import attn
+
+    # the oracle build this process loads (first use below): the one the CPU
+    # baseline times, which also checks the outputs after the timed steps
+    build = None if args.no_cpu_baseline else attn.use_timing_build()
+
     import torch
 
     dev = torch.device("cuda", 0)
@@ -938,7 +1202,6 @@ def main():
     g = torch.Generator(device=dev)
     g.manual_seed(args.seed)
     w = make_workload(args.workload, args.seed)
-    w.setup(dev, g)
 
     if args.copy_calibration_mib:
         src = torch.randn(args.copy_calibration_mib * 2**18, device=dev, generator=g)
@@ -948,83 +1211,19 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    stream = torch.cuda.current_stream()
-    for _ in range(args.warmup):
-        w.step(stream)
-    torch.cuda.synchronize()
-
-    nl = w.launches_per_step()
-    events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(nl)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    if w.flush:
-        # the flushes between launches are not part of the step: only the
-        # launches, each between its own pair of events, are timed
-        for i in range(args.steps):
-            w.step(stream, events[i])
-        torch.cuda.synchronize()
-        elapsed = None
-    elif not getattr(w, "event_pass", True):
-        # a step that is a whole serving run: its events bracket the run
-        t0 = time.perf_counter()
-        for i in range(args.steps):
-            w.step(stream, events[i])
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-    else:
-        # the steps back to back with nothing recorded between their launches
-        # (replays of one HIP graph for a workload whose step is many short
-        # launches), then the same number again, eagerly, with an event pair around
-        # every launch.  A spin kernel queued ahead of each step of that pass lets
-        # the host enqueue the whole step before the GPU reaches it, so the events
-        # time the launches back to back rather than the host's launch rate.
-        graph = None
-        if getattr(w, "graph", False):
-            graph = capture_step(torch, w)
-        t0 = time.perf_counter()
-        for i in range(args.steps):
-            if graph is not None:
-                graph.replay()
-            else:
-                w.step(stream)
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-        if graph is not None:
-            w.check_graph_replay()
-        spin = spin_cycles(torch, 1.0)
-        for i in range(args.steps):
-            torch.cuda._sleep(spin)
-            if graph is not None:
-                # one event pair around each replay: a launch's share of it
-                events[i][0][0].record(stream)
-                graph.replay()
-                events[i][0][1].record(stream)
-            else:
-                w.step(stream, events[i])
-        torch.cuda.synchronize()
-        if graph is not None:
-            events = [ev[:1] for ev in events]
-    launch_ms = [a.elapsed_time(b) for ev in events for a, b in ev]
-    kernel_ms = float(np.mean(launch_ms))
-    if getattr(w, "graph", False) and not w.flush:
-        kernel_ms /= nl
+    ms_per_step, kernel_ms, form = measure(torch, w, dev, g, args.steps, args.warmup)
     w.check()
     assert (w.device_errors() if hasattr(w, "device_errors") else w.pool.take_device_errors()) == 0
-
-    work = w.work_per_launch()
-    hbm_work = w.hbm_bytes_per_launch() if hasattr(w, "hbm_bytes_per_launch") else work
-    if w.flush:
-        ms_per_step = kernel_ms * nl
-    else:
-        ms_per_step = elapsed / args.steps * 1e3
-    kernel_s = kernel_ms * 1e-3
-    if w.bound == "hbm":
-        unit, scale, peak = "GB/s", 1e9, HBM_PEAK_GBPS
-    else:
-        unit, scale, peak = "TFLOP/s", 1e12, FP32_PEAK_TFLOPS
-    step_rate = work * nl / (ms_per_step * 1e-3) / scale
-    kernel_rate = hbm_work / kernel_s / scale
     default = args.workload == DEFAULT_WORKLOAD
+    try:
+        # the headline: two sequences (the first and the last) through the oracle
+        parity = (w.verify(sample=[0, w.B - 1]) if default else w.verify()) if hasattr(w, "verify") else None
+    except ParityError as e:
+        print(f"bench.py: parity check failed after the timed steps: {e}", file=sys.stderr, flush=True)
+        sys.exit(3)
+
+    nl = w.launches_per_step()
+    unit, peak, step_rate, kernel_rate, hbm_work = rates(w, ms_per_step, kernel_ms)
     traffic_profile = args.traffic_profile or (
         os.path.join(ROOT, "profiles", TRAFFIC_PROFILES[args.workload])
         if args.workload in TRAFFIC_PROFILES else None)
@@ -1054,23 +1253,37 @@ def main():
             "frac": round(kernel_rate / peak, 4),
             "traffic": measured_traffic(traffic_profile) if traffic_profile else None,
             ("bytes_per_launch" if w.bound == "hbm" else "flops_per_launch"): hbm_work,
-            "kernel_ms": round(kernel_ms, 4),
+            "kernel_ms": round(kernel_ms, 5),
+            "timing": TIMING[form].format(steps=args.steps, nl=nl),
         },
+        "parity": parity,
         "cpu_baseline": None,
     }
     if hasattr(w, "headline"):
         line.update(w.headline(ms_per_step))
-    line.update(w.extra(kernel_s))
+    line.update(w.extra(kernel_ms * 1e-3))
     if not args.no_cpu_baseline:
-        from oracle import attn
-
-        build = attn.use_timing_build()
         line["cpu_baseline"] = w.cpu_baseline(args.cpu_seconds, args.cpu_sample)
         if line["cpu_baseline"]:
             line["cpu_baseline"]["host"] = host_cpu()
             if line["cpu_baseline"].get("kind") == "port":
                 line["cpu_baseline"]["build"] = build
             line["cpu_baseline"]["timing"] = "2 warm-up runs, then the median of >= 5 timed runs"
+    if default and not args.no_configs:
+        if hasattr(w, "release"):
+            w.release()
+        del w
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        configs = {}
+        try:
+            for i, name in enumerate(CONFIG_WORKLOADS):
+                print(f"bench.py: config {i + 1}: {name}", file=sys.stderr, flush=True)
+                configs[name] = {"config": i + 1, **config_entry(torch, name, dev, args)}
+        except ParityError as e:
+            print(f"bench.py: parity check failed after the timed steps: {e}", file=sys.stderr, flush=True)
+            sys.exit(3)
+        line["configs"] = configs
     print(json.dumps(line), flush=True)
 
 

@@ -133,6 +133,15 @@ typedef struct nitro_kvpool nitro_kvpool;
 int nitro_kvpool_create(int32_t num_pages, int32_t num_layers, int32_t kv_dim, nitro_kvpool** out);
 int nitro_kvpool_wrap(float* k_pool, float* v_pool, int32_t num_pages, int32_t num_layers,
                       int32_t kv_dim, nitro_kvpool** out);
+/* The non-paged cache of forward (src/model_q8.cpp:189-222): borrows the
+ * RunState key_cache / value_cache, each [num_layers][seq_len][kv_dim] floats
+ * (src/model_q8.cpp:54-70), as a pool of seq_len/16 pages per layer, page p of
+ * a layer being its rows 16p..16p+15.  Under the identity block table
+ * {0, 1, .., pos/16} the decode entry points below compute forward's attention
+ * (:193-222) and nitro_kv_append its cache write (:189-191) at the same
+ * addresses.  seq_len must be a multiple of 16 (NITRO_ERR_UNSUPPORTED). */
+int nitro_kvpool_wrap_contiguous(float* key_cache, float* value_cache, int32_t seq_len,
+                                 int32_t num_layers, int32_t kv_dim, nitro_kvpool** out);
 int nitro_kvpool_destroy(nitro_kvpool* pool); /* ~KVBlock_Manager, src/pagedMemory.hpp:157-160 */
 int nitro_kvpool_data(const nitro_kvpool* pool, float** k_pool, float** v_pool);
 int nitro_kvpool_shape(const nitro_kvpool* pool, int32_t* num_pages, int32_t* num_layers,
@@ -419,9 +428,12 @@ int nitro_rpc_recv_structured_query(int32_t fd, int32_t dim, uint64_t* subset_ma
  * (req_counter, :27-34); each nitro_server_step runs one nitro_sched_step,
  * sends every request's new tokens as bare int32 values and closes the
  * connections of finished requests, whose requests it forgets once the
- * scheduler has released them.  *active = has_active_requests.  A prompt the
- * scheduler refuses (nitro_sched_add_request) fails nitro_server_accept_fd;
- * the fd then stays the caller's, as it does after any failure there. */
+ * scheduler has released them.  *active = has_active_requests.
+ * nitro_server_accept_fd takes the fd whatever it returns: a prompt the
+ * scheduler refuses (nitro_sched_add_request: one the model cannot finish) or
+ * that cannot be read fails the call, and the server has then closed the fd
+ * without sending a token, which is what a client whose request the
+ * scheduler refuses at a later step receives too. */
 typedef struct nitro_server nitro_server;
 int nitro_server_create(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* pool, int32_t semantics,
                         int32_t max_prompt_tokens, nitro_server** out);

@@ -77,6 +77,7 @@ SIGNATURES = {
     "nitro_pack_block_tables": [ctypes.POINTER(_vp), _i32, _i32, _i32p],
     "nitro_kvpool_create": [_i32, _i32, _i32, ctypes.POINTER(_vp)],
     "nitro_kvpool_wrap": [_fp, _fp, _i32, _i32, _i32, ctypes.POINTER(_vp)],
+    "nitro_kvpool_wrap_contiguous": [_fp, _fp, _i32, _i32, _i32, ctypes.POINTER(_vp)],
     "nitro_kvpool_destroy": [_vp],
     "nitro_kvpool_data": [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp)],
     "nitro_kvpool_shape": [_vp, _i32p, _i32p, _i32p],

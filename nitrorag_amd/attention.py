@@ -44,7 +44,8 @@ def _host_i32(a) -> np.ndarray:
 class KVPool:
     """Device K/V pools with the reference layout, plus the uploaded batches."""
 
-    def __init__(self, num_pages: int, num_layers: int, kv_dim: int, k=None, v=None):
+    def __init__(self, num_pages: int, num_layers: int, kv_dim: int, k=None, v=None,
+                 contiguous: bool = False):
         h = ctypes.c_void_p()
         if k is None:
             N.call("nitro_kvpool_create", num_pages, num_layers, kv_dim, ctypes.byref(h))
@@ -53,8 +54,12 @@ class KVPool:
             need = num_pages * num_layers * 16 * kv_dim
             if k.numel() != need or v.numel() != need:
                 raise ValueError(f"pool tensors need {need} elements")
-            N.call("nitro_kvpool_wrap", _dev(k, "k"), _dev(v, "v"), num_pages, num_layers,
-                   kv_dim, ctypes.byref(h))
+            if contiguous:
+                N.call("nitro_kvpool_wrap_contiguous", _dev(k, "k"), _dev(v, "v"), num_pages * 16,
+                       num_layers, kv_dim, ctypes.byref(h))
+            else:
+                N.call("nitro_kvpool_wrap", _dev(k, "k"), _dev(v, "v"), num_pages, num_layers,
+                       kv_dim, ctypes.byref(h))
             self._keep = (k, v)
         self._h = h
         self.num_pages, self.num_layers, self.kv_dim = num_pages, num_layers, kv_dim
@@ -73,6 +78,17 @@ class KVPool:
         pages, layers, rows, kv_dim = k.shape
         assert rows == 16 and v.shape == k.shape
         return cls(pages, layers, kv_dim, k, v)
+
+    @classmethod
+    def wrap_contiguous(cls, key_cache, value_cache):
+        """Borrow forward's non-paged caches shaped [layers][seq_len][kv_dim]
+        (src/model_q8.cpp:189-222) as seq_len/16 pages per layer; the identity
+        block table [0, 1, .., pos/16] then addresses rows 0..pos of a layer."""
+        layers, seq_len, kv_dim = key_cache.shape
+        assert value_cache.shape == key_cache.shape
+        if seq_len % 16:
+            raise ValueError("seq_len must be a multiple of 16")
+        return cls(seq_len // 16, layers, kv_dim, key_cache, value_cache, contiguous=True)
 
     @property
     def handle(self):

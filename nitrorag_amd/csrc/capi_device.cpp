@@ -577,8 +577,10 @@ void set_device_decode_groups(nitro_kvpool* pool, const int32_t* tables, int max
 
 extern "C" {
 
+// seq_len > 0: a borrowed contiguous cache [num_layers][seq_len][kv_dim]
+// viewed as seq_len / 16 pages per layer (page p = rows 16p..16p+15).
 static int make_pool(float* k, float* v, bool owned, int32_t num_pages, int32_t num_layers,
-                     int32_t kv_dim, nitro_kvpool** out) {
+                     int32_t kv_dim, nitro_kvpool** out, int32_t seq_len = 0) {
     return guarded([&] {
         require(out != nullptr, ERR_INVALID_ARGUMENT, "null output pointer");
         *out = nullptr;
@@ -595,6 +597,8 @@ static int make_pool(float* k, float* v, bool owned, int32_t num_pages, int32_t 
             pool->num_layers = num_layers;
             pool->kv_dim = kv_dim;
             pool->owned = owned;
+            pool->page_elems = (int64_t)(seq_len > 0 ? 1 : num_layers) * BLOCK_SIZE * kv_dim;
+            pool->layer_elems = (int64_t)(seq_len > 0 ? seq_len : BLOCK_SIZE) * kv_dim;
             const size_t bytes = (size_t)num_pages * num_layers * BLOCK_SIZE * kv_dim * sizeof(float);
             if (owned) {
                 hip_check(hipMalloc((void**)&pool->k, bytes), "hipMalloc(K pool)");
@@ -630,6 +634,19 @@ int nitro_kvpool_create(int32_t num_pages, int32_t num_layers, int32_t kv_dim, n
 int nitro_kvpool_wrap(float* k_pool, float* v_pool, int32_t num_pages, int32_t num_layers,
                       int32_t kv_dim, nitro_kvpool** out) {
     return make_pool(k_pool, v_pool, false, num_pages, num_layers, kv_dim, out);
+}
+
+int nitro_kvpool_wrap_contiguous(float* key_cache, float* value_cache, int32_t seq_len,
+                                 int32_t num_layers, int32_t kv_dim, nitro_kvpool** out) {
+    if (out) *out = nullptr;
+    const int st = guarded([&] {
+        require(seq_len > 0, ERR_INVALID_ARGUMENT, "seq_len must be positive");
+        require(seq_len % BLOCK_SIZE == 0, ERR_UNSUPPORTED,
+                "seq_len must be a multiple of 16 (whole pages per layer)");
+    });
+    if (st != NITRO_OK) return st;
+    return make_pool(key_cache, value_cache, false, seq_len / BLOCK_SIZE, num_layers, kv_dim, out,
+                     seq_len);
 }
 
 int nitro_kvpool_destroy(nitro_kvpool* pool) {

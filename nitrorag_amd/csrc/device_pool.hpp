@@ -166,8 +166,15 @@ struct nitro_kvpool {
     nitro::DeviceBuffer<int32_t> bad_pages;   // [1] device error counter
     nitro::Staging decode_staging, prefill_staging;
 
-    int64_t page_stride() const { return (int64_t)num_layers * nitro::BLOCK_SIZE * kv_dim; }
-    int64_t layer_offset(int layer) const { return (int64_t)layer * nitro::BLOCK_SIZE * kv_dim; }
+    // Element strides every kernel addresses the pools with: row r of page p
+    // in layer l starts at p * page_elems + l * layer_elems + r * kv_dim.
+    // Paged pool [page][layer][16][kv_dim]: page_elems = L*16*kv_dim,
+    // layer_elems = 16*kv_dim.  Contiguous cache [layer][seq_len][kv_dim]
+    // (nitro_kvpool_wrap_contiguous): page_elems = 16*kv_dim, layer_elems =
+    // seq_len*kv_dim, so page p of a layer is its rows 16p..16p+15.
+    int64_t page_elems = 0, layer_elems = 0;
+    int64_t page_stride() const { return page_elems; }
+    int64_t layer_offset(int layer) const { return (int64_t)layer * layer_elems; }
 };
 
 namespace nitro {

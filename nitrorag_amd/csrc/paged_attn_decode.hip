@@ -39,7 +39,18 @@
 //    the counter to zero for the next launch.  Nothing waits on another
 //    workgroup, and no fence writes back or invalidates a whole L2 (agent-
 //    scope release/acquire fences do both on gfx950; measured, those halved
-//    throughput at two splits).
+//    throughput at two splits).  Why the publish holds without them: every
+//    access to a partial is itself a relaxed agent-scope atomic, which the
+//    AMDGPU backend lowers to global_store / global_load with sc1 (LLVM's
+//    GFX942 memory-model table, which gfx950 follows), coherent across the
+//    XCDs' L2s on its own.  Of an agent-scope release sequence (buffer_wbl2
+//    sc1; s_waitcnt vmcnt(0); the releasing access) that leaves the wait:
+//    the L2 write-back only serves non-atomic stores, and there are none
+//    here.  Likewise the acquire's buffer_inv sc1 only serves non-atomic
+//    loads.  What remains is the order the compiler emits: a workgroup-
+//    scope fence (inside __syncthreads on the split path, explicit on the
+//    member path; on gfx950 it emits at most a wait) keeps the stores above
+//    the wait and the counter bump, and the merge's loads below it.
 //  - Fused append (k_new / v_new given): row pos_b = ctx_b - 1 is read from
 //    the new K/V rows instead of the pool, and the workgroup holding that
 //    row (head sub-group 0 of the last split) writes them into the pool slot,
@@ -403,6 +414,18 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
     }
 
     ctx = max(0, min(ctx, a.ctx_limit));  // a position past the table (or the splits) reads no further
+    if (ctx == 0) {
+        // A device position below 0 (implied items only: uploaded positions
+        // are checked on the host, and listed items carry ctx >= 1): the
+        // sequence has no keys.  Split 0 writes zeros for its query heads, and
+        // one workgroup of the sequence counts it in *bad_pages, as a page id
+        // outside the pool is counted.
+        if (split == 0) {
+            for (int i = threadIdx.x; i < QH * hd; i += threads) a.out[(size_t)bh0 * hd + i] = 0.0f;
+            if (threadIdx.x == 0 && bh_in_seq == 0) atomicAdd(a.bad_pages, 1);
+        }
+        return;
+    }
     const int n_tiles = (ctx + TILE - 1) / TILE;
     if (tile_begin >= n_tiles) return;  // uniform for the workgroup (implied items only)
     // the tiles this workgroup streams: a member item's whole chunk, or the
@@ -660,6 +683,11 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
                     store_coherent(part + hd + 1, l[0]);
                 }
             }
+            // The same publish as the split path's below: the fence keeps the
+            // compiler from moving the partial stores past the wait and the
+            // counter bump (it is the fence __syncthreads carries there), and
+            // the one after the bump keeps the merge's loads below it.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             wait_vector_memory();
             int last = 0;
             if (lane == 0) {
@@ -668,6 +696,7 @@ __global__ __launch_bounds__(QH == 1 ? MAX_THREADS : MAX_THREADS / 2) void paged
                 last = before == mem_parts - 1;
                 if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
             if (__builtin_amdgcn_readfirstlane(last))
                 merge_parts<MERGE_BATCH>(a, mem_slot, mem_parts, n_heads, bh_in_seq, hd, lane, 64,
                                           (size_t)mem_b * n_heads + bh_in_seq);

@@ -185,19 +185,25 @@ int nitro_server_destroy(nitro_server* server) {
 }
 
 int nitro_server_accept_fd(nitro_server* server, int32_t fd, int32_t* req_id) {
-    return guarded([&] {
+    // The fd is the server's from the call on.  A prompt it refuses (add_request
+    // refuses one the model cannot finish) or cannot read is answered as a
+    // request the scheduler refuses later is: no tokens, and the connection
+    // closed.
+    const int st = guarded([&] {
         require(server != nullptr && req_id != nullptr, ERR_INVALID_ARGUMENT, "null pointer");
         // tcp_listener_thread (src/Server_Inference.cpp:28-35): the prompt, then a request
         std::vector<int32_t> prompt(server->max_prompt);
         const int32_t n = recv_count(fd, server->max_prompt);
         if (n) recv_all(fd, prompt.data(), 4 * (size_t)n);
-        // add_request refuses a prompt the model cannot finish (the fd stays the caller's)
+        server->conns.reserve(server->conns.size() + 1);  // nothing throws once the request is in
         const int32_t id = server->next_id;
         server->sched->host.add_request(id, prompt.data(), n);
         server->next_id++;
         server->conns.push_back({id, fd});
         *req_id = id;
     });
+    if (st != NITRO_OK && fd >= 0) ::close(fd);
+    return st;
 }
 
 int nitro_server_step(nitro_server* server, void* stream, int32_t* active) {

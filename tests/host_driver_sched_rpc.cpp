@@ -271,20 +271,28 @@ int run_server() {
     struct Client {
         std::vector<int32_t> prompt;
         int fd = -1, rid = -1, status = 0;
+        bool truncated = false;  // sends its count, part of the prompt, then shuts down
     };
-    std::vector<Client> clients(5);
+    std::vector<Client> clients(6);
     for (int i = 0; i < 40; i++) clients[0].prompt.push_back(i % 90 + 1);
     clients[1].prompt = std::vector<int32_t>(61, 3);  // 61 + 4 > 64: cannot finish
     clients[2].prompt = {5, 6, 7};
     clients[3].prompt = {5, 100};                     // a token outside the vocabulary
     for (int i = 0; i < 60; i++) clients[4].prompt.push_back(i % 50 + 2);  // 60 + 4 = 64: fits
+    clients[5].prompt = {8, 9, 10, 11};
+    clients[5].truncated = true;                      // the server cannot read its prompt
     for (auto& c : clients) {
         int sv[2];
         socketpair(AF_UNIX, SOCK_STREAM, 0, sv);
-        nitro_rpc_send_ints(sv[1], c.prompt.data(), (int32_t)c.prompt.size());
+        if (c.truncated) {
+            const int32_t head[3] = {(int32_t)c.prompt.size(), c.prompt[0], c.prompt[1]};
+            if (::send(sv[1], head, sizeof head, MSG_NOSIGNAL) != (ssize_t)sizeof head) return 6;
+            ::shutdown(sv[1], SHUT_WR);
+        } else {
+            nitro_rpc_send_ints(sv[1], c.prompt.data(), (int32_t)c.prompt.size());
+        }
         int32_t rid = -1;
-        c.status = nitro_server_accept_fd(srv, sv[0], &rid);
-        if (c.status != NITRO_OK) ::close(sv[0]);  // refused: the fd stays the caller's
+        c.status = nitro_server_accept_fd(srv, sv[0], &rid);  // the fd is the server's
         c.rid = rid;
         c.fd = sv[1];
     }

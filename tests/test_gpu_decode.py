@@ -319,10 +319,13 @@ def test_decode_argument_errors():
 
 
 def test_full_size_b64_ctx4096_32x128_subset_vs_oracle():
-    """The benchmark workload at its real size (B=64, ctx 4096, 32 heads x 128,
-    20k-page pool): every sequence decoded on the GPU; four checked against the
-    oracle on host copies of just their pages; all outputs finite, and the
-    batch is invariant to the order of sequences."""
+    """The benchmark's call at its real size (B=64, ctx 4096, 32 heads x 128,
+    20k-page pool): append + attend in one launch (decode_append).  All 64
+    appended K/V rows read back bit-exact from their pages; four sequences
+    checked against the oracle on host copies of just their pages (the new
+    rows included); the launch equals the separate append + decode launches
+    bit for bit; all outputs finite, and the batch is invariant to the order
+    of sequences."""
     import torch
 
     import nitrorag_amd as na
@@ -335,16 +338,27 @@ def test_full_size_b64_ctx4096_32x128_subset_vs_oracle():
     k = torch.randn((pages, 1, 16, kv_dim), device="cuda", generator=g)
     v = torch.randn((pages, 1, 16, kv_dim), device="cuda", generator=g)
     q = torch.randn((B, kv_dim), device="cuda", generator=g)
+    knew = torch.randn((B, kv_dim), device="cuda", generator=g)
+    vnew = torch.randn((B, kv_dim), device="cuda", generator=g)
     rng = np.random.default_rng(5)
     tables = random_tables(rng, np.full(B, ctx), pages)
     positions = np.full(B, ctx - 1, np.int32)
     pool = na.KVPool.wrap(k, v)
     pool.upload_decode_batch(tables, positions)
     out = torch.empty_like(q)
-    pool.decode(0, q, out, H, H, hd)
+    pool.decode_append(0, q, knew, vnew, out, H, H, hd)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     assert np.all(np.isfinite(got))
+    new_pages = torch.from_numpy(tables[np.arange(B), positions >> 4].astype(np.int64)).cuda()
+    rows = torch.from_numpy((positions & 15).astype(np.int64)).cuda()
+    assert torch.equal(k[new_pages, 0, rows], knew) and torch.equal(v[new_pages, 0, rows], vnew)
+    # the separate launches (append, then attend over the pool) give the same bits
+    sep = torch.empty_like(q)
+    pool.kv_append(0, knew, vnew)
+    pool.decode(0, q, sep, H, H, hd)
+    torch.cuda.synchronize()
+    assert np.array_equal(sep.cpu().numpy(), got)
     for b in (0, 17, 42, 63):
         idx = torch.from_numpy(tables[b].astype(np.int64)).cuda()
         kb = k.index_select(0, idx).cpu().numpy()
@@ -623,6 +637,16 @@ def test_decode_counts_and_skips_page_ids_outside_the_pool(max_context_split):
     pg = tables[1][keep // 16].astype(np.int64)
     want = cf.attention_f64(q[1], k[pg, 0, keep % 16], v[pg, 0, keep % 16], H, Hkv, hd)
     assert_parity(got[1:2], want[None, :].astype(np.float32), "sequence with bad page ids")
+    # a device position below 0: that sequence attends nothing and its output
+    # rows are zeros (counted once per sequence); the others are unchanged
+    say(f"negative device position, split={max_context_split}")
+    neg = positions.copy()
+    neg[1], neg[2] = -1, -9
+    pos_d = to_gpu(neg)
+    got = run(tables)
+    assert pool.take_device_errors() == 2
+    assert np.array_equal(got[0], clean[0])
+    assert np.all(got[1:] == 0.0)
 
 
 def test_decode_random_shapes():

@@ -70,6 +70,7 @@ FRESH = {
     "fresh_hd32": (3, 6, 1, 70, 4, 4, 32, 1, 0, 0, 0),
     "fresh_single_tokens_hd64": (5, 5, 1, 1, 4, 4, 64, 1, 0, 0, 0),
     "fresh_gqa_16x4_hd64_long": (14, 2, 900, 2100, 16, 4, 64, 1, 0, 0, 0),
+    "fresh_gqa_8x2_hd128_long": (15, 2, 2500, 4000, 8, 2, 128, 1, 0, 0, 0),
 }
 
 
@@ -82,6 +83,7 @@ FRESH = {
     ("fresh_hd32", True),
     ("fresh_single_tokens_hd64", True),
     ("fresh_gqa_16x4_hd64_long", True),
+    ("fresh_gqa_8x2_hd128_long", True),
     ("continued_chunks_gqa_8x2_hd128", False),
     ("short_chunks_hd32", False),
     ("mha_hd256", False),
@@ -92,6 +94,31 @@ def test_append_matches_two_launches(name, one_launch):
     say(f"prefill append {name}")
     seed, B, lo, hi, H, Hkv, hd, layers, layer, slo, shi = (FRESH.get(name) or CASES[name])
     check(prefill_batch_case(seed, B, lo, hi, H, Hkv, hd, layers, layer, slo, shi), one_launch, name)
+
+
+def test_append_prompt_near_the_table_limit():
+    """One fresh 32,000-token prompt at hd 64 (2,000 pages, just below the
+    2,048 table entries a workgroup keeps in LDS): the one-launch form leaves
+    the output and both pools bit-identical to the two launches, and sampled
+    query rows (first, last, and 30 in between) match the oracle, each row
+    computed as a one-row chunk at its position over the written pool (a row's
+    output depends only on keys 0..pos)."""
+    from oracle import attn
+
+    say("prefill append, 32000-token prompt at hd 64")
+    c = prefill_batch_case(16, 1, 32000, 32000, 2, 2, 64, 1, 0, 0, 0)
+    got, gk, gv, counts = run(c, True)
+    assert counts == (1, 1)
+    want, wk, wv, _ = run(c, False)
+    assert np.array_equal(gk, wk) and np.array_equal(gv, wv)
+    assert np.array_equal(got, want)
+    k, v = c["k"].copy(), c["v"].copy()
+    attn.kv_scatter_prefill(k, v, 0, c["kc"], c["vc"], c["tables"][0], 0)
+    assert np.array_equal(gk, k) and np.array_equal(gv, v)
+    rng = np.random.default_rng(16)
+    for t in sorted({0, 31999, *rng.integers(1, 31999, size=30).tolist()}):
+        ref = attn.prefill_chunk(k, v, 0, c["q"][t:t + 1], c["tables"][0], t, 2, 2, 64)
+        assert_parity(got[t:t + 1], ref, f"row {t}")
 
 
 def test_append_random_batches():

@@ -158,11 +158,15 @@ def test_serving_loop_under_asan_ubsan(sched_rpc_driver):
     """The serving loop over socket pairs with a stand-in device step: clients
     whose prompts fit get max_generated tokens each and their connections
     closed; a prompt that cannot finish inside seq_len, or holds a token outside
-    the vocabulary, is refused at accept; finished requests are forgotten."""
+    the vocabulary, is refused at accept, and so is one cut short by its client:
+    each of those clients sees its connection closed by the server with no
+    token (the driver no longer closes a refused fd itself, so a descriptor
+    leaked or closed twice on that path shows up); finished requests are
+    forgotten."""
     out = run_driver(sched_rpc_driver, "server")
     clients = [ln.split() for ln in out if ln.startswith("CLIENT")]
-    assert [c[1] for c in clients] == ["0", "1", "0", "1", "0"]       # statuses
+    assert [c[1] for c in clients] == ["0", "1", "0", "1", "0", "1"]  # statuses
     assert [c[2] for c in clients if c[1] == "0"] == ["0", "1", "2"]   # request ids in accept order
-    assert [c[3] for c in clients] == ["5", "0", "5", "0", "5"]        # tokens received
+    assert [c[3] for c in clients] == ["5", "0", "5", "0", "5", "0"]   # tokens received
     assert all(c[4] == "1" for c in clients)                           # the stand-in step's tokens
     assert out[-1].startswith("REQUESTS 0 ")

@@ -107,6 +107,16 @@ def test_structured_queries_match_reference(cases):
         assert np.array_equal(got[:dim], vec)
 
 
+def closed_without_a_token(sock) -> bool:
+    """The peer closed the connection before sending anything: end of stream,
+    or a reset where the closing side still held unread bytes of ours."""
+    sock.settimeout(10)
+    try:
+        return sock.recv(64) == b""
+    except ConnectionResetError:
+        return True
+
+
 def test_oversize_count_is_refused():
     """The reference resizes to whatever count the peer names; here a count
     above the caller's limit is an error and nothing more is read."""
@@ -138,14 +148,17 @@ def test_server_intake_numbers_requests_like_the_reference():
         pairs.append((a, b))
     st = sc.decode_state(sched.state_words())
     assert st["waiting"] == [0, 1, 2] and [r["next"] for r in st["requests"]] == [5, 9, 0]
-    # a prompt over the limit is refused and adds nothing
+    # a prompt over the limit is refused and adds nothing; the server closes
+    # the connection without sending a token
     a, b = socket.socketpair()
     b.sendall(np.asarray([65] + [1] * 65, np.int32).tobytes())
     rid = ctypes.c_int32()
-    assert N.lib().nitro_server_accept_fd(srv, a.fileno(), ctypes.byref(rid)) == N.INVALID_ARGUMENT
+    assert N.lib().nitro_server_accept_fd(srv, a.detach(), ctypes.byref(rid)) == N.INVALID_ARGUMENT
     assert sc.decode_state(sched.state_words())["waiting"] == [0, 1, 2]
+    assert closed_without_a_token(b)
+    b.close()
     N.call("nitro_server_destroy", srv)  # closes the three duplicated descriptors
-    for x, y in pairs + [(a, b)]:
+    for x, y in pairs:
         x.close(), y.close()
 
 
@@ -153,7 +166,8 @@ def test_server_refuses_prompts_the_model_cannot_finish():
     """With the model's limits set on the scheduler, a prompt of n tokens is
     admitted only if its last decode (position n + max_generated - 2) lies
     below seq_len and every token is in the vocabulary; a refused prompt adds
-    no request, takes no request id and leaves the fd with the caller."""
+    no request and takes no request id, and its client sees the connection
+    closed with no token (what a request refused at a later step receives)."""
     from oracle import scheduler as sc
 
     bm = na.BlockManager(16)
@@ -171,14 +185,14 @@ def test_server_refuses_prompts_the_model_cannot_finish():
         a, b = socket.socketpair()
         b.sendall(np.asarray([len(prompt)] + prompt, np.int32).tobytes())
         rid = ctypes.c_int32(-7)
-        fd = os.dup(a.fileno())
+        fd = a.detach()  # the server's from the call on
         st = N.lib().nitro_server_accept_fd(srv, fd, ctypes.byref(rid))
         if ok:
             assert st == N.OK and rid.value == len(want_ids)
             want_ids.append(rid.value)
         else:
             assert st == N.INVALID_ARGUMENT and rid.value == -7
-            os.close(fd)  # still the caller's
+            assert closed_without_a_token(b)  # closed by the server, no token sent
         pairs.append((a, b))
     st = sc.decode_state(sched.state_words())
     assert st["waiting"] == want_ids
