@@ -48,8 +48,8 @@ Q8 products and the serving loop):
   prefill-long-16384-32x128  one 16384-token prompt, 32x128 (its CPU baseline runs the whole
                          prompt: minutes; --no-cpu-baseline skips it)
   prefill-b8-12x64       B=8 prompts, lengths ~ U[128,1024], 12x64, KV scattered into
-                         fresh pages then attended causally, in one launch per layer,
-                         12 layers as one HIP graph; FLOPs = sum 2*H*hd*L(L+1)
+                         fresh pages then attended causally, in one launch; 12 such
+                         steps per HIP graph; FLOPs = sum 2*H*hd*L(L+1)
   q8-gemv-7b-ffn         Q8_0 product, W 11008 x 4096 BlockQ8, 1 activation row
   q8-matmul-110m-b32     Q8_0 product, W 2048 x 768 BlockQ8, 32 activation rows
   model-110m-decode-b32  one decode step of a 110M-shaped Q8 model, B=32 at context 512
@@ -60,7 +60,9 @@ Short launches are timed as HIP graphs of a step's launches: K replays back to
 back under the wall clock, then K more between one pair of events (kernel time
 = their time / launches).  One layer of the mixed-length or prefix-shared batch
 fits in the 256 MB Infinity Cache, but a step's 12 layers are 1.1-1.2 GB of
-distinct rows, so every launch reads rows the cache no longer holds.  Long
+distinct rows, so every launch reads rows the cache no longer holds.  The
+prefill step's graph holds 12 steps over the same prompts: their q/k/v stay in
+the caches, as the q/k/v product just before the attention leaves them.  Long
 launches (the headline) run K steps back to back under the wall clock, then K
 more with an event pair around every launch.  The -flushed single-sequence form
 reads 1 GiB before every launch and times each launch between its own events.
@@ -877,11 +879,14 @@ def make_workload(name, seed):
         return prefix_shared_workload(seed)
     if name == "prefill-b8-12x64":
         rng = np.random.default_rng(seed)
-        return PrefillWorkload(name, 8, 12, 12, 64, rng.integers(128, 1025, size=8), seed,
-                               describe=("causal prefill, B=8 prompts, lengths ~ U[128,1024], "
-                                         "12 heads x 64, fresh 16-token pages (LIFO ids) of a 12-layer "
-                                         "pool; a step is the 12 layers' prefill (KV scatter + attention "
-                                         "per layer), one HIP graph"), layers=12)
+        w = PrefillWorkload(name, 8, 12, 12, 64, rng.integers(128, 1025, size=8), seed,
+                            describe=("causal prefill, B=8 prompts, lengths ~ U[128,1024], "
+                                      "12 heads x 64, fresh 16-token pages (LIFO ids); a step is one "
+                                      "layer's KV scatter + attention (one launch), 12 steps per HIP "
+                                      "graph, the prompts' q/k/v left in the caches between them as the "
+                                      "q/k/v product before the attention leaves them"))
+        w.graph, w.graph_reps = True, 12
+        return w
     if name == "model-110m-decode-b32":
         return ModelDecodeWorkload(name, (768, 2048, 12, 12, 12, 32000, 1024), 32, 512, seed,
                                    describe=("one decode step of a Llama-2-110M-shaped model "
@@ -1013,15 +1018,16 @@ def spin_cycles(torch, ms: float) -> int:
 
 
 def capture_step(torch, w):
-    """One HIP graph holding a step's launches (captured after the warm-up, so
-    every buffer the launches use is already allocated)."""
+    """One HIP graph holding the launches of w.graph_reps steps (captured after
+    the warm-up, so every buffer the launches use is already allocated)."""
     torch.cuda.synchronize()
     w.step(torch.cuda.current_stream())
     torch.cuda.synchronize()
     w.eager_out = w.out.clone()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        w.step(torch.cuda.current_stream())
+        for _ in range(getattr(w, "graph_reps", 1)):
+            w.step(torch.cuda.current_stream())
     torch.cuda.synchronize()
     return graph
 
@@ -1057,11 +1063,12 @@ def measure(torch, w, dev, g, steps, warmup):
     nl = w.launches_per_step()
     if getattr(w, "graph", False) and not w.flush:
         graph = capture_step(torch, w)
+        reps = getattr(w, "graph_reps", 1)
         t0 = time.perf_counter()
         for _ in range(steps):
             graph.replay()
         torch.cuda.synchronize()
-        ms_per_step = (time.perf_counter() - t0) / steps * 1e3
+        ms_per_step = (time.perf_counter() - t0) / (steps * reps) * 1e3
         w.check_graph_replay()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda._sleep(spin_cycles(torch, 5.0 + 0.05 * steps))
@@ -1072,7 +1079,7 @@ def measure(torch, w, dev, g, steps, warmup):
         torch.cuda.synchronize()
         w.check_graph_replay()
         del graph
-        return ms_per_step, a.elapsed_time(b) / (steps * nl), "graph"
+        return ms_per_step, a.elapsed_time(b) / (steps * reps * nl), "graph"
     events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(nl)] for _ in range(steps)]
     if w.flush:
@@ -1105,8 +1112,9 @@ def measure(torch, w, dev, g, steps, warmup):
 
 
 TIMING = {
-    "graph": "one HIP graph per step; kernel_ms = the time of {steps} back-to-back replays between "
-             "one event pair on the launch stream / ({steps} x {nl} launches)",
+    "graph": "one HIP graph of {reps} step(s) of {nl} launch(es); kernel_ms = the time of {steps} "
+             "back-to-back replays between one event pair on the launch stream / ({steps} x {reps} x {nl} "
+             "launches)",
     "flush": "an event pair around each launch, a 1 GiB read before it (not timed)",
     "run": "an event pair around each run",
     "eager": "an event pair around each launch, the launches queued behind a spin kernel",
@@ -1152,7 +1160,7 @@ def config_entry(torch, name, dev, args):
                     if name in TRAFFIC_PROFILES else None),
         "step_rate": round(step_rate, 2 if unit == "GB/s" else 4),
         "tokens_per_s": round(w.tokens_per_step() / (ms_per_step * 1e-3), 1),
-        "timing": TIMING[form].format(steps=args.steps, nl=nl),
+        "timing": TIMING[form].format(steps=args.steps, nl=nl, reps=getattr(w, "graph_reps", 1)),
         "parity": parity,
     }
     entry.update(w.extra(kernel_ms * 1e-3))
@@ -1254,7 +1262,7 @@ def main():
             "traffic": measured_traffic(traffic_profile) if traffic_profile else None,
             ("bytes_per_launch" if w.bound == "hbm" else "flops_per_launch"): hbm_work,
             "kernel_ms": round(kernel_ms, 5),
-            "timing": TIMING[form].format(steps=args.steps, nl=nl),
+            "timing": TIMING[form].format(steps=args.steps, nl=nl, reps=getattr(w, "graph_reps", 1)),
         },
         "parity": parity,
         "cpu_baseline": None,
