@@ -47,6 +47,8 @@ Q8 products and the serving loop):
   decode-long-131072-32x128  one sequence of 131072 tokens, 32x128 (a long retrieved context)
   prefill-long-16384-32x128  one 16384-token prompt, 32x128 (its CPU baseline runs the whole
                          prompt: minutes; --no-cpu-baseline skips it)
+  prefill-chunks-b8-256-12x64  8 chunks of 256 tokens after 256-768 cached tokens each
+                         (the reference scheduler's chunked prefill), 12x64, one launch
   prefill-b8-12x64       B=8 prompts, lengths ~ U[128,1024], 12x64, KV scattered into
                          fresh pages then attended causally, in one launch; 12 such
                          steps per HIP graph; FLOPs = sum 2*H*hd*L(L+1)
@@ -323,14 +325,17 @@ class DecodeWorkload:
 
 class PrefillWorkload:
     """Causal paged prefill: the scatter of the chunk's K/V rows into the pool and
-    the attention, in one launch (nitro_paged_attn_prefill_append).  Rates are
-    the algorithmic fp32 FLOPs (QK^T and PV) against the fp32 matrix-core peak; the
-    default kernel reaches fp32 accuracy on the bf16 matrix cores (split operands)."""
+    the attention, in one launch (nitro_paged_attn_prefill_append).  A chunk of
+    lens[b] tokens starts at position starts[b] (0: a fresh prompt; otherwise the
+    keys before it are cached in the pool).  Rates are the algorithmic fp32 FLOPs
+    (QK^T and PV over keys 0..pos of every chunk row) against the fp32 matrix-core
+    peak; the default kernel reaches fp32 accuracy on the bf16 matrix cores
+    (split operands)."""
 
     bound = "mfma"
     flush = False
 
-    def __init__(self, name, B, H, Hkv, hd, lens, seed, describe, layers=1):
+    def __init__(self, name, B, H, Hkv, hd, lens, seed, describe, layers=1, starts=None):
         import nitrorag_amd as na
 
         self.name, self.B, self.H, self.Hkv, self.hd = name, B, H, Hkv, hd
@@ -338,15 +343,15 @@ class PrefillWorkload:
         self.layers = layers
         self.graph = layers > 1
         self.lens = np.asarray(lens, dtype=np.int64)
-        self.starts = np.zeros(B, np.int32)
+        self.starts = np.zeros(B, np.int64) if starts is None else np.asarray(starts, dtype=np.int64)
         self.seed, self.describe = seed, describe
-        self.pages = int(((self.lens + 15) // 16).sum())
+        self.pages = int(((self.starts + self.lens + 15) // 16).sum())
         bm = na.BlockManager(self.pages)  # fresh pool: LIFO page ids, as the reference hands out
         seqs = []
         rng = np.random.default_rng(seed)
         for b in range(B):
             s = na.Sequence(b)
-            s.ingest_prompt(rng.integers(1, 32000, size=int(self.lens[b])), bm, False)
+            s.ingest_prompt(rng.integers(1, 32000, size=int(self.starts[b] + self.lens[b])), bm, False)
             seqs.append(s)
         self.tables = na.pack_block_tables(seqs)
 
@@ -358,8 +363,9 @@ class PrefillWorkload:
         kv_dim = self.Hkv * self.hd
         total = int(self.lens.sum())
         L = self.layers
-        self.k = torch.zeros((self.pages, L, 16, kv_dim), device=dev)
-        self.v = torch.zeros_like(self.k)
+        # the cached keys before each chunk (random; fresh prompts have none)
+        self.k = torch.randn((self.pages, L, 16, kv_dim), device=dev, generator=g)
+        self.v = torch.randn((self.pages, L, 16, kv_dim), device=dev, generator=g)
         self.q = torch.randn((L, total, self.H * self.hd), device=dev, generator=g)
         self.kc = torch.randn((L, total, kv_dim), device=dev, generator=g)
         self.vc = torch.randn((L, total, kv_dim), device=dev, generator=g)
@@ -398,7 +404,7 @@ class PrefillWorkload:
         k, v = self.k.cpu().numpy(), self.v.cpu().numpy()
         kc, vc = self.kc.cpu().numpy(), self.vc.cpu().numpy()
         for b in range(self.B):
-            t = np.arange(int(self.lens[b]))
+            t = int(self.starts[b]) + np.arange(int(self.lens[b]))
             pg = self.tables[b][t >> 4]
             rows = slice(int(off[b]), int(off[b + 1]))
             if not (np.array_equal(k[pg, :, t & 15].transpose(1, 0, 2), kc[:, rows]) and
@@ -408,7 +414,8 @@ class PrefillWorkload:
             q, out = self.q[layer].cpu().numpy(), self.out[layer].cpu().numpy()
             for b in sel:
                 rows = slice(int(off[b]), int(off[b + 1]))
-                want = attn.prefill_chunk(k, v, layer, q[rows], self.tables[b], 0, self.H, self.Hkv, self.hd)
+                want = attn.prefill_chunk(k, v, layer, q[rows], self.tables[b], int(self.starts[b]), self.H,
+                                          self.Hkv, self.hd)
                 check_parity(out[rows], want, f"{self.name} prompt {b} layer {layer}")
         return (f"{len(sel)} of {self.B} prompts x {len(layers)} of {self.layers} layer(s) vs the oracle "
                 f"within 1e-4 + 1e-3|cpu|; every prompt's K/V rows in its pages bit-exact")
@@ -420,7 +427,9 @@ class PrefillWorkload:
                 delattr(self, name)
 
     def work_per_launch(self):
-        return int((2 * self.H * self.hd * self.lens * (self.lens + 1)).sum())
+        # sum over chunk rows at positions s..s+n-1 of 4*H*hd*(pos+1)
+        n, s = self.lens, self.starts
+        return int((2 * self.H * self.hd * n * (2 * s + n + 1)).sum())
 
     def tokens_per_step(self):
         return int(self.lens.sum())
@@ -447,12 +456,14 @@ class PrefillWorkload:
         def run():
             for b in range(sample):
                 rows = slice(int(off[b]), int(off[b + 1]))
-                attn.kv_scatter_prefill(k, v, 0, kc[rows], vc[rows], self.tables[b], 0)
-                attn.prefill_chunk(k, v, 0, q[rows], self.tables[b], 0, self.H, self.Hkv,
+                s = int(self.starts[b])
+                attn.kv_scatter_prefill(k, v, 0, kc[rows], vc[rows], self.tables[b], s)
+                attn.prefill_chunk(k, v, 0, q[rows], self.tables[b], s, self.H, self.Hkv,
                                    self.hd, threads)
 
         per_rep, reps, el = time_cpu(run, seconds)
-        flops = float((2 * self.H * self.hd * self.lens[:sample] * (self.lens[:sample] + 1)).sum())
+        n, s = self.lens[:sample], self.starts[:sample]
+        flops = float((2 * self.H * self.hd * n * (2 * s + n + 1)).sum())
         toks = int(self.lens[:sample].sum())
         return {"value": round(flops / per_rep / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
                 "kind": "port",
@@ -887,6 +898,17 @@ def make_workload(name, seed):
                                       "q/k/v product before the attention leaves them"))
         w.graph, w.graph_reps = True, 12
         return w
+    if name == "prefill-chunks-b8-256-12x64":
+        # the reference scheduler's chunked prefill: 256-token chunks
+        # (src/pagedMemory.hpp:360-379), here the second to fourth chunk of 8 prompts
+        rng = np.random.default_rng(seed)
+        w = PrefillWorkload(name, 8, 12, 12, 64, np.full(8, 256), seed,
+                            describe=("chunked prefill, B=8 chunks of 256 tokens after 256-768 cached "
+                                      "tokens each, 12 heads x 64; a step is one layer's KV scatter + "
+                                      "attention (one launch), 12 steps per HIP graph"),
+                            starts=256 * rng.integers(1, 4, size=8))
+        w.graph, w.graph_reps = True, 12
+        return w
     if name == "model-110m-decode-b32":
         return ModelDecodeWorkload(name, (768, 2048, 12, 12, 12, 32000, 1024), 32, 512, seed,
                                    describe=("one decode step of a Llama-2-110M-shaped model "
@@ -935,7 +957,7 @@ TRAFFIC_PROFILES = {
 }
 
 WORKLOADS = ["decode-b64-ctx4096", "decode-single-110m", "decode-single-110m-flushed", "decode-b32-mixed",
-             "decode-prefix-shared", "decode-long-131072-32x128", "prefill-b8-12x64",
+             "decode-prefix-shared", "decode-long-131072-32x128", "prefill-b8-12x64", "prefill-chunks-b8-256-12x64",
              "prefill-long-16384-32x128", "q8-gemv-7b-ffn", "q8-matmul-110m-b32",
              "model-110m-decode-b32", "model-7b-decode-b1", "model-7b-decode-b2", "model-7b-decode-b8", "serve-110m-u1", "serve-110m-u4", "serve-110m-u8",
              "serve-110m-u16", "serve-110m-u32"]
@@ -964,9 +986,11 @@ def kernel_name(w) -> str:
         return f"paged_attn_prefill_kernel<{w.hd}> (VALU)"
     if kern == "mfma32":
         return f"paged_attn_prefill_mfma_kernel<{w.hd}> (fp32 matrix cores)"
-    append = os.environ.get("NITRO_PREFILL_APPEND", "1") != "0" and bool((w.starts == 0).all())
+    append = os.environ.get("NITRO_PREFILL_APPEND", "1") != "0"
+    cached = bool((w.starts > 0).any())
     return (f"paged_attn_prefill_x3_kernel<{w.hd}> (bf16 matrix cores, three-part splits"
-            + (", KV scatter inside the launch)" if append else ")"))
+            + ((", KV scatter inside the launch" + (", cached keys from the pool)" if cached else ")"))
+               if append else "; the scatter as a launch of its own)"))
 
 
 def host_cpu():

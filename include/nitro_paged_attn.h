@@ -239,10 +239,12 @@ int nitro_paged_attn_prefill(nitro_kvpool* pool, int32_t layer, const float* q, 
  * reference's prefill layer step, src/model_q8.cpp:473-484 then :485-523
  * (nitro_kv_append_prefill followed by nitro_paged_attn_prefill, with the same
  * pool contents and output).  k, v: device [total_tokens][kv_dim].  With the
- * matrix-core kernel (head_dim 32, 64, 128), a batch of fresh prompts (every
- * start_pos 0, positions below 32768) and no page written from two table
- * entries (checked at upload), one launch reads the keys from k / v and
- * appends them; otherwise the scatter and the attention run as two launches. */
+ * matrix-core kernel (head_dim 32, 64, 128), positions below 32768, and no
+ * page that a chunk row lands on named by any other table entry (checked at
+ * upload), one launch reads each chunk's keys from k / v (keys cached before
+ * start_pos from the pool) and appends the chunk: fresh prompts, later chunks
+ * of a chunked prefill, suffixes after prefix-cache hits.  Otherwise the
+ * scatter and the attention run as two launches. */
 int nitro_paged_attn_prefill_append(nitro_kvpool* pool, int32_t layer, const float* q, const float* k,
                                     const float* v, float* out, int32_t n_heads, int32_t n_kv_heads,
                                     int32_t head_dim, void* stream);

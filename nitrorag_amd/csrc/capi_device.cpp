@@ -813,21 +813,30 @@ int nitro_paged_attn_decode_append(nitro_kvpool* pool, int32_t layer, const floa
     });
 }
 
-// Whether attention may read a prefill batch's keys from the new rows while
-// the same launch writes them into the pool: every chunk starts at position 0
-// (a fresh prompt: no cached keys are read) and no page is written from two
-// table entries.
-static bool fresh_prompts_unshared(const int32_t* tables, const int32_t* start_pos,
-                                 const int32_t* num_tokens, int batch, int max_pages) {
+// Whether attention may read a prefill batch's chunk keys from the new rows
+// (and the cached keys below each chunk from the pool) while the same launch
+// writes the chunk rows into the pool: no page is written from two table
+// entries, and no page a chunk row lands on is also a cached-key page of any
+// sequence (the page of a chunk's first row may hold the chunk's own cached
+// rows: those are other rows of the same entry).
+static bool chunk_pages_private(const int32_t* tables, const int32_t* start_pos,
+                                const int32_t* num_tokens, int batch, int max_pages) {
     std::unordered_map<int32_t, std::pair<int, int>> written;  // page -> (seq, table index)
     for (int b = 0; b < batch; b++) {
         if (num_tokens[b] == 0) continue;
-        if (start_pos[b] != 0) return false;
         const int32_t* row = tables + (size_t)b * max_pages;
         for (int i = start_pos[b] >> 4; i <= (start_pos[b] + num_tokens[b] - 1) >> 4; i++) {
             const auto at = written.emplace(row[i], std::make_pair(b, i));
             if (!at.second) return false;
         }
+    }
+    // a cached key's page (below a chunk's first page) must not be one a
+    // chunk row lands on
+    for (int b = 0; b < batch; b++) {
+        if (num_tokens[b] == 0) continue;
+        const int32_t* row = tables + (size_t)b * max_pages;
+        for (int i = 0; i < start_pos[b] >> 4; i++)
+            if (written.count(row[i])) return false;
     }
     return true;
 }
@@ -930,7 +939,9 @@ int nitro_prefill_batch_upload(nitro_kvpool* pool, const int32_t* tables, const 
         for (int b = 0; b < batch; b++)
             if (num_tokens[b] > 0) max_pos = std::max(max_pos, start_pos[b] + num_tokens[b] - 1);
         p.max_pos = max_pos;
-        p.append_in_launch = fresh_prompts_unshared(tables, start_pos, num_tokens, batch, max_pages);
+        p.append_in_launch = chunk_pages_private(tables, start_pos, num_tokens, batch, max_pages);
+        p.append_mixed = false;
+        for (int b = 0; b < batch; b++) p.append_mixed |= num_tokens[b] > 0 && start_pos[b] > 0;
         p.work_items = (int32_t)items.size();
         p.work_block_m = bm;
         p.work_items_wide = (int32_t)wide.size();
@@ -1026,6 +1037,7 @@ int nitro_paged_attn_prefill_append(nitro_kvpool* pool, int32_t layer, const flo
             env_int("NITRO_PREFILL_APPEND", 1) != 0) {
             a.k_new = k;
             a.v_new = v;
+            a.append_mixed = p.append_mixed ? 1 : 0;
             hip_check(launch_paged_attn_prefill(a, s), "paged_attn_prefill append launch");
             p.fused_launches++;
         } else {

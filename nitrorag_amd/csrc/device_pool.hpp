@@ -140,10 +140,11 @@ struct PrefillBatch {
     DeviceBuffer<int32_t> work_wide;  // the same for items of PREFILL_WIDE_ROWS rows
     int32_t work_items_wide = 0;
     int32_t max_pos = 0;              // largest position of any row
-    // Every chunk starts at position 0 and no page is written from two table
-    // entries: attention may then read the keys from the new rows while the
-    // same launch writes them into the pool.
+    // No table entry but a chunk row's own names the page that row lands on:
+    // attention may then read the chunk's keys from the new rows (and older
+    // keys from the pool) while the same launch writes the rows into the pool.
     bool append_in_launch = false;
+    bool append_mixed = false;  // ... and some chunk starts after cached keys
     uint64_t append_launches = 0, fused_launches = 0;  // nitro_paged_attn_prefill_append calls / one-launch form
 };
 
@@ -350,6 +351,7 @@ struct PrefillLaunch {
     // the same launch.  nullptr: every key is read from the pool.
     const float* k_new;
     const float* v_new;
+    int32_t append_mixed;  // appending form: some chunk starts after cached keys (read from the pool)
     int32_t max_pos;  // largest position of the batch
     const int32_t* tables;
     const int32_t* start_pos;

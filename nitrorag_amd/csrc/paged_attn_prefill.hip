@@ -596,15 +596,17 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_mfma_kern
 // per thread; V one d of four consecutive keys per thread (a wave's lanes
 // cover consecutive d of a row, so the loads coalesce), which becomes one
 // 8-byte store per plane into the transposed tile.
-// APPEND: the launch also appends the chunk, for a batch of fresh prompts
-// (every chunk starts at position 0).  The keys are read from the new rows
-// k_new / v_new (the same values, so the output is the same as after a
-// separate scatter), and the workgroup of
-// the first head of each kv group stores its query rows' K/V into the pool
-// from the registers the tile loads left them in.  No workgroup reads those
-// pool rows: the host takes this form only when no sequence reads a page a
-// chunk row lands on.
-template <int HD, int QT, int KSPLIT, int BNM, bool APPEND>
+// APPEND (1, 2): the launch also appends the chunk.  The chunk's keys are
+// read from the new rows k_new / v_new (the same values, so the output is the
+// same as after a separate scatter), and the workgroup of the first head of
+// each kv group stores its query rows' K/V into the pool from the registers
+// the tile loads left them in.  No workgroup reads those pool rows: the host
+// takes this form only when no table entry but the row's own names a page a
+// chunk row lands on.  APPEND 1: a batch of fresh prompts (every chunk starts
+// at position 0), every key new.  APPEND 2: chunks after cached keys; a key
+// below its chunk's start is read from the pool, the others from the new
+// rows, chosen per key (a tile may hold both).
+template <int HD, int QT, int KSPLIT, int BNM, int APPEND>
 // Up to hd 64 two workgroups share a CU (LDS), which takes at most 128
 // VGPRs (4 waves per SIMD); hd 128 runs one workgroup per CU.
 __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn_prefill_x3_kernel(PrefillLaunch a) {
@@ -745,16 +747,16 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
     const size_t vrow_b = (size_t)a.kv_dim * sizeof(float);
     // FULL: every key of the tile is at most last_pos (wave-uniform), so
     // only the page ids decide validity and no index needs clamping.
-    // SRC: the keys are read from the pool (POOL) or, in an APPEND launch
-    // (every chunk starts at position 0), from the new rows (NEW), where the
-    // sequence's row j holds position start + j.  A key at page index p and
-    // the thread's fixed row is new row 16 p + row - start, i.e. at kb + dk +
-    // p * 16 rows: the same per-thread pointer plus a workgroup-uniform
-    // offset, so the new rows cost no registers of their own.  (A form that
-    // also reads cached keys from the pool in the same launch pushed the
-    // kernel past 128 VGPRs into spills and measured slower than the scatter
-    // and the attention as two launches.)
-    constexpr int POOL = 0, NEW = 1;
+    // SRC: the keys are read from the pool (POOL) or, in an APPEND launch,
+    // from the new rows (NEW), where the sequence's row j holds position
+    // start + j, or per key from either (MIXED: below start from the pool).
+    // A key at page index p and the thread's fixed row is new row 16 p + row
+    // - start, i.e. at kb + dk + p * 16 rows: the same per-thread pointer plus
+    // a workgroup-uniform offset, so the new rows cost no registers of their
+    // own, and MIXED picks one of two offsets from the same pointer.  (An
+    // earlier form that read cached keys through a separate pool pointer went
+    // past 128 VGPRs into spills.)
+    constexpr int POOL = 0, NEW = 1, MIXED = 2;
     const bool appends = APPEND && h % a.kv_mul == 0;
     const int own_first = start + q0;
     const size_t rows16_b = 16 * vrow_b;
@@ -779,7 +781,9 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
             kmask |= (uint32_t)ok << i;
             const size_t pool_off = (size_t)(uint32_t)(ok ? page : 0) * stride_b;
             const size_t new_off = dk + (size_t)(uint32_t)(kc >> 4) * rows16_b;
-            const size_t off = SRC == POOL ? pool_off : (ok ? new_off : 0);
+            const size_t off = SRC == POOL                  ? pool_off
+                               : SRC == MIXED && kc < start ? pool_off
+                                                            : (ok ? new_off : 0);
             kreg[i] = *reinterpret_cast<const float4*>(kb + off);
         }
 #pragma unroll
@@ -794,7 +798,7 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
             for (int e = 0; e < 4; e++) {
                 // a new row past last_pos is not read (the sequence's rows end there)
                 const int ec = FULL ? e : max(0, min(e, last_pos - key0));
-                const char* p = SRC == POOL ? vp + e * vrow_b : vn + ec * vrow_b;
+                const char* p = SRC == POOL || (SRC == MIXED && key0 + e < start) ? vp + e * vrow_b : vn + ec * vrow_b;
                 vreg[i][e] = *reinterpret_cast<const float*>(p);
             }
             if (FULL) {
@@ -815,7 +819,9 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
     const bool fast_fetch = table_in_lds && (uint64_t)a.page_stride * sizeof(float) < (1ull << 32);
     // inlined: as a call (several forms, two call sites) it measured 4x slower
     auto fetch = [&](int tile) __attribute__((always_inline)) {
-        if constexpr (APPEND) {
+        if constexpr (APPEND == 2) {
+            fetch_lds(tile, std::integral_constant<int, MIXED>{});
+        } else if constexpr (APPEND == 1) {
             fetch_lds(tile, std::integral_constant<int, NEW>{});
         } else if (fast_fetch) {
             fetch_lds(tile, std::integral_constant<int, POOL>{});
@@ -1106,19 +1112,27 @@ hipError_t launch_paged_attn_prefill(const PrefillLaunch& a, hipStream_t stream)
     if ((a.k_new != nullptr) != (a.v_new != nullptr) ||
         (a.k_new && !prefill_appends_in_launch(a.kernel, a.head_dim, a.max_pos, a.page_stride)))
         return hipErrorInvalidValue;  // only the bf16 matrix-core kernel appends, with the table in LDS
+    if (a.kernel == PREFILL_KERNEL_DEFAULT && a.k_new && !a.append_mixed) {
+        switch (a.head_dim) {
+            case 32: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<32, 4, 2, 64, 1>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 64: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<64, 4, 2, 64, 1>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 128: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<128, 8, 1, 32, 1>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            default: return hipErrorInvalidValue;
+        }
+    }
     if (a.kernel == PREFILL_KERNEL_DEFAULT && a.k_new) {
         switch (a.head_dim) {
-            case 32: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<32, 4, 2, 64, true>), grid, dim3(512), 0, stream, a); return hipGetLastError();
-            case 64: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<64, 4, 2, 64, true>), grid, dim3(512), 0, stream, a); return hipGetLastError();
-            case 128: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<128, 8, 1, 32, true>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 32: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<32, 4, 2, 64, 2>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 64: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<64, 4, 2, 64, 2>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 128: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<128, 8, 1, 32, 2>), grid, dim3(512), 0, stream, a); return hipGetLastError();
             default: return hipErrorInvalidValue;
         }
     }
     if (a.kernel == PREFILL_KERNEL_DEFAULT) {
         switch (a.head_dim) {
-            case 32: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<32, 4, 2, 64, false>), grid, dim3(512), 0, stream, a); return hipGetLastError();
-            case 64: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<64, 4, 2, 64, false>), grid, dim3(512), 0, stream, a); return hipGetLastError();
-            case 128: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<128, 8, 1, 32, false>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 32: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<32, 4, 2, 64, 0>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 64: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<64, 4, 2, 64, 0>), grid, dim3(512), 0, stream, a); return hipGetLastError();
+            case 128: hipLaunchKernelGGL((paged_attn_prefill_x3_kernel<128, 8, 1, 32, 0>), grid, dim3(512), 0, stream, a); return hipGetLastError();
             default: break;  // other head sizes: VALU kernel
         }
     }

@@ -1,10 +1,11 @@
 """GPU: the prefill step with the KV scatter inside the attention launch
 (nitro_paged_attn_prefill_append) against the scatter and the attention as two
 launches (src/model_q8.cpp:473-484 then :485-523) and against the oracle.  The
-one-launch form (a batch of fresh prompts) reads the keys from the new rows
-instead of the pool, the same floats in the same order, so the output and both
-pools must be bit-identical to the two-launch form's; other batches run the
-two launches behind the same call."""
+one-launch form reads a chunk's keys from the new rows instead of the pool (and
+keys cached before the chunk from the pool), the same floats in the same order,
+so the output and both pools must be bit-identical to the two-launch form's.
+It runs when no page a chunk row lands on is named by another table entry;
+other batches run the two launches behind the same call."""
 import sys
 
 import numpy as np
@@ -71,12 +72,18 @@ FRESH = {
     "fresh_single_tokens_hd64": (5, 5, 1, 1, 4, 4, 64, 1, 0, 0, 0),
     "fresh_gqa_16x4_hd64_long": (14, 2, 900, 2100, 16, 4, 64, 1, 0, 0, 0),
     "fresh_gqa_8x2_hd128_long": (15, 2, 2500, 4000, 8, 2, 128, 1, 0, 0, 0),
+    # chunks after cached keys (random starts: tiles and V groups straddle them)
+    "continued_12x64": (17, 5, 1, 300, 12, 12, 64, 2, 1, 1, 700),
+    "continued_gqa_16x4_hd64": (18, 3, 100, 900, 16, 4, 64, 1, 0, 500, 1500),
+    # the reference scheduler's 256-token chunks (src/pagedMemory.hpp:360-379)
+    "chunk_256_after_512_hd64": (19, 4, 256, 256, 12, 12, 64, 1, 0, 512, 512),
+    "chunk_256_after_256_hd128": (20, 3, 200, 256, 8, 8, 128, 1, 0, 256, 256),
 }
 
 
-# fresh prompts at head sizes 32, 64, 128 take the one-launch form; chunks after
-# cached keys, head size 256 and padded sizes, and keys past the LDS copy of the
-# table (32k tokens) run the two launches behind the same call
+# fresh prompts and chunks after cached keys at head sizes 32, 64, 128 take the
+# one-launch form; head size 256 and padded sizes, and keys past the LDS copy of
+# the table (32k tokens) run the two launches behind the same call
 @pytest.mark.parametrize("name,one_launch", [
     ("prompts_b8_12x64", True),
     ("fresh_gqa_8x2_hd128", True),
@@ -84,8 +91,13 @@ FRESH = {
     ("fresh_single_tokens_hd64", True),
     ("fresh_gqa_16x4_hd64_long", True),
     ("fresh_gqa_8x2_hd128_long", True),
-    ("continued_chunks_gqa_8x2_hd128", False),
-    ("short_chunks_hd32", False),
+    ("continued_chunks_gqa_8x2_hd128", True),
+    ("short_chunks_hd32", True),
+    ("single_token_chunks", True),
+    ("continued_12x64", True),
+    ("continued_gqa_16x4_hd64", True),
+    ("chunk_256_after_512_hd64", True),
+    ("chunk_256_after_256_hd128", True),
     ("mha_hd256", False),
     ("hd48", False),
     ("beyond_lds_table_hd64", False),
@@ -122,21 +134,46 @@ def test_append_prompt_near_the_table_limit():
 
 
 def test_append_random_batches():
-    """Twelve seeded random batches of fresh prompts at head sizes 32, 64 and
-    128: 1-6 prompts of 1-300 tokens, MHA and GQA, 1-2 layers."""
+    """Sixteen seeded random batches at head sizes 32, 64 and 128: 1-6 chunks
+    of 1-300 tokens, fresh prompts in half of them and chunks after 1-400
+    cached keys in the other half, MHA and GQA, 1-2 layers; all one launch."""
     rng = np.random.default_rng(20261204)
-    for i in range(12):
+    for i in range(16):
         B = int(rng.integers(1, 7))
         kv_mul = int(rng.choice([1, 2, 4]))
         hd = int(rng.choice([32, 64, 128]))
         Hkv = int(rng.integers(1, 4))
         layers = int(rng.integers(1, 3))
         layer = int(rng.integers(0, layers))
-        name = f"random append {i}: B={B} H={Hkv * kv_mul} Hkv={Hkv} hd={hd}"
+        slo, shi = (0, 0) if i % 2 == 0 else (1, 400)
+        name = f"random append {i}: B={B} H={Hkv * kv_mul} Hkv={Hkv} hd={hd} starts {slo}..{shi}"
         say(name)
         c = prefill_batch_case(int(rng.integers(1 << 30)), B, 1, 300, Hkv * kv_mul, Hkv, hd, layers,
-                               layer, 0, 0)
+                               layer, slo, shi)
         check(c, True, name)
+
+
+def test_append_chunks_after_shared_cached_pages():
+    """Two sequences whose cached keys sit on the same two pages (prefix-cache
+    hits) each prefill a chunk onto pages of their own: the one-launch form
+    runs (the shared pages are only read) and matches the two launches bit for
+    bit and the oracle."""
+    rng = np.random.default_rng(8)
+    H, Hkv, hd = 4, 2, 64
+    kv_dim = Hkv * hd
+    tables = np.array([[0, 1, 2, 4], [0, 1, 3, 5]], dtype=np.int32)
+    starts = np.array([32, 40])   # the second chunk starts inside its page 2 (id 3)
+    lens = np.array([30, 21])
+    total = int(lens.sum())
+    c = dict(k=rng.standard_normal((6, 1, 16, kv_dim)).astype(np.float32),
+             v=rng.standard_normal((6, 1, 16, kv_dim)).astype(np.float32),
+             tables=tables, starts=starts, lens=lens,
+             q=rng.standard_normal((total, H * hd)).astype(np.float32),
+             kc=rng.standard_normal((total, kv_dim)).astype(np.float32),
+             vc=rng.standard_normal((total, kv_dim)).astype(np.float32),
+             H=H, Hkv=Hkv, hd=hd, layer=0)
+    say("prefill append after shared cached pages")
+    check(c, True, "shared cached pages")
 
 
 def test_append_page_read_by_another_sequence():
