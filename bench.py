@@ -952,6 +952,7 @@ TRAFFIC_PROFILES = {
     "decode-prefix-shared": "paged_attn_decode_prefix_shared_b48_12x64.md",
     "decode-long-131072-32x128": "paged_attn_decode_long_131072_32x128.md",
     "prefill-b8-12x64": "paged_attn_prefill_b8_12x64.md",
+    "prefill-chunks-b8-256-12x64": "paged_attn_prefill_chunks_b8_256_12x64.md",
     "prefill-long-16384-32x128": "paged_attn_prefill_long_16384_32x128.md",
     "model-7b-decode-b1": "model_7b_decode_b1.md",
 }
