@@ -86,7 +86,7 @@ SIGNATURES = {
     "nitro_paged_attn_decode": [_vp, _i32, _fp, _fp, _i32, _i32, _i32, _vp],
     "nitro_paged_attn_decode_append": [_vp, _i32, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _vp],
     "nitro_paged_attn_decode_static": [_vp, _i32, _fp, _fp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32,
-                                       _vp],
+                                       _i32, _vp],
     "nitro_prefill_batch_upload": [_vp, _i32p, _i32p, _i32p, _i32, _i32, _vp],
     "nitro_kv_append_prefill": [_vp, _i32, _fp, _fp, _vp],
     "nitro_paged_attn_prefill": [_vp, _i32, _fp, _fp, _i32, _i32, _i32, _vp],

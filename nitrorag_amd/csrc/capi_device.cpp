@@ -744,11 +744,12 @@ int nitro_paged_attn_decode(nitro_kvpool* pool, int32_t layer, const float* q, f
 int nitro_paged_attn_decode_static(nitro_kvpool* pool, int32_t layer, const float* q, float* out,
                                    const int32_t* tables, const int32_t* positions, int32_t batch,
                                    int32_t max_pages, int32_t max_context, int32_t n_heads, int32_t n_kv_heads,
-                                   int32_t head_dim, void* stream) {
+                                   int32_t head_dim, int32_t pages_private, void* stream) {
     return guarded([&] {
         require_pool(pool);
         require(q != nullptr && out != nullptr && tables != nullptr && positions != nullptr,
                 ERR_INVALID_ARGUMENT, "null q/out/tables/positions");
+        require(pages_private == 0 || pages_private == 1, ERR_INVALID_ARGUMENT, "pages_private must be 0 or 1");
         check_shape(pool, layer, n_heads, n_kv_heads, head_dim);
         require(batch > 0 && max_pages > 0, ERR_INVALID_ARGUMENT, "batch and max_pages must be positive");
         require(max_context > 0 && max_context <= max_pages * BLOCK_SIZE, ERR_INVALID_ARGUMENT,
@@ -759,8 +760,9 @@ int nitro_paged_attn_decode_static(nitro_kvpool* pool, int32_t layer, const floa
         const DecodeShape sh = plan_decode_shape(pool, batch, ctx, n_heads, n_kv_heads, head_dim);
         const int tile = decode_tile_rows(head_dim);
         const int splits = ((max_context + tile - 1) / tile + sh.tps - 1) / sh.tps;
-        // page sharing is unknown here: plain (cacheable) K/V loads
-        DecodeLaunch a = decode_launch_base(pool, layer, q, out, n_heads, n_kv_heads, head_dim, sh, true);
+        // page sharing is the caller's to say: plain (cacheable) K/V loads
+        // unless no page is read twice
+        DecodeLaunch a = decode_launch_base(pool, layer, q, out, n_heads, n_kv_heads, head_dim, sh, !pages_private);
         float* ws = nullptr;
         if (splits > 1) {
             const size_t counters = (size_t)batch * (n_heads / sh.qh);

@@ -619,7 +619,7 @@ def test_decode_counts_and_skips_page_ids_outside_the_pool(max_context_split):
         st = N.lib().nitro_paged_attn_decode_static(
             pool.handle, 0, ctypes.c_void_p(dq.data_ptr()), ctypes.c_void_p(out.data_ptr()),
             ctypes.c_void_p(tab_d.data_ptr()), ctypes.c_void_p(pos_d.data_ptr()), len(ctx),
-            tab.shape[1], int(ctx.max()), H, Hkv, hd, None)
+            tab.shape[1], int(ctx.max()), H, Hkv, hd, 0, None)
         assert st == N.OK, N.last_error()
         torch.cuda.synchronize()
         return out.cpu().numpy()

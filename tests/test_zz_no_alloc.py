@@ -29,13 +29,14 @@ def free_device_bytes():
     return free.value
 
 
-def static_decode(pool, layer, q, out, tables_d, pos_d, batch, max_pages, max_context, H, Hkv, hd):
+def static_decode(pool, layer, q, out, tables_d, pos_d, batch, max_pages, max_context, H, Hkv, hd,
+                  pages_private=0):
     from nitrorag_amd import _native as N
 
     st = N.lib().nitro_paged_attn_decode_static(
         pool.handle, layer, ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(out.data_ptr()),
         ctypes.c_void_p(tables_d.data_ptr()), ctypes.c_void_p(pos_d.data_ptr()), batch, max_pages,
-        max_context, H, Hkv, hd, None)
+        max_context, H, Hkv, hd, pages_private, None)
     assert st == N.OK, N.last_error()
 
 
@@ -77,11 +78,14 @@ def test_static_decode_matches_decode_on_two_calls():
         assert_parity(got, ref.cpu().numpy(), f"call {call} vs nitro_paged_attn_decode")
         assert_parity(got, attn.decode_batch(k, v, 1, q, tables, positions, H, Hkv, hd),
                       f"call {call} vs oracle")
-        # repeated launches are bit-identical (the counters were left at zero)
-        again = torch.full_like(dq, float("nan"))
-        static_decode(pool, 1, dq, again, tables_d, pos_d, B, tables.shape[1], int(ctx.max()), H, Hkv, hd)
-        torch.cuda.synchronize()
-        assert np.array_equal(again.cpu().numpy(), got)
+        # repeated launches are bit-identical (the counters were left at zero), and
+        # so is the launch with non-temporal K/V loads (these tables share no page)
+        for private in (0, 1):
+            again = torch.full_like(dq, float("nan"))
+            static_decode(pool, 1, dq, again, tables_d, pos_d, B, tables.shape[1], int(ctx.max()), H, Hkv, hd,
+                          private)
+            torch.cuda.synchronize()
+            assert np.array_equal(again.cpu().numpy(), got)
     assert pool.take_device_errors() == 0
 
 
@@ -105,11 +109,15 @@ def test_static_decode_refuses_what_its_workspace_cannot_hold(monkeypatch):
         return N.lib().nitro_paged_attn_decode_static(
             pool.handle, 0, ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(q.data_ptr()),
             ctypes.c_void_p(tables.data_ptr()), ctypes.c_void_p(pos.data_ptr()), 64, max_pages, max_context,
-            32, 32, 128, None)
+            32, 32, 128, 0, None)
 
     monkeypatch.setenv("NITRO_DECODE_SPLIT_TILES", "1")
     assert call(256, 4096) == N.INVALID_ARGUMENT
     assert "static workspace" in N.last_error()
     monkeypatch.delenv("NITRO_DECODE_SPLIT_TILES")
     assert call(256, 4097) == N.INVALID_ARGUMENT  # max_context past the table
+    assert N.lib().nitro_paged_attn_decode_static(
+        pool.handle, 0, ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(q.data_ptr()),
+        ctypes.c_void_p(tables.data_ptr()), ctypes.c_void_p(pos.data_ptr()), 64, 256, 4096,
+        32, 32, 128, 2, None) == N.INVALID_ARGUMENT  # pages_private is 0 or 1
     torch.cuda.synchronize()
