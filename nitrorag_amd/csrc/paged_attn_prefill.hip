@@ -634,6 +634,7 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
     uint16_t* const v_lds = kv_lds + 3 * KPLANE;
     __shared__ int32_t s_table[TABLE_LDS];
     __shared__ float s_ml[KSPLIT > 1 ? QT * (KSPLIT - 1) * 16 * 2 : 1];
+    __shared__ int32_t s_wave_bad[NT / 64];
 
     const int h = blockIdx.x % a.n_heads;
     const int item = blockIdx.x / a.n_heads;
@@ -669,19 +670,6 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
         qraw[c][1] = src[1];
     }
 
-    // The LDS copy of the table holds -1 for an id outside the pool (counted
-    // here, once per workgroup), so the tile fetch checks only the sign.
-    const int n_pages = min((last_pos >> 4) + 1, TABLE_LDS);
-    for (int i = threadIdx.x; i < n_pages; i += NT) {
-        int p = trow[i];
-        if ((unsigned)p >= (unsigned)a.num_pages) {
-            atomicAdd(a.bad_pages, 1);
-            p = -1;
-        }
-        s_table[i] = p;
-    }
-    __syncthreads();
-
     f32x4 acc[NB];
 #pragma unroll
     for (int n = 0; n < NB; n++) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -698,6 +686,8 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
     // the LDS copy of the table when all of the work item's pages are in it
     // (block-uniform); otherwise pages past the copy are read from memory.
     static_assert(LOADS <= 32 && 4 * VSLOTS <= 32, "validity masks");
+    constexpr uint32_t KFULL = LOADS == 32 ? ~0u : (1u << LOADS) - 1;
+    constexpr uint32_t VFULL = 4 * VSLOTS == 32 ? ~0u : (1u << (4 * VSLOTS)) - 1;
     const bool table_in_lds = (last_pos >> 4) < TABLE_LDS;
     uint32_t kmask = 0, vmask = 0;
     auto fetch_with = [&](int tile, auto page_of) {
@@ -755,6 +745,9 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
     // SRC: the keys are read from the pool (POOL) or, in an APPEND launch,
     // from the new rows (NEW), where the sequence's row j holds position
     // start + j, or per key from either (MIXED: below start from the pool).
+    // NEW reads by position alone, without the table: its masks record only
+    // which keys are real, and staging clears the keys on pages outside the
+    // pool (the workgroup knows whether it has any) as the other forms do.
     // A key at page index p and the thread's fixed row is new row 16 p + row
     // - start, i.e. at kb + dk + p * 16 rows: the same per-thread pointer plus
     // a workgroup-uniform offset, so the new rows cost no registers of their
@@ -773,15 +766,40 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
                                         reinterpret_cast<uintptr_t>(a.v_pool + a.layer_off)) -
                                    (size_t)start * vrow_b
                              : 0;
+    // NEW over a full tile: a thread's load i of tile t reads page index
+    // t * BNM/16 + (its page within the tile) + i * (pages per NT threads),
+    // so the address is one per-thread base (kn, vn) plus a block-uniform
+    // multiple of the 16-row pitch (scalar arithmetic).
+    const char* const kn = kb + dk + (size_t)(uint32_t)((threadIdx.x / F4) >> 4) * rows16_b;
+    const char* const vn = vb + dv + (size_t)(uint32_t)((4 * (threadIdx.x / HD)) >> 4) * rows16_b;
     auto fetch_lds_as = [&](int tile, auto full, auto src) __attribute__((always_inline)) {
         constexpr bool FULL = decltype(full)::value;
         constexpr int SRC = decltype(src)::value;
+        if constexpr (SRC == NEW && FULL) {
+            kmask = KFULL;
+            vmask = VFULL;
+            // (readfirstlane keeps each page index opaque: folded into kn / vn,
+            // the compiler holds a 64-bit base per load and spills them)
+#pragma unroll
+            for (int i = 0; i < LOADS; i++) {
+                const int pg = __builtin_amdgcn_readfirstlane(tile * (BNM / 16) + i * (NT / F4 / 16));
+                kreg[i] = *reinterpret_cast<const float4*>(kn + (size_t)(uint32_t)pg * rows16_b);
+            }
+#pragma unroll
+            for (int i = 0; i < VSLOTS; i++) {
+                const int pg = __builtin_amdgcn_readfirstlane(tile * (BNM / 16) + i * (4 * NT / HD / 16));
+                const char* p = vn + (size_t)(uint32_t)pg * rows16_b;
+#pragma unroll
+                for (int e = 0; e < 4; e++) vreg[i][e] = *reinterpret_cast<const float*>(p + e * vrow_b);
+            }
+            return;
+        }
         kmask = vmask = 0;
 #pragma unroll
         for (int i = 0; i < LOADS; i++) {
             const int key = tile * BNM + (int)(threadIdx.x + i * NT) / F4;
             const int kc = FULL ? key : min(key, last_pos);
-            const int page = s_table[kc >> 4];  // -1: outside the pool
+            const int page = SRC == NEW ? 0 : s_table[kc >> 4];  // -1: outside the pool
             const bool ok = (FULL || key <= last_pos) && page >= 0;
             kmask |= (uint32_t)ok << i;
             const size_t pool_off = (size_t)(uint32_t)(ok ? page : 0) * stride_b;
@@ -795,7 +813,7 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
         for (int i = 0; i < VSLOTS; i++) {
             const int key0 = tile * BNM + 4 * ((int)(threadIdx.x + i * NT) / HD);  // 4 keys, one page
             const int kc = FULL ? key0 : min(key0, last_pos);
-            const int page = s_table[kc >> 4];
+            const int page = SRC == NEW ? 0 : s_table[kc >> 4];
             const bool ok = (FULL || key0 <= last_pos) && page >= 0;
             const char* vp = vb + (size_t)(uint32_t)(ok ? page : 0) * stride_b;
             const char* vn = vb + (ok ? dv + (size_t)(uint32_t)(kc >> 4) * rows16_b : 0);
@@ -841,7 +859,31 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, c, 0, 0, 0);
     };
 
-    fetch(0);
+    // The first tile of the new rows is requested before the table, so the
+    // two latencies overlap.  The LDS copy of the table holds -1 for an id
+    // outside the pool (counted here, once per workgroup), so the tile fetch
+    // checks only the sign.
+    if constexpr (APPEND == 1) fetch(0);
+    const int n_pages = min((last_pos >> 4) + 1, TABLE_LDS);
+    bool bad = false;
+    for (int i = threadIdx.x; i < n_pages; i += NT) {
+        int p = trow[i];
+        if ((unsigned)p >= (unsigned)a.num_pages) {
+            atomicAdd(a.bad_pages, 1);
+            p = -1;
+            bad = true;
+        }
+        s_table[i] = p;
+    }
+    // Whether any page of the item is outside the pool: one flag per wave,
+    // each written by its own wave, read by all after the barrier.
+    const bool wave_bad = __builtin_amdgcn_ballot_w64(bad) != 0;
+    if (lane == 0) s_wave_bad[wave] = wave_bad;
+    __syncthreads();
+    bool any_bad = false;  // block-uniform
+#pragma unroll
+    for (int w = 0; w < NT / 64; w++) any_bad |= s_wave_bad[w] != 0;
+    if constexpr (APPEND != 1) fetch(0);
     bf16x8 qp[3][NC];  // Q (pre-scaled) in parts
 #pragma unroll
     for (int c = 0; c < NC; c++) {
@@ -890,8 +932,20 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
                 stage4(&v_lds[(sl % HD) * VST + 4 * (sl / HD)], VPLANE, v4);
             }
         };
-        constexpr uint32_t KFULL = LOADS == 32 ? ~0u : (1u << LOADS) - 1;
-        constexpr uint32_t VFULL = 4 * VSLOTS == 32 ? ~0u : (1u << (4 * VSLOTS)) - 1;
+        if constexpr (APPEND == 1) {
+            if (any_bad) {  // block-uniform: keys on pages outside the pool are staged as zero
+#pragma unroll
+                for (int i = 0; i < LOADS; i++) {
+                    const int key = tile * BNM + (int)(threadIdx.x + i * NT) / F4;
+                    if (s_table[min(key, last_pos) >> 4] < 0) kmask &= ~(1u << i);
+                }
+#pragma unroll
+                for (int i = 0; i < VSLOTS; i++) {
+                    const int key0 = tile * BNM + 4 * ((int)(threadIdx.x + i * NT) / HD);  // 4 keys, one page
+                    if (s_table[min(key0, last_pos) >> 4] < 0) vmask &= ~(0xFu << (4 * i));
+                }
+            }
+        }
         if (__builtin_amdgcn_ballot_w64(kmask != KFULL || vmask != VFULL) != 0)  // wave-uniform
             stage_tile(true);
         else
