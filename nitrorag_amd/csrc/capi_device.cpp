@@ -376,7 +376,11 @@ bool plan_prefix(nitro_kvpool* pool, int n_heads, int n_kv_heads, int head_dim) 
                     make_int4(-1 - base, count | (c << 8), c * ch, std::min(ch, tiles - c * ch));
         }
     }
-    // The splits of each sequence's own rows, shortest first.
+    // The splits of each sequence's own rows, longest first.  With the member
+    // items the launch can hold more workgroups than the GPU runs at once;
+    // the ones dispatched last start when the first finish, and short ones
+    // there end the launch sooner (48 sequences sharing 512 rows, 12 x 64:
+    // 22.8-23.4 us against 24.2-24.4 shortest first).
     std::vector<std::pair<int, int4>> order;  // (tiles, item)
     for (int b = 0; b < B; b++) {
         const int first_tile = shared_rows[b] / tile;
@@ -384,7 +388,7 @@ bool plan_prefix(nitro_kvpool* pool, int n_heads, int n_kv_heads, int head_dim) 
             order.push_back({std::min(sh.tps, own_tiles(b) - x * sh.tps),
                              make_int4(b, x | (first_tile << 8), first_slot[b] | (parts[b] << 16), ctx(b))});
     }
-    std::stable_sort(order.begin(), order.end(), [](const auto& x, const auto& y) { return x.first < y.first; });
+    std::stable_sort(order.begin(), order.end(), [](const auto& x, const auto& y) { return x.first > y.first; });
     for (const auto& o : order) d.arg_list.item[n++] = o.second;
     d.main_items = n;
     d.main_tps = sh.tps;
