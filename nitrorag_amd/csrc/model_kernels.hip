@@ -291,14 +291,16 @@ __global__ __launch_bounds__(64 * F32F_WAVES) void f32_flat_kernel(const float* 
 
 // More rows on fp32 MFMA: out^T[16 rows][16 batch] per wave and tile pair, 4
 // waves split k by 64-k chunks; lane (r, g) feeds w[row][64c + 16g + m] and
-// x[b][64c + 16g + m] to instruction m.  A workgroup takes F32M_RTILES
-// 16-row tiles, so each x value a lane loads serves that many rows' products
-// (with one tile, the x reads from L2 were twice the weight reads from HBM:
-// the Llama-2-110M classifier, 32000 x 768 at batch 32, took 37.7 us).
+// x[b][64c + 16g + m] to instruction m.  A workgroup takes RT 16-row tiles,
+// so each x value a lane loads serves that many rows' products: two for two
+// or more batch tiles (with one, the x reads from L2 were twice the weight
+// reads from HBM: the Llama-2-110M classifier, 32000 x 768 at batch 32, 37.7
+// against 31.7 us), one otherwise (the 7B classifier, 32000 x 4096 at batch
+// 8, took 129 us with two, 113 with one: half the workgroups).
 constexpr int F32M_WAVES = 4;
 constexpr int F32M_BTILES = 4;
-constexpr int F32M_RTILES = 2;
 
+template <int F32M_RTILES>
 __global__ __launch_bounds__(64 * F32M_WAVES) void f32_matmul_mfma_kernel(const float* __restrict__ w,
                                                                           const float* __restrict__ x,
                                                                           float* __restrict__ out,
@@ -459,10 +461,13 @@ hipError_t launch_f32_matmul(const float* w, const float* x, float* out, int bat
         }
         return hipGetLastError();
     }
-    const dim3 grid((unsigned)((d + 16 * F32M_RTILES - 1) / (16 * F32M_RTILES)),
-                    (unsigned)((batch + 16 * F32M_BTILES - 1) / (16 * F32M_BTILES)));
-    hipLaunchKernelGGL(f32_matmul_mfma_kernel, grid, dim3(64 * F32M_WAVES), 0, stream, w, x, out, batch,
-                       n, d);
+    const unsigned by = (unsigned)((batch + 16 * F32M_BTILES - 1) / (16 * F32M_BTILES));
+    if (batch > 16)
+        hipLaunchKernelGGL(f32_matmul_mfma_kernel<2>, dim3((unsigned)((d + 31) / 32), by), dim3(64 * F32M_WAVES), 0,
+                           stream, w, x, out, batch, n, d);
+    else
+        hipLaunchKernelGGL(f32_matmul_mfma_kernel<1>, dim3((unsigned)((d + 15) / 16), by), dim3(64 * F32M_WAVES), 0,
+                           stream, w, x, out, batch, n, d);
     return hipGetLastError();
 }
 

@@ -1054,8 +1054,12 @@ __global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Gro
 // one round of weights is always in flight behind the one in use (the x
 // loads go first because a wait covers every older load).  At the end the
 // waves' tiles are added through LDS in a fixed wave order, one thread per
-// (member, batch row, row), and the shared epilogue runs.
-constexpr int MMA_WAVES = 16;
+// (member, batch row, row), and the shared epilogue runs.  8 waves: at the
+// model shapes the rows' blocks are few (24 for k = 768), and 16 waves spent
+// longer in that reduction than they saved in the loop (Llama-2-110M-shaped
+// step at batch 32: 0.598 against 0.607 ms; 7B-shaped at batch 8: 4.36
+// against 4.41 ms; 4 waves: 0.625 and 4.83 ms).
+constexpr int MMA_WAVES = 8;
 constexpr int MMA_TILE_STRIDE = 20;  // floats per batch row of a staged tile (stores hit 64 distinct banks)
 
 
@@ -1069,8 +1073,8 @@ __device__ __forceinline__ bf16x8 q8_bf16(uint32_t w0, uint32_t w1) {
     return __builtin_bit_cast(bf16x8, r);
 }
 
-// Blocks per wave per round: two rounds of weights and x stay within the 128
-// registers of 16 waves per CU.
+// Blocks per wave per round: two rounds of weights and x stay within 128
+// registers (two 8-wave workgroups per CU).
 template <int NMAT, int BT>
 constexpr int mma_unroll() {
     return BT == 1 ? (NMAT == 3 ? 1 : 2) : 1;
