@@ -899,12 +899,45 @@ __global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Gro
                 sl[m][r] = load_slice_raw(grp.w[m] + (size_t)row * rowbytes, bk, lane & 1);
             }
     };
-    Q8Slice sa[NMAT][R], sb[NMAT][R];
-    load_item(sa, i0);  // in flight while x is staged
+    // The prologue's loads go out in the order they are needed: the first
+    // XE float4 of x per thread (and of the norm weights; all of x for one
+    // row of 4096 at 8 waves), the first PE rms partials per lane (all of
+    // them for n <= 4096), then the first item's weights.  Loads complete in
+    // order, so the waits for those x and partials do not wait for the
+    // weights, which stay in flight while x is staged.  (Issued before them,
+    // the weights were waited for with them; holding all of x early takes
+    // too many registers.)  A float4 index past the end is clamped to the
+    // last one, whose value its threads store again.
+    constexpr int XE = XV < 2 ? XV : 2, PE = 4;
+    const int total = NB * n / 4, nv = (total + NT - 1) / NT;  // uniform
+    float4 xr[XV], wr[XV];
+    auto load_x = [&](int v) {
+        const int t = min((int)threadIdx.x + v * NT, total - 1);
+        xr[v] = reinterpret_cast<const float4*>(x)[t];
+        if constexpr (NORM) wr[v] = reinterpret_cast<const float4*>(nm.weight)[t % (n / 4)];
+    };
+#pragma unroll
+    for (int v = 0; v < XE; v++)
+        if (v < nv) load_x(v);
+    // rms partials of batch row b = wave < NB, lane i taking partials i,
+    // i + 64, ... in order (every wave loads, the others a clamped row,
+    // unused)
+    float pv[PE];
     if constexpr (NORM) {
-        // wave b < NB adds row b's partials (lane i takes i, i + 64, ...)
+        const int pb = min(wave, NB - 1);
+#pragma unroll
+        for (int i = 0; i < PE; i++) pv[i] = nm.ss[(size_t)min(lane + i * 64, nm.nparts - 1) * nm.ss_stride + pb];
+    }
+    Q8Slice sa[NMAT][R], sb[NMAT][R];
+    __builtin_amdgcn_sched_barrier(0);  // (left free, the scheduler puts the partials last)
+    load_item(sa, i0);                  // in flight while x is staged
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NORM) {
         if (wave < NB) {
-            float v = partial_sum(nm, wave, lane, 64);
+            float v = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PE; i++) v += lane + i * 64 < nm.nparts ? pv[i] : 0.0f;
+            for (int p = lane + PE * 64; p < nm.nparts; p += 64) v += nm.ss[(size_t)p * nm.ss_stride + wave];
 #pragma unroll
             for (int msk = 32; msk > 0; msk >>= 1) v += __shfl_xor(v, msk);
             if (lane == 0) inv_s[wave] = inv_rms(v, n);
@@ -912,18 +945,10 @@ __global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Gro
         __syncthreads();
     }
     {
-        // x -> LDS: every load of this thread first (only uniform branches
-        // between them), then the stores; a float4 index past the end is
-        // clamped to the last one, whose value its threads store again
-        const int total = NB * n / 4, nv = (total + NT - 1) / NT;  // uniform
-        float4 xr[XV], wr[XV];
+        // the rest of x, then x -> LDS (rms-normalised when NORM)
 #pragma unroll
-        for (int v = 0; v < XV; v++)
-            if (v < nv) {
-                const int t = min((int)threadIdx.x + v * NT, total - 1);
-                xr[v] = reinterpret_cast<const float4*>(x)[t];
-                if constexpr (NORM) wr[v] = reinterpret_cast<const float4*>(nm.weight)[t % (n / 4)];
-            }
+        for (int v = XE; v < XV; v++)
+            if (v < nv) load_x(v);
 #pragma unroll
         for (int v = 0; v < XV; v++)
             if (v < nv) {
