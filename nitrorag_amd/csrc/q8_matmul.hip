@@ -816,8 +816,11 @@ __device__ __forceinline__ Q8Slice load_slice_raw(const uint8_t* wrow, int blk, 
 }
 
 // Batches of 1..NB rows over long rows (n >= 2048) whose activations fit LDS
-// (NB * n <= flat_x_max floats).  x, rms-normalised when NORM, is staged in
-// LDS once per workgroup, so a wave's only loads from memory in its loop are
+// (NB * n <= flat_x_max floats).  x is staged in LDS once per workgroup
+// (times the norm weights when NORM: rms_norm's 1/rms is one scalar per
+// activation row, applied to the row sums in the epilogue, so staging x
+// waits on no reduction; the reference scales x first, the two agree to fp32
+// rounding), so a wave's only loads from memory in its loop are
 // weights: x reads wait on the LDS counter, and the next item's weights stay
 // in flight while the current item is used.  Persistent workgroups own
 // balanced ranges of row units (16 rows with the residual epilogue, whose
@@ -932,20 +935,10 @@ __global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Gro
     __builtin_amdgcn_sched_barrier(0);  // (left free, the scheduler puts the partials last)
     load_item(sa, i0);                  // in flight while x is staged
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (NORM) {
-        if (wave < NB) {
-            float v = 0.0f;
-#pragma unroll
-            for (int i = 0; i < PE; i++) v += lane + i * 64 < nm.nparts ? pv[i] : 0.0f;
-            for (int p = lane + PE * 64; p < nm.nparts; p += 64) v += nm.ss[(size_t)p * nm.ss_stride + wave];
-#pragma unroll
-            for (int msk = 32; msk > 0; msk >>= 1) v += __shfl_xor(v, msk);
-            if (lane == 0) inv_s[wave] = inv_rms(v, n);
-        }
-        __syncthreads();
-    }
     {
-        // the rest of x, then x -> LDS (rms-normalised when NORM)
+        // the rest of x, then x -> LDS (times the norm weights when NORM; the
+        // row's rms factor, a scalar per batch row, scales the row sums in
+        // the epilogue, so staging x waits on no reduction)
 #pragma unroll
         for (int v = XE; v < XV; v++)
             if (v < nv) load_x(v);
@@ -954,11 +947,7 @@ __global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Gro
             if (v < nv) {
                 const int t = min((int)threadIdx.x + v * NT, total - 1);
                 float4 o = xr[v];
-                if constexpr (NORM) {
-                    const float inv = inv_s[t / (n / 4)];
-                    o = make_float4(wr[v].x * (inv * o.x), wr[v].y * (inv * o.y), wr[v].z * (inv * o.z),
-                                    wr[v].w * (inv * o.w));
-                }
+                if constexpr (NORM) o = make_float4(wr[v].x * o.x, wr[v].y * o.y, wr[v].z * o.z, wr[v].w * o.w);
                 reinterpret_cast<float4*>(xs)[t] = o;
             }
     }
@@ -1028,6 +1017,18 @@ __global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Gro
         step(sb, sa, i + 1);
     }
     if (i < i1) step(sa, sb, i);
+    if constexpr (NORM) {
+        // wave b < NB adds batch row b's partials (loaded in the prologue)
+        if (wave < NB) {
+            float v = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PE; i++) v += lane + i * 64 < nm.nparts ? pv[i] : 0.0f;
+            for (int p = lane + PE * 64; p < nm.nparts; p += 64) v += nm.ss[(size_t)p * nm.ss_stride + wave];
+#pragma unroll
+            for (int msk = 32; msk > 0; msk >>= 1) v += __shfl_xor(v, msk);
+            if (lane == 0) inv_s[wave] = inv_rms(v, n);
+        }
+    }
     __syncthreads();
 
     // epilogue: thread (b, local row il), rows in order within each batch row
@@ -1041,7 +1042,7 @@ __global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Gro
             float v = 0.0f;
 #pragma unroll
             for (int w = 0; w < W; w++) v += red[((il * NMAT + m) * NB + b) * W + w];
-            sum[m] = v;
+            sum[m] = NORM ? v * inv_s[b] : v;
         }
         if constexpr (ROPE) {
             // RoPE pairs are local rows (il, il ^ 1)
@@ -1050,7 +1051,7 @@ __global__ __launch_bounds__(64 * flat_waves<RESID>()) void q8_flat_kernel(Q8Gro
                 float v = 0.0f;
 #pragma unroll
                 for (int w = 0; w < W; w++) v += red[(((il ^ 1) * NMAT + m) * NB + b) * W + w];
-                pair[m] = v;
+                pair[m] = NORM ? v * inv_s[b] : v;
             }
         }
         store_row_sums<NMAT, SWIGLU, RESID, ROPE>(grp, resid, rope, b, row0 + il, sum, pair);
