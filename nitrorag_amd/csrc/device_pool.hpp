@@ -322,6 +322,13 @@ hipError_t launch_gather_last_rows(const float* x, const float* ffn, const int32
 hipError_t launch_swiglu(float* hb, const float* hb2, size_t n, hipStream_t stream);
 hipError_t launch_f32_matmul(const float* w, const float* x, float* out, int batch, int n, int d,
                              hipStream_t stream);
+// The classifier over rms_norm(x) with the norm folded in (nm as for the Q8
+// products: weights, and the partial sums of squares the last residual
+// product left): launched only where the flat kernel takes the batch
+// (batch <= 4, batch * n <= 16384, n % 64 == 0); false (nothing launched)
+// otherwise, and the caller normalises x and calls launch_f32_matmul.
+bool launch_f32_matmul_norm(const float* w, const float* x, const Q8Norm& nm, float* out, int batch, int n, int d,
+                            hipStream_t stream);
 hipError_t launch_rope_kv_append(float* k_pool, float* v_pool, float* q, float* k, const float* v,
                                  const float* freq_real, const float* freq_imag,
                                  const int32_t* tables, const int32_t* positions,

@@ -107,6 +107,22 @@ void upload_tokens(nitro_model* m, const int32_t* tokens, int rows, hipStream_t 
     m->staging.finish(s);
 }
 
+// logits = wcls . rms_norm(x) for `rows` rows of the residual stream x, which
+// are rows first .. first + rows - 1 of the `total` rows the last residual
+// product left partial sums of squares for (src/model_q8.cpp:553-555,
+// :687-692).  The norm rides in the classifier launch where its flat kernel
+// takes the batch (x stays unnormalised); otherwise x is normalised in place
+// first.
+void final_logits(nitro_model* m, float* x, int first, int total, int rows, float* logits, hipStream_t s) {
+    const Q8Norm nm{m->f32(m->o_rms_final), m->ss.ptr + first, (m->dim + 15) / 16, total};
+    if (launch_f32_matmul_norm(m->f32(m->o_emb), x, nm, logits, rows, m->dim, m->vocab, s)) {
+        hip_check(hipGetLastError(), "classifier launch");
+        return;
+    }
+    hip_check(launch_add_rmsnorm(x, nullptr, m->f32(m->o_rms_final), x, rows, m->dim, s), "rmsnorm launch");
+    hip_check(launch_f32_matmul(m->f32(m->o_emb), x, logits, rows, m->dim, m->vocab, s), "classifier launch");
+}
+
 // The layer loop shared by the decode, prefill and mixed forwards.  x is the
 // residual stream; rms_norm is folded into the products that read it (wq/wk/wv
 // and w1/w3 take rms_norm(x, rms_att / rms_ffn) as input), and wo and w2 add
@@ -256,9 +272,7 @@ void forward_mixed(nitro_model* m, nitro_kvpool* pool, const int32_t* tokens, in
     const int out_rows = P + B - first;
     if (out_rows == 0) return;
     float* x = m->x.ptr + first * dim;
-    hip_check(launch_add_rmsnorm(x, nullptr, m->f32(m->o_rms_final), x, out_rows, m->dim, s), "rmsnorm launch");
-    hip_check(launch_f32_matmul(m->f32(m->o_emb), x, logits, out_rows, m->dim, m->vocab, s),
-              "classifier launch");
+    final_logits(m, x, first, P + B, out_rows, logits, s);
     hip_check(launch_argmax_rows(logits, next, out_rows, m->vocab, s), "argmax launch");
     pool->last_stream = s;
 }
@@ -375,11 +389,8 @@ int nitro_forward_decode_batch(nitro_model* m, nitro_kvpool* pool, const int32_t
                                             m->head_size, stream) == NITRO_OK,
                     ERR_INVALID_ARGUMENT, nitro_last_error());
         });
-        // x = rms_norm(x) in place; logits = wcls . x (:687-692)
-        hip_check(launch_add_rmsnorm(m->x.ptr, nullptr, m->f32(m->o_rms_final), m->x.ptr, batch, m->dim, s),
-                  "rmsnorm launch");
-        hip_check(launch_f32_matmul(m->f32(m->o_emb), m->x.ptr, logits, batch, m->dim, m->vocab, s),
-                  "classifier launch");
+        // logits = wcls . rms_norm(x) (:687-692)
+        final_logits(m, m->x.ptr, 0, batch, batch, logits, s);
         pool->last_stream = s;
     });
 }

@@ -188,20 +188,29 @@ __global__ __launch_bounds__(64 * F32_WAVES) void f32_gemv_kernel(const float* _
 // in its loop are weights and the next item's stay in flight while the
 // current one is used.  Persistent workgroups own balanced ranges of 2-row
 // groups; items are (group, 1024-k chunk), split between the 8 waves in
-// contiguous runs.  Lane l takes k = 1024*chunk + 16*l .. +15 of both rows
-// (64 contiguous bytes; a wave reads 4 KB of a row per chunk).  At a group's
-// last chunk (or the end of the wave's run) each row's 64 lanes are summed
-// with a fixed butterfly into the wave's LDS slot; the slots are added in
-// wave order.
+// contiguous runs.  Lane l takes float4 l, l + 64, l + 128, l + 192 of the
+// chunk in both rows, so each load instruction reads 1 KB of a row
+// contiguously.  At a group's last chunk (or the end of the wave's run) each
+// row's 64 lanes are summed with a fixed butterfly into the wave's LDS slot;
+// the slots are added in wave order.
+// NORM (the final rms_norm folded in, nm as for the Q8 products): x is staged
+// times the norm weights and each row sum is scaled by the row's 1/rms,
+// summed from the partial sums of squares the last residual product left
+// (src/model_q8.cpp:687-692 normalises x first; the two agree to fp32
+// rounding).  The prologue's loads go out x first, then the partials, then
+// the first item's weights, so the waits for x and the partials leave the
+// weights in flight.
 constexpr int F32F_WAVES = 8;
 constexpr int F32F_X_MAX = 16384;
 
-template <int NB>
+template <int NB, bool NORM>
 __global__ __launch_bounds__(64 * F32F_WAVES) void f32_flat_kernel(const float* __restrict__ w,
                                                                    const float* __restrict__ x,
-                                                                   float* __restrict__ out, int n, int d) {
-    constexpr int W = F32F_WAVES, NT = 64 * W, R = 2;
-    extern __shared__ __attribute__((aligned(16))) float f32f_lds[];  // [NB][n] x, then [rows][NB][W] sums
+                                                                   float* __restrict__ out, int n, int d,
+                                                                   Q8Norm nm) {
+    constexpr int W = F32F_WAVES, NT = 64 * W, R = 2, PE = 4;
+    // [NB][n] x, then [rows][NB][W] sums, then [NB] 1/rms
+    extern __shared__ __attribute__((aligned(16))) float f32f_lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nch = (n + 1023) / 1024;
     const int groups = (d + R - 1) / R;
@@ -209,25 +218,53 @@ __global__ __launch_bounds__(64 * F32F_WAVES) void f32_flat_kernel(const float* 
     const int g1 = (int)((long long)groups * (blockIdx.x + 1) / gridDim.x);
     const int items = (g1 - g0) * nch;
     const int i0 = items * wave / W, i1 = items * (wave + 1) / W;
+    const int rows = (g1 - g0) * R;
     float* xs = f32f_lds;
     float* red = f32f_lds + NB * n;
+    float* inv_s = red + rows * NB * W;
     auto load_item = [&](float4 (&v)[R][4], int i) {
         i = max(min(i, i1 - 1), 0);  // clamped into the run: a wave with no items loads in range, never used
         const int g = g0 + i / nch, c = i % nch;
-        const int k = min(1024 * c + 16 * lane, n - 16);  // a lane past the row rereads the last 16 (x zeroed)
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const float4* p = reinterpret_cast<const float4*>(w + (size_t)min(g * R + r, d - 1) * n + k);
+            const float* rowp = w + (size_t)min(g * R + r, d - 1) * n;
 #pragma unroll
-            for (int q = 0; q < 4; q++) v[r][q] = p[q];
+            for (int q = 0; q < 4; q++)  // past the row: the last float4 again (its x are zeroed)
+                v[r][q] = *reinterpret_cast<const float4*>(rowp + min(1024 * c + 4 * lane + 256 * q, n - 4));
         }
     };
+    // x (and the norm weights): NB * n / 4 float4, at most 2 per thread for a
+    // 4096-wide row at NB <= 2 (XV per thread in all)
+    constexpr int XV = (F32F_X_MAX / 4 + NT - 1) / NT;
+    const int total = NB * n / 4;
+    float4 xr[XV], wr[XV];
+#pragma unroll
+    for (int v = 0; v < XV; v++) {
+        const int t = min((int)threadIdx.x + v * NT, total - 1);
+        if ((int)threadIdx.x + v * NT < total) {
+            xr[v] = reinterpret_cast<const float4*>(x)[t];
+            if constexpr (NORM) wr[v] = reinterpret_cast<const float4*>(nm.weight)[t % (n / 4)];
+        }
+    }
+    float pv[PE];
+    if constexpr (NORM) {
+        const int pb = min(wave, NB - 1);
+#pragma unroll
+        for (int k = 0; k < PE; k++) pv[k] = nm.ss[(size_t)min(lane + k * 64, nm.nparts - 1) * nm.ss_stride + pb];
+    }
     float4 va[R][4], vb[R][4];
+    __builtin_amdgcn_sched_barrier(0);  // (left free, the scheduler issues the weights first)
     load_item(va, i0);
-    // x -> LDS (NB * n / 4 float4, at most 2 per thread for a 4096-wide row)
-    for (int t = threadIdx.x; t < NB * n / 4; t += NT)
-        reinterpret_cast<float4*>(xs)[t] = reinterpret_cast<const float4*>(x)[t];
-    const int rows = (g1 - g0) * R;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int v = 0; v < XV; v++) {
+        const int t = (int)threadIdx.x + v * NT;
+        if (t < total) {
+            float4 o = xr[v];
+            if constexpr (NORM) o = make_float4(wr[v].x * o.x, wr[v].y * o.y, wr[v].z * o.z, wr[v].w * o.w);
+            reinterpret_cast<float4*>(xs)[t] = o;
+        }
+    }
     for (int t = threadIdx.x; t < rows * NB * W; t += NT) red[t] = 0.0f;
     __syncthreads();
     float acc[R][NB];
@@ -238,16 +275,14 @@ __global__ __launch_bounds__(64 * F32F_WAVES) void f32_flat_kernel(const float* 
     auto step = [&](const float4 (&now)[R][4], float4 (&next)[R][4], int i) {
         load_item(next, i + 1);
         const int gl = i / nch, c = i % nch;
-        const int k = 1024 * c + 16 * lane;
-        const bool valid = k < n;
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            const float4* xp = reinterpret_cast<const float4*>(xs + b * n + (valid ? k : 0));
             float4 xv[4];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                const float4 t = xp[q];
-                xv[q] = valid ? t : make_float4(0.f, 0.f, 0.f, 0.f);
+                const int k = 1024 * c + 4 * lane + 256 * q;
+                const float4 t = *reinterpret_cast<const float4*>(xs + b * n + (k < n ? k : 0));
+                xv[q] = k < n ? t : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
             for (int r = 0; r < R; r++)
@@ -278,6 +313,18 @@ __global__ __launch_bounds__(64 * F32F_WAVES) void f32_flat_kernel(const float* 
         step(vb, va, i + 1);
     }
     if (i < i1) step(va, vb, i);
+    if constexpr (NORM) {
+        // wave b < NB adds batch row b's partials in order (as the Q8 products do)
+        if (wave < NB) {
+            float v = 0.0f;
+#pragma unroll
+            for (int k = 0; k < PE; k++) v += lane + k * 64 < nm.nparts ? pv[k] : 0.0f;
+            for (int p = lane + PE * 64; p < nm.nparts; p += 64) v += nm.ss[(size_t)p * nm.ss_stride + wave];
+#pragma unroll
+            for (int msk = 32; msk > 0; msk >>= 1) v += __shfl_xor(v, msk);
+            if (lane == 0) inv_s[wave] = 1.0f / sqrtf(v / (float)n + 1e-5f);
+        }
+    }
     __syncthreads();
     for (int t = threadIdx.x; t < NB * rows; t += NT) {
         const int b = t / rows, il = t - b * rows;
@@ -285,7 +332,7 @@ __global__ __launch_bounds__(64 * F32F_WAVES) void f32_flat_kernel(const float* 
         float v = 0.0f;
 #pragma unroll
         for (int ww = 0; ww < W; ww++) v += red[(il * NB + b) * W + ww];
-        if (row < d) out[(size_t)b * d + row] = v;
+        if (row < d) out[(size_t)b * d + row] = NORM ? v * inv_s[b] : v;
     }
 }
 
@@ -430,18 +477,20 @@ int f32_device_cus() {
 
 // f32_flat_kernel, one round of workgroups (2 per CU at up to 2 activation
 // rows, whose registers allow it, else 1), if x and the sums fit 64 KiB of LDS.
-bool launch_f32_flat(const float* w, const float* x, float* out, int batch, int n, int d, hipStream_t stream) {
+template <bool NORM>
+bool launch_f32_flat(const float* w, const float* x, float* out, int batch, int n, int d, const Q8Norm& nm,
+                     hipStream_t stream) {
     const int groups_total = (d + 1) / 2;
     const int wgs = std::min(groups_total, (batch <= 2 ? 2 : 1) * f32_device_cus());
     const size_t rows_max = (size_t)((groups_total + wgs - 1) / wgs) * 2;
-    const size_t lds = ((size_t)batch * n + rows_max * batch * F32F_WAVES) * sizeof(float);
+    const size_t lds = ((size_t)batch * n + rows_max * batch * F32F_WAVES + batch) * sizeof(float);
     if (lds > 64 * 1024) return false;  // the default dynamic LDS limit
     const dim3 grid((unsigned)wgs), block(64 * F32F_WAVES);
     switch (batch) {
-        case 1: hipLaunchKernelGGL(f32_flat_kernel<1>, grid, block, lds, stream, w, x, out, n, d); break;
-        case 2: hipLaunchKernelGGL(f32_flat_kernel<2>, grid, block, lds, stream, w, x, out, n, d); break;
-        case 3: hipLaunchKernelGGL(f32_flat_kernel<3>, grid, block, lds, stream, w, x, out, n, d); break;
-        default: hipLaunchKernelGGL(f32_flat_kernel<4>, grid, block, lds, stream, w, x, out, n, d); break;
+        case 1: hipLaunchKernelGGL((f32_flat_kernel<1, NORM>), grid, block, lds, stream, w, x, out, n, d, nm); break;
+        case 2: hipLaunchKernelGGL((f32_flat_kernel<2, NORM>), grid, block, lds, stream, w, x, out, n, d, nm); break;
+        case 3: hipLaunchKernelGGL((f32_flat_kernel<3, NORM>), grid, block, lds, stream, w, x, out, n, d, nm); break;
+        default: hipLaunchKernelGGL((f32_flat_kernel<4, NORM>), grid, block, lds, stream, w, x, out, n, d, nm); break;
     }
     return true;
 }
@@ -450,7 +499,8 @@ bool launch_f32_flat(const float* w, const float* x, float* out, int batch, int 
 hipError_t launch_f32_matmul(const float* w, const float* x, float* out, int batch, int n, int d,
                              hipStream_t stream) {
     if (n % 64 != 0) return hipErrorInvalidValue;
-    if (batch <= 4 && batch * n <= F32F_X_MAX && launch_f32_flat(w, x, out, batch, n, d, stream)) return hipGetLastError();
+    if (batch <= 4 && batch * n <= F32F_X_MAX && launch_f32_flat<false>(w, x, out, batch, n, d, Q8Norm{}, stream))
+        return hipGetLastError();
     if (batch <= 4) {
         const dim3 grid((unsigned)((d + 15) / 16)), block(64 * F32_WAVES);
         switch (batch) {
@@ -469,6 +519,12 @@ hipError_t launch_f32_matmul(const float* w, const float* x, float* out, int bat
         hipLaunchKernelGGL(f32_matmul_mfma_kernel<1>, dim3((unsigned)((d + 15) / 16), by), dim3(64 * F32M_WAVES), 0,
                            stream, w, x, out, batch, n, d);
     return hipGetLastError();
+}
+
+bool launch_f32_matmul_norm(const float* w, const float* x, const Q8Norm& nm, float* out, int batch, int n, int d,
+                            hipStream_t stream) {
+    if (n % 64 != 0 || batch > 4 || batch * n > F32F_X_MAX) return false;
+    return launch_f32_flat<true>(w, x, out, batch, n, d, nm, stream);
 }
 
 }  // namespace nitro
