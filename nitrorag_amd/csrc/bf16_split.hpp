@@ -54,4 +54,21 @@ __device__ __forceinline__ void split3(const float (&v)[8], bf16x8& hi, bf16x8& 
     lo = __builtin_bit_cast(bf16x8, l);
 }
 
+// Eight values as two bf16x8 operands, hi and mid (each a truncation): v
+// minus hi + mid is below 2^-16 |v| (16 significant bits kept).  For factors
+// whose products need only that (the attention weights, each added into a
+// sum of thousands of terms: a relative error of 2^-16 per weight moves the
+// output by about 1e-5 of its size).
+__device__ __forceinline__ void split2(const float (&v)[8], bf16x8& hi, bf16x8& mid) {
+    u32x4 h, m;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const float a = v[2 * p], b = v[2 * p + 1];
+        h[p] = bf16_pair(a, b);
+        m[p] = bf16_pair(a - upper16(a), b - upper16(b));
+    }
+    hi = __builtin_bit_cast(bf16x8, h);
+    mid = __builtin_bit_cast(bf16x8, m);
+}
+
 }  // namespace nitro

@@ -576,11 +576,16 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_mfma_kern
 
 // paged_attn_prefill_x3_kernel<hd, KSPLIT, BNM>: the MFMA kernel's work
 // split and softmax with both products on the bf16 matrix cores at fp32
-// accuracy.  Q, K, V and the probabilities P are each split into three bf16
-// parts (hi, mid, lo; exact, 24 significant bits in all), and each product
-// takes the six part products whose order is at most 2 (hi.hi, hi.mid,
-// mid.hi, hi.lo, mid.mid, lo.hi; the dropped ones are below 2^-24 of the
-// total), smallest first, accumulated in fp32 by v_mfma_f32_16x16x32_bf16:
+// accuracy.  Q, K and V are each split into three bf16 parts (hi, mid, lo;
+// exact, 24 significant bits in all), and S = K Q^T takes the six part
+// products whose order is at most 2 (hi.hi, hi.mid, mid.hi, hi.lo, mid.mid,
+// lo.hi; the dropped ones are below 2^-24 of the total).  The probabilities P
+// are split into two (hi, mid: 16 significant bits, the rest below 2^-16 of
+// each weight), and O takes the five products V.P of order at most 2 (V's
+// lo.hi, mid.mid, mid.hi, hi.mid, hi.hi): a weight's relative error of at
+// most 2^-16, added into thousands of terms, moves the output by about 1e-5
+// of its size.  All accumulate in fp32 by v_mfma_f32_16x16x32_bf16, smallest
+// first:
 //  - S^T = K Q^T per 16-key block and 32 d: lane l supplies K[key l%16] and
 //    Q[query l%16] at d = 32c + 8*(l/16) .. +8, so the accumulator leaves lane
 //    l holding S[query l%16][keys 4g..4g+3] (g = l/16) as before;
@@ -1070,8 +1075,8 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
                 if (2 * jj < nvb) {  // wave-uniform
                     const float pv[8] = {p[2 * jj][0],     p[2 * jj][1],     p[2 * jj][2],     p[2 * jj][3],
                                          p[2 * jj + 1][0], p[2 * jj + 1][1], p[2 * jj + 1][2], p[2 * jj + 1][3]};
-                    bf16x8 ph, pm, pl;
-                    split3(pv, ph, pm, pl);
+                    bf16x8 ph, pm;
+                    split2(pv, ph, pm);
                     const int key_a = (kg + 2 * jj * KSPLIT) * 16 + 4 * g;        // within the tile
                     const int key_b = (kg + (2 * jj + 1) * KSPLIT) * 16 + 4 * g;
 #pragma unroll
@@ -1089,7 +1094,6 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
                         f32x4 o = acc[n];
                         o = mfma(vp[2], ph, o);
                         o = mfma(vp[1], pm, o);
-                        o = mfma(vp[0], pl, o);
                         o = mfma(vp[1], ph, o);
                         o = mfma(vp[0], pm, o);
                         o = mfma(vp[0], ph, o);
