@@ -576,16 +576,16 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_mfma_kern
 
 // paged_attn_prefill_x3_kernel<hd, KSPLIT, BNM>: the MFMA kernel's work
 // split and softmax with both products on the bf16 matrix cores at fp32
-// accuracy.  Q, K and V are each split into three bf16 parts (hi, mid, lo;
+// accuracy.  Q and K are each split into three bf16 parts (hi, mid, lo;
 // exact, 24 significant bits in all), and S = K Q^T takes the six part
 // products whose order is at most 2 (hi.hi, hi.mid, mid.hi, hi.lo, mid.mid,
-// lo.hi; the dropped ones are below 2^-24 of the total).  The probabilities P
-// are split into two (hi, mid: 16 significant bits, the rest below 2^-16 of
-// each weight), and O takes the five products V.P of order at most 2 (V's
-// lo.hi, mid.mid, mid.hi, hi.mid, hi.hi): a weight's relative error of at
-// most 2^-16, added into thousands of terms, moves the output by about 1e-5
-// of its size.  All accumulate in fp32 by v_mfma_f32_16x16x32_bf16, smallest
-// first:
+// lo.hi; the dropped ones are below 2^-24 of the total): an error in S moves
+// every weight exponentially, so S keeps fp32 accuracy.  V and the
+// probabilities P are split into two (hi, mid: 16 significant bits, the rest
+// below 2^-16 of each value), and O takes the four products V.P (mid.mid,
+// mid.hi, hi.mid, hi.hi): O is a weighted average of V, so relative errors
+// of at most 2^-16 in V and P move it by at most about 3e-5 of the values'
+// size.  All accumulate in fp32 by v_mfma_f32_16x16x32_bf16, smallest first:
 //  - S^T = K Q^T per 16-key block and 32 d: lane l supplies K[key l%16] and
 //    Q[query l%16] at d = 32c + 8*(l/16) .. +8, so the accumulator leaves lane
 //    l holding S[query l%16][keys 4g..4g+3] (g = l/16) as before;
@@ -596,8 +596,8 @@ __global__ __launch_bounds__(64 * QT * KSPLIT) void paged_attn_prefill_mfma_kern
 // A workgroup serves one work item of 16*QT query rows (QT = 8: 128 rows,
 // the wide work list, so each staged tile serves twice the queries) with QT
 // query sub-tiles x KSPLIT key groups of waves.
-// K and V are split once, when a tile is staged: three bf16 planes each in
-// LDS, K as [key][d] and V as [d][key].  K is loaded a float4 of one key row
+// K and V are split once, when a tile is staged: three bf16 planes of K and
+// two of V in LDS, K as [key][d] and V as [d][key].  K is loaded a float4 of one key row
 // per thread; V one d of four consecutive keys per thread (a wave's lanes
 // cover consecutive d of a row, so the loads coalesce), which becomes one
 // 8-byte store per plane into the transposed tile.
@@ -633,8 +633,9 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
     constexpr int VSLOTS = BNM * HD / (4 * NT);  // V (d, 4-key group) slots per thread per tile
     static_assert(LOADS >= 1 && BNM * F4 % NT == 0 && VSLOTS >= 1 && BNM * HD % (4 * NT) == 0, "tile shape");
     constexpr int KPLANE = BNM * KST, VPLANE = HD * VST;
-    static_assert((KSPLIT - 1) * QT * 16 * HD * 4 <= 3 * (KPLANE + VPLANE) * 2, "partials fit the tile planes");
-    __shared__ __attribute__((aligned(16))) uint16_t kv_lds[3 * (KPLANE + VPLANE)];
+    static_assert((KSPLIT - 1) * QT * 16 * HD * 4 <= (3 * KPLANE + 2 * VPLANE) * 2, "partials fit the tile planes");
+    // K in three bf16 planes, V^T in two
+    __shared__ __attribute__((aligned(16))) uint16_t kv_lds[3 * KPLANE + 2 * VPLANE];
     uint16_t* const k_lds = kv_lds;
     uint16_t* const v_lds = kv_lds + 3 * KPLANE;
     __shared__ int32_t s_table[TABLE_LDS];
@@ -906,6 +907,13 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
         // 50.3 vs 51.6-52.5 us by trace; priority 3, or priority 1 also around
         // the matrix-core blocks, were no better).
         __builtin_amdgcn_s_setprio(1);
+        // four values as two bf16 planes (hi, mid), one 8-byte store each
+        auto stage4v = [](uint16_t* dst, int plane, const float (&v)[4]) {
+            const float r0 = v[0] - upper16(v[0]), r1 = v[1] - upper16(v[1]);
+            const float r2 = v[2] - upper16(v[2]), r3 = v[3] - upper16(v[3]);
+            *reinterpret_cast<uint2*>(dst) = make_uint2(bf16_pair(v[0], v[1]), bf16_pair(v[2], v[3]));
+            *reinterpret_cast<uint2*>(dst + plane) = make_uint2(bf16_pair(r0, r1), bf16_pair(r2, r3));
+        };
         // four values as three bf16 planes, one 8-byte store each
         auto stage4 = [](uint16_t* dst, int plane, const float (&v)[4]) {
             const float r0 = v[0] - upper16(v[0]), r1 = v[1] - upper16(v[1]);
@@ -934,7 +942,7 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
                 float v4[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) v4[e] = !masked || ((vmask >> (4 * i + e)) & 1) ? vreg[i][e] : 0.f;
-                stage4(&v_lds[(sl % HD) * VST + 4 * (sl / HD)], VPLANE, v4);
+                stage4v(&v_lds[(sl % HD) * VST + 4 * (sl / HD)], VPLANE, v4);
             }
         };
         if constexpr (APPEND == 1) {
@@ -1082,9 +1090,9 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
 #pragma unroll
                     for (int n = 0; n < NB; n++) {
                         const uint16_t* vr = &v_lds[(16 * n + ql) * VST];
-                        bf16x8 vp[3];
+                        bf16x8 vp[2];
 #pragma unroll
-                        for (int q = 0; q < 3; q++) {
+                        for (int q = 0; q < 2; q++) {
                             const uint2 x0 = *reinterpret_cast<const uint2*>(vr + q * VPLANE + key_a);
                             const uint2 x1 = *reinterpret_cast<const uint2*>(vr + q * VPLANE + key_b);
                             u32x4 t;
@@ -1092,7 +1100,6 @@ __global__ __launch_bounds__(64 * QT * KSPLIT, HD <= 64 ? 4 : 1) void paged_attn
                             vp[q] = __builtin_bit_cast(bf16x8, t);
                         }
                         f32x4 o = acc[n];
-                        o = mfma(vp[2], ph, o);
                         o = mfma(vp[1], pm, o);
                         o = mfma(vp[1], ph, o);
                         o = mfma(vp[0], pm, o);
