@@ -23,6 +23,16 @@ inline void hip_check(hipError_t e, const char* what) {
     }
 }
 
+// Capacity for a buffer that must hold n elements and holds `have`: at least
+// twice what it had (and 1024 elements), so a buffer sized per step (batch
+// rows, table pages, upload words) is reallocated a few times over a serving
+// run rather than whenever it grows.  A reallocation frees the old block, and
+// hipFree / hipHostFree wait for the device.
+inline size_t grown_capacity(size_t n, size_t have) {
+    const size_t twice = 2 * have > 1024 ? 2 * have : 1024;
+    return n > twice ? n : twice;
+}
+
 // A device allocation that only grows (hipMalloc outside any capture).
 template <class T>
 struct DeviceBuffer {
@@ -38,12 +48,14 @@ struct DeviceBuffer {
         count = 0;
     }
     // Ensures room for n elements; returns true when (re)allocated (contents
-    // of a fresh allocation are undefined).
+    // of a fresh allocation are undefined).  count is the capacity, which may
+    // exceed n (grown_capacity).
     bool reserve(size_t n) {
         if (n <= count && ptr) return false;
+        const size_t cap = grown_capacity(n, count);
         reset();
-        hip_check(hipMalloc((void**)&ptr, (n ? n : 1) * sizeof(T)), "hipMalloc");
-        count = n;
+        hip_check(hipMalloc((void**)&ptr, cap * sizeof(T)), "hipMalloc");
+        count = cap;
         return true;
     }
 };
@@ -70,11 +82,12 @@ struct Staging {
             pending = false;
         }
         if (n > count || !host) {
+            const size_t cap = grown_capacity(n, count);
             if (host) hip_check(hipHostFree(host), "hipHostFree");
             host = nullptr;
             count = 0;
-            hip_check(hipHostMalloc((void**)&host, (n ? n : 1) * sizeof(int32_t)), "hipHostMalloc");
-            count = n;
+            hip_check(hipHostMalloc((void**)&host, cap * sizeof(int32_t)), "hipHostMalloc");
+            count = cap;
         }
         return host;
     }

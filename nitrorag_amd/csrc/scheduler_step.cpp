@@ -279,11 +279,12 @@ int nitro_sched_step(nitro_scheduler* sched, nitro_model* model, nitro_kvpool* p
                           semantics, s);
         }
         if ((size_t)out_rows > d.readback_count) {
+            const size_t cap = grown_capacity(out_rows, d.readback_count);
             if (d.readback) hip_check(hipHostFree(d.readback), "hipHostFree");
             d.readback = nullptr;
             d.readback_count = 0;
-            hip_check(hipHostMalloc((void**)&d.readback, sizeof(int32_t) * out_rows), "hipHostMalloc");
-            d.readback_count = out_rows;
+            hip_check(hipHostMalloc((void**)&d.readback, sizeof(int32_t) * cap), "hipHostMalloc");
+            d.readback_count = cap;
         }
         if (out_rows > 0)
             hip_check(hipMemcpyAsync(d.readback, d.next.ptr, sizeof(int32_t) * out_rows, hipMemcpyDeviceToHost, s),
