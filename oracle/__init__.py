@@ -3,8 +3,8 @@
 Restates the reference's algorithm (nvivek17/NitroRAG src/model_q8.cpp
 attention loops, src/pagedMemory.hpp page bookkeeping) so the HIP path can be
 checked against it.  Only tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg may import this package, and only as the checker or as the
-timed CPU baseline; the shipped library (nitrorag_amd) never does.
+cpu_baseline leg may import this package, and only to check results against
+or as the timed CPU baseline; the shipped library (nitrorag_amd) never does.
 
 Modules:
   attn          ctypes wrappers over the C restatement (attn_oracle.c)

@@ -4,8 +4,8 @@
  * A plain-C restatement of the reference's attention loops, kept loop-for-loop
  * with src/model_q8.cpp so that it can stand in for the reference where the
  * reference cannot be called as a unit.  Only tests/, __graft_entry__.smoke()
- * and bench.py's cpu_baseline leg may link or call it, and only as the checker
- * (or as the timed CPU baseline); the shipped library never does.
+ * and bench.py's cpu_baseline leg may link or call it, and only to check results
+ * against (or as the timed CPU baseline); the shipped library never does.
  *
  * KV pool layout (src/pagedMemory.hpp:86-106, src/model_q8.cpp:284-287,620-623,639):
  *   pool[page][layer][tok 0..15][kv_dim], kv_dim = n_kv_heads * head_dim, fp32.
