@@ -197,6 +197,9 @@ def test_full_row_products_over_many_rows(name):
     # w2 over rows of 18944 k (a Qwen2-7B FFN width): 2 rows = 37888 floats of x, the
     # top of the residual flat kernel's budget, where every thread stages 10 float4
     ("ffn18944", (512, 18944, 1, 8, 8, 300, 64)),
+    # a classifier larger than the 256 MB Infinity Cache (66000 x 1024 fp32, 270 MB),
+    # whose weights the classifier launch reads with non-temporal loads
+    ("vocab66000", (1024, 1024, 1, 8, 8, 66000, 64)),
     # w2 over rows of 11008 k (Llama-2-7B): 3 rows = 33024 floats on the flat kernel
     ("ffn11008", (512, 11008, 1, 8, 8, 300, 64)),
 ])
