@@ -181,6 +181,74 @@ struct Q8Group {
 
 namespace {
 
+// The epilogue of one 16 x 16 output tile held as fp32 MFMA accumulators: lane
+// l holds out^T[row0 + 4*(l/16) + j][bb] (j = 0..3) of each group member, bb
+// = the tile's batch row l%16.  ROPE rotates q and k and appends k, v to the
+// pools; RESID adds into x and writes the tile's sums of squares per batch
+// row (partial `tile` of row bb; every lane must take part); SWIGLU or plain
+// stores otherwise.
+template <int NMAT, bool SWIGLU, bool RESID, bool ROPE>
+__device__ __forceinline__ void store_mma_tile(const Q8Group& grp, const Q8Resid& resid, const Q8Rope& rope,
+                                               const f32x4 (&s)[NMAT], int row0, int tile, int bb, int batch,
+                                               int lane) {
+    if constexpr (ROPE) {
+        // q, k, v for features f0..f0+3 of row bb: two RoPE pairs
+        if (bb >= batch) return;
+        const RopeRow rr = rope_row(rope, bb);
+        const int f0 = row0 + 4 * (lane >> 4);
+        if (f0 < grp.d[0]) {
+            const float2 a = rotate_pair(rope, rr.pos, f0, s[0][0], s[0][1]);
+            const float2 c = rotate_pair(rope, rr.pos, f0 + 2, s[0][2], s[0][3]);
+            *reinterpret_cast<float4*>(grp.out[0] + (size_t)bb * grp.d[0] + f0) = make_float4(a.x, a.y, c.x, c.y);
+        }
+        if (f0 < grp.d[1]) {
+            if (rr.page_ok) {
+                const size_t o = (size_t)rr.page * rope.page_stride + rope.layer_off +
+                                 (size_t)rr.in_page * grp.d[1] + f0;
+                const float2 a = rotate_pair(rope, rr.pos, f0, s[1][0], s[1][1]);
+                const float2 c = rotate_pair(rope, rr.pos, f0 + 2, s[1][2], s[1][3]);
+                *reinterpret_cast<float4*>(rope.k_pool + o) = make_float4(a.x, a.y, c.x, c.y);
+                *reinterpret_cast<float4*>(rope.v_pool + o) = make_float4(s[2][0], s[2][1], s[2][2], s[2][3]);
+            } else if (f0 == 0) {
+                atomicAdd(rope.bad_pages, 1);  // once per row: the lane holding feature 0
+            }
+        }
+    } else if constexpr (RESID) {
+        // x[bb][row] += product; the squares of the tile's 16 new entries
+        // of row bb are summed over the four lane groups (rows 4*(l/16) + j)
+        float ssq = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int row = row0 + 4 * (lane >> 4) + j;
+            if (bb < batch && row < grp.d[0]) {
+                float* xe = grp.out[0] + (size_t)bb * grp.d[0] + row;
+                const float v = *xe + s[0][j];
+                *xe = v;
+                ssq = fmaf(v, v, ssq);
+            }
+        }
+        ssq = sum_over_rows(ssq);
+        if (lane < 16 && bb < batch) resid.ss[(size_t)tile * resid.ss_stride + bb] = ssq;
+    } else {
+        if (bb >= batch) return;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int row = row0 + 4 * (lane >> 4) + j;
+            if constexpr (SWIGLU) {
+                if (row < grp.d[0]) {
+                    float h = s[0][j];
+                    h *= 1.0f / (1.0f + expf(-h));
+                    grp.out[0][(size_t)bb * grp.d[0] + row] = h * s[1][j];
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < NMAT; m++)
+                    if (row < grp.d[m]) grp.out[m][(size_t)bb * grp.d[m] + row] = s[m][j];
+            }
+        }
+    }
+}
+
 // fp32 matrix cores (v_mfma_f32_16x16x4_f32): a workgroup owns 16 output
 // rows; out^T[16 rows][16 batch] += W[16 rows][4 k] . x^T[4 k][16 batch] per
 // instruction.  Per 64-k chunk (two blocks), lane l = (r = l%16, g = l/16)
@@ -327,66 +395,69 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
 #pragma unroll
             for (int v = 0; v < Q8_WAVES - 1; v++) s[m] += red[v][m][t][lane];
         }
-        const int bb = b0 + t * 16 + (lane & 15);
-        if constexpr (ROPE) {
-            // q, k, v for features f0..f0+3 of row bb: two RoPE pairs
-            if (bb >= batch) continue;
-            const RopeRow rr = rope_row(rope, bb);
-            const int f0 = row0 + 4 * (lane >> 4);
-            if (f0 < grp.d[0]) {
-                const float2 a = rotate_pair(rope, rr.pos, f0, s[0][0], s[0][1]);
-                const float2 c = rotate_pair(rope, rr.pos, f0 + 2, s[0][2], s[0][3]);
-                *reinterpret_cast<float4*>(grp.out[0] + (size_t)bb * grp.d[0] + f0) = make_float4(a.x, a.y, c.x, c.y);
-            }
-            if (f0 < grp.d[1]) {
-                if (rr.page_ok) {
-                    const size_t o = (size_t)rr.page * rope.page_stride + rope.layer_off +
-                                     (size_t)rr.in_page * grp.d[1] + f0;
-                    const float2 a = rotate_pair(rope, rr.pos, f0, s[1][0], s[1][1]);
-                    const float2 c = rotate_pair(rope, rr.pos, f0 + 2, s[1][2], s[1][3]);
-                    *reinterpret_cast<float4*>(rope.k_pool + o) = make_float4(a.x, a.y, c.x, c.y);
-                    *reinterpret_cast<float4*>(rope.v_pool + o) = make_float4(s[2][0], s[2][1], s[2][2], s[2][3]);
-                } else if (f0 == 0) {
-                    atomicAdd(rope.bad_pages, 1);  // once per row: the lane holding feature 0
-                }
-            }
-            continue;
-        }
-        if constexpr (RESID) {
-            // x[bb][row] += product; the squares of the tile's 16 new entries
-            // of row bb are summed over the four lane groups (rows 4*(l/16) + j)
-            float ssq = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int row = row0 + 4 * (lane >> 4) + j;
-                if (bb < batch && row < grp.d[0]) {
-                    float* xe = grp.out[0] + (size_t)bb * grp.d[0] + row;
-                    const float v = *xe + s[0][j];
-                    *xe = v;
-                    ssq = fmaf(v, v, ssq);
-                }
-            }
-            ssq = sum_over_rows(ssq);
-            if (lane < 16 && bb < batch) resid.ss[(size_t)blockIdx.x * resid.ss_stride + bb] = ssq;
-        } else {
-            if (bb >= batch) continue;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int row = row0 + 4 * (lane >> 4) + j;
-                if constexpr (SWIGLU) {
-                    if (row < grp.d[0]) {
-                        float h = s[0][j];
-                        h *= 1.0f / (1.0f + expf(-h));
-                        grp.out[0][(size_t)bb * grp.d[0] + row] = h * s[1][j];
-                    }
-                } else {
-#pragma unroll
-                    for (int m = 0; m < NMAT; m++)
-                        if (row < grp.d[m]) grp.out[m][(size_t)bb * grp.d[m] + row] = s[m][j];
-                }
-            }
-        }
+        store_mma_tile<NMAT, SWIGLU, RESID, ROPE>(grp, resid, rope, s, row0, blockIdx.x, b0 + t * 16 + (lane & 15),
+                                                  batch, lane);
     }
+}
+
+// matmul_bulk (src/model_q8.cpp:382-420: each output row keeps only its last
+// 32-column block, the block loop storing over the previous block's sum) for
+// more than 4 activation rows.  A workgroup covers 16 output rows (of each
+// group member) and 64 batch rows, one wave per batch tile of 16.  Every load
+// a wave needs goes out at its start, in one round trip: the rows' last
+// blocks (lane (r, g): weights 8g..8g+7 of row row0 + r and the row's scale),
+// x of batch row 16t + r at the same 8 k, and with the norm folded in that
+// row's norm weights and rms partials (lane group g adding partials g, g + 4,
+// ..., the four groups then summed by permutes).  Eight fp32 MFMAs per member
+// cover the block (MFMA j takes k = 8g + j in k-slot g), and each wave runs
+// the epilogue on its own tile: no reduction across waves, no barrier.  (The
+// general kernel above ran the block on one wave of four, half its 16 MFMAs on
+// zeros, behind the partials' round trip and three barriers.)
+template <int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
+__global__ __launch_bounds__(64 * Q8_WAVES) void q8_last_kernel(Q8Group grp, const float* __restrict__ x, int batch,
+                                                                 int n, Q8Norm nm, Q8Resid resid, Q8Rope rope) {
+    static_assert(Q8_MAX_BTILES == Q8_WAVES, "the launch grid gives each launch row one wave per batch tile");
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int row0 = blockIdx.x * 16;
+    const int t = blockIdx.y * Q8_WAVES + wave;  // this wave's batch tile
+    if (t * 16 >= batch) return;                 // wave-uniform; the kernel has no barrier
+    const int nb = n / Q8_BLOCK;
+    const int k0 = (nb - 1) * Q8_BLOCK + 8 * g;  // the lane's 8 k of the last block
+    const int bx = min(t * 16 + r, batch - 1);   // the batch row it feeds (clamped: never stored)
+    uint32_t q[NMAT][2];
+    float sc[NMAT];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+        const uint8_t* bp = grp.w[m] + ((size_t)min(row0 + r, grp.d[m] - 1) * nb + nb - 1) * Q8_BLOCK_BYTES;
+        const uint32_t* qp = reinterpret_cast<const uint32_t*>(bp + 4 + 8 * g);
+        q[m][0] = qp[0];
+        q[m][1] = qp[1];
+        sc[m] = *reinterpret_cast<const float*>(bp);
+    }
+    const float4* xp = reinterpret_cast<const float4*>(x + (size_t)bx * n + k0);
+    const float4 xa = xp[0], xb = xp[1];
+    float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    if constexpr (NORM) {
+        const float4* wp = reinterpret_cast<const float4*>(nm.weight + k0);
+        const float4 wa = wp[0], wb = wp[1];
+        const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+        const float inv = inv_rms(sum_over_rows(partial_sum(nm, bx, g, 4)), n);
+#pragma unroll
+        for (int j = 0; j < 8; j++) xv[j] = wv[j] * (inv * xv[j]);
+    }
+    f32x4 s[NMAT];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+        s[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (row0 >= grp.d[m]) continue;  // uniform: no rows of member m in this tile
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            s[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(dequant(q[m][j >> 2], j & 3, sc[m]), xv[j], s[m], 0, 0, 0);
+    }
+    store_mma_tile<NMAT, SWIGLU, RESID, ROPE>(grp, resid, rope, s, row0, blockIdx.x, t * 16 + r, batch, lane);
 }
 
 // Batches of 1..NB rows on the VALU: lane (r, g) dots its 16 weights of row
@@ -1488,8 +1559,8 @@ void launch_group(const Q8Group& grp, const float* x, int batch, int n, int dmax
     }
     const dim3 block(64 * Q8_WAVES);
     if (last)
-        hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, true, NORM, RESID, ROPE>), grid, block, 0, stream, grp,
-                           x, batch, n, nm, rs, rp);
+        hipLaunchKernelGGL((q8_last_kernel<NMAT, SWIGLU, NORM, RESID, ROPE>), grid, block, 0, stream, grp, x, batch,
+                           n, nm, rs, rp);
     else
         hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, false, NORM, RESID, ROPE>), grid, block, 0, stream, grp,
                            x, batch, n, nm, rs, rp);
