@@ -13,16 +13,16 @@
 //    32 columns of every row reach the output.
 //
 // Kernels, by activation rows and semantics (the launcher picks):
-//  - 1..4 rows: VALU dot products.  Full rows of >= 2048 k take
+//  - last block only, any rows: q8_last_kernel on v_mfma_f32_16x16x4_f32
+//    (fp32 in, fp32 accumulate), one wave per 16 activation rows.
+//  - full rows, 1..4 rows: VALU dot products.  Rows of >= 2048 k take
 //    q8_flat_kernel when the activations fit its LDS (batch x n <= 16384
-//    floats), else q8_rowdot_kernel; q8_gemv_kernel covers short rows and the
-//    last-block form.
-//  - more rows, full rows: q8_mma_kernel, the bf16 matrix cores at fp32
+//    floats), else q8_rowdot_kernel; q8_gemv_kernel covers short rows.
+//  - full rows, more rows: q8_mma_kernel, the bf16 matrix cores at fp32
 //    accuracy (x split into three exact bf16 parts), over the model's
 //    tile-layout copy of the matrix when there is one (Q8Tiled) or the BlockQ8
-//    rows otherwise.
-//  - more rows, last block only (and NITRO_Q8_MMA=f32): q8_matmul_kernel on
-//    v_mfma_f32_16x16x4_f32 (fp32 in, fp32 accumulate).
+//    rows otherwise; q8_matmul_kernel on v_mfma_f32_16x16x4_f32 under
+//    NITRO_Q8_MMA=f32 or where the bf16 kernel's 32-bit offsets do not fit.
 // Each kernel's comment gives its lane layout.
 //
 // A launch may cover a group of up to 3 matrices with the same input x and
@@ -259,7 +259,7 @@ __device__ __forceinline__ void store_mma_tile(const Q8Group& grp, const Q8Resid
 // lane).  The four waves take chunks round-robin (U at a time, loads issued
 // before use) and add their partial tiles through LDS.  Batches of more than
 // 16 rows reuse the dequantised weights for every 16-row batch tile.
-template <int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY, bool NORM, bool RESID, bool ROPE>
+template <int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
 __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, const float* __restrict__ x,
                                                                    int batch, int n, Q8Norm nm, Q8Resid resid,
                                                                    Q8Rope rope) {
@@ -302,14 +302,13 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
 #pragma unroll
         for (int t = 0; t < Q8_MAX_BTILES; t++) acc[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int first = LAST_BLOCK_ONLY ? nchunk - 1 : 0;
-    // Wave w takes chunks first + (round*Q8_WAVES + w)*U + u.
-    for (int base = first + wave * U; base < nchunk; base += Q8_WAVES * U) {
+    // Wave w takes chunks (round*Q8_WAVES + w)*U + u.
+    for (int base = wave * U; base < nchunk; base += Q8_WAVES * U) {
         Q8Slice sl[U][NMAT];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int blk = 2 * (base + u) + (g >> 1);
-            const bool valid = base + u < nchunk && blk < nb && (!LAST_BLOCK_ONLY || blk == nb - 1);
+            const bool valid = base + u < nchunk && blk < nb;
 #pragma unroll
             for (int m = 0; m < NMAT; m++) sl[u][m] = load_slice(wrow[m], blk, g & 1, valid && act[m]);
         }
@@ -323,7 +322,7 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int blk = 2 * (base + u) + (g >> 1);
-                const bool valid = base + u < nchunk && blk < nb && (!LAST_BLOCK_ONLY || blk == nb - 1);
+                const bool valid = base + u < nchunk && blk < nb;
                 if (valid && bb < batch) {
                     const int k0 = blk * Q8_BLOCK + 16 * (g & 1);
                     const float4* xp = reinterpret_cast<const float4*>(x + (size_t)bb * n + k0);
@@ -401,8 +400,8 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
 }
 
 // matmul_bulk (src/model_q8.cpp:382-420: each output row keeps only its last
-// 32-column block, the block loop storing over the previous block's sum) for
-// more than 4 activation rows.  A workgroup covers 16 output rows (of each
+// 32-column block, the block loop storing over the previous block's sum), for
+// any number of activation rows.  A workgroup covers 16 output rows (of each
 // group member) and 64 batch rows, one wave per batch tile of 16.  Every load
 // a wave needs goes out at its start, in one round trip: the rows' last
 // blocks (lane (r, g): weights 8g..8g+7 of row row0 + r and the row's scale),
@@ -410,9 +409,11 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_matmul_kernel(Q8Group grp, c
 // row's norm weights and rms partials (lane group g adding partials g, g + 4,
 // ..., the four groups then summed by permutes).  Eight fp32 MFMAs per member
 // cover the block (MFMA j takes k = 8g + j in k-slot g), and each wave runs
-// the epilogue on its own tile: no reduction across waves, no barrier.  (The
-// general kernel above ran the block on one wave of four, half its 16 MFMAs on
-// zeros, behind the partials' round trip and three barriers.)
+// the epilogue on its own tile: no reduction across waves, no barrier.  (As a
+// mode of the full-row kernels, q8_matmul_kernel ran the block on one wave of
+// four, half its 16 MFMAs on zeros, behind the partials' round trip and three
+// barriers, and q8_gemv_kernel staged the block's x through LDS: continuous
+// batching at 32 users took 22.8-23.7 ms per run then, 18.8-20.0 now.)
 template <int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
 __global__ __launch_bounds__(64 * Q8_WAVES) void q8_last_kernel(Q8Group grp, const float* __restrict__ x, int batch,
                                                                  int n, Q8Norm nm, Q8Resid resid, Q8Rope rope) {
@@ -474,7 +475,7 @@ constexpr int GEMV_WAVES = 8;
 #ifndef NITRO_GEMV_UNROLL
 #define NITRO_GEMV_UNROLL 8
 #endif
-template <int NB, int NMAT, bool SWIGLU, bool LAST_BLOCK_ONLY, bool NORM, bool RESID, bool ROPE>
+template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
 __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, const float* __restrict__ x,
                                                                    int n, Q8Norm nm, Q8Resid resid, Q8Rope rope) {
     // chunks in flight per wave: a slab covers 4096 k of one matrix (2048 of a group)
@@ -515,15 +516,13 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, c
 #pragma unroll
         for (int b = 0; b < NB; b++) acc[m][b] = 0.0f;
 
-    // In the last-block form only the final chunk matters: one slab holding it.
-    const int k_begin = LAST_BLOCK_ONLY ? (nchunk - 1) * 64 : 0;
-    for (int slab = k_begin; slab < n; slab += SLAB) {
+    for (int slab = 0; slab < n; slab += SLAB) {
         const int c0 = slab / 64 + wave * U;  // this wave's first chunk
         Q8Slice sl[U][NMAT];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int blk = 2 * (c0 + u) + (g >> 1);
-            const bool valid = c0 + u < nchunk && blk < nb && (!LAST_BLOCK_ONLY || blk == nb - 1);
+            const bool valid = c0 + u < nchunk && blk < nb;
 #pragma unroll
             for (int m = 0; m < NMAT; m++) sl[u][m] = load_slice(wrow[m], blk, g & 1, valid && act[m]);
         }
@@ -544,7 +543,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q8_gemv_kernel(Q8Group grp, c
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int blk = 2 * (c0 + u) + (g >> 1);
-            const bool valid = c0 + u < nchunk && blk < nb && (!LAST_BLOCK_ONLY || blk == nb - 1);
+            const bool valid = c0 + u < nchunk && blk < nb;
             if (!valid) continue;  // no cross-lane work inside the chunk loop
             const int kl = blk * Q8_BLOCK + 16 * (g & 1) - slab;  // k within the slab
 #pragma unroll
@@ -1464,12 +1463,12 @@ bool launch_flat(const Q8Group& grp, const float* x, int n, int dmax, const Q8No
 }
 
 template <int NB, int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
-void launch_gemv(const Q8Group& grp, const float* x, int n, int dmax, bool last, const Q8Norm& nm,
-                 const Q8Resid& rs, const Q8Rope& rp, hipStream_t stream) {
-    if (!last && n >= ROWDOT_MIN_N && gemv_choice() == 2 &&
+void launch_gemv(const Q8Group& grp, const float* x, int n, int dmax, const Q8Norm& nm, const Q8Resid& rs,
+                 const Q8Rope& rp, hipStream_t stream) {
+    if (n >= ROWDOT_MIN_N && gemv_choice() == 2 &&
         launch_flat<NB, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, nm, rs, rp, stream))
         return;
-    if (!last && n >= ROWDOT_MIN_N && gemv_choice() >= 1) {
+    if (n >= ROWDOT_MIN_N && gemv_choice() >= 1) {
         constexpr int ROWS = ROWDOT_SETS * 4 * rowdot_rows<NB, NMAT>();
         const int ntiles = (dmax + ROWS - 1) / ROWS;
         const dim3 grid((unsigned)std::min(ntiles, ROWDOT_MAX_GROUPS)), block(512);
@@ -1478,12 +1477,8 @@ void launch_gemv(const Q8Group& grp, const float* x, int n, int dmax, bool last,
         return;
     }
     const dim3 grid((unsigned)((dmax + 15) / 16)), block(64 * GEMV_WAVES);
-    if (last)
-        hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, true, NORM, RESID, ROPE>), grid, block, 0, stream,
-                           grp, x, n, nm, rs, rp);
-    else
-        hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, false, NORM, RESID, ROPE>), grid, block, 0, stream,
-                           grp, x, n, nm, rs, rp);
+    hipLaunchKernelGGL((q8_gemv_kernel<NB, NMAT, SWIGLU, NORM, RESID, ROPE>), grid, block, 0, stream, grp, x, n, nm,
+                       rs, rp);
 }
 
 template <int NMAT, bool TILED, bool SWIGLU, bool NORM, bool RESID, bool ROPE>
@@ -1534,21 +1529,27 @@ __global__ __launch_bounds__(64) void q8_tile_kernel(const uint8_t* __restrict__
 template <int NMAT, bool SWIGLU, bool NORM, bool RESID, bool ROPE = false>
 void launch_group(const Q8Group& grp, const float* x, int batch, int n, int dmax, bool last, const Q8Norm& nm,
                   const Q8Resid& rs, hipStream_t stream, const Q8Rope& rp = Q8Rope{}) {
+    const dim3 grid((unsigned)((dmax + 15) / 16),
+                    (unsigned)((batch + 16 * Q8_MAX_BTILES - 1) / (16 * Q8_MAX_BTILES)));
+    const dim3 block(64 * Q8_WAVES);
+    if (last) {
+        hipLaunchKernelGGL((q8_last_kernel<NMAT, SWIGLU, NORM, RESID, ROPE>), grid, block, 0, stream, grp, x, batch,
+                           n, nm, rs, rp);
+        return;
+    }
     if (batch <= Q8_GEMV_MAX_BATCH) {
         switch (batch) {
-            case 1: launch_gemv<1, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, last, nm, rs, rp, stream); break;
-            case 2: launch_gemv<2, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, last, nm, rs, rp, stream); break;
-            case 3: launch_gemv<3, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, last, nm, rs, rp, stream); break;
-            default: launch_gemv<4, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, last, nm, rs, rp, stream); break;
+            case 1: launch_gemv<1, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, nm, rs, rp, stream); break;
+            case 2: launch_gemv<2, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, nm, rs, rp, stream); break;
+            case 3: launch_gemv<3, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, nm, rs, rp, stream); break;
+            default: launch_gemv<4, NMAT, SWIGLU, NORM, RESID, ROPE>(grp, x, n, dmax, nm, rs, rp, stream); break;
         }
         return;
     }
-    const dim3 grid((unsigned)((dmax + 15) / 16),
-                    (unsigned)((batch + 16 * Q8_MAX_BTILES - 1) / (16 * Q8_MAX_BTILES)));
     // the bf16 kernel addresses weights and x with 32-bit offsets
     const bool mma_fits = q8_tiled_bytes(dmax, n) < (1ull << 32) && (size_t)batch * n < (1ull << 32) &&
                           (!NORM || n <= MMA_NORM_MAX_N);
-    if (!last && use_mma() && mma_fits) {
+    if (use_mma() && mma_fits) {
         bool tiled = true;
         for (int m = 0; m < NMAT; m++) tiled = tiled && grp.wt[m] != nullptr;
         if (tiled)
@@ -1557,13 +1558,8 @@ void launch_group(const Q8Group& grp, const float* x, int batch, int n, int dmax
             launch_mma<NMAT, false, SWIGLU, NORM, RESID, ROPE>(grp, x, batch, n, dmax, nm, rs, rp, stream);
         return;
     }
-    const dim3 block(64 * Q8_WAVES);
-    if (last)
-        hipLaunchKernelGGL((q8_last_kernel<NMAT, SWIGLU, NORM, RESID, ROPE>), grid, block, 0, stream, grp, x, batch,
-                           n, nm, rs, rp);
-    else
-        hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, false, NORM, RESID, ROPE>), grid, block, 0, stream, grp,
-                           x, batch, n, nm, rs, rp);
+    hipLaunchKernelGGL((q8_matmul_kernel<NMAT, SWIGLU, NORM, RESID, ROPE>), grid, block, 0, stream, grp, x, batch, n,
+                       nm, rs, rp);
 }
 
 }  // namespace
