@@ -449,6 +449,21 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_last_kernel(Q8Group grp, con
 #pragma unroll
         for (int j = 0; j < 8; j++) xv[j] = wv[j] * (inv * xv[j]);
     }
+    // RoPE: the lane's output features f0..f0+3 (two pairs of one head) of
+    // batch row bx.  Its position and slot, and the pairs' cos / sin, load
+    // here too, so their two dependent round trips overlap the products'
+    // loads (the wq/wk/wv launch at 32 rows: 4.47 -> 4.30 us).
+    const int f0 = row0 + 4 * g;
+    RopeRow rr{};
+    float rc[2] = {0.f, 0.f}, rs[2] = {0.f, 0.f};
+    if constexpr (ROPE) {
+        rr = rope_row(rope, bx);
+        const size_t fi = (size_t)rr.pos * (rope.head_dim >> 1) + ((f0 % rope.head_dim) >> 1);
+        rc[0] = rope.freq_real[fi];
+        rs[0] = rope.freq_imag[fi];
+        rc[1] = rope.freq_real[fi + 1];
+        rs[1] = rope.freq_imag[fi + 1];
+    }
     f32x4 s[NMAT];
 #pragma unroll
     for (int m = 0; m < NMAT; m++) {
@@ -458,7 +473,32 @@ __global__ __launch_bounds__(64 * Q8_WAVES) void q8_last_kernel(Q8Group grp, con
         for (int j = 0; j < 8; j++)
             s[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(dequant(q[m][j >> 2], j & 3, sc[m]), xv[j], s[m], 0, 0, 0);
     }
-    store_mma_tile<NMAT, SWIGLU, RESID, ROPE>(grp, resid, rope, s, row0, blockIdx.x, t * 16 + r, batch, lane);
+    if constexpr (ROPE) {
+        // store_mma_tile's RoPE epilogue on the prefetched angles
+        // (rotate_pair's (x*c - y*sn, x*sn + y*c))
+        const int bb = t * 16 + r;
+        if (bb >= batch) return;
+        auto rot = [&](int p, float u, float v) { return make_float2(u * rc[p] - v * rs[p], u * rs[p] + v * rc[p]); };
+        if (f0 < grp.d[0]) {
+            const float2 a = rot(0, s[0][0], s[0][1]);
+            const float2 c = rot(1, s[0][2], s[0][3]);
+            *reinterpret_cast<float4*>(grp.out[0] + (size_t)bb * grp.d[0] + f0) = make_float4(a.x, a.y, c.x, c.y);
+        }
+        if (f0 < grp.d[1]) {
+            if (rr.page_ok) {
+                const size_t o = (size_t)rr.page * rope.page_stride + rope.layer_off +
+                                 (size_t)rr.in_page * grp.d[1] + f0;
+                const float2 a = rot(0, s[1][0], s[1][1]);
+                const float2 c = rot(1, s[1][2], s[1][3]);
+                *reinterpret_cast<float4*>(rope.k_pool + o) = make_float4(a.x, a.y, c.x, c.y);
+                *reinterpret_cast<float4*>(rope.v_pool + o) = make_float4(s[2][0], s[2][1], s[2][2], s[2][3]);
+            } else if (f0 == 0) {
+                atomicAdd(rope.bad_pages, 1);  // once per row: the lane holding feature 0
+            }
+        }
+    } else {
+        store_mma_tile<NMAT, SWIGLU, RESID, ROPE>(grp, resid, rope, s, row0, blockIdx.x, t * 16 + r, batch, lane);
+    }
 }
 
 // Batches of 1..NB rows on the VALU: lane (r, g) dots its 16 weights of row
