@@ -1064,16 +1064,29 @@ def capture_step(torch, w):
 CONFIG_WORKLOADS = ["decode-single-110m", "decode-b32-mixed", "prefill-b8-12x64", "decode-prefix-shared"]
 
 
+# Untimed GPU work before each timed pass of a HIP graph.  The GPU's clocks
+# drop while it idles (the host's checks between passes, the one-wave spin
+# kernel that lets the host enqueue the replays) and take about 20 ms of
+# sustained work to come back: in a kernel trace of 1200 launches of the
+# 8-prompt prefill, each pass began at about 55 us per launch and settled at
+# 44-45 us.  A pass of short launches (240 launches of ~46 us are 11 ms) would
+# otherwise time that ramp rather than the kernel.
+WARM_MS = 30.0
+
+
 def measure(torch, w, dev, g, steps, warmup):
     """Sets the workload up, runs `warmup` untimed steps, then the timed ones.
 
     Three forms, by workload:
       graph  a step's launches captured as one HIP graph (many short launches):
-             `steps` replays back to back under the wall clock (ms_per_step),
-             each checked bit for bit against the eager step; then, behind a
-             spin kernel that lets the host enqueue every replay first, another
-             `steps` replays between one pair of HIP events on the launch
-             stream: kernel_ms = that time / (steps * launches per step)
+             a first pass of `steps` replays sizes the warm-up, w.warm_replays
+             = enough replays for WARM_MS of GPU work; then that many untimed
+             replays and `steps` replays back to back under the wall clock
+             (ms_per_step), each checked bit for bit against the eager step;
+             then, behind a spin kernel that lets the host enqueue every replay
+             first, the warm replays again and another `steps` replays between
+             one pair of HIP events on the launch stream: kernel_ms = that time
+             / (steps * launches per step)
       flush  a cache flush before every launch, and an event pair around each
              launch (only the launches are timed)
       eager  `steps` steps back to back under the wall clock, then `steps` more
@@ -1093,10 +1106,22 @@ def measure(torch, w, dev, g, steps, warmup):
         for _ in range(steps):
             graph.replay()
         torch.cuda.synchronize()
+        per_replay_ms = (time.perf_counter() - t0) / steps * 1e3
+        warm = int(min(4000, max(warmup, np.ceil(WARM_MS / max(per_replay_ms, 1e-3)))))
+        w.warm_replays = warm
+        for _ in range(warm):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+        torch.cuda.synchronize()
         ms_per_step = (time.perf_counter() - t0) / (steps * reps) * 1e3
         w.check_graph_replay()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(spin_cycles(torch, 5.0 + 0.05 * steps))
+        torch.cuda._sleep(spin_cycles(torch, 5.0 + 0.05 * (warm + steps)))
+        for _ in range(warm):
+            graph.replay()
         a.record(stream)
         for _ in range(steps):
             graph.replay()
@@ -1139,7 +1164,8 @@ def measure(torch, w, dev, g, steps, warmup):
 TIMING = {
     "graph": "one HIP graph of {reps} step(s) of {nl} launch(es); kernel_ms = the time of {steps} "
              "back-to-back replays between one event pair on the launch stream / ({steps} x {reps} x {nl} "
-             "launches)",
+             "launches), after {warm} untimed replays (about 30 ms of GPU work, so the clocks are at their "
+             "steady state)",
     "flush": "an event pair around each launch, a 1 GiB read before it (not timed)",
     "run": "an event pair around each run",
     "eager": "an event pair around each launch, the launches queued behind a spin kernel",
@@ -1185,7 +1211,8 @@ def config_entry(torch, name, dev, args):
                     if name in TRAFFIC_PROFILES else None),
         "step_rate": round(step_rate, 2 if unit == "GB/s" else 4),
         "tokens_per_s": round(w.tokens_per_step() / (ms_per_step * 1e-3), 1),
-        "timing": TIMING[form].format(steps=args.steps, nl=nl, reps=getattr(w, "graph_reps", 1)),
+        "timing": TIMING[form].format(steps=args.steps, nl=nl, reps=getattr(w, "graph_reps", 1),
+                                      warm=getattr(w, "warm_replays", 0)),
         "parity": parity,
     }
     entry.update(w.extra(kernel_ms * 1e-3))
@@ -1287,7 +1314,8 @@ def main():
             "traffic": measured_traffic(traffic_profile) if traffic_profile else None,
             ("bytes_per_launch" if w.bound == "hbm" else "flops_per_launch"): hbm_work,
             "kernel_ms": round(kernel_ms, 5),
-            "timing": TIMING[form].format(steps=args.steps, nl=nl, reps=getattr(w, "graph_reps", 1)),
+            "timing": TIMING[form].format(steps=args.steps, nl=nl, reps=getattr(w, "graph_reps", 1),
+                                          warm=getattr(w, "warm_replays", 0)),
         },
         "parity": parity,
         "cpu_baseline": None,
